@@ -1,0 +1,258 @@
+// capi.hip -- extern "C" entry points declared in include/cxxgpt_attn.h:
+// argument checks, workspace handling and dispatch to the kernel launchers.
+#include "../../include/cxxgpt_attn.h"
+#include "launch.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <limits.h>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace cxg {
+
+// ---------------------------------------------------------------------------
+// timing hook
+// ---------------------------------------------------------------------------
+namespace {
+struct ProfRec {
+    hipEvent_t a, b;
+    std::string name;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRec> g_prof_recs;
+std::vector<hipEvent_t> g_prof_free;
+
+hipEvent_t prof_event()
+{
+    hipEvent_t e = nullptr;
+    if (!g_prof_free.empty()) {
+        e = g_prof_free.back();
+        g_prof_free.pop_back();
+        return e;
+    }
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+} // namespace
+
+bool prof_enabled() { return g_prof_on; }
+
+int prof_begin(hipStream_t s)
+{
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    ProfRec r;
+    r.a = prof_event();
+    r.b = prof_event();
+    if (!r.a || !r.b)
+        return -1;
+    (void)hipEventRecord(r.a, s);
+    g_prof_recs.push_back(r);
+    return (int)g_prof_recs.size() - 1;
+}
+
+void prof_end(int token, hipStream_t s, const char* name)
+{
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    if (token < 0 || token >= (int)g_prof_recs.size())
+        return;
+    g_prof_recs[token].name = name;
+    (void)hipEventRecord(g_prof_recs[token].b, s);
+}
+
+// ---------------------------------------------------------------------------
+// status helpers
+// ---------------------------------------------------------------------------
+static thread_local int t_last_hip = 0;
+
+static int hip_status(hipError_t e)
+{
+    if (e == hipSuccess)
+        return CXG_OK;
+    t_last_hip = (int)e;
+    return CXG_ERR_HIP;
+}
+
+static bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
+
+// Stream-ordered scratch: caller memory if provided, else hipMallocAsync for
+// the duration of the call.
+struct Scratch {
+    void* p = nullptr;
+    bool owned = false;
+    hipStream_t st = nullptr;
+    int acquire(void* ws, size_t ws_bytes, size_t need, hipStream_t s)
+    {
+        st = s;
+        if (need == 0)
+            return CXG_OK;
+        if (ws != nullptr) {
+            if (ws_bytes < need)
+                return CXG_ERR_WORKSPACE;
+            p = ws;
+            return CXG_OK;
+        }
+        hipError_t e = hipMallocAsync(&p, need, s);
+        if (e != hipSuccess) {
+            t_last_hip = (int)e;
+            p = nullptr;
+            return CXG_ERR_WORKSPACE;
+        }
+        owned = true;
+        return CXG_OK;
+    }
+    ~Scratch()
+    {
+        if (owned && p)
+            (void)hipFreeAsync(p, st);
+    }
+};
+
+static size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+} // namespace cxg
+
+using namespace cxg;
+
+extern "C" {
+
+const char* cxg_status_str(int status)
+{
+    switch (status) {
+    case CXG_OK: return "ok";
+    case CXG_ERR_NULL: return "null pointer argument";
+    case CXG_ERR_DIMS: return "invalid dimensions";
+    case CXG_ERR_HEAD_DIM: return "head_dim > 256 not supported";
+    case CXG_ERR_HIP: return "HIP runtime error";
+    case CXG_ERR_WORKSPACE: return "workspace too small or allocation failed";
+    default: return "unknown status";
+    }
+}
+
+int cxg_last_hip_error(void) { return t_last_hip; }
+
+const char* cxg_version(void) { return "cxxgpt-attn-gfx950 0.1"; }
+
+// ---------------------------------------------------------------------------
+// softmax MHA
+// ---------------------------------------------------------------------------
+static int mha_check(size_t B, size_t S, size_t H, size_t Dh, bool* empty)
+{
+    *empty = (B == 0 || S == 0 || H == 0);
+    if (Dh == 0)
+        return CXG_ERR_DIMS;
+    if (Dh > 256)
+        return CXG_ERR_HEAD_DIM;
+    if (*empty)
+        return CXG_OK;
+    if (!fits_int(B) || !fits_int(S) || !fits_int(H) || !fits_int(B * H))
+        return CXG_ERR_DIMS;
+    const size_t ntile = (S + 63) / 64;
+    // grid x = tiles * B * H workgroups of 256 threads must stay below 2^32 threads
+    if (ntile * B * H > ((size_t)1 << 23))
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+int cxg_mha_fwd(const float* Q, const float* K, const float* V, float* O, float* lse,
+                size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream)
+{
+    bool empty;
+    int st = mha_check(B, S, H, Dh, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O)
+        return CXG_ERR_NULL;
+    return hip_status(mha_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)H, (int)Dh,
+                                     (hipStream_t)stream));
+}
+
+size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh)
+{
+    (void)Dh;
+    const size_t rows = B * H * S;
+    return 2 * round_up(rows * sizeof(float), 256);
+}
+
+int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
+                const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                size_t B, size_t S, size_t H, size_t Dh, void* workspace,
+                size_t workspace_bytes, cxg_stream_t stream)
+{
+    bool empty;
+    int st = mha_check(B, S, H, Dh, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t half = round_up(B * H * S * sizeof(float), 256);
+    Scratch ws;
+    st = ws.acquire(workspace, workspace_bytes, cxg_mha_bwd_workspace_size(B, S, H, Dh), s);
+    if (st != CXG_OK)
+        return st;
+    float* Di = (float*)ws.p;
+    float* lse_ws = (float*)((char*)ws.p + half);
+    const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
+    hipError_t e;
+    if (lse == nullptr) {
+        // statistics-only forward pass (the reference recomputes them too)
+        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s);
+        if (e != hipSuccess)
+            return hip_status(e);
+        lse = lse_ws;
+    }
+    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
+    if (e != hipSuccess)
+        return hip_status(e);
+    e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s);
+    return hip_status(e);
+}
+
+// ---------------------------------------------------------------------------
+// timing hook
+// ---------------------------------------------------------------------------
+void cxg_prof_enable(int on)
+{
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof_on = on != 0;
+}
+
+void cxg_prof_reset(void)
+{
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    for (auto& r : g_prof_recs) {
+        (void)hipEventSynchronize(r.b);
+        g_prof_free.push_back(r.a);
+        g_prof_free.push_back(r.b);
+    }
+    g_prof_recs.clear();
+}
+
+int cxg_prof_query(const char* kernel_name, double* total_ms, int* count)
+{
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    double tot = 0.0;
+    int n = 0;
+    for (auto& r : g_prof_recs) {
+        if (r.name != kernel_name)
+            continue;
+        (void)hipEventSynchronize(r.b);
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+            tot += ms;
+            n++;
+        }
+    }
+    if (total_ms)
+        *total_ms = tot;
+    if (count)
+        *count = n;
+    return n > 0 ? 0 : -1;
+}
+
+} // extern "C"

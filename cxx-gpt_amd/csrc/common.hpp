@@ -1,0 +1,107 @@
+// common.hpp -- device helpers shared by the gfx950 attention kernels.
+//
+// MFMA fragment convention used throughout (v_mfma_f32_16x16x4_f32, wave64):
+//   lane l, l16 = l % 16, g = l / 16
+//   A operand (16 x 4):  lane l holds A[i = l16][k = g]
+//   B operand (4 x 16):  lane l holds B[k = g][j = l16]
+//   C/D (16 x 16, f4):   lane l, element r holds D[i = 4*g + r][j = l16]
+// A contraction over a long axis is split into 4-wide steps; which physical
+// index feeds (instruction, k-slot) is free as long as A and B agree, and the
+// kernels pick the mapping that lets an accumulator feed the next MFMA
+// directly: instruction r, k-slot g <-> index 4*g + r of a 16-block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cxg {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma16(float a, float b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f4 f4zero()
+{
+    f4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+    return z;
+}
+
+__device__ __forceinline__ f4 f4splat(float v)
+{
+    f4 z = {v, v, v, v};
+    return z;
+}
+
+// 2^x on the hardware transcendental unit (v_exp_f32); 2^-inf = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Sum / max over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float xrow_sum(float v)
+{
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+__device__ __forceinline__ float xrow_max(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+// Sum over the 16 lanes of one row (lanes sharing l / 16).
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += __shfl_xor(v, 8, 64);
+    v += __shfl_xor(v, 4, 64);
+    v += __shfl_xor(v, 2, 64);
+    v += __shfl_xor(v, 1, 64);
+    return v;
+}
+
+// Guarded 4-wide load of row[c..c+3] (columns >= n read as 0).  VEC requires
+// the row base to be 16-byte aligned and n % 4 == 0.
+template <bool VEC>
+__device__ __forceinline__ f4 load4(const float* __restrict__ row, int c, int n, bool ok)
+{
+    f4 v = f4zero();
+    if (!ok)
+        return v;
+    if (VEC) {
+        if (c < n)
+            v = *reinterpret_cast<const f4*>(row + c);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (c + i < n)
+                v[i] = row[c + i];
+    }
+    return v;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store4(float* __restrict__ row, int c, int n, f4 v)
+{
+    if (VEC) {
+        if (c < n)
+            *reinterpret_cast<f4*>(row + c) = v;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (c + i < n)
+                row[c + i] = v[i];
+    }
+}
+
+__device__ __forceinline__ void atomic_add_f32(float* p, float v)
+{
+    unsafeAtomicAdd(p, v);
+}
+
+} // namespace cxg

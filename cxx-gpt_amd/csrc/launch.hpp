@@ -1,0 +1,49 @@
+// launch.hpp -- host-side launch helpers shared by the kernel files and the
+// C-ABI: argument checks, the optional per-kernel timing hook and the
+// internal launcher declarations.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cxg {
+
+// ---- per-kernel timing hook (off by default) --------------------------------
+// When enabled, every kernel launch is bracketed by two hipEvents recorded on
+// the launch stream; prof_query() synchronises them and reports the summed
+// device time per kernel name.  Used by the benchmark to attribute time to
+// the dominant kernel; costs nothing when disabled.
+bool prof_enabled();
+int prof_begin(hipStream_t s);
+void prof_end(int token, hipStream_t s, const char* name);
+
+struct ProfScope {
+    int tok;
+    hipStream_t s;
+    const char* name;
+    ProfScope(hipStream_t st, const char* n) : tok(-1), s(st), name(n)
+    {
+        if (prof_enabled())
+            tok = prof_begin(s);
+    }
+    ~ProfScope()
+    {
+        if (tok >= 0)
+            prof_end(tok, s, name);
+    }
+};
+
+// ---- launchers (defined next to their kernels) -----------------------------
+// Softmax MHA.  Layout (B*S, H*Dh) row-major.  lse is [B*H][S] (natural log of
+// the softmax denominator of the scaled scores, max included).
+hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                          float* lse, int B, int S, int H, int Dh, hipStream_t st);
+hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ,
+                               int B, int S, int H, int Dh, hipStream_t st);
+hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
+                               const float* dO, const float* lse, const float* Di,
+                               float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,
+                               hipStream_t st);
+
+} // namespace cxg

@@ -1,0 +1,207 @@
+"""ctypes binding of libcxxgpt_attn.so (the C ABI in include/cxxgpt_attn.h).
+
+Every call goes through the C ABI with raw device pointers, exactly as a C++
+or FFI caller would; torch is used only to own device memory and to supply
+the current HIP stream.  There is no fallback: if the library is missing
+or a call fails, an exception is raised.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libcxxgpt_attn.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "cxxgpt_attn.h")
+
+CXG_OK = 0
+CXG_ERR_NULL = 1
+CXG_ERR_DIMS = 2
+CXG_ERR_HEAD_DIM = 3
+CXG_ERR_HIP = 4
+CXG_ERR_WORKSPACE = 5
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+
+# name -> argument types (all return int unless listed in _RESTYPES)
+SIGNATURES = {
+    "cxg_status_str": [ctypes.c_int],
+    "cxg_last_hip_error": [],
+    "cxg_version": [],
+    "cxg_mha_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
+    "cxg_mha_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz,
+                    _vp],
+    "cxg_mha_bwd_workspace_size": [_sz, _sz, _sz, _sz],
+    "cxg_kattn_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
+    "cxg_kattn_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
+    "cxg_kattn_bwd_dQ": [_vp] * 8 + [_sz] * 4 + [_vp],
+    "cxg_kattn_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
+    "cxg_lin_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
+    "cxg_lin_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
+    "cxg_lin_bwd_dQ": [_vp] * 7 + [_sz] * 4 + [_vp],
+    "cxg_lin_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
+    "cxg_phi_elu_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_phi_hexp_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_prof_enable": [ctypes.c_int],
+    "cxg_prof_reset": [],
+    "cxg_prof_query": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                       ctypes.POINTER(ctypes.c_int)],
+}
+_RESTYPES = {
+    "cxg_status_str": ctypes.c_char_p,
+    "cxg_version": ctypes.c_char_p,
+    "cxg_mha_bwd_workspace_size": ctypes.c_size_t,
+    "cxg_prof_enable": None,
+    "cxg_prof_reset": None,
+}
+
+_lib = None
+
+
+class CxgError(RuntimeError):
+    def __init__(self, fn, status, hip_err):
+        self.status = status
+        self.hip_error = hip_err
+        msg = lib().cxg_status_str(status).decode()
+        super().__init__(f"{fn} failed: status {status} ({msg}), hip error {hip_err}")
+
+
+def lib():
+    """Load the library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} not built: run __graft_entry__.build() or "
+                               f"make -C {_HERE}")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in SIGNATURES.items():
+            if not hasattr(L, name):
+                continue  # reported by missing_symbols(); calling it raises
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = L
+    return _lib
+
+
+def missing_symbols():
+    """Entry points of the binding table that the built library lacks."""
+    L = lib()
+    return [n for n in SIGNATURES if not hasattr(L, n)]
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _call(name, *args):
+    st = getattr(lib(), name)(*args)
+    if st != CXG_OK:
+        raise CxgError(name, st, lib().cxg_last_hip_error())
+    return st
+
+
+def call_status(name, *args):
+    """Raw call returning the status code (for error-path tests)."""
+    return getattr(lib(), name)(*args)
+
+
+# ------------------------------------------------------------------ softmax MHA
+def mha_fwd(Q, K, V, O, B, S, H, Dh, lse=None, stream=None):
+    _call("cxg_mha_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(lse), B, S, H, Dh,
+          _stream(stream))
+
+
+def mha_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, workspace=None, stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _call("cxg_mha_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
+          _ptr(dK), _ptr(dV), B, S, H, Dh, _ptr(workspace), ws_bytes, _stream(stream))
+
+
+def mha_bwd_workspace_size(B, S, H, Dh):
+    return lib().cxg_mha_bwd_workspace_size(B, S, H, Dh)
+
+
+# ------------------------------------------------------------------ ELU+1, two_stage API
+def kattn_fwd(Q, K, V, O, den, zc, S_buf, z_buf, B, S, D, E, stream=None):
+    _call("cxg_kattn_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(den), _ptr(zc),
+          _ptr(S_buf), _ptr(z_buf), B, S, D, E, _stream(stream))
+
+
+def kattn_bwd_step1(O, dO, den, dnum, dden, N, E, stream=None):
+    _call("cxg_kattn_bwd_step1", _ptr(O), _ptr(dO), _ptr(den), _ptr(dnum), _ptr(dden), N, E,
+          _stream(stream))
+
+
+def kattn_bwd_dQ(K, V, dnum, dden, zc, Q, dQ, S_buf, B, S, D, E, stream=None):
+    _call("cxg_kattn_bwd_dQ", _ptr(K), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(zc), _ptr(Q),
+          _ptr(dQ), _ptr(S_buf), B, S, D, E, _stream(stream))
+
+
+def kattn_bwd_dKdV(Q, K, V, dnum, dden, dK, dV, B, S, D, E, stream=None):
+    _call("cxg_kattn_bwd_dKdV", _ptr(Q), _ptr(K), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(dK),
+          _ptr(dV), B, S, D, E, _stream(stream))
+
+
+# ------------------------------------------------------------------ linear_cuda API
+def lin_fwd(Qp, Kp, V, O, den, zc, S_buf, z_buf, B, S, D, E, stream=None):
+    _call("cxg_lin_fwd", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(den), _ptr(zc),
+          _ptr(S_buf), _ptr(z_buf), B, S, D, E, _stream(stream))
+
+
+def lin_bwd_step1(O, dO, den, dnum, dden, N, E, stream=None):
+    _call("cxg_lin_bwd_step1", _ptr(O), _ptr(dO), _ptr(den), _ptr(dnum), _ptr(dden), N, E,
+          _stream(stream))
+
+
+def lin_bwd_dQ(Kp, V, dnum, dden, zc, dQp, S_buf, B, S, D, E, stream=None):
+    _call("cxg_lin_bwd_dQ", _ptr(Kp), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(zc), _ptr(dQp),
+          _ptr(S_buf), B, S, D, E, _stream(stream))
+
+
+def lin_bwd_dKdV(Qp, Kp, V, dnum, dden, dKp, dV, B, S, D, E, stream=None):
+    _call("cxg_lin_bwd_dKdV", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(dKp),
+          _ptr(dV), B, S, D, E, _stream(stream))
+
+
+def phi_elu_fwd(x, phi, N, D, E, stream=None):
+    _call("cxg_phi_elu_fwd", _ptr(x), _ptr(phi), N, D, E, _stream(stream))
+
+
+def phi_elu_bwd(dphi, x, dx, N, D, E, stream=None):
+    _call("cxg_phi_elu_bwd", _ptr(dphi), _ptr(x), _ptr(dx), N, D, E, _stream(stream))
+
+
+def phi_hexp_fwd(x, phi, N, D, E, stream=None):
+    _call("cxg_phi_hexp_fwd", _ptr(x), _ptr(phi), N, D, E, _stream(stream))
+
+
+def phi_hexp_bwd(dphi, x, dx, N, D, E, stream=None):
+    _call("cxg_phi_hexp_bwd", _ptr(dphi), _ptr(x), _ptr(dx), N, D, E, _stream(stream))
+
+
+# ------------------------------------------------------------------ timing hook
+def prof_enable(on=True):
+    lib().cxg_prof_enable(1 if on else 0)
+
+
+def prof_reset():
+    lib().cxg_prof_reset()
+
+
+def prof_query(name):
+    """(total_ms, count) of the kernel launches recorded under `name`."""
+    tot = ctypes.c_double(0.0)
+    n = ctypes.c_int(0)
+    lib().cxg_prof_query(name.encode(), ctypes.byref(tot), ctypes.byref(n))
+    return tot.value, n.value

@@ -1,0 +1,165 @@
+/*
+ * cxxgpt_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Drop-in replacement for CXX-GPT's attention kernels: one entry point per
+ * C++ function the reference's callers bind (two_stage_cuda:: and
+ * linear_cuda::), taking raw device pointers, the reference's size_t
+ * dimensions and a HIP stream.  The header needs no HIP or C++ headers.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (hipMalloc'd or equivalent), fp32,
+ *     row-major, dense.  Outputs are fully overwritten.
+ *   - stream: a hipStream_t passed as void*; NULL is the legacy default
+ *     stream, which is what the reference launches on.
+ *   - Launches are asynchronous; no entry point synchronises the device.
+ *   - Return value: CXG_OK or one of the CXG_ERR_* codes below.  A call with
+ *     an error code launched nothing (except CXG_ERR_HIP, reported by the
+ *     HIP runtime at launch).
+ *   - Empty problems (B, S, H or N equal to 0) return CXG_OK and launch
+ *     nothing.
+ *
+ * Citations are relative to the reference tree (yauntyour/CXX-GPT).
+ */
+#ifndef CXXGPT_ATTN_H
+#define CXXGPT_ATTN_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *cxg_stream_t; /* hipStream_t */
+
+enum {
+    CXG_OK = 0,
+    CXG_ERR_NULL = 1,      /* a required pointer is NULL */
+    CXG_ERR_DIMS = 2,      /* a dimension is zero where it may not be, or too large */
+    CXG_ERR_HEAD_DIM = 3,  /* softmax head_dim > 256 (the reference aborts) */
+    CXG_ERR_HIP = 4,       /* the HIP runtime reported an error */
+    CXG_ERR_WORKSPACE = 5  /* workspace too small, or its allocation failed */
+};
+
+/* Human-readable name of a status code (static string). */
+const char *cxg_status_str(int status);
+/* hipError_t of the last CXG_ERR_HIP on this thread (0 if none). */
+int cxg_last_hip_error(void);
+/* Library version string. */
+const char *cxg_version(void);
+
+/* ===================== fused causal softmax MHA =====================
+ * Q/K/V/O/dO/dQ/dK/dV: (B*S, H*Dh); head h of row r at [(r*H+h)*Dh, +Dh).
+ * scale = 1/sqrt(Dh), causal mask key <= query.  1 <= Dh <= 256.
+ */
+
+/* two_stage_cuda::fused_mha_fwd (src/TwoStage/two_stage_cuda_kernels.cuh:18-20,
+ * two_stage_cuda_kernels.cu:285-326).  lse (nullable): [B*H][S] natural-log
+ * softmax normaliser of the scaled scores (row max included); passing it to
+ * cxg_mha_bwd skips the backward's statistics pass. */
+int cxg_mha_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
+                size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream);
+
+/* two_stage_cuda::fused_mha_bwd (two_stage_cuda_kernels.cuh:22-27,
+ * two_stage_cuda_kernels.cu:830-882).  lse: as written by cxg_mha_fwd, or NULL
+ * to recompute it (the reference's signature has no lse).  workspace: at least
+ * cxg_mha_bwd_workspace_size() bytes of device memory, or NULL to let the
+ * library allocate stream-ordered scratch for the call. */
+int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
+                const float *dO, const float *lse, float *dQ, float *dK, float *dV,
+                size_t B, size_t S, size_t H, size_t Dh, void *workspace,
+                size_t workspace_bytes, cxg_stream_t stream);
+size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh);
+
+/* ============ ELU+1 linear "kernel" attention, two_stage_cuda API ============
+ * phi(x) = x > 0 ? x + 1 : exp(x), fused.  Q/K (B*S, D), V/O (B*S, E); one
+ * sequence per b (multi-head callers pass B = batch*heads, head-major rows).
+ * den_cache (B*S) excludes eps; O = num / (den + 1e-8).
+ */
+
+/* two_stage_cuda::kernel_attn_fwd (two_stage_cuda_kernels.cuh:39-44,
+ * two_stage_cuda_kernels.cu:1133-1185).  z_cache (B*S, D): inclusive cumsum of
+ * phi(K).  S_buf (B*E, D) and z_buf (B, D): scratch, contents unspecified
+ * after the call (may be NULL). */
+int cxg_kattn_fwd(const float *Q, const float *K, const float *V, float *O,
+                  float *den_cache, float *z_cache, float *S_buf, float *z_buf,
+                  size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* two_stage_cuda::kernel_attn_bwd_step1 (two_stage_cuda_kernels.cuh:46-49,
+ * two_stage_cuda_kernels.cu:1190-1248): dnum = dO/den, dden = -sum_e dO*O/den. */
+int cxg_kattn_bwd_step1(const float *O, const float *dO, const float *den_cache,
+                        float *dnum, float *dden, size_t N, size_t E,
+                        cxg_stream_t stream);
+
+/* two_stage_cuda::kernel_attn_bwd_dQ (two_stage_cuda_kernels.cuh:51-55,
+ * two_stage_cuda_kernels.cu:1253-1453).  S_buf: scratch (may be NULL). */
+int cxg_kattn_bwd_dQ(const float *K, const float *V, const float *dnum,
+                     const float *dden, const float *z_cache, const float *Q, float *dQ,
+                     float *S_buf, size_t B, size_t S, size_t D, size_t E,
+                     cxg_stream_t stream);
+
+/* two_stage_cuda::kernel_attn_bwd_dKdV (two_stage_cuda_kernels.cuh:57-61,
+ * two_stage_cuda_kernels.cu:1467-1809). */
+int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
+                       const float *dnum, const float *dden, float *dK, float *dV,
+                       size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* ============ causal linear attention, linear_cuda API (phi outside) ==========
+ * Inputs are feature-mapped already: Q_phi/K_phi (B*S, D), V/O (B*S, E).
+ * State layout [d][e]; den_cache includes eps (den = phiQ.z + 1e-8).
+ */
+
+/* linear_cuda::causal_linear_attention_fwd (src/LinearAttention/
+ * linear_cuda_kernels.cuh:11-16, linear_cuda_kernels.cu:10-99).  S_buf (B*D, E)
+ * and z_buf (B, D) receive the final state (may be NULL). */
+int cxg_lin_fwd(const float *Q_phi, const float *K_phi, const float *V, float *O,
+                float *den_cache, float *z_cache, float *S_buf, float *z_buf,
+                size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* linear_cuda::causal_linear_attention_bwd_step1 (linear_cuda_kernels.cuh:18-22,
+ * linear_cuda_kernels.cu:101-150). */
+int cxg_lin_bwd_step1(const float *O, const float *dO, const float *den_cache,
+                      float *dnum, float *dden, size_t N, size_t E, cxg_stream_t stream);
+
+/* linear_cuda::causal_linear_attention_bwd_dQ (linear_cuda_kernels.cuh:24-29,
+ * linear_cuda_kernels.cu:152-215).  S_buf: scratch (may be NULL). */
+int cxg_lin_bwd_dQ(const float *K_phi, const float *V, const float *dnum,
+                   const float *dden, const float *z_cache, float *dQ_phi, float *S_buf,
+                   size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* linear_cuda::causal_linear_attention_bwd_dKdV (linear_cuda_kernels.cuh:31-37,
+ * linear_cuda_kernels.cu:217-298). */
+int cxg_lin_bwd_dKdV(const float *Q_phi, const float *K_phi, const float *V,
+                     const float *dnum, const float *dden, float *dK_phi, float *dV,
+                     size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* linear_cuda::phi_elu_forward / phi_elu_backward (linear_cuda_kernels.cuh:39-46,
+ * linear_cuda_kernels.cu:305-378).  x (N, E) -> phi (N, D), columns >= E zero;
+ * dx (N, E) = dphi[:, :E] * phi'(x). */
+int cxg_phi_elu_fwd(const float *x, float *phi, size_t N, size_t D, size_t E,
+                    cxg_stream_t stream);
+int cxg_phi_elu_bwd(const float *dphi, const float *x, float *dx, size_t N, size_t D,
+                    size_t E, cxg_stream_t stream);
+
+/* Hadamard+Exp feature map.  No counterpart in the reference's code; it
+ * plugs into the linear_cuda API the way phi_elu_* does (same argument
+ * meaning).  phi[n, 64j+i] = exp((H_64 x[n, 64j:64j+64])_i / 8) with H_64 the
+ * Sylvester Hadamard matrix; E % 64 == 0, D >= E, columns >= E zero.
+ * Backward: dx = H_64 (dphi * phi(x)) / 8 per 64-block. */
+int cxg_phi_hexp_fwd(const float *x, float *phi, size_t N, size_t D, size_t E,
+                     cxg_stream_t stream);
+int cxg_phi_hexp_bwd(const float *dphi, const float *x, float *dx, size_t N, size_t D,
+                     size_t E, cxg_stream_t stream);
+
+/* ===================== per-kernel timing hook =====================
+ * Off by default.  When on, each kernel launch is bracketed by HIP events on
+ * its stream; cxg_prof_query synchronises them and returns the summed device
+ * time (ms) and launch count for a kernel name ("mha_fwd", "mha_bwd", ...).
+ * Returns 0 if the name was seen, -1 otherwise. */
+void cxg_prof_enable(int on);
+void cxg_prof_reset(void);
+int cxg_prof_query(const char *kernel_name, double *total_ms, int *count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CXXGPT_ATTN_H */
