@@ -2,6 +2,7 @@
 // argument checks, workspace handling and dispatch to the kernel launchers.
 #include "../../include/cxxgpt_attn.h"
 #include "launch.hpp"
+#include "linattn.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -211,6 +212,225 @@ int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
         return hip_status(e);
     e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s);
     return hip_status(e);
+}
+
+// ---------------------------------------------------------------------------
+// linear attention
+// ---------------------------------------------------------------------------
+// Dimensions of a (B sequences x S rows) problem with Q/K width D and V width E.
+static int lin_check(size_t B, size_t S, size_t D, size_t E, bool* empty)
+{
+    *empty = (B == 0 || S == 0);
+    if (D == 0 || E == 0)
+        return CXG_ERR_DIMS;
+    if (*empty)
+        return CXG_OK;
+    if (!fits_int(B) || !fits_int(S) || !fits_int(D) || !fits_int(E) || !fits_int(B * S))
+        return CXG_ERR_DIMS;
+    // element offsets stay within 63 bits and the generic state fits memory indexing
+    if (B * S > ((size_t)1 << 40) / (D > E ? D : E) || B * D * E > ((size_t)1 << 40))
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, const float* K,
+                          const float* V, float* O, float* den, float* zc, float* S_buf,
+                          float* z_buf, size_t B, size_t S, size_t D, size_t E,
+                          cxg_stream_t stream)
+{
+    bool empty;
+    int st = lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O || !den || !zc)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
+    if (st != CXG_OK)
+        return st;
+    return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de, den_eps,
+                                     (int)B, (int)S, (int)D, (int)E, ws.p, s));
+}
+
+static int lin_step1_common(const float* O, const float* dO, const float* den, float* dnum,
+                            float* dden, size_t N, size_t E, cxg_stream_t stream)
+{
+    if (E == 0)
+        return CXG_ERR_DIMS;
+    if (N == 0)
+        return CXG_OK;
+    if (!fits_int(E) || N > ((size_t)1 << 40) / E || N * 16 > ((size_t)1 << 31) * 255)
+        return CXG_ERR_DIMS;
+    if (!O || !dO || !den || !dnum || !dden)
+        return CXG_ERR_NULL;
+    return hip_status(lin_step1_launch(O, dO, den, dnum, dden, (long)N, (int)E,
+                                       (hipStream_t)stream));
+}
+
+static int lin_dq_common(int phi, const float* K, const float* V, const float* dnum,
+                         const float* dden, const float* zc, const float* Q, float* dQ,
+                         size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
+{
+    bool empty;
+    int st = lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!K || !V || !dnum || !dden || !zc || !dQ || (phi == PHI_ELU1 && !Q))
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
+    if (st != CXG_OK)
+        return st;
+    return hip_status(lin_dq_launch(phi, K, V, dnum, dden, zc, Q, dQ, (int)B, (int)S, (int)D,
+                                    (int)E, ws.p, s));
+}
+
+static int lin_dkdv_common(int phi, const float* Q, const float* K, const float* V,
+                           const float* dnum, const float* dden, float* dK, float* dV, size_t B,
+                           size_t S, size_t D, size_t E, cxg_stream_t stream)
+{
+    bool empty;
+    int st = lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !dnum || !dden || !dK || !dV)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
+    if (st != CXG_OK)
+        return st;
+    return hip_status(lin_dkdv_launch(phi, Q, K, V, dnum, dden, dK, dV, (int)B, (int)S, (int)D,
+                                      (int)E, ws.p, s));
+}
+
+int cxg_kattn_fwd(const float* Q, const float* K, const float* V, float* O, float* den_cache,
+                  float* z_cache, float* S_buf, float* z_buf, size_t B, size_t S, size_t D,
+                  size_t E, cxg_stream_t stream)
+{
+    return lin_fwd_common(PHI_ELU1, 0, 0, Q, K, V, O, den_cache, z_cache, S_buf, z_buf, B, S, D,
+                          E, stream);
+}
+
+int cxg_kattn_bwd_step1(const float* O, const float* dO, const float* den_cache, float* dnum,
+                        float* dden, size_t N, size_t E, cxg_stream_t stream)
+{
+    return lin_step1_common(O, dO, den_cache, dnum, dden, N, E, stream);
+}
+
+int cxg_kattn_bwd_dQ(const float* K, const float* V, const float* dnum, const float* dden,
+                     const float* z_cache, const float* Q, float* dQ, float* S_buf, size_t B,
+                     size_t S, size_t D, size_t E, cxg_stream_t stream)
+{
+    (void)S_buf;   // scratch in the reference; the scan keeps its state on chip
+    return lin_dq_common(PHI_ELU1, K, V, dnum, dden, z_cache, Q, dQ, B, S, D, E, stream);
+}
+
+int cxg_kattn_bwd_dKdV(const float* Q, const float* K, const float* V, const float* dnum,
+                       const float* dden, float* dK, float* dV, size_t B, size_t S, size_t D,
+                       size_t E, cxg_stream_t stream)
+{
+    return lin_dkdv_common(PHI_ELU1, Q, K, V, dnum, dden, dK, dV, B, S, D, E, stream);
+}
+
+int cxg_lin_fwd(const float* Q_phi, const float* K_phi, const float* V, float* O,
+                float* den_cache, float* z_cache, float* S_buf, float* z_buf, size_t B, size_t S,
+                size_t D, size_t E, cxg_stream_t stream)
+{
+    return lin_fwd_common(PHI_NONE, 1, 1, Q_phi, K_phi, V, O, den_cache, z_cache, S_buf, z_buf,
+                          B, S, D, E, stream);
+}
+
+int cxg_lin_bwd_step1(const float* O, const float* dO, const float* den_cache, float* dnum,
+                      float* dden, size_t N, size_t E, cxg_stream_t stream)
+{
+    return lin_step1_common(O, dO, den_cache, dnum, dden, N, E, stream);
+}
+
+int cxg_lin_bwd_dQ(const float* K_phi, const float* V, const float* dnum, const float* dden,
+                   const float* z_cache, float* dQ_phi, float* S_buf, size_t B, size_t S,
+                   size_t D, size_t E, cxg_stream_t stream)
+{
+    (void)S_buf;
+    return lin_dq_common(PHI_NONE, K_phi, V, dnum, dden, z_cache, nullptr, dQ_phi, B, S, D, E,
+                         stream);
+}
+
+int cxg_lin_bwd_dKdV(const float* Q_phi, const float* K_phi, const float* V, const float* dnum,
+                     const float* dden, float* dK_phi, float* dV, size_t B, size_t S, size_t D,
+                     size_t E, cxg_stream_t stream)
+{
+    return lin_dkdv_common(PHI_NONE, Q_phi, K_phi, V, dnum, dden, dK_phi, dV, B, S, D, E,
+                           stream);
+}
+
+static int phi_check(size_t N, size_t D, size_t E, bool hexp, bool* empty)
+{
+    *empty = (N == 0);
+    if (D == 0 || E == 0 || D < E)
+        return CXG_ERR_DIMS;
+    if (hexp && E % 64 != 0)
+        return CXG_ERR_DIMS;
+    if (*empty)
+        return CXG_OK;
+    if (!fits_int(D) || N > ((size_t)1 << 38) / D)
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+int cxg_phi_elu_fwd(const float* x, float* phi, size_t N, size_t D, size_t E,
+                    cxg_stream_t stream)
+{
+    bool empty;
+    int st = phi_check(N, D, E, false, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!x || !phi)
+        return CXG_ERR_NULL;
+    return hip_status(phi_elu_fwd_launch(x, phi, (long)N, (int)D, (int)E, (hipStream_t)stream));
+}
+
+int cxg_phi_elu_bwd(const float* dphi, const float* x, float* dx, size_t N, size_t D, size_t E,
+                    cxg_stream_t stream)
+{
+    bool empty;
+    int st = phi_check(N, D, E, false, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!dphi || !x || !dx)
+        return CXG_ERR_NULL;
+    return hip_status(
+        phi_elu_bwd_launch(dphi, x, dx, (long)N, (int)D, (int)E, (hipStream_t)stream));
+}
+
+int cxg_phi_hexp_fwd(const float* x, float* phi, size_t N, size_t D, size_t E,
+                     cxg_stream_t stream)
+{
+    bool empty;
+    int st = phi_check(N, D, E, true, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!x || !phi)
+        return CXG_ERR_NULL;
+    return hip_status(phi_hexp_fwd_launch(x, phi, (long)N, (int)D, (int)E, (hipStream_t)stream));
+}
+
+int cxg_phi_hexp_bwd(const float* dphi, const float* x, float* dx, size_t N, size_t D, size_t E,
+                     cxg_stream_t stream)
+{
+    bool empty;
+    int st = phi_check(N, D, E, true, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!dphi || !x || !dx)
+        return CXG_ERR_NULL;
+    return hip_status(
+        phi_hexp_bwd_launch(dphi, x, dx, (long)N, (int)D, (int)E, (hipStream_t)stream));
 }
 
 // ---------------------------------------------------------------------------

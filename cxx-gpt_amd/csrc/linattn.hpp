@@ -1,0 +1,45 @@
+// linattn.hpp -- internal interface of the linear-attention kernels (linattn.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace cxg {
+
+enum { PHI_ELU1 = 0, PHI_NONE = 1 };
+
+// floats per segment record in the scan workspace: 64x64 state [d][e] + z[64]
+constexpr int LIN_WS = 64 * 64 + 64;
+
+struct LinPlan {
+    bool fast;   // D <= 64 and E <= 64: chunked MFMA scan
+    int nseg;    // segments per sequence (fast path)
+    int L;       // rows per segment (multiple of 16)
+};
+
+LinPlan lin_plan(int Bq, int S, int D, int E);
+// device scratch (bytes) the fwd / dQ / dKdV launchers need for this plan
+size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E);
+
+// den_eps: 1 stores den + 1e-8 (linear_cuda), 0 stores den (two_stage).  O is
+// num / (den + 1e-8) either way.  Sfin/zfin (nullable) receive the final state,
+// sfin_de selecting [d][e] (1) or [e][d] (0) layout.
+hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
+                          float* den, float* zc, float* Sfin, float* zfin, int sfin_de,
+                          int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st);
+hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, float* dnum,
+                            float* dden, long N, int E, hipStream_t st);
+hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* dnum,
+                         const float* dden, const float* zc, const float* Q, float* dQ, int Bq,
+                         int S, int D, int E, void* ws, hipStream_t st);
+hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float* V,
+                           const float* dnum, const float* dden, float* dK, float* dV, int Bq,
+                           int S, int D, int E, void* ws, hipStream_t st);
+hipError_t phi_elu_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st);
+hipError_t phi_elu_bwd_launch(const float* dphi, const float* x, float* dx, long N, int D, int E,
+                              hipStream_t st);
+hipError_t phi_hexp_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st);
+hipError_t phi_hexp_bwd_launch(const float* dphi, const float* x, float* dx, long N, int D,
+                               int E, hipStream_t st);
+
+} // namespace cxg

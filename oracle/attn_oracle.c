@@ -734,16 +734,23 @@ void orc_phi_hexp_forward(const float *x, float *phi, size_t N, size_t D, size_t
     }
 }
 
-void orc_phi_hexp_backward(const float *dphi, const float *phi, float *dx,
+void orc_phi_hexp_backward(const float *dphi, const float *x, float *dx,
                            size_t N, size_t D, size_t E)
 {
+    float phi[64];
     for (size_t n = 0; n < N; n++)
-        for (size_t blk = 0; blk + 64 <= E; blk += 64)
+        for (size_t blk = 0; blk + 64 <= E; blk += 64) {
+            for (int i = 0; i < 64; i++) {
+                float y = 0.0f;
+                for (int j = 0; j < 64; j++)
+                    y += orc_hadamard_entry(i, j) * x[n * E + blk + (size_t)j];
+                phi[i] = expf(y * 0.125f);
+            }
             for (int j = 0; j < 64; j++) {
                 float acc = 0.0f;
                 for (int i = 0; i < 64; i++)
-                    acc += orc_hadamard_entry(j, i) *
-                           (dphi[n * D + blk + (size_t)i] * phi[n * D + blk + (size_t)i]);
+                    acc += orc_hadamard_entry(j, i) * (dphi[n * D + blk + (size_t)i] * phi[i]);
                 dx[n * E + blk + (size_t)j] = acc * 0.125f;
             }
+        }
 }

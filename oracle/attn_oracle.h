@@ -143,10 +143,10 @@ void orc_phi_elu_backward(const float *dphi, const float *x, float *dx,
  * phi(x) = exp(H_64 x / 8) per 64-wide block of a row, H_64 the Sylvester
  * Hadamard matrix (H[i][j] = (-1)^popcount(i&j)).  Follows the phi_elu_*
  * convention: x (N,E) with E % 64 == 0, phi (N,D) with columns d>=E zero.
- * Backward: dx = H_64 (dphi * phi) / 8 per block (H symmetric). */
+ * Backward: dx = H_64 (dphi * phi(x)) / 8 per block (H symmetric). */
 float orc_hadamard_entry(int i, int j);
 void orc_phi_hexp_forward(const float *x, float *phi, size_t N, size_t D, size_t E);
-void orc_phi_hexp_backward(const float *dphi, const float *phi, float *dx,
+void orc_phi_hexp_backward(const float *dphi, const float *x, float *dx,
                            size_t N, size_t D, size_t E);
 
 #ifdef __cplusplus

@@ -242,9 +242,9 @@ def phi_hexp_forward(x, D, E):
     return phi
 
 
-def phi_hexp_backward(dphi, phi, D, E):
-    dphi, phi = _c(dphi), _c(phi)
-    N = phi.size // D
+def phi_hexp_backward(dphi, x, D, E):
+    dphi, x = _c(dphi), _c(x)
+    N = x.size // E
     dx = _z(N, E)
-    lib().orc_phi_hexp_backward(_p(dphi), _p(phi), _p(dx), _sz(N), _sz(D), _sz(E))
+    lib().orc_phi_hexp_backward(_p(dphi), _p(x), _p(dx), _sz(N), _sz(D), _sz(E))
     return dx
