@@ -1,34 +1,39 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Headline step ("C2"): causal softmax MHA forward +
+Headline step ("c2"): causal softmax MHA forward +
 backward, FP32, B=8 H=12 S=256 Dh=64, through the C ABI of
 libcxxgpt_attn.so -- cxg_mha_fwd (writes O and the row log-sum-exp) then
-cxg_mha_bwd (consumes it), the pair the reference's two_stage_cuda::
-fused_mha_fwd / fused_mha_bwd replace (src/TwoStage/two_stage_gpt.hpp:106,
-:171).  value = algorithmic TFLOP/s of the step, counting
-4*Dh*P (fwd) + 8*Dh*P (bwd) FLOPs per (b,h) with P = S(S+1)/2 causal pairs;
-recomputation is not credited.
+cxg_mha_bwd (consumes it); these replace the reference's two_stage_cuda::
+fused_mha_fwd / fused_mha_bwd (src/TwoStage/two_stage_gpt.hpp:106, :171).
+value = algorithmic TFLOP/s of the step, counting 4*Dh*P (fwd) + 8*Dh*P
+(bwd) FLOPs per (b,h) with P = S(S+1)/2 causal pairs; recomputation is not
+credited.
 
-Secondary lines (same JSON object, key "secondary"):
-  * C2 through the legacy signatures (no lse: the backward recomputes it),
-  * C3 ELU+1 linear attention fwd+bwd at S=4096 (B' = 96, D = E = 64) through
-    the two_stage API chain kernel_attn_fwd -> bwd_step1 -> bwd_dQ ->
-    bwd_dKdV, metered in GB/s of compulsory I/O (12*S*D + 2*S floats per
-    sequence),
-  * C4 Hadamard+Exp linear attention (S=1024) through the linear_cuda API,
-  * C5 long-sequence MHA (B2 H12 S4096 Dh64) fwd+bwd.
+Other workloads (run after the headline unless --no-secondary; any one of
+them can be made the reported workload with --workload NAME):
+  c2legacy  C2 through the legacy signatures (no lse: the backward recomputes it)
+  c3        ELU+1 linear attention fwd+bwd, B' = 96 sequences, S=4096, D=E=64,
+            two_stage API chain kernel_attn_fwd -> bwd_step1 -> bwd_dQ ->
+            bwd_dKdV; GB/s of compulsory I/O, (12*S*D + 2*S)*4 bytes/sequence
+  c3s256    the same at S=256
+  c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
+            (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
+  c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
 
-Inputs are synthetic N(0,1) tensors generated on the GPU from a fixed seed
-and resident in HBM before timing starts.  The roofline object is measured
-live: after the timed region the same steps run again with the library's
-per-launch HIP-event hook on (events recorded on the launch stream), which
-gives each kernel's mean duration.  The CPU baseline times the C oracle
-(the restated CPU reference, test infrastructure) on the host cores over a
-bounded sample of the same workload.
+Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
+resident in HBM before timing starts.  Timing: W warmup steps, then K steps
+between two HIP events on the launch stream.  The roofline object is
+measured live: after the timed region the same steps run again with the
+library's per-launch HIP-event hook on (events recorded on the launch
+stream), giving each kernel's mean duration; the dominant kernel's
+algorithmic FLOPs (or bytes) per launch divided by that duration is
+`achieved`.  The CPU baseline times the C oracle (the restated CPU reference,
+test infrastructure) on the host cores over a bounded sample of the same
+workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-       [--no-secondary]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]
+                       [--no-secondary] [--no-cpu] [--cpu-budget SECONDS]
 """
 import argparse
 import ctypes
@@ -42,22 +47,32 @@ sys.path.insert(0, os.path.join(ROOT, "cxx-gpt_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 MFMA
+METRIC = "attn fwd+bwd TFLOP/s (% MFMA peak) B8H12S256D64 fp32; lin-attn HBM GB/s"
 
-# Traffic factors from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (KiB per
-# dispatch), scaled by the same counters' reading on a plain copy kernel of
-# known size.  Keys: kernel tag -> HBM bytes per launch.  Filled from the
-# committed counter summary when present.
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE, scaled by
+# the same counters' reading on a copy kernel of known size; written from the
+# committed counter summaries (profiles/).  Key "<workload>/<kernel tag>".
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 
 
 def mha_flops(B, S, H, Dh, fwd=True, bwd=True):
     P = S * (S + 1) // 2
-    per = (4 * Dh * P if fwd else 0) + (8 * Dh * P if bwd else 0)
-    return per * B * H
+    return ((4 * Dh * P if fwd else 0) + (8 * Dh * P if bwd else 0)) * B * H
 
 
 def lin_bytes(Bq, S, D):
+    """Compulsory fused I/O of linear attention fwd+bwd (12 S D + 2 S floats/sequence)."""
     return (12 * S * D + 2 * S) * 4 * Bq
+
+
+def lin_kernel_bytes(Bq, S, D):
+    """Per-launch bytes each linear-attention entry point must move through its
+    own (legacy, split) signature: inputs read once, outputs written once."""
+    T, r = Bq * S * D * 4, Bq * S * 4   # one (rows x 64) tensor, one per-row vector
+    return {"lin_fwd": 3 * T + 2 * T + r,        # Q,K,V -> O, z_cache, den
+            "lin_step1": 2 * T + r + T + r,      # O, dO, den -> dnum, dden
+            "lin_dq": 5 * T + r + T,             # K, V, dnum, z_cache, Q, dden -> dQ
+            "lin_dkdv": 4 * T + r + 2 * T}       # Q, K, V, dnum, dden -> dK, dV
 
 
 def _ptr(t):
@@ -84,18 +99,16 @@ def timed(step, steps, warmup, stream):
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    w0 = time.perf_counter()
     e0.record(stream)
     for _ in range(steps):
         step()
     e1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    return e0.elapsed_time(e1) / steps, wall
+    return e0.elapsed_time(e1) / steps
 
 
-def attribute(cx, step, steps, names):
-    """Mean device duration (ms) per launch of each kernel tag, from the
+def attribute(cx, step, steps):
+    """Mean device duration (ms) and launch count per kernel tag, from the
     library's per-launch HIP events on the launch stream."""
     import torch
     torch.cuda.synchronize()
@@ -106,10 +119,11 @@ def attribute(cx, step, steps, names):
     torch.cuda.synchronize()
     cx.prof_enable(False)
     out = {}
-    for n in names:
+    for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
+              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "phi_hexp_fwd", "phi_hexp_bwd"):
         tot, cnt = cx.prof_query(n)
         if cnt:
-            out[n] = (tot / cnt, cnt)
+            out[n] = (tot / cnt, cnt / steps)
     cx.prof_reset()
     return out
 
@@ -127,80 +141,115 @@ def cpu_threads():
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
-    # the GPU box grants one GPU's share of the host (16 threads)
+    # the GPU box grants one GPU's share of the host (OMP_NUM_THREADS = 16 there)
     return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
 
 
-# ----------------------------------------------------------------------------
-def bench_mha(cx, torch, dev, stream, B, S, H, Dh, steps, warmup, use_lse, seed):
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+# ---------------------------------------------------------------------------- workloads
+class Ctx:
+    def __init__(self, cx, torch, steps, warmup):
+        self.cx, self.torch, self.steps, self.warmup = cx, torch, steps, warmup
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream(self.dev)
+        self.sp = ctypes.c_void_p(self.stream.cuda_stream)
+        self.traffic = load_traffic()
+
+    def randn(self, g, *shape, std=1.0):
+        t = self.torch.randn(*shape, device=self.dev, generator=g)
+        return t * std if std != 1.0 else t
+
+    def gen(self, seed):
+        g = self.torch.Generator(device=self.dev)
+        g.manual_seed(seed)
+        return g
+
+    def empty(self, *shape):
+        return self.torch.empty(*shape, device=self.dev)
+
+
+def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup):
+    g = c.gen(seed)
     shp = (B * S, H * Dh)
-    Q, K, V, dO = [torch.randn(shp, device=dev, generator=g) for _ in range(4)]
-    O = torch.empty(shp, device=dev)
-    dQ, dK, dV = torch.empty_like(O), torch.empty_like(O), torch.empty_like(O)
-    lse = torch.empty(B * H * S, device=dev) if use_lse else None
-    ws_bytes = cx.mha_bwd_workspace_size(B, S, H, Dh)
-    ws = torch.empty(max(1, ws_bytes // 4), device=dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    calls = [
-        ("cxg_mha_fwd", (_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(lse), B, S, H, Dh, sp)),
-        ("cxg_mha_bwd", (_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
-                         _ptr(dK), _ptr(dV), B, S, H, Dh, _ptr(ws), ws_bytes, sp)),
-    ]
-    step = Stepper(cx.lib(), calls)
-    ms, wall = timed(step, steps, warmup, stream)
-    att = attribute(cx, step, max(10, min(steps, 100)),
-                    ["mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd"])
-    return dict(ms=ms, wall=wall, att=att,
-                tensors=dict(Q=Q, K=K, V=V, dO=dO, O=O))
+    Q, K, V, dO = [c.randn(g, *shp) for _ in range(4)]
+    O, dQ, dK, dV = c.empty(*shp), c.empty(*shp), c.empty(*shp), c.empty(*shp)
+    lse = c.empty(B * H * S) if use_lse else None
+    ws_bytes = c.cx.mha_bwd_workspace_size(B, S, H, Dh)
+    ws = c.empty(max(1, ws_bytes // 4))
+    P = _ptr
+    step = Stepper(c.cx.lib(), [
+        ("cxg_mha_fwd", (P(Q), P(K), P(V), P(O), P(lse), B, S, H, Dh, c.sp)),
+        ("cxg_mha_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(lse), P(dQ), P(dK), P(dV),
+                         B, S, H, Dh, P(ws), ws_bytes, c.sp)),
+    ])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    flops = mha_flops(B, S, H, Dh)
+    value = flops / (ms * 1e-3) / 1e12
+    kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
+              "mha_bwd": mha_flops(B, S, H, Dh, fwd=False)}
+    dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
+    ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"),
+            "flops_per_launch": kflops[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: causal softmax MHA fwd+bwd ("
+                                    + ("cxg_mha_fwd with lse -> cxg_mha_bwd" if use_lse else
+                                       "legacy signatures, no lse") + ")",
+                        "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops},
+                frac=value / FP32_MFMA_PEAK_TFLOPS,
+                cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
 
 
-def bench_kattn(cx, torch, dev, stream, Bq, S, D, E, steps, warmup, seed):
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
-    N = Bq * S
-    Q = torch.randn(N, D, device=dev, generator=g)
-    K = torch.randn(N, D, device=dev, generator=g)
-    V = torch.randn(N, E, device=dev, generator=g)
-    dO = torch.randn(N, E, device=dev, generator=g)
-    O, den, zc = torch.empty(N, E, device=dev), torch.empty(N, device=dev), \
-        torch.empty(N, D, device=dev)
-    dnum, dden = torch.empty(N, E, device=dev), torch.empty(N, device=dev)
-    dQ, dK, dV = torch.empty(N, D, device=dev), torch.empty(N, D, device=dev), \
-        torch.empty(N, E, device=dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    calls = [
-        ("cxg_kattn_fwd", (_ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(den), _ptr(zc), None, None,
-                           Bq, S, D, E, sp)),
-        ("cxg_kattn_bwd_step1", (_ptr(O), _ptr(dO), _ptr(den), _ptr(dnum), _ptr(dden), N, E, sp)),
-        ("cxg_kattn_bwd_dQ", (_ptr(K), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(zc), _ptr(Q),
-                              _ptr(dQ), None, Bq, S, D, E, sp)),
-        ("cxg_kattn_bwd_dKdV", (_ptr(Q), _ptr(K), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(dK),
-                                _ptr(dV), Bq, S, D, E, sp)),
-    ]
-    step = Stepper(cx.lib(), calls)
-    ms, wall = timed(step, steps, warmup, stream)
-    return dict(ms=ms, wall=wall, tensors=dict(Q=Q, K=K, V=V, dO=dO))
+def _kattn(c, name, Bq, S, D, seed, steps, warmup):
+    g = c.gen(seed)
+    E, N = D, Bq * S
+    Q, K, V, dO = c.randn(g, N, D), c.randn(g, N, D), c.randn(g, N, E), c.randn(g, N, E)
+    O, den, zc = c.empty(N, E), c.empty(N), c.empty(N, D)
+    dnum, dden = c.empty(N, E), c.empty(N)
+    dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
+    P = _ptr
+    step = Stepper(c.cx.lib(), [
+        ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E, c.sp)),
+        ("cxg_kattn_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, c.sp)),
+        ("cxg_kattn_bwd_dQ", (P(K), P(V), P(dnum), P(dden), P(zc), P(Q), P(dQ), None,
+                              Bq, S, D, E, c.sp)),
+        ("cxg_kattn_bwd_dKdV", (P(Q), P(K), P(V), P(dnum), P(dden), P(dK), P(dV),
+                                Bq, S, D, E, c.sp)),
+    ])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    total = lin_bytes(Bq, S, D)
+    value = total / (ms * 1e-3) / 1e9
+    kb = lin_kernel_bytes(Bq, S, D)
+    dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
+    ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, two_stage API "
+                                    "chain (fwd, step1, dQ, dKdV)",
+                        "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
 
-def bench_hexp(cx, torch, dev, stream, Bq, S, steps, warmup, seed):
-    """C4: phi_hexp_fwd x2 -> linear_cuda fwd -> step1 -> dQ -> dKdV -> phi_hexp_bwd x2."""
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+def _hexp(c, name, Bq, S, seed, steps, warmup):
+    g = c.gen(seed)
     D = E = 64
     N = Bq * S
-    Xq = 0.5 * torch.randn(N, D, device=dev, generator=g)
-    Xk = 0.5 * torch.randn(N, D, device=dev, generator=g)
-    V = torch.randn(N, E, device=dev, generator=g)
-    dO = torch.randn(N, E, device=dev, generator=g)
-    e = lambda *s: torch.empty(*s, device=dev)  # noqa: E731
+    Xq, Xk = c.randn(g, N, D, std=0.5), c.randn(g, N, D, std=0.5)
+    V, dO = c.randn(g, N, E), c.randn(g, N, E)
+    e = c.empty
     pq, pk, O, den, zc = e(N, D), e(N, D), e(N, E), e(N), e(N, D)
     dnum, dden, dpq, dpk, dV, dxq, dxk = e(N, E), e(N), e(N, D), e(N, D), e(N, E), e(N, D), \
         e(N, D)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-    P = _ptr
-    calls = [
+    P, sp = _ptr, c.sp
+    step = Stepper(c.cx.lib(), [
         ("cxg_phi_hexp_fwd", (P(Xq), P(pq), N, D, E, sp)),
         ("cxg_phi_hexp_fwd", (P(Xk), P(pk), N, D, E, sp)),
         ("cxg_lin_fwd", (P(pq), P(pk), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E, sp)),
@@ -211,68 +260,95 @@ def bench_hexp(cx, torch, dev, stream, Bq, S, steps, warmup, seed):
                               sp)),
         ("cxg_phi_hexp_bwd", (P(dpq), P(Xq), P(dxq), N, D, E, sp)),
         ("cxg_phi_hexp_bwd", (P(dpk), P(Xk), P(dxk), N, D, E, sp)),
-    ]
-    step = Stepper(cx.lib(), calls)
-    ms, wall = timed(step, steps, warmup, stream)
-    return dict(ms=ms, wall=wall)
+    ])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    total = lin_bytes(Bq, S, D)
+    value = total / (ms * 1e-3) / 1e9
+    kb = lin_kernel_bytes(Bq, S, D)
+    dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
+    ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: Hadamard+Exp linear attention fwd+bwd, "
+                                    "linear_cuda API chain incl. feature map",
+                        "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
 
-# ----------------------------------------------------------------------------
-def cpu_baseline_mha(t, B, S, H, Dh, nthreads, budget_s):
+def run_workload(c, name, steps, warmup):
+    if name == "c2":
+        return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
+    if name == "c2legacy":
+        return _mha(c, name, 8, 256, 12, 64, False, 1234, steps, warmup)
+    if name == "c5":
+        return _mha(c, name, 2, 4096, 12, 64, True, 555, max(10, steps // 10),
+                    max(3, warmup // 4))
+    if name == "c3":
+        return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2))
+    if name == "c3s256":
+        return _kattn(c, name, 96, 256, 64, 78, steps, warmup)
+    if name == "c4":
+        return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
+    raise ValueError(f"unknown workload {name}")
+
+
+# ---------------------------------------------------------------------------- CPU baseline
+def cpu_baseline(name, inputs, nthreads, budget_s):
     """Time the C oracle (restated reference CPU math) on the host cores over
-    whole C2 fwd+bwd passes, repeated until budget_s of wall time is used."""
+    whole fwd+bwd passes of the workload, repeated until budget_s is used."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as orc
-    Q, K, V, dO = [np.ascontiguousarray(t[k].float().cpu().numpy()) for k in ("Q", "K", "V", "dO")]
-    reps = 0
-    t0 = time.perf_counter()
+    host = [np.ascontiguousarray(t.float().cpu().numpy()) for t in inputs[:4]]
+    Q, K, V, dO = host
+    dims = inputs[4:]
+    reps, t0 = 0, time.perf_counter()
     while True:
-        O = orc.mha_fwd(Q, K, V, B, S, H, Dh, nthreads=nthreads)
-        orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=nthreads)
+        if name.startswith("c2") or name == "c5":
+            B, S, H, Dh = dims
+            O = orc.mha_fwd(Q, K, V, B, S, H, Dh, nthreads=nthreads)
+            orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=nthreads)
+        else:
+            Bq, S, D, E = dims
+            O, den, zc = orc.kattn_fwd(Q, K, V, Bq, S, D, E, nthreads=nthreads)
+            dnum, dden = orc.kattn_bwd_step1(O, dO, den, Bq * S, E)
+            orc.kattn_bwd_dQ(K, V, dnum, dden, zc, Q, Bq, S, D, E, nthreads=nthreads)
+            orc.kattn_bwd_dKdV(Q, K, V, dnum, dden, Bq, S, D, E, nthreads=nthreads)
         reps += 1
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 1000:
             break
     per = el / reps
-    return dict(value=mha_flops(B, S, H, Dh) / per / 1e12, unit="TFLOP/s", cores=nthreads,
+    if name.startswith("c2") or name == "c5":
+        B, S, H, Dh = dims
+        return dict(value=round(mha_flops(B, S, H, Dh) / per / 1e12, 6), unit="TFLOP/s",
+                    cores=nthreads, kind="port",
+                    sample=f"{reps} complete fwd+bwd passes of {name} (B{B} H{H} S{S} Dh{Dh}) "
+                           f"through the C oracle (row-form ref_mha_fwd + literal ref_mha_bwd "
+                           f"restatement), {nthreads} threads over (b,h); {el:.1f} s wall, "
+                           f"{per * 1e3:.1f} ms/pass")
+    Bq, S, D, E = dims
+    return dict(value=round(lin_bytes(Bq, S, D) / per / 1e9, 4), unit="GB/s", cores=nthreads,
                 kind="port",
-                sample=f"{reps} full C2 fwd+bwd passes (B{B} H{H} S{S} Dh{Dh}) of the C oracle "
-                       f"(orc_mha_fwd row form + literal ref_mha_bwd restatement), "
-                       f"{nthreads} threads over (b,h), {el:.1f} s wall, {per * 1e3:.1f} ms/pass")
+                sample=f"{reps} complete fwd+bwd chains of {name} (B'{Bq} S{S} D{D} E{E}) "
+                       f"through the C oracle's O(S*D*E) scans, {nthreads} threads over "
+                       f"sequences; {el:.1f} s wall, {per * 1e3:.1f} ms/pass")
 
 
-def cpu_baseline_kattn(t, Bq, S, D, E, nthreads, budget_s):
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    import oracle as orc
-    Q, K, V, dO = [np.ascontiguousarray(t[k].float().cpu().numpy()) for k in ("Q", "K", "V", "dO")]
-    N = Bq * S
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        O, den, zc = orc.kattn_fwd(Q, K, V, Bq, S, D, E, nthreads=nthreads)
-        dnum, dden = orc.kattn_bwd_step1(O, dO, den, N, E)
-        orc.kattn_bwd_dQ(K, V, dnum, dden, zc, Q, Bq, S, D, E, nthreads=nthreads)
-        orc.kattn_bwd_dKdV(Q, K, V, dnum, dden, Bq, S, D, E, nthreads=nthreads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
-            break
-    per = el / reps
-    return dict(value=lin_bytes(Bq, S, D) / per / 1e9, unit="GB/s", cores=nthreads, kind="port",
-                sample=f"{reps} full C3 fwd+bwd chains (B'{Bq} S{S} D{D} E{E}) of the C oracle "
-                       f"(O(S*D*E) scans), {nthreads} threads over sequences, {el:.1f} s wall")
-
-
-# ----------------------------------------------------------------------------
+# ---------------------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2",
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5"])
+    ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-secondary", action="store_true", help="only the headline config")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
     args = ap.parse_args()
 
@@ -288,105 +364,45 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
-    cx.lib()  # raises if the HIP library is not built: no fallback
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream(dev)
-    steps, warmup = args.steps, args.warmup
-    traffic = load_traffic()
+    cx.lib()  # raises if the HIP library is not built: there is no fallback
+    c = Ctx(cx, torch, args.steps, args.warmup)
 
-    # ---------------- headline: C2 softmax MHA fwd+bwd (extended ABI with lse)
-    B, S, H, Dh = 8, 256, 12, 64
-    r = bench_mha(cx, torch, dev, stream, B, S, H, Dh, steps, warmup, True, 1234)
-    flops = mha_flops(B, S, H, Dh)
-    tflops = flops / (r["ms"] * 1e-3) / 1e12
-    att = r["att"]
-    dom = max(att, key=lambda k: att[k][0])
-    kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
-              "mha_bwd": mha_flops(B, S, H, Dh, fwd=False)}
-    dom_ms = att[dom][0]
-    ach = kflops.get(dom, 0) / (dom_ms * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
-            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": traffic.get(f"C2/{dom}"),
-            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()},
-            "step_frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4)}
-
+    r = run_workload(c, args.workload, args.steps, args.warmup)
     out = {
-        "metric": "attn fwd+bwd TFLOP/s (% MFMA peak) B8H12S256D64 fp32; lin-attn HBM GB/s",
-        "value": round(tflops, 3),
-        "unit": "TFLOP/s",
+        "metric": METRIC,
+        "value": round(r["value"], 3),
+        "unit": r["unit"],
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
+        "steps": args.steps,
+        "warmup": args.warmup,
         "ms_per_step": round(r["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic N(0,1) Q/K/V/dO, seeded, resident in HBM",
-        "config": {"workload": "C2 causal softmax MHA fwd+bwd (cxg_mha_fwd with lse -> "
-                               "cxg_mha_bwd)", "B": B, "H": H, "S": S, "Dh": Dh,
-                   "flops_per_step": flops},
-        "roofline": roof,
-        "wall_s_timed": round(r["wall"], 4),
+        "data": "synthetic N(0,1) tensors from a seeded GPU generator, resident in HBM",
+        "config": r["config"],
+        "roofline": r["roofline"],
+        "step_frac_of_peak": round(r["frac"], 4),
     }
-
     sec = {}
-    if not args.no_secondary:
-        # C2 through the legacy signatures (no lse)
-        rl = bench_mha(cx, torch, dev, stream, B, S, H, Dh, steps, warmup, False, 1234)
-        sec["C2_legacy_no_lse"] = {
-            "value": round(flops / (rl["ms"] * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-            "ms_per_step": round(rl["ms"], 5),
-            "kernel_ms": {k: round(v[0], 5) for k, v in rl["att"].items()}}
-        del rl
-        # C3 ELU+1 linear attention, S=4096
-        Bq, S3, D = 96, 4096, 64
-        rk = bench_kattn(cx, torch, dev, stream, Bq, S3, D, D, max(20, steps // 4),
-                         max(5, warmup // 2), 77)
-        gbs = lin_bytes(Bq, S3, D) / (rk["ms"] * 1e-3) / 1e9
-        sec["C3_elu_S4096"] = {"value": round(gbs, 1), "unit": "GB/s",
-                               "ms_per_step": round(rk["ms"], 5),
-                               "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                               "bytes_per_step": lin_bytes(Bq, S3, D)}
-        kt = rk["tensors"]
-        rk256 = bench_kattn(cx, torch, dev, stream, Bq, 256, D, D, steps, warmup, 78)
-        gbs = lin_bytes(Bq, 256, D) / (rk256["ms"] * 1e-3) / 1e9
-        sec["C3_elu_S256"] = {"value": round(gbs, 1), "unit": "GB/s",
-                              "ms_per_step": round(rk256["ms"], 5),
-                              "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-        del rk256
-        # C4 Hadamard+Exp, S=1024
-        rh = bench_hexp(cx, torch, dev, stream, 96, 1024, max(20, steps // 2), warmup, 79)
-        gbs = lin_bytes(96, 1024, 64) / (rh["ms"] * 1e-3) / 1e9
-        sec["C4_hexp_S1024"] = {"value": round(gbs, 1), "unit": "GB/s",
-                                "ms_per_step": round(rh["ms"], 5),
-                                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-        # C5 long-sequence MHA
-        B5, S5 = 2, 4096
-        r5 = bench_mha(cx, torch, dev, stream, B5, S5, H, Dh, max(10, steps // 10),
-                       max(3, warmup // 4), True, 555)
-        f5 = mha_flops(B5, S5, H, Dh)
-        t5 = f5 / (r5["ms"] * 1e-3) / 1e12
-        sec["C5_mha_S4096"] = {"value": round(t5, 3), "unit": "TFLOP/s",
-                               "ms_per_step": round(r5["ms"], 5),
-                               "frac_mfma": round(t5 / FP32_MFMA_PEAK_TFLOPS, 4),
-                               "kernel_ms": {k: round(v[0], 5) for k, v in r5["att"].items()}}
-        del r5
+    if not args.no_secondary and args.workload == "c2":
+        for name in ("c2legacy", "c3", "c3s256", "c4", "c5"):
+            s = run_workload(c, name, args.steps, args.warmup)
+            sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
+                         "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),
+                         "roofline": s["roofline"], "config": s["config"]}
+            if name == "c3":
+                c3_inputs = s["cpu_inputs"]
         out["secondary"] = sec
-
     if not args.no_cpu:
         nth = cpu_threads()
-        out["cpu_baseline"] = cpu_baseline_mha(r["tensors"], B, S, H, Dh, nth, args.cpu_budget)
-        out["cpu_baseline"]["value"] = round(out["cpu_baseline"]["value"], 6)
-        if not args.no_secondary:
-            cb = cpu_baseline_kattn(kt, 96, 4096, 64, 64, nth, args.cpu_budget)
-            cb["value"] = round(cb["value"], 3)
-            sec["C3_elu_S4096"]["cpu_baseline"] = cb
+        out["cpu_baseline"] = cpu_baseline(args.workload, r["cpu_inputs"], nth, args.cpu_budget) \
+            if r["cpu_inputs"] is not None else None
+        if "c3" in sec:
+            sec["c3"]["cpu_baseline"] = cpu_baseline("c3", c3_inputs, nth, args.cpu_budget)
     else:
         out["cpu_baseline"] = None
-
     print(json.dumps(out), flush=True)
 
 
