@@ -11,14 +11,21 @@
 // Layout: Q/K/V/O/dO/dQ/dK/dV are (B*S, H*Dh) row-major; head h of row r is
 // [(r*H + h)*Dh, +Dh).  lse and Di are [B*H][S].
 //
-// Work decomposition (one workgroup = 4 waves = 256 threads):
-//   forward : a workgroup owns 64 query rows of one (b,h); wave w owns rows
-//             16w..16w+15.  Scores are computed transposed (S^T = K Q^T) so
-//             lane l holds query l%16 and the softmax statistics are per lane.
-//   backward: a workgroup owns 64 key rows of one (b,h); wave w owns keys
-//             16w..16w+15 with K/V held in registers, accumulates dK^T/dV^T in
-//             registers over all later query tiles, and adds its dQ tile into
-//             the zero-initialised dQ with float atomics.
+// Work decomposition.  A workgroup has 4*NSPLIT waves: four "row groups" of
+// 16 rows times NSPLIT "splits", so two waves share each SIMD and hide one
+// another's LDS / exp / memory latency behind MFMA work.
+//   forward : a workgroup owns 64 query rows of one (b,h); wave (qg, ks) owns
+//             queries 16qg..16qg+15 and keys [64/NSPLIT * ks, +64/NSPLIT) of
+//             every 64-key tile, keeping its own online-softmax state; the
+//             NSPLIT partial states are merged through LDS at the end.
+//             Scores are computed transposed (S^T = K Q^T) so a lane holds one
+//             query and the softmax statistics need one cross-row shuffle.
+//   backward: a workgroup owns 64 key rows of one (b,h); wave (kg, qs) owns
+//             keys 16kg..16kg+15 (K/V in registers) and rows
+//             [BM/NSPLIT * qs, +BM/NSPLIT) of every BM-row query tile; it
+//             accumulates partial dK^T/dV^T in registers (summed over the
+//             splits through LDS at the end) and adds dQ = dS K into the
+//             zero-initialised dQ with float atomics.
 // The flat grid index is (tile * B*H + bh): heavy causal tiles dispatch first,
 // and when B*H is a multiple of 8 all tiles of a head share an XCD (and its
 // L2), since workgroups are dealt to the 8 XCDs round-robin.
@@ -31,36 +38,124 @@ namespace cxg {
 
 constexpr int MHA_BM = 64;   // query rows per tile
 constexpr int MHA_BN = 64;   // key rows per tile
-constexpr int MHA_THREADS = 256;
+
+// Clamped 4-wide load for streamed tiles: the row and column are clamped into
+// the valid data, so the load always issues and never needs a guard.  Padded
+// positions (rows >= S, columns >= Dh) therefore hold copies of real, finite
+// inputs; the kernels neutralise them elsewhere: the operand they meet in a
+// product is zero (Q/K/V registers zeroed beyond Dh) or the probability they
+// carry is masked to exactly 0.  Keeping loads unconditional lets a thread put
+// all of a tile's loads in flight at once.  VEC: n % 4 == 0 and the row base
+// is 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ f4 load4c(const float* __restrict__ row, int c, int n)
+{
+    f4 v;
+    if (VEC) {
+        v = *reinterpret_cast<const f4*>(row + (c < n ? c : n - 4));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = row[c + i < n ? c + i : n - 1];
+    }
+    return v;
+}
+
+// ROWS x DHP fp32 tile of one head, held in registers between its global load
+// and its LDS store (so the next tile's loads overlap the current tile's math).
+// Thread tid of NT owns f4 units u = tid + i*NT: row u / (DHP/4), column
+// 4*(u % (DHP/4)).  Rows past S repeat row S-1 and columns past Dh repeat real
+// columns (load4c).
+template <int DHP, int ROWS, int NT, bool VEC>
+struct TileRegs {
+    static constexpr int CPR = DHP / 4;   // f4 units per row
+    static constexpr int NU = ROWS * CPR;
+    static constexpr int UPT = (NU + NT - 1) / NT;
+    f4 r[UPT];
+
+    __device__ __forceinline__ void load(const float* __restrict__ X, long base, long rs,
+                                         int row0, int S, int Dh, int tid)
+    {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = min(tid + i * NT, NU - 1);
+            const int row = u / CPR, c = 4 * (u - row * CPR);
+            const int gr = min(row0 + row, S - 1);
+            r[i] = load4c<VEC>(X + base + (long)gr * rs, c, Dh);
+        }
+    }
+    // row-major [row][c] with row stride LD floats
+    template <int LD>
+    __device__ __forceinline__ void store(float* __restrict__ T, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + i * NT;
+            if (NU % NT == 0 || u < NU) {
+                const int row = u / CPR, c = 4 * (u - row * CPR);
+                *reinterpret_cast<f4*>(&T[row * LD + c]) = r[i];
+            }
+        }
+    }
+    // transposed [c][row] with row stride LD floats
+    template <int LD>
+    __device__ __forceinline__ void store_t(float* __restrict__ T, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + i * NT;
+            if (NU % NT == 0 || u < NU) {
+                const int row = u / CPR, c = 4 * (u - row * CPR);
+                T[(c + 0) * LD + row] = r[i][0];
+                T[(c + 1) * LD + row] = r[i][1];
+                T[(c + 2) * LD + row] = r[i][2];
+                T[(c + 3) * LD + row] = r[i][3];
+            }
+        }
+    }
+};
 
 // ----------------------------------------------------------------------------
 // forward (and statistics-only) kernel
 // ----------------------------------------------------------------------------
-template <int DHP, bool VEC, bool WRITE_O>
-__global__ __launch_bounds__(MHA_THREADS) void mha_fwd_kernel(
+template <int DHP, int NSPLIT>
+struct FwdSmem {
+    static constexpr int KS = DHP + 4;      // Ks[key][d] row stride (floats)
+    static constexpr int VS = MHA_BN + 4;   // Vt[d][key] row stride
+    static constexpr int MS = DHP + 4;      // merge record: o[DHP], m, l
+    static constexpr int TILES = MHA_BN * KS + DHP * VS;
+    static constexpr int MERGE = (NSPLIT - 1) * MHA_BM * MS;
+    static constexpr int FLOATS = TILES > MERGE ? TILES : MERGE;
+};
+
+template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
+__global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
     float qscale)
 {
-    constexpr int KS = DHP + 4;       // Ks[key][d] row stride (floats)
-    constexpr int VS = MHA_BN + 4;    // Vt[d][key] row stride
+    using SM = FwdSmem<DHP, NSPLIT>;
+    constexpr int NT = 256 * NSPLIT;
+    constexpr int KS = SM::KS, VS = SM::VS, MS = SM::MS;
     constexpr int NDT = DHP / 16;
-    constexpr int NU = MHA_BN * (DHP / 4);   // float4 units per tile
-    __shared__ __attribute__((aligned(16))) float Ks[MHA_BN * KS];
-    __shared__ __attribute__((aligned(16))) float Vt[WRITE_O ? DHP * VS : 4];
+    constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
+    __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
+    float* Ks = smem;
+    float* Vt = smem + MHA_BN * KS;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
+    const int qg = wave & 3, ks = wave >> 2;
     const int qi = blockIdx.x / BH, bh = blockIdx.x - qi * BH;
     const int qb = nqb - 1 - qi;
     const int b = bh / H, h = bh - b * H;
     const long rs = (long)H * Dh;
     const long base = (long)b * S * rs + (long)h * Dh;
 
-    const int myq = qb * MHA_BM + wave * 16 + l16;
+    const int myq = qb * MHA_BM + qg * 16 + l16;
     const bool qok = myq < S;
     // B operand of S^T = K Q^T: lane holds Q[myq][16*dt + 4*g + r], pre-scaled
-    // by scale*log2(e) so scores land in the exp2 domain.
+    // by scale*log2(e) so scores land in the exp2 domain; zero past Dh.
     f4 qreg[NDT];
     {
         const float* qrow = Q + base + (long)(qok ? myq : 0) * rs;
@@ -75,29 +170,36 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_fwd_kernel(
     float m_run = -1e30f, l_run = 0.0f;
 
     const int nkb = qb + 1;   // causal: key tiles 0..qb (MHA_BM == MHA_BN)
+    // K/V tiles: loaded into registers one tile ahead (DHP <= 128), stored to
+    // LDS at the top of the iteration that uses them.
+    constexpr bool PREFETCH = DHP <= 128;
+    TileRegs<DHP, MHA_BN, NT, VEC> kr, vr;
+    kr.load(K, base, rs, 0, S, Dh, tid);
+    if (WRITE_O)
+        vr.load(V, base, rs, 0, S, Dh, tid);
     for (int kb = 0; kb < nkb; kb++) {
         const int k0 = kb * MHA_BN;
-        __syncthreads();
-        for (int u = tid; u < NU; u += MHA_THREADS) {
-            const int row = u / (DHP / 4), c = 4 * (u - row * (DHP / 4));
-            const int key = k0 + row;
-            const bool ok = key < S;
-            const long off = base + (long)(ok ? key : 0) * rs;
-            *reinterpret_cast<f4*>(&Ks[row * KS + c]) = load4<VEC>(K + off, c, Dh, ok);
-            if (WRITE_O) {
-                f4 vv = load4<VEC>(V + off, c, Dh, ok);
-                Vt[(c + 0) * VS + row] = vv[0];
-                Vt[(c + 1) * VS + row] = vv[1];
-                Vt[(c + 2) * VS + row] = vv[2];
-                Vt[(c + 3) * VS + row] = vv[3];
-            }
+        if (!PREFETCH && kb > 0) {
+            kr.load(K, base, rs, k0, S, Dh, tid);
+            if (WRITE_O)
+                vr.load(V, base, rs, k0, S, Dh, tid);
         }
         __syncthreads();
+        kr.template store<KS>(Ks, tid);
+        if (WRITE_O)
+            vr.template store_t<VS>(Vt, tid);
+        __syncthreads();
+        if (PREFETCH && kb + 1 < nkb) {
+            kr.load(K, base, rs, k0 + MHA_BN, S, Dh, tid);
+            if (WRITE_O)
+                vr.load(V, base, rs, k0 + MHA_BN, S, Dh, tid);
+        }
 
-        // S^T tile: lane holds query l16, keys k0 + 16*kt + 4*g + r.
-        f4 sacc[4];
+        // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
+        f4 sacc[NKT];
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
+        for (int kk = 0; kk < NKT; kk++) {
+            const int kt = ks * NKT + kk;
             f4 acc = f4zero();
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
@@ -106,32 +208,30 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_fwd_kernel(
                 for (int r = 0; r < 4; r++)
                     acc = mfma16(kv[r], qreg[dt][r], acc);
             }
-            sacc[kt] = acc;
-        }
-        if (kb == qb) {   // diagonal tile: causal mask key > query
-#pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+            if (kb == qb) {   // diagonal tile: causal mask key > query
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     if (k0 + 16 * kt + 4 * g + r > myq)
-                        sacc[kt][r] = -INFINITY;
+                        acc[r] = -INFINITY;
+            }
+            sacc[kk] = acc;
         }
         float mloc = -INFINITY;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int kk = 0; kk < NKT; kk++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                mloc = fmaxf(mloc, sacc[kt][r]);
+                mloc = fmaxf(mloc, sacc[kk][r]);
         mloc = xrow_max(mloc);
         const float m_new = fmaxf(m_run, mloc);
         const float alpha = fast_exp2(m_run - m_new);
         float psum = 0.0f;
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++)
+        for (int kk = 0; kk < NKT; kk++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float p = fast_exp2(sacc[kt][r] - m_new);
-                sacc[kt][r] = p;
+                const float p = fast_exp2(sacc[kk][r] - m_new);
+                sacc[kk][r] = p;
                 psum += p;
             }
         l_run = l_run * alpha + psum;
@@ -142,17 +242,61 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_fwd_kernel(
             for (int dt = 0; dt < NDT; dt++) {
                 f4 acc = oacc[dt] * alpha;
 #pragma unroll
-                for (int kt = 0; kt < 4; kt++) {
+                for (int kk = 0; kk < NKT; kk++) {
+                    const int kt = ks * NKT + kk;
                     const f4 vv = *reinterpret_cast<const f4*>(&Vt[(16 * dt + l16) * VS + 16 * kt + 4 * g]);
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(vv[r], sacc[kt][r], acc);
+                        acc = mfma16(vv[r], sacc[kk][r], acc);
                 }
                 oacc[dt] = acc;
             }
         }
     }
-    const float l_tot = xrow_sum(l_run);
+    float l_tot = xrow_sum(l_run);
+
+    if (NSPLIT > 1) {
+        // Merge the key splits: split ks > 0 publishes (o, m, l) per query row,
+        // split 0 rescales everything to the common maximum.
+        float* mb = smem;
+        __syncthreads();   // every wave is done with the K/V tiles
+        const int qrow = qg * 16 + l16;
+        if (ks > 0) {
+            float* rec = mb + ((ks - 1) * MHA_BM + qrow) * MS;
+            if (WRITE_O)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+                    *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = oacc[dt];
+            if (g == 0) {
+                rec[DHP] = m_run;
+                rec[DHP + 1] = l_tot;
+            }
+        }
+        __syncthreads();
+        if (ks > 0)
+            return;
+        float m_all = m_run;
+#pragma unroll
+        for (int j = 1; j < NSPLIT; j++)
+            m_all = fmaxf(m_all, mb[((j - 1) * MHA_BM + qrow) * MS + DHP]);
+        const float a0 = fast_exp2(m_run - m_all);
+        l_tot *= a0;
+        if (WRITE_O)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                oacc[dt] = oacc[dt] * a0;
+#pragma unroll
+        for (int j = 1; j < NSPLIT; j++) {
+            const float* rec = mb + ((j - 1) * MHA_BM + qrow) * MS;
+            const float aj = fast_exp2(rec[DHP] - m_all);
+            l_tot += rec[DHP + 1] * aj;
+            if (WRITE_O)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+                    oacc[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]) * aj;
+        }
+        m_run = m_all;
+    }
     if (qok) {
         if (WRITE_O) {
             const float inv = 1.0f / l_tot;
@@ -199,39 +343,51 @@ __global__ __launch_bounds__(256) void mha_bwd_prep_kernel(
 }
 
 // ----------------------------------------------------------------------------
-// backward main kernel.  BM query rows per inner tile (64, or 32 for the
-// widest heads so the LDS tiles fit in 160 KB).
+// backward main kernel.  BM query rows per tile (64, or 32 for the widest
+// heads so the LDS tiles fit in 160 KB), split over NSPLIT wave groups.
 // ----------------------------------------------------------------------------
-template <int DHP, int BM, bool VEC>
-__global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
+template <int DHP, int BM>
+struct BwdSmem {
+    static constexpr int QS = DHP + 4;      // Qs/dOs [q][d] row stride
+    static constexpr int TS = MHA_BN + 4;   // Kt [d][key] and dSs [q][key] row stride
+    static constexpr int FLOATS = 2 * BM * QS + DHP * TS + BM * TS + 2 * BM;
+};
+
+template <int DHP, int BM, int NSPLIT, bool VEC>
+__global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
     int BH, int nkb, float scale, float c2)
 {
+    using SM = BwdSmem<DHP, BM>;
+    constexpr int NT = 256 * NSPLIT;
+    constexpr int NW = NT / 64;
     constexpr int NDT = DHP / 16;
-    constexpr int NQT = BM / 16;
-    constexpr int QS = DHP + 4;        // Qs/dOs [q][d] row stride
-    constexpr int TS = MHA_BN + 4;     // Kt [d][key] and dSs [q][key] row stride
-    constexpr int NU = BM * (DHP / 4);
-    __shared__ __attribute__((aligned(16))) float Qs[BM * QS];
-    __shared__ __attribute__((aligned(16))) float dOs[BM * QS];
-    __shared__ __attribute__((aligned(16))) float Kt[DHP * TS];
-    __shared__ __attribute__((aligned(16))) float dSs[BM * TS];
-    __shared__ __attribute__((aligned(16))) float lse_s[BM];
-    __shared__ __attribute__((aligned(16))) float di_s[BM];
+    constexpr int NQT = BM / 16;        // 16-row query blocks per tile
+    constexpr int NQW = NQT / NSPLIT;   // ... per wave
+    constexpr int QS = SM::QS, TS = SM::TS;
+    static_assert(NQW >= 1, "query split too fine for BM");
+    __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
+    float* Qs = smem;
+    float* dOs = Qs + BM * QS;
+    float* Kt = dOs + BM * QS;
+    float* dSs = Kt + DHP * TS;
+    float* lse_s = dSs + BM * TS;
+    float* di_s = lse_s + BM;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
+    const int kg = wave & 3, qs = wave >> 2;
     const int kb = blockIdx.x / BH, bh = blockIdx.x - kb * BH;
     const int b = bh / H, h = bh - b * H;
     const long rs = (long)H * Dh;
     const long base = (long)b * S * rs + (long)h * Dh;
     const int k0 = kb * MHA_BN;
-    const int mykey = k0 + wave * 16 + l16;
+    const int mykey = k0 + kg * 16 + l16;
     const bool kok = mykey < S;
 
-    // B operands for S = Q K^T and dP = dO V^T: K/V[mykey][16dt + 4g + r].
+    // B operands for S = Q K^T and dP = dO V^T: K/V[mykey][16dt + 4g + r], zero past Dh.
     f4 kreg[NDT], vreg[NDT];
     {
         const long off = base + (long)(kok ? mykey : 0) * rs;
@@ -242,15 +398,10 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
         }
     }
     // K^T tile for the dQ product.
-    for (int u = tid; u < MHA_BN * (DHP / 4); u += MHA_THREADS) {
-        const int row = u / (DHP / 4), c = 4 * (u - row * (DHP / 4));
-        const int key = k0 + row;
-        const bool ok = key < S;
-        const f4 kv = load4<VEC>(K + base + (long)(ok ? key : 0) * rs, c, Dh, ok);
-        Kt[(c + 0) * TS + row] = kv[0];
-        Kt[(c + 1) * TS + row] = kv[1];
-        Kt[(c + 2) * TS + row] = kv[2];
-        Kt[(c + 3) * TS + row] = kv[3];
+    {
+        TileRegs<DHP, MHA_BN, NT, VEC> kt;
+        kt.load(K, base, rs, k0, S, Dh, tid);
+        kt.template store_t<TS>(Kt, tid);
     }
 
     f4 dk[NDT], dv[NDT];
@@ -261,30 +412,43 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
     }
 
     const int nqb = (S + BM - 1) / BM;
-    for (int qb = (k0 / BM); qb < nqb; qb++) {
+    // Q/dO tiles and their lse/Di entries: loaded into registers one query
+    // tile ahead (DHP <= 128), stored to LDS at the top of the iteration.
+    constexpr bool PREFETCH = DHP <= 128;
+    TileRegs<DHP, BM, NT, VEC> qr, dor;
+    float lse_r = 0.0f, di_r = 0.0f;
+    auto load_q = [&](int q0) {
+        qr.load(Q, base, rs, q0, S, Dh, tid);
+        dor.load(dO, base, rs, q0, S, Dh, tid);
+        if (tid < BM) {   // rows past S repeat row S-1; their P is masked to 0
+            const long i = (long)bh * S + min(q0 + tid, S - 1);
+            lse_r = lse[i] * kLog2e;
+            di_r = Di[i];
+        }
+    };
+    const int qb0 = k0 / BM;
+    load_q(qb0 * BM);
+    for (int qb = qb0; qb < nqb; qb++) {
         const int q0 = qb * BM;
+        if (!PREFETCH && qb > qb0)
+            load_q(q0);
         __syncthreads();
-        for (int u = tid; u < NU; u += MHA_THREADS) {
-            const int row = u / (DHP / 4), c = 4 * (u - row * (DHP / 4));
-            const int q = q0 + row;
-            const bool ok = q < S;
-            const long off = base + (long)(ok ? q : 0) * rs;
-            *reinterpret_cast<f4*>(&Qs[row * QS + c]) = load4<VEC>(Q + off, c, Dh, ok);
-            *reinterpret_cast<f4*>(&dOs[row * QS + c]) = load4<VEC>(dO + off, c, Dh, ok);
-        }
+        qr.template store<QS>(Qs, tid);
+        dor.template store<QS>(dOs, tid);
         if (tid < BM) {
-            const int q = q0 + tid;
-            const bool ok = q < S;
-            lse_s[tid] = ok ? lse[(long)bh * S + q] * kLog2e : INFINITY;
-            di_s[tid] = ok ? Di[(long)bh * S + q] : 0.0f;
+            lse_s[tid] = lse_r;
+            di_s[tid] = di_r;
         }
         __syncthreads();
+        if (PREFETCH && qb + 1 < nqb)
+            load_q(q0 + BM);
 
         // S = Q K^T and dP = dO V^T: lane holds key l16, queries 16qt + 4g + r.
         const bool diag = q0 < k0 + MHA_BN;   // tile touches the causal boundary
-        f4 P[NQT], dS[NQT];
+        f4 P[NQW], dS[NQW];
 #pragma unroll
-        for (int qt = 0; qt < NQT; qt++) {
+        for (int qq = 0; qq < NQW; qq++) {
+            const int qt = qs * NQW + qq;
             f4 sa = f4zero(), da = f4zero();
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
@@ -301,32 +465,34 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int q = q0 + 16 * qt + 4 * g + r;
-                const bool ok = !diag || (mykey <= q);
+                const bool ok = (!diag || mykey <= q) && q < S;
                 const float p = ok ? fast_exp2(sa[r] * c2 - l4[r]) : 0.0f;
-                P[qt][r] = p;
-                dS[qt][r] = p * (da[r] - d4[r]);
-                dSs[(16 * qt + 4 * g + r) * TS + wave * 16 + l16] = dS[qt][r];
+                P[qq][r] = p;
+                dS[qq][r] = p * (da[r] - d4[r]);
+                dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
             }
         }
-        // dV^T += dO^T P and dK^T += Q^T dS (contraction over the BM queries).
+        // dV^T += dO^T P and dK^T += Q^T dS (contraction over this wave's queries).
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             f4 av = dv[dt], ak = dk[dt];
 #pragma unroll
-            for (int qt = 0; qt < NQT; qt++)
+            for (int qq = 0; qq < NQW; qq++) {
+                const int qt = qs * NQW + qq;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int row = (16 * qt + 4 * g + r) * QS + 16 * dt + l16;
-                    av = mfma16(dOs[row], P[qt][r], av);
-                    ak = mfma16(Qs[row], dS[qt][r], ak);
+                    av = mfma16(dOs[row], P[qq][r], av);
+                    ak = mfma16(Qs[row], dS[qq][r], ak);
                 }
+            }
             dv[dt] = av;
             dk[dt] = ak;
         }
         __syncthreads();
         // dQ tiles (qt, dt) of this query block, dealt round-robin to the waves:
         // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.
-        for (int job = wave; job < NQT * NDT; job += MHA_THREADS / 64) {
+        for (int job = wave; job < NQT * NDT; job += NW) {
             const int qt = job % NQT, dt = job / NQT;
             f4 acc = f4zero();
 #pragma unroll
@@ -346,6 +512,37 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
             }
         }
     }
+
+    if (NSPLIT > 1) {
+        // Sum the per-split partial dK^T/dV^T: splits qs > 0 publish through
+        // LDS (reusing the Q/dO tiles), split 0 adds and stores.
+        constexpr int RS = 2 * DHP + 4;   // record per (split, key): dk[DHP], dv[DHP]
+        static_assert((NSPLIT - 1) * MHA_BN * RS <= 2 * BM * QS + DHP * TS,
+                      "dK/dV reduction buffer does not fit");
+        float* rb = smem;
+        __syncthreads();   // every wave is done with the tiles
+        const int krow = kg * 16 + l16;
+        if (qs > 0) {
+            float* rec = rb + ((qs - 1) * MHA_BN + krow) * RS;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = dk[dt];
+                *reinterpret_cast<f4*>(&rec[DHP + 16 * dt + 4 * g]) = dv[dt];
+            }
+        }
+        __syncthreads();
+        if (qs > 0)
+            return;
+#pragma unroll
+        for (int j = 1; j < NSPLIT; j++) {
+            const float* rec = rb + ((j - 1) * MHA_BN + krow) * RS;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                dk[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]);
+                dv[dt] += *reinterpret_cast<const f4*>(&rec[DHP + 16 * dt + 4 * g]);
+            }
+        }
+    }
     if (kok) {
         const long off = base + (long)mykey * rs;
 #pragma unroll
@@ -361,21 +558,30 @@ __global__ __launch_bounds__(MHA_THREADS) void mha_bwd_kernel(
 // ----------------------------------------------------------------------------
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Wave groups per workgroup: two per SIMD wherever registers allow.
+template <int DHP>
+struct MhaSplits {
+    static constexpr int FWD = DHP <= 128 ? 2 : 1;
+    static constexpr int BWD = DHP <= 64 ? 2 : 1;
+    static constexpr int BWD_BM = DHP <= 128 ? 64 : 32;
+};
+
 template <int DHP, bool VEC>
 static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, float* O,
                                 float* lse, int B, int S, int H, int Dh, hipStream_t st)
 {
+    constexpr int NS = MhaSplits<DHP>::FWD;
     const int BH = B * H;
     const int nqb = (S + MHA_BM - 1) / MHA_BM;
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid((unsigned)(nqb * BH)), block(MHA_THREADS);
+    dim3 grid((unsigned)(nqb * BH)), block(256 * NS);
     if (O != nullptr) {
         ProfScope ps(st, "mha_fwd");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, VEC, true>), grid, block, 0, st, Q, K, V, O, lse,
-                           S, H, Dh, BH, nqb, qscale);
+        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true>), grid, block, 0, st, Q, K, V, O,
+                           lse, S, H, Dh, BH, nqb, qscale);
     } else {
         ProfScope ps(st, "mha_stats");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, VEC, false>), grid, block, 0, st, Q, K, V, O,
+        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, false>), grid, block, 0, st, Q, K, V, O,
                            lse, S, H, Dh, BH, nqb, qscale);
     }
     return hipGetLastError();
@@ -422,24 +628,25 @@ hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float
     return hipGetLastError();
 }
 
-template <int DHP, int BM>
+template <int DHP>
 static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
                                float* dV, int B, int S, int H, int Dh, hipStream_t st)
 {
+    constexpr int NS = MhaSplits<DHP>::BWD, BM = MhaSplits<DHP>::BWD_BM;
     const int BH = B * H;
     const int nkb = (S + MHA_BN - 1) / MHA_BN;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid((unsigned)(nkb * BH)), block(MHA_THREADS);
+    dim3 grid((unsigned)(nkb * BH)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, "mha_bwd");
     if (vec)
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, true>), grid, block, 0, st, Q, K, V, dO, lse, Di,
-                           dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
+        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, true>), grid, block, 0, st, Q, K, V, dO,
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
     else
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, false>), grid, block, 0, st, Q, K, V, dO, lse,
-                           Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
+        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, false>), grid, block, 0, st, Q, K, V, dO,
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
     return hipGetLastError();
 }
 
@@ -448,14 +655,14 @@ hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V, c
                                float* dV, int B, int S, int H, int Dh, hipStream_t st)
 {
     if (Dh <= 16)
-        return bwd_dispatch<16, 64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        return bwd_dispatch<16>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
     if (Dh <= 32)
-        return bwd_dispatch<32, 64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        return bwd_dispatch<32>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
     if (Dh <= 64)
-        return bwd_dispatch<64, 64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        return bwd_dispatch<64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
     if (Dh <= 128)
-        return bwd_dispatch<128, 64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
-    return bwd_dispatch<256, 32>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        return bwd_dispatch<128>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+    return bwd_dispatch<256>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
 }
 
 } // namespace cxg
