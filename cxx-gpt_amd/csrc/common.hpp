@@ -99,6 +99,28 @@ __device__ __forceinline__ void store4(float* __restrict__ row, int c, int n, f4
     }
 }
 
+// Clamped 4-wide load for streamed tiles: the row and column are clamped into
+// the valid data, so the load always issues and never needs a guard.  Padded
+// positions (rows >= S, columns >= Dh) therefore hold copies of real, finite
+// inputs; the kernels neutralise them elsewhere: the operand they meet in a
+// product is zero (Q/K/V registers zeroed beyond Dh) or the probability they
+// carry is masked to exactly 0.  Keeping loads unconditional lets a thread put
+// all of a tile's loads in flight at once.  VEC: n % 4 == 0 and the row base
+// is 16-byte aligned.
+template <bool VEC>
+__device__ __forceinline__ f4 load4c(const float* __restrict__ row, int c, int n)
+{
+    f4 v;
+    if (VEC) {
+        v = *reinterpret_cast<const f4*>(row + (c < n ? c : n - 4));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = row[c + i < n ? c + i : n - 1];
+    }
+    return v;
+}
+
 __device__ __forceinline__ void atomic_add_f32(float* p, float v)
 {
     unsafeAtomicAdd(p, v);

@@ -15,13 +15,20 @@
 //             dV_t = S*_t^T phi(K_t), dK_t = (z*_t + S*_t V_t) * phi'(K_t)
 //
 // Fast path (D <= 64 and E <= 64, padded to 64): the sequence is cut into
-// segments of L rows; one wave owns one segment and walks it in 16-row
-// chunks, holding the 64x64 state in MFMA accumulator registers.  Per chunk
-// the contribution of earlier chunks is one state product (phi(Q) S) and the
-// contribution inside the chunk is a masked 16x16 product, all on
+// segments of L rows; a segment is walked in 16-row chunks with the 64x64
+// state in MFMA accumulator registers (one wave per segment; the dK/dV scan
+// splits a segment over two waves, one holding S* for dV and one S*^T for
+// dK).  Per chunk, the contribution of earlier chunks is one state product
+// and the contribution inside the chunk a masked 16x16 product, all on
 // v_mfma_f32_16x16x4_f32.  A segment's starting state comes from a
-// per-segment aggregate kernel (lin_agg) followed by an exclusive scan over
-// segments (lin_scan); with one segment per sequence both are skipped.
+// per-segment aggregate kernel (lin_agg) and an exclusive scan over segments
+// (lin_scan); with one segment per sequence both are skipped.
+//
+// Memory pipeline: each chunk's rows are fetched with 16-byte row loads one
+// chunk ahead (in flight while the current chunk computes).  The operands
+// that need a row index as the MFMA contraction index (column layout) are
+// re-read from a small LDS buffer the chunk is written to; buffers are private
+// to a wave (or shared by the two waves of a dK/dV segment).
 //
 // Wider D/E take the generic kernels at the end of the file (one workgroup
 // per sequence, serial over t, state in global scratch).
@@ -37,6 +44,8 @@ namespace cxg {
 
 constexpr int LIN_THREADS = 256;
 constexpr int LIN_WAVES = LIN_THREADS / 64;
+constexpr int CLD = 68;             // LDS row stride of a staged 16 x 64 chunk
+constexpr int CHUNK = 16 * CLD;     // floats per staged chunk matrix
 
 template <int PHI>
 struct Phi;
@@ -45,52 +54,99 @@ struct Phi<PHI_ELU1> {
     // two_stage_cuda_kernels.cu:1027-1031 / kernel_test.cpp:16-17
     static __device__ __forceinline__ float f(float x) { return x > 0.0f ? x + 1.0f : __expf(x); }
     static __device__ __forceinline__ float d(float x) { return x > 0.0f ? 1.0f : __expf(x); }
+    // phi'(x) from phi(x): phi(x) = x+1 > 1 for x > 0 and exp(x) <= 1 otherwise
+    static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
 };
 template <>
 struct Phi<PHI_NONE> {
     static __device__ __forceinline__ float f(float x) { return x; }
     static __device__ __forceinline__ float d(float) { return 1.0f; }
+    static __device__ __forceinline__ float d_from_f(float) { return 1.0f; }
 };
 
 // ---------------------------------------------------------------------------
-// chunk loaders.  Rows >= S and columns >= ncol read as 0; APPLY_PHI maps the
-// valid entries through phi and leaves padding at exactly 0.
+// chunk staging helpers
 // ---------------------------------------------------------------------------
-template <bool VEC, int PHI, bool APPLY_PHI>
-__device__ __forceinline__ void load_R(f4 (&v)[4], const float* __restrict__ M, long ld,
-                                       long row, bool rok, int ncol, int g)
+// Raw R-layout registers of chunk rows: lane (l16, g) holds row t (clamped to
+// tlast), columns 16ct + 4g .. +3 (clamped to ncol).  Masked by finR.
+template <bool VEC>
+__device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ M, int ld, long rb,
+                                    int t, int tlast, int ncol, int g)
 {
-    const float* p = M + (rok ? row : 0) * ld;
+    const float* p = M + (rb + (t < tlast ? t : tlast)) * (long)ld;
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++) {
-        const int c = 16 * ct + 4 * g;
-        f4 x = load4<VEC>(p, c, ncol, rok);
-        if (APPLY_PHI) {
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                x[i] = (rok && c + i < ncol) ? Phi<PHI>::f(x[i]) : 0.0f;
-        }
-        v[ct] = x;
-    }
+    for (int ct = 0; ct < 4; ct++)
+        v[ct] = load4c<VEC>(p, 16 * ct + 4 * g, ncol);
 }
 
-template <int PHI, bool APPLY_PHI>
-__device__ __forceinline__ void load_C(f4 (&v)[4], const float* __restrict__ M, long ld,
-                                       long row0, int nvalid, int ncol, int l16)
+// Zero the entries outside the valid rows / columns; apply phi to the rest.
+template <int PHI, bool APPLY>
+__device__ __forceinline__ void finR(f4 (&v)[4], bool rok, int ncol, int g)
 {
-    // rows row0 + r for r < nvalid are in range
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++) {
-        const int c = 16 * ct + l16;
+    for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const bool ok = (r < nvalid) && (c < ncol);
-            float x = ok ? M[(row0 + r) * ld + c] : 0.0f;
-            if (APPLY_PHI)
-                x = ok ? Phi<PHI>::f(x) : 0.0f;
-            v[ct][r] = x;
+        for (int i = 0; i < 4; i++) {
+            const bool ok = rok && (16 * ct + 4 * g + i < ncol);
+            const float x = v[ct][i];
+            v[ct][i] = ok ? (APPLY ? Phi<PHI>::f(x) : x) : 0.0f;
         }
+}
+
+__device__ __forceinline__ void putR(float* __restrict__ buf, const f4 (&v)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]) = v[ct];
+}
+
+__device__ __forceinline__ void getR(const float* __restrict__ buf, f4 (&v)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+        v[ct] = *reinterpret_cast<const f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]);
+}
+
+__device__ __forceinline__ void getC(const float* __restrict__ buf, f4 (&c)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            c[ct][r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
+}
+
+// Per-row scalars of the chunk rows 4g+r (clamped), column layout.
+__device__ __forceinline__ f4 ldRowsC(const float* __restrict__ w, long rb, int t0, int tlast,
+                                      int g)
+{
+    f4 v;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int t = t0 + 4 * g + r;
+        v[r] = w[rb + (t < tlast ? t : tlast)];
     }
+    return v;
+}
+
+// Inclusive prefix sum over the 16 chunk rows of a column-layout value
+// (rows 4g+r of column l16); returns the prefixes and the column total.
+__device__ __forceinline__ f4 col_prefix16(f4 c, float& total, int lane)
+{
+    const int g = lane >> 4;
+    f4 p;
+    p[0] = c[0];
+    p[1] = p[0] + c[1];
+    p[2] = p[1] + c[2];
+    p[3] = p[2] + c[3];
+    float x = p[3];
+    float y = __shfl_up(x, 16, 64);
+    x = g >= 1 ? x + y : x;
+    y = __shfl_up(x, 32, 64);
+    x = g >= 2 ? x + y : x;   // inclusive prefix of the 4-row totals over g
+    const float excl = x - p[3];
+    total = __shfl(x, 48 + (lane & 15), 64);
+    return p + excl;
 }
 
 // ---------------------------------------------------------------------------
@@ -103,13 +159,16 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_agg_kernel(
     const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ w,
     float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L)
 {
+    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x * LIN_WAVES + wave;
     if (wid >= Bq * nseg)
         return;
+    float* bX = lds + wave * 2 * CHUNK;
+    float* bY = bX + CHUNK;
     const int seq = wid / nseg, seg = wid - seq * nseg;
-    const int tbeg = seg * L, tend = min(S, tbeg + L);
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
 
     f4 St[4][4];
@@ -120,20 +179,38 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_agg_kernel(
             St[a][c] = f4zero();
     float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
+    f4 nx[4], ny[4], nw = f4splat(1.0f);
+    ldR<VEC>(nx, X, D, rb, tbeg + l16, tlast, D, g);
+    ldR<VEC>(ny, Y, E, rb, tbeg + l16, tlast, E, g);
+    if (w != nullptr)
+        nw = ldRowsC(w, rb, tbeg, tlast, g);
     for (int t0 = tbeg; t0 < tend; t0 += 16) {
-        const int nv = min(4, max(0, tend - (t0 + 4 * g)));
-        f4 xC[4], yC[4];
-        load_C<PHI, true>(xC, X, D, rb + t0 + 4 * g, nv, D, l16);
-        load_C<PHI, false>(yC, Y, E, rb + t0 + 4 * g, nv, E, l16);
-        float wr[4];
+        f4 x[4], y[4];
+        f4 wc = nw;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            wr[r] = (w == nullptr) ? 1.0f : (r < nv ? w[rb + t0 + 4 * g + r] : 0.0f);
+        for (int i = 0; i < 4; i++) {
+            x[i] = nx[i];
+            y[i] = ny[i];
+        }
+        if (t0 + 16 < tend) {
+            ldR<VEC>(nx, X, D, rb, t0 + 16 + l16, tlast, D, g);
+            ldR<VEC>(ny, Y, E, rb, t0 + 16 + l16, tlast, E, g);
+            if (w != nullptr)
+                nw = ldRowsC(w, rb, t0 + 16, tlast, g);
+        }
+        const bool rok = t0 + l16 < tend;
+        finR<PHI, true>(x, rok, D, g);
+        finR<PHI, false>(y, rok, E, g);
+        putR(bX, x, l16, g);
+        putR(bY, y, l16, g);
+        f4 xC[4], yC[4];
+        getC(bX, xC, l16, g);
+        getC(bY, yC, l16, g);
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                zp[dt] += wr[r] * xC[dt][r];
+                zp[dt] += wc[r] * xC[dt][r];   // rows past the segment hold xC = 0
 #pragma unroll
             for (int et = 0; et < 4; et++) {
                 f4 acc = St[dt][et];
@@ -187,18 +264,23 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
     int sfin_de, int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L)
 {
+    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x * LIN_WAVES + wave;
     if (wid >= Bq * nseg)
         return;
+    float* bK = lds + wave * 2 * CHUNK;
+    float* bV = bK + CHUNK;
     const int seq = wid / nseg, seg = wid - seq * nseg;
-    const int tbeg = seg * L, tend = min(S, tbeg + L);
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
 
     // state S[d][e]: St[dt][et] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
-    // z[d]:          zr[dt]   element r <-> d = 16dt + 4g + r (same in every lane row)
-    f4 St[4][4], zr[4];
+    // z (prefix of phi(K) before the chunk) in two layouts:
+    //   zC[dt] = z[16dt + l16]      zR[dt][i] = z[16dt + 4g + i]
+    f4 St[4][4], zR[4];
+    float zC[4];
     if (ws != nullptr) {
         const float* P = ws + (long)wid * LIN_WS;
 #pragma unroll
@@ -208,7 +290,8 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     St[dt][et][r] = P[(16 * dt + 4 * g + r) * 64 + 16 * et + l16];
-            zr[dt] = *reinterpret_cast<const f4*>(P + 4096 + 16 * dt + 4 * g);
+            zR[dt] = *reinterpret_cast<const f4*>(P + 4096 + 16 * dt + 4 * g);
+            zC[dt] = P[4096 + 16 * dt + l16];
         }
     } else {
 #pragma unroll
@@ -216,19 +299,38 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
 #pragma unroll
             for (int et = 0; et < 4; et++)
                 St[dt][et] = f4zero();
-            zr[dt] = f4zero();
+            zR[dt] = f4zero();
+            zC[dt] = 0.0f;
         }
     }
 
+    f4 nq[4], nk[4], nv[4];
+    ldR<VEC>(nq, Q, D, rb, tbeg + l16, tlast, D, g);
+    ldR<VEC>(nk, K, D, rb, tbeg + l16, tlast, D, g);
+    ldR<VEC>(nv, V, E, rb, tbeg + l16, tlast, E, g);
     for (int t0 = tbeg; t0 < tend; t0 += 16) {
+        f4 q[4], k[4], v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            q[i] = nq[i];
+            k[i] = nk[i];
+            v[i] = nv[i];
+        }
+        if (t0 + 16 < tend) {   // next chunk's rows, in flight during this chunk
+            ldR<VEC>(nq, Q, D, rb, t0 + 16 + l16, tlast, D, g);
+            ldR<VEC>(nk, K, D, rb, t0 + 16 + l16, tlast, D, g);
+            ldR<VEC>(nv, V, E, rb, t0 + 16 + l16, tlast, E, g);
+        }
         const long trow = rb + t0 + l16;
         const bool rok = t0 + l16 < tend;
-        const int nv = min(4, max(0, tend - (t0 + 4 * g)));
-        f4 q[4], kR[4], kC[4], vC[4];
-        load_R<VEC, PHI, true>(q, Q, D, trow, rok, D, g);
-        load_R<VEC, PHI, true>(kR, K, D, trow, rok, D, g);
-        load_C<PHI, true>(kC, K, D, rb + t0 + 4 * g, nv, D, l16);
-        load_C<PHI, false>(vC, V, E, rb + t0 + 4 * g, nv, E, l16);
+        finR<PHI, true>(q, rok, D, g);
+        finR<PHI, true>(k, rok, D, g);
+        finR<PHI, false>(v, rok, E, g);
+        putR(bK, k, l16, g);
+        putR(bV, v, l16, g);
+        f4 kC[4], vC[4];
+        getC(bK, kC, l16, g);
+        getC(bV, vC, l16, g);
 
         // A^T[s][t] = phi(K_s).phi(Q_t), lane t = l16, element r <-> s = 4g + r; keep s <= t
         f4 At = f4zero();
@@ -236,42 +338,41 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                At = mfma16(kR[dt][r], q[dt][r], At);
-        f4 Lt;   // lower-triangular ones, as the B operand of the z_cache product
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const bool keep = 4 * g + r <= l16;
-            At[r] = keep ? At[r] : 0.0f;
-            Lt[r] = keep ? 1.0f : 0.0f;
-        }
-        // z_t (R-layout of row t = l16) = z_prev + sum_{s<=t} phi(K_s)
-        f4 zc[4];
+                At = mfma16(k[dt][r], q[dt][r], At);
+        // den_t = phi(Q_t).z_prev + sum_{s<=t in chunk} A[t][s]
         float dpart = 0.0f;
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            f4 acc = zr[dt];
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                acc = mfma16(kC[dt][r], Lt[r], acc);
-            zc[dt] = acc;
-            dpart += q[dt][0] * acc[0] + q[dt][1] * acc[1] + q[dt][2] * acc[2] + q[dt][3] * acc[3];
+        for (int r = 0; r < 4; r++) {
+            At[r] = (4 * g + r <= l16) ? At[r] : 0.0f;
+            dpart += At[r];
         }
-        const float dn = xrow_sum(dpart);        // den_t = phi(Q_t) . z_t
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            dpart += q[dt][0] * zR[dt][0] + q[dt][1] * zR[dt][1] + q[dt][2] * zR[dt][2] +
+                     q[dt][3] * zR[dt][3];
+        const float dn = xrow_sum(dpart);
         const float inv = 1.0f / (dn + 1e-8f);
-        if (rok) {
-            if (g == 0)
-                den[trow] = den_incl_eps ? dn + 1e-8f : dn;
-            if (zcache != nullptr)
+        if (rok && g == 0)
+            den[trow] = den_incl_eps ? dn + 1e-8f : dn;
+        // z_t (column layout) = z_prev + inclusive prefix of phi(K) over the chunk
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++)
-                    store4<VEC>(zcache + trow * D, 16 * dt + 4 * g, D, zc[dt]);
+        for (int dt = 0; dt < 4; dt++) {
+            float tot;
+            const f4 pz = col_prefix16(kC[dt], tot, lane);
+            if (zcache != nullptr && 16 * dt + l16 < D)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int t = t0 + 4 * g + r;
+                    if (t < tend)
+                        zcache[(rb + t) * D + 16 * dt + l16] = zC[dt] + pz[r];
+                }
+            zC[dt] += tot;
         }
-        // next chunk's z = z_t of row 15
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                zr[dt][r] = __shfl(zc[dt][r], (lane & 48) | 15, 64);
+            for (int i = 0; i < 4; i++)
+                zR[dt][i] = __shfl(zC[dt], 4 * g + i, 64);
 
         // O^T[e][t] = sum_d S[d][e] phi(Q_t)[d] + sum_s V_s[e] A^T[s][t]
 #pragma unroll
@@ -314,15 +415,11 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
                     if (d < D && e < E)
                         Sp[sfin_de ? (long)d * E + e : (long)e * D + d] = St[dt][et][r];
                 }
-        if (zfin != nullptr && l16 == 0)
+        if (zfin != nullptr && g == 0)
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int d = 16 * dt + 4 * g + r;
-                    if (d < D)
-                        zfin[(long)seq * D + d] = zr[dt][r];
-                }
+                if (16 * dt + l16 < D)
+                    zfin[(long)seq * D + 16 * dt + l16] = zC[dt];
     }
 }
 
@@ -363,14 +460,18 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
     float* __restrict__ dQ, const float* __restrict__ ws, int Bq, int S, int D, int E, int nseg,
     int L)
 {
+    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x * LIN_WAVES + wave;
     if (wid >= Bq * nseg)
         return;
+    float* bK = lds + wave * 2 * CHUNK;
+    float* bV = bK + CHUNK;
     const int seq = wid / nseg, seg = wid - seq * nseg;
-    const int tbeg = seg * L, tend = min(S, tbeg + L);
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
+    constexpr bool HAS_Q = PHI != PHI_NONE;
 
     // state transposed: StT[et][dt] lane (d = 16dt + l16), element r <-> e = 16et + 4g + r
     f4 StT[4][4];
@@ -389,19 +490,42 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
                 StT[et][dt] = f4zero();
     }
 
+    f4 nk[4], nv[4], ndn[4], nzc[4], nq[4];
+    float ndd;
+    auto fetch = [&](int t0) {
+        const int t = t0 + l16;
+        ldR<VEC>(nk, K, D, rb, t, tlast, D, g);
+        ldR<VEC>(nv, V, E, rb, t, tlast, E, g);
+        ldR<VEC>(ndn, dnum, E, rb, t, tlast, E, g);
+        ldR<VEC>(nzc, zcache, D, rb, t, tlast, D, g);
+        if (HAS_Q)
+            ldR<VEC>(nq, Q, D, rb, t, tlast, D, g);
+        ndd = dden[rb + (t < tlast ? t : tlast)];
+    };
+    fetch(tbeg);
     for (int t0 = tbeg; t0 < tend; t0 += 16) {
+        f4 k[4], v[4], dn[4], zc[4], q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            k[i] = nk[i];
+            v[i] = nv[i];
+            dn[i] = ndn[i];
+            zc[i] = nzc[i];
+            q[i] = HAS_Q ? nq[i] : f4zero();
+        }
+        const float dd = ndd;
+        if (t0 + 16 < tend)
+            fetch(t0 + 16);
         const long trow = rb + t0 + l16;
         const bool rok = t0 + l16 < tend;
-        const int nv = min(4, max(0, tend - (t0 + 4 * g)));
-        f4 kC[4], vR[4], vC[4], dnR[4], zcR[4], qR[4];
-        load_C<PHI, true>(kC, K, D, rb + t0 + 4 * g, nv, D, l16);
-        load_R<VEC, PHI, false>(vR, V, E, trow, rok, E, g);
-        load_C<PHI, false>(vC, V, E, rb + t0 + 4 * g, nv, E, l16);
-        load_R<VEC, PHI, false>(dnR, dnum, E, trow, rok, E, g);
-        load_R<VEC, PHI, false>(zcR, zcache, D, trow, rok, D, g);
-        if (PHI != PHI_NONE)
-            load_R<VEC, PHI, false>(qR, Q, D, trow, rok, D, g);
-        const float dd = rok ? dden[trow] : 0.0f;
+        finR<PHI, true>(k, rok, D, g);
+        finR<PHI, false>(v, rok, E, g);
+        finR<PHI, false>(dn, rok, E, g);
+        putR(bK, k, l16, g);
+        putR(bV, v, l16, g);
+        f4 kC[4], vC[4];
+        getC(bK, kC, l16, g);
+        getC(bV, vC, l16, g);
 
         // G^T[s][t] = V_s . dnum_t, lane t = l16, element r <-> s = 4g + r; keep s <= t
         f4 G = f4zero();
@@ -409,7 +533,7 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
         for (int et = 0; et < 4; et++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                G = mfma16(vR[et][r], dnR[et][r], G);
+                G = mfma16(v[et][r], dn[et][r], G);
 #pragma unroll
         for (int r = 0; r < 4; r++)
             G[r] = (4 * g + r <= l16) ? G[r] : 0.0f;
@@ -417,19 +541,19 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
         // dQ^T[d][t] = z_t[d] dden_t + sum_e S[d][e] dnum_t[e] + sum_s phi(K_s)[d] G^T[s][t]
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
-            f4 acc = zcR[dt] * dd;
+            f4 acc = zc[dt] * dd;
 #pragma unroll
             for (int et = 0; et < 4; et++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(StT[et][dt][r], dnR[et][r], acc);
+                    acc = mfma16(StT[et][dt][r], dn[et][r], acc);
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 acc = mfma16(kC[dt][r], G[r], acc);
-            if (PHI != PHI_NONE) {
+            if (HAS_Q) {
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[i] *= Phi<PHI>::d(qR[dt][i]);
+                    acc[i] *= Phi<PHI>::d(q[dt][i]);
             }
             if (rok)
                 store4<VEC>(dQ + trow * D, 16 * dt + 4 * g, D, acc);
@@ -449,147 +573,202 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV (reverse-direction scan)
+// dK, dV (reverse-direction scan).  Two waves per segment share the staged
+// chunk through LDS: wave 0 holds S*[d][e] and produces dV, wave 1 holds
+// S*^T and z* and produces dK.
 // ---------------------------------------------------------------------------
+constexpr int DKDV_THREADS = 128;
+constexpr int DKDV_STAGE = 4 * CHUNK + 16;   // phi(Q), phi(K), V, dnum chunks + dden rows
+
 template <int PHI, bool VEC>
-__global__ __launch_bounds__(LIN_THREADS) void lin_dkdv_kernel(
+__global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dnum, const float* __restrict__ dden, float* __restrict__ dK,
     float* __restrict__ dV, const float* __restrict__ ws, int Bq, int S, int D, int E, int nseg,
     int L)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float lds[2 * DKDV_STAGE];   // double buffered
+    const int lane = threadIdx.x & 63, role = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int wid = blockIdx.x * LIN_WAVES + wave;
-    if (wid >= Bq * nseg)
-        return;
+    const int wid = blockIdx.x;   // segment
     const int seq = wid / nseg, seg = wid - seq * nseg;
-    const int tbeg = seg * L, tend = min(S, tbeg + L);
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
 
-    // suffix state S*[d][e] in two layouts:
-    //   Sd[dt][et]  lane (e = 16et + l16), element r <-> d = 16dt + 4g + r   (dV product)
-    //   SdT[et][dt] lane (d = 16dt + l16), element r <-> e = 16et + 4g + r   (dK product)
-    // z*[d]: zs[dt] element r <-> d = 16dt + 4g + r
-    f4 Sd[4][4], SdT[4][4], zs[4];
-    if (ws != nullptr) {
-        const float* P = ws + (long)wid * LIN_WS;
+    // role 0: S[dt][et] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r   (dV product)
+    // role 1: S[et][dt] lane (d = 16dt + l16), element r <-> e = 16et + 4g + r   (dK product)
+    //         zs[dt] element r <-> d = 16dt + 4g + r
+    f4 Sm[4][4], zs[4];
+    {
+        const float* P = ws != nullptr ? ws + (long)wid * LIN_WS : nullptr;
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
+        for (int a = 0; a < 4; a++) {
 #pragma unroll
-            for (int et = 0; et < 4; et++) {
+            for (int c = 0; c < 4; c++) {
+                if (P == nullptr) {
+                    Sm[a][c] = f4zero();
+                } else if (role == 0) {
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    Sd[dt][et][r] = P[(16 * dt + 4 * g + r) * 64 + 16 * et + l16];
-                SdT[et][dt] = *reinterpret_cast<const f4*>(P + (16 * dt + l16) * 64 + 16 * et + 4 * g);
+                    for (int r = 0; r < 4; r++)
+                        Sm[a][c][r] = P[(16 * a + 4 * g + r) * 64 + 16 * c + l16];
+                } else {
+                    Sm[a][c] = *reinterpret_cast<const f4*>(P + (16 * c + l16) * 64 + 16 * a + 4 * g);
+                }
             }
-            zs[dt] = *reinterpret_cast<const f4*>(P + 4096 + 16 * dt + 4 * g);
-        }
-    } else {
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-#pragma unroll
-            for (int et = 0; et < 4; et++) {
-                Sd[dt][et] = f4zero();
-                SdT[et][dt] = f4zero();
-            }
-            zs[dt] = f4zero();
+            zs[a] = P != nullptr ? *reinterpret_cast<const f4*>(P + 4096 + 16 * a + 4 * g) : f4zero();
         }
     }
 
+    // role 0 fetches Q and K rows, role 1 V and dnum rows (+ dden)
+    f4 na[4], nb[4];
+    float ndd = 0.0f;
+    auto fetch = [&](int t0) {
+        const int t = t0 + l16;
+        if (role == 0) {
+            ldR<VEC>(na, Q, D, rb, t, tlast, D, g);
+            ldR<VEC>(nb, K, D, rb, t, tlast, D, g);
+        } else {
+            ldR<VEC>(na, V, E, rb, t, tlast, E, g);
+            ldR<VEC>(nb, dnum, E, rb, t, tlast, E, g);
+            ndd = dden[rb + (t < tlast ? t : tlast)];
+        }
+    };
     const int nchunk = (tend - tbeg + 15) / 16;
+    fetch(tbeg + 16 * (nchunk - 1));
     for (int c = nchunk - 1; c >= 0; c--) {
         const int t0 = tbeg + 16 * c;
+        float* st = lds + (c & 1) * DKDV_STAGE;
+        float* bQ = st;
+        float* bK = st + CHUNK;
+        float* bV = st + 2 * CHUNK;
+        float* bN = st + 3 * CHUNK;
+        float* bd = st + 4 * CHUNK;
+        f4 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            a[i] = na[i];
+            b[i] = nb[i];
+        }
+        const float dd = ndd;
+        if (c > 0)
+            fetch(t0 - 16);
         const long trow = rb + t0 + l16;
         const bool rok = t0 + l16 < tend;
-        const int nv = min(4, max(0, tend - (t0 + 4 * g)));
-        f4 qR[4], qC[4], kraw[4], kR[4], vR[4], dnR[4], dnC[4];
-        load_R<VEC, PHI, true>(qR, Q, D, trow, rok, D, g);
-        load_C<PHI, true>(qC, Q, D, rb + t0 + 4 * g, nv, D, l16);
-        load_R<VEC, PHI, false>(kraw, K, D, trow, rok, D, g);
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                kR[dt][i] = (rok && 16 * dt + 4 * g + i < D) ? Phi<PHI>::f(kraw[dt][i]) : 0.0f;
-        load_R<VEC, PHI, false>(vR, V, E, trow, rok, E, g);
-        load_R<VEC, PHI, false>(dnR, dnum, E, trow, rok, E, g);
-        load_C<PHI, false>(dnC, dnum, E, rb + t0 + 4 * g, nv, E, l16);
-        f4 ddC;
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            ddC[r] = r < nv ? dden[rb + t0 + 4 * g + r] : 0.0f;
-
-        // M1^T[s][t] = phi(Q_s).phi(K_t); M2^T[s][t] = dnum_s.V_t + dden_s;
-        // lane t = l16, element r <-> s = 4g + r; keep s >= t
-        f4 M1 = f4zero(), M2 = f4zero();
-#pragma unroll
-        for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                M1 = mfma16(qR[ct][r], kR[ct][r], M1);
-                M2 = mfma16(dnR[ct][r], vR[ct][r], M2);
-            }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const bool keep = 4 * g + r >= l16;
-            M1[r] = keep ? M1[r] : 0.0f;
-            M2[r] = keep ? M2[r] + ddC[r] : 0.0f;
+        if (role == 0) {
+            finR<PHI, true>(a, rok, D, g);
+            finR<PHI, true>(b, rok, D, g);
+            putR(bQ, a, l16, g);
+            putR(bK, b, l16, g);
+        } else {
+            finR<PHI, false>(a, rok, E, g);
+            finR<PHI, false>(b, rok, E, g);
+            putR(bV, a, l16, g);
+            putR(bN, b, l16, g);
+            if (g == 0)
+                bd[l16] = rok ? dd : 0.0f;
         }
-        // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_s dnum_s[e] M1^T[s][t]
+        __syncthreads();
+
+        f4 qC[4], dnC[4];
+        getC(bQ, qC, l16, g);
+        getC(bN, dnC, l16, g);
+        if (role == 0) {
+            f4 qR[4], kR[4];
+            getR(bQ, qR, l16, g);
+            getR(bK, kR, l16, g);
+            // M1^T[s][t] = phi(Q_s).phi(K_t); lane t = l16, element r <-> s = 4g + r; keep s >= t
+            f4 M1 = f4zero();
 #pragma unroll
-        for (int et = 0; et < 4; et++) {
-            f4 acc = f4zero();
+            for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    M1 = mfma16(qR[ct][r], kR[ct][r], M1);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                M1[r] = (4 * g + r >= l16) ? M1[r] : 0.0f;
+            // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_s dnum_s[e] M1^T[s][t]
+#pragma unroll
+            for (int et = 0; et < 4; et++) {
+                f4 acc = f4zero();
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc = mfma16(Sm[dt][et][r], kR[dt][r], acc);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc = mfma16(dnC[et][r], M1[r], acc);
+                if (rok)
+                    store4<VEC>(dV + trow * E, 16 * et + 4 * g, E, acc);
+            }
+            // S* += phi(Q)^T dnum
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc = mfma16(Sd[dt][et][r], kR[dt][r], acc);
+                for (int et = 0; et < 4; et++) {
+                    f4 acc = Sm[dt][et];
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc = mfma16(qC[dt][r], dnC[et][r], acc);
+                    Sm[dt][et] = acc;
+                }
+        } else {
+            f4 vR[4], dnR[4], kR[4];
+            getR(bV, vR, l16, g);
+            getR(bN, dnR, l16, g);
+            getR(bK, kR, l16, g);
+            f4 ddC;
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                acc = mfma16(dnC[et][r], M1[r], acc);
-            if (rok)
-                store4<VEC>(dV + trow * E, 16 * et + 4 * g, E, acc);
-        }
-        // dK^T[d][t] = (z*[d] + sum_e S*[d][e] V_t[e] + sum_s phi(Q_s)[d] M2^T[s][t]) phi'(K_t[d])
+                ddC[r] = bd[4 * g + r];
+            // M2^T[s][t] = dnum_s.V_t + dden_s; lane t = l16, element r <-> s = 4g + r; keep s >= t
+            f4 M2 = f4zero();
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            f4 acc = zs[dt];
+            for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    M2 = mfma16(dnR[ct][r], vR[ct][r], M2);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                M2[r] = (4 * g + r >= l16) ? M2[r] + ddC[r] : 0.0f;
+            // dK^T[d][t] = (z*[d] + sum_e S*[d][e] V_t[e] + sum_s phi(Q_s)[d] M2^T[s][t]) phi'(K_t[d])
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                f4 acc = zs[dt];
+#pragma unroll
+                for (int et = 0; et < 4; et++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc = mfma16(Sm[et][dt][r], vR[et][r], acc);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc = mfma16(qC[dt][r], M2[r], acc);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    acc[i] *= Phi<PHI>::d_from_f(kR[dt][i]);
+                if (rok)
+                    store4<VEC>(dK + trow * D, 16 * dt + 4 * g, D, acc);
+            }
+            // S*^T += dnum^T phi(Q); z* += phi(Q)^T dden (column sums, VALU)
 #pragma unroll
             for (int et = 0; et < 4; et++)
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc = mfma16(SdT[et][dt][r], vR[et][r], acc);
+                for (int dt = 0; dt < 4; dt++) {
+                    f4 acc = Sm[et][dt];
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                acc = mfma16(qC[dt][r], M2[r], acc);
-            if (PHI != PHI_NONE) {
+                    for (int r = 0; r < 4; r++)
+                        acc = mfma16(dnC[et][r], qC[dt][r], acc);
+                    Sm[et][dt] = acc;
+                }
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                float zp = qC[dt][0] * ddC[0] + qC[dt][1] * ddC[1] + qC[dt][2] * ddC[2] +
+                           qC[dt][3] * ddC[3];
+                zp = xrow_sum(zp);   // column total for d = 16dt + l16
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[i] *= Phi<PHI>::d(kraw[dt][i]);
+                    zs[dt][i] += __shfl(zp, 4 * g + i, 64);
             }
-            if (rok)
-                store4<VEC>(dK + trow * D, 16 * dt + 4 * g, D, acc);
-        }
-        // S* += phi(Q)^T dnum (both layouts), z* += phi(Q)^T dden
-#pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-#pragma unroll
-            for (int et = 0; et < 4; et++) {
-                f4 a = Sd[dt][et], b = SdT[et][dt];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    a = mfma16(qC[dt][r], dnC[et][r], a);
-                    b = mfma16(dnC[et][r], qC[dt][r], b);
-                }
-                Sd[dt][et] = a;
-                SdT[et][dt] = b;
-            }
-            f4 z = zs[dt];
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                z = mfma16(qC[dt][r], ddC[r], z);
-            zs[dt] = z;
         }
     }
 }
@@ -1023,8 +1202,7 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
     } else {
         wsf = nullptr;
     }
-    const int nw = Bq * p.nseg;
-    dim3 grid((unsigned)((nw + LIN_WAVES - 1) / LIN_WAVES)), block(LIN_THREADS);
+    dim3 grid((unsigned)(Bq * p.nseg)), block(DKDV_THREADS);
     ProfScope ps(st, "lin_dkdv");
     if (vec)
         hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true>), grid, block, 0, st, Q, K, V, dnum, dden,

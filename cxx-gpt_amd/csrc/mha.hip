@@ -39,28 +39,6 @@ namespace cxg {
 constexpr int MHA_BM = 64;   // query rows per tile
 constexpr int MHA_BN = 64;   // key rows per tile
 
-// Clamped 4-wide load for streamed tiles: the row and column are clamped into
-// the valid data, so the load always issues and never needs a guard.  Padded
-// positions (rows >= S, columns >= Dh) therefore hold copies of real, finite
-// inputs; the kernels neutralise them elsewhere: the operand they meet in a
-// product is zero (Q/K/V registers zeroed beyond Dh) or the probability they
-// carry is masked to exactly 0.  Keeping loads unconditional lets a thread put
-// all of a tile's loads in flight at once.  VEC: n % 4 == 0 and the row base
-// is 16-byte aligned.
-template <bool VEC>
-__device__ __forceinline__ f4 load4c(const float* __restrict__ row, int c, int n)
-{
-    f4 v;
-    if (VEC) {
-        v = *reinterpret_cast<const f4*>(row + (c < n ? c : n - 4));
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            v[i] = row[c + i < n ? c + i : n - 1];
-    }
-    return v;
-}
-
 // ROWS x DHP fp32 tile of one head, held in registers between its global load
 // and its LDS store (so the next tile's loads overlap the current tile's math).
 // Thread tid of NT owns f4 units u = tid + i*NT: row u / (DHP/4), column
