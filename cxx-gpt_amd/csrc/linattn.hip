@@ -67,30 +67,54 @@ struct Phi<PHI_NONE> {
 // ---------------------------------------------------------------------------
 // chunk staging helpers
 // ---------------------------------------------------------------------------
-// Raw R-layout registers of chunk rows: lane (l16, g) holds row t (clamped to
-// tlast), columns 16ct + 4g .. +3 (clamped to ncol).  Masked by finR.
+// Template flags of the fast-path kernels: VEC = widths multiple of 4 and
+// 16-byte aligned rows (16-byte loads / stores), FW = D == E == 64 (no column
+// masks at all).  Row addresses are a wave-uniform chunk base plus a 32-bit
+// per-lane offset.
+
+// Raw R-layout registers of a chunk: lane (l16, g) holds chunk row `ro` (the
+// caller clamps it into the segment), columns 16ct + 4g .. +3 (clamped to ncol).
 template <bool VEC>
-__device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ M, int ld, long rb,
-                                    int t, int tlast, int ncol, int g)
+__device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ base, int ld, int ro,
+                                    int ncol, int g)
 {
-    const float* p = M + (rb + (t < tlast ? t : tlast)) * (long)ld;
+    const float* p = base + ro * ld;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
         v[ct] = load4c<VEC>(p, 16 * ct + 4 * g, ncol);
 }
 
-// Zero the entries outside the valid rows / columns; apply phi to the rest.
-template <int PHI, bool APPLY>
-__device__ __forceinline__ void finR(f4 (&v)[4], bool rok, int ncol, int g)
+// Apply phi, then zero the entries outside the valid columns (unless the
+// width is full) and rows (only in a partial chunk; `full` is wave-uniform).
+template <int PHI, bool APPLY, bool FW>
+__device__ __forceinline__ void finR(f4 (&v)[4], bool full, bool rok, int ncol, int g)
 {
+    if (APPLY && PHI != PHI_NONE)
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++)
+        for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool ok = rok && (16 * ct + 4 * g + i < ncol);
-            const float x = v[ct][i];
-            v[ct][i] = ok ? (APPLY ? Phi<PHI>::f(x) : x) : 0.0f;
-        }
+            for (int i = 0; i < 4; i++)
+                v[ct][i] = Phi<PHI>::f(v[ct][i]);
+    if (!FW)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[ct][i] = (16 * ct + 4 * g + i < ncol) ? v[ct][i] : 0.0f;
+    if (!full)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+            v[ct] = rok ? v[ct] : f4zero();
+}
+
+// Store an R-layout f4 of one row: no guard for a full width.
+template <bool VEC, bool FW>
+__device__ __forceinline__ void stR(float* __restrict__ row, int c, int n, f4 v)
+{
+    if (FW)
+        *reinterpret_cast<f4*>(row + c) = v;
+    else
+        store4<VEC>(row, c, n, v);
 }
 
 __device__ __forceinline__ void putR(float* __restrict__ buf, const f4 (&v)[4], int l16, int g)
@@ -116,16 +140,13 @@ __device__ __forceinline__ void getC(const float* __restrict__ buf, f4 (&c)[4], 
             c[ct][r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
 }
 
-// Per-row scalars of the chunk rows 4g+r (clamped), column layout.
-__device__ __forceinline__ f4 ldRowsC(const float* __restrict__ w, long rb, int t0, int tlast,
-                                      int g)
+// Per-row scalars of chunk rows 4g+r (row offsets clamped to rmax), column layout.
+__device__ __forceinline__ f4 ldRowsC(const float* __restrict__ w, int rmax, int g)
 {
     f4 v;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int t = t0 + 4 * g + r;
-        v[r] = w[rb + (t < tlast ? t : tlast)];
-    }
+    for (int r = 0; r < 4; r++)
+        v[r] = w[min(4 * g + r, rmax)];
     return v;
 }
 
@@ -150,88 +171,129 @@ __device__ __forceinline__ f4 col_prefix16(f4 c, float& total, int lane)
 }
 
 // ---------------------------------------------------------------------------
+// Segment kernels.  A workgroup of NW waves owns one segment; the 64x64
+// state is split between the waves by 32-column halves, so a wave keeps only
+// a 64x32 slice in registers.  Each chunk's rows are loaded (one chunk ahead)
+// by the wave that owns that input, transformed (phi, masks) and written to a
+// double-buffered LDS stage; one barrier per chunk publishes the stage to
+// the other waves.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f4 colC(const float* __restrict__ buf, int ct, int l16, int g)
+{
+    f4 c;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        c[r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
+    return c;
+}
+
+// ---------------------------------------------------------------------------
 // per-segment aggregates: dS = sum_s phi(X_s)^T Y_s (64 x 64), dz = sum_s w_s phi(X_s)
 // (w = 1 when null).  Forward direction: X = K, Y = V.  Reverse: X = Q, Y = dnum,
 // w = dden.  Written row-major [d][e] followed by z[d], LIN_WS floats per segment.
+// Wave h accumulates columns e of tiles et = 2h, 2h+1.
 // ---------------------------------------------------------------------------
-template <int PHI, bool VEC>
-__global__ __launch_bounds__(LIN_THREADS) void lin_agg_kernel(
+constexpr int AGG_THREADS = 128;
+constexpr int AGG_STAGE = 2 * CHUNK + 16;
+
+template <int PHI, bool VEC, bool FW>
+__global__ __launch_bounds__(AGG_THREADS) void lin_agg_kernel(
     const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ w,
     float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L)
 {
-    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float lds[2 * AGG_STAGE];
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int wid = blockIdx.x * LIN_WAVES + wave;
-    if (wid >= Bq * nseg)
-        return;
-    float* bX = lds + wave * 2 * CHUNK;
-    float* bY = bX + CHUNK;
+    const int wid = blockIdx.x;
     const int seq = wid / nseg, seg = wid - seq * nseg;
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
 
-    f4 St[4][4];
+    f4 St[4][2];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            St[a][c] = f4zero();
+        for (int j = 0; j < 2; j++)
+            St[a][j] = f4zero();
     float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    f4 nx[4], ny[4], nw = f4splat(1.0f);
-    ldR<VEC>(nx, X, D, rb, tbeg + l16, tlast, D, g);
-    ldR<VEC>(ny, Y, E, rb, tbeg + l16, tlast, E, g);
-    if (w != nullptr)
-        nw = ldRowsC(w, rb, tbeg, tlast, g);
-    for (int t0 = tbeg; t0 < tend; t0 += 16) {
-        f4 x[4], y[4];
-        f4 wc = nw;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            x[i] = nx[i];
-            y[i] = ny[i];
-        }
-        if (t0 + 16 < tend) {
-            ldR<VEC>(nx, X, D, rb, t0 + 16 + l16, tlast, D, g);
-            ldR<VEC>(ny, Y, E, rb, t0 + 16 + l16, tlast, E, g);
+    f4 na[4];
+    float nw = 1.0f;
+    auto fetch = [&](int t0) {
+        const int ro = min(l16, tlast - t0);
+        if (h == 0) {
+            ldR<VEC>(na, X + (rb + t0) * D, D, ro, D, g);
             if (w != nullptr)
-                nw = ldRowsC(w, rb, t0 + 16, tlast, g);
+                nw = w[rb + t0 + ro];
+        } else {
+            ldR<VEC>(na, Y + (rb + t0) * E, E, ro, E, g);
         }
-        const bool rok = t0 + l16 < tend;
-        finR<PHI, true>(x, rok, D, g);
-        finR<PHI, false>(y, rok, E, g);
-        putR(bX, x, l16, g);
-        putR(bY, y, l16, g);
-        f4 xC[4], yC[4];
+    };
+    fetch(tbeg);
+    int c = 0;
+    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+        float* st = lds + (c & 1) * AGG_STAGE;
+        float* bX = st;
+        float* bY = st + CHUNK;
+        float* bw = st + 2 * CHUNK;
+        f4 a[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            a[i] = na[i];
+        const float wv = nw;
+        if (t0 + 16 < tend)
+            fetch(t0 + 16);
+        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        if (h == 0) {
+            finR<PHI, true, FW>(a, full, rok, D, g);
+            putR(bX, a, l16, g);
+            if (g == 0)
+                bw[l16] = wv;
+        } else {
+            finR<PHI, false, FW>(a, full, rok, E, g);
+            putR(bY, a, l16, g);
+        }
+        __syncthreads();
+        f4 xC[4], yC[2];
         getC(bX, xC, l16, g);
-        getC(bY, yC, l16, g);
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
+        for (int j = 0; j < 2; j++)
+            yC[j] = colC(bY, 2 * h + j, l16, g);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                zp[dt] += wc[r] * xC[dt][r];   // rows past the segment hold xC = 0
+        for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int et = 0; et < 4; et++) {
-                f4 acc = St[dt][et];
+            for (int j = 0; j < 2; j++) {
+                f4 acc = St[dt][j];
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(xC[dt][r], yC[et][r], acc);
-                St[dt][et] = acc;
+                    acc = mfma16(xC[dt][r], yC[j][r], acc);
+                St[dt][j] = acc;
             }
+        if (h == 0) {
+            f4 wc;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                wc[r] = bw[4 * g + r];
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    zp[dt] += wc[r] * xC[dt][r];   // rows past the segment hold xC = 0
         }
     }
     float* P = ws + (long)wid * LIN_WS;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
-        for (int et = 0; et < 4; et++)
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                P[(16 * dt + 4 * g + r) * 64 + 16 * et + l16] = St[dt][et][r];
-        const float z = xrow_sum(zp[dt]);
-        if (g == 0)
-            P[4096 + 16 * dt + l16] = z;
+                P[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16] = St[dt][j][r];
+        if (h == 0) {
+            const float z = xrow_sum(zp[dt]);
+            if (g == 0)
+                P[4096 + 16 * dt + l16] = z;
+        }
     }
 }
 
@@ -255,41 +317,41 @@ __global__ __launch_bounds__(256) void lin_scan_kernel(float* __restrict__ ws, i
 }
 
 // ---------------------------------------------------------------------------
-// forward
+// forward.  Wave h produces output columns of tiles et = 2h, 2h+1 and keeps
+// that half of the state; both waves track z (wave 0 writes den and z_cache).
 // ---------------------------------------------------------------------------
-template <int PHI, bool VEC>
-__global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
+constexpr int FWD_THREADS = 128;
+constexpr int FWD_STAGE = 3 * CHUNK;   // phi(Q), phi(K), V
+
+template <int PHI, bool VEC, bool FW>
+__global__ __launch_bounds__(FWD_THREADS) void lin_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zcache,
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
     int sfin_de, int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L)
 {
-    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float lds[2 * FWD_STAGE + CHUNK];
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int wid = blockIdx.x * LIN_WAVES + wave;
-    if (wid >= Bq * nseg)
-        return;
-    float* bK = lds + wave * 2 * CHUNK;
-    float* bV = bK + CHUNK;
+    const int wid = blockIdx.x;
     const int seq = wid / nseg, seg = wid - seq * nseg;
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
+    float* bZ = lds + 2 * FWD_STAGE;   // wave 0: z rows for the z_cache store
 
-    // state S[d][e]: St[dt][et] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
-    // z (prefix of phi(K) before the chunk) in two layouts:
-    //   zC[dt] = z[16dt + l16]      zR[dt][i] = z[16dt + 4g + i]
-    f4 St[4][4], zR[4];
+    // state slice S[d][e], et = 2h + j: St[dt][j] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
+    // z (prefix of phi(K) before the chunk): zC[dt] = z[16dt + l16], zR[dt][i] = z[16dt + 4g + i]
+    f4 St[4][2], zR[4];
     float zC[4];
     if (ws != nullptr) {
         const float* P = ws + (long)wid * LIN_WS;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
-            for (int et = 0; et < 4; et++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    St[dt][et][r] = P[(16 * dt + 4 * g + r) * 64 + 16 * et + l16];
+                    St[dt][j][r] = P[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16];
             zR[dt] = *reinterpret_cast<const f4*>(P + 4096 + 16 * dt + 4 * g);
             zC[dt] = P[4096 + 16 * dt + l16];
         }
@@ -297,40 +359,56 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
-            for (int et = 0; et < 4; et++)
-                St[dt][et] = f4zero();
+            for (int j = 0; j < 2; j++)
+                St[dt][j] = f4zero();
             zR[dt] = f4zero();
             zC[dt] = 0.0f;
         }
     }
 
-    f4 nq[4], nk[4], nv[4];
-    ldR<VEC>(nq, Q, D, rb, tbeg + l16, tlast, D, g);
-    ldR<VEC>(nk, K, D, rb, tbeg + l16, tlast, D, g);
-    ldR<VEC>(nv, V, E, rb, tbeg + l16, tlast, E, g);
-    for (int t0 = tbeg; t0 < tend; t0 += 16) {
-        f4 q[4], k[4], v[4];
+    // wave 0 fetches Q and K rows, wave 1 V rows
+    f4 na[4], nb[4];
+    auto fetch = [&](int t0) {
+        const int ro = min(l16, tlast - t0);
+        if (h == 0) {
+            ldR<VEC>(na, Q + (rb + t0) * D, D, ro, D, g);
+            ldR<VEC>(nb, K + (rb + t0) * D, D, ro, D, g);
+        } else {
+            ldR<VEC>(na, V + (rb + t0) * E, E, ro, E, g);
+#pragma unroll
+            for (int i = 0; i < 4; i++)   // keeps nb defined on both paths (no stack copy)
+                nb[i] = na[i];
+        }
+    };
+    fetch(tbeg);
+    int c = 0;
+    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+        float* st = lds + (c & 1) * FWD_STAGE;
+        float* bQ = st;
+        float* bK = st + CHUNK;
+        float* bV = st + 2 * CHUNK;
+        f4 a[4], b[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            q[i] = nq[i];
-            k[i] = nk[i];
-            v[i] = nv[i];
+            a[i] = na[i];
+            b[i] = nb[i];
         }
-        if (t0 + 16 < tend) {   // next chunk's rows, in flight during this chunk
-            ldR<VEC>(nq, Q, D, rb, t0 + 16 + l16, tlast, D, g);
-            ldR<VEC>(nk, K, D, rb, t0 + 16 + l16, tlast, D, g);
-            ldR<VEC>(nv, V, E, rb, t0 + 16 + l16, tlast, E, g);
+        if (t0 + 16 < tend)   // next chunk's rows, in flight during this chunk
+            fetch(t0 + 16);
+        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        if (h == 0) {
+            finR<PHI, true, FW>(a, full, rok, D, g);
+            finR<PHI, true, FW>(b, full, rok, D, g);
+            putR(bQ, a, l16, g);
+            putR(bK, b, l16, g);
+        } else {
+            finR<PHI, false, FW>(a, full, rok, E, g);
+            putR(bV, a, l16, g);
         }
-        const long trow = rb + t0 + l16;
-        const bool rok = t0 + l16 < tend;
-        finR<PHI, true>(q, rok, D, g);
-        finR<PHI, true>(k, rok, D, g);
-        finR<PHI, false>(v, rok, E, g);
-        putR(bK, k, l16, g);
-        putR(bV, v, l16, g);
-        f4 kC[4], vC[4];
-        getC(bK, kC, l16, g);
-        getC(bV, vC, l16, g);
+        __syncthreads();
+        f4 q[4], k[4];
+        getR(bQ, q, l16, g);
+        getR(bK, k, l16, g);
 
         // A^T[s][t] = phi(K_s).phi(Q_t), lane t = l16, element r <-> s = 4g + r; keep s <= t
         f4 At = f4zero();
@@ -352,20 +430,22 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
                      q[dt][3] * zR[dt][3];
         const float dn = xrow_sum(dpart);
         const float inv = 1.0f / (dn + 1e-8f);
-        if (rok && g == 0)
-            den[trow] = den_incl_eps ? dn + 1e-8f : dn;
-        // z_t (column layout) = z_prev + inclusive prefix of phi(K) over the chunk
+
+        f4 kC[4], vC[2];
+        getC(bK, kC, l16, g);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            vC[j] = colC(bV, 2 * h + j, l16, g);
+        // z_t = z_prev + inclusive prefix of phi(K) over the chunk (column
+        // layout); wave 0 turns it into rows through LDS for 16-byte stores
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
             float tot;
             const f4 pz = col_prefix16(kC[dt], tot, lane);
-            if (zcache != nullptr && 16 * dt + l16 < D)
+            if (h == 0)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int t = t0 + 4 * g + r;
-                    if (t < tend)
-                        zcache[(rb + t) * D + 16 * dt + l16] = zC[dt] + pz[r];
-                }
+                for (int r = 0; r < 4; r++)
+                    bZ[(4 * g + r) * CLD + 16 * dt + l16] = zC[dt] + pz[r];
             zC[dt] += tot;
         }
 #pragma unroll
@@ -375,31 +455,50 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
                 zR[dt][i] = __shfl(zC[dt], 4 * g + i, 64);
 
         // O^T[e][t] = sum_d S[d][e] phi(Q_t)[d] + sum_s V_s[e] A^T[s][t]
+        f4 o[2];
 #pragma unroll
-        for (int et = 0; et < 4; et++) {
+        for (int j = 0; j < 2; j++) {
             f4 acc = f4zero();
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(St[dt][et][r], q[dt][r], acc);
+                    acc = mfma16(St[dt][j][r], q[dt][r], acc);
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                acc = mfma16(vC[et][r], At[r], acc);
-            if (rok)
-                store4<VEC>(O + trow * E, 16 * et + 4 * g, E, acc * inv);
+                acc = mfma16(vC[j][r], At[r], acc);
+            o[j] = acc * inv;
         }
-        // S += phi(K)^T V
+        // S += phi(K)^T V (this wave's columns)
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int et = 0; et < 4; et++) {
-                f4 acc = St[dt][et];
+            for (int j = 0; j < 2; j++) {
+                f4 acc = St[dt][j];
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(kC[dt][r], vC[et][r], acc);
-                St[dt][et] = acc;
+                    acc = mfma16(kC[dt][r], vC[j][r], acc);
+                St[dt][j] = acc;
             }
+        // outputs of row t0 + l16
+        if (full || rok) {
+            float* orow = O + (rb + t0 + l16) * E;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                stR<VEC, FW>(orow, 16 * (2 * h + j) + 4 * g, E, o[j]);
+            if (h == 0) {
+                if (zcache != nullptr) {
+                    f4 zrow[4];
+                    getR(bZ, zrow, l16, g);
+                    float* zrw = zcache + (rb + t0 + l16) * D;
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++)
+                        stR<VEC, FW>(zrw, 16 * ct + 4 * g, D, zrow[ct]);
+                }
+                if (g == 0)
+                    den[rb + t0 + l16] = den_incl_eps ? dn + 1e-8f : dn;
+            }
+        }
     }
 
     if (Sfin != nullptr && seg == nseg - 1) {
@@ -408,14 +507,14 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_fwd_kernel(
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int et = 0; et < 4; et++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int d = 16 * dt + 4 * g + r, e = 16 * et + l16;
+                    const int d = 16 * dt + 4 * g + r, e = 16 * (2 * h + j) + l16;
                     if (d < D && e < E)
-                        Sp[sfin_de ? (long)d * E + e : (long)e * D + d] = St[dt][et][r];
+                        Sp[sfin_de ? (long)d * E + e : (long)e * D + d] = St[dt][j][r];
                 }
-        if (zfin != nullptr && g == 0)
+        if (zfin != nullptr && h == 0 && g == 0)
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
                 if (16 * dt + l16 < D)
@@ -451,81 +550,101 @@ __global__ __launch_bounds__(256) void lin_step1_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// dQ (forward-direction scan)
+// dQ (forward-direction scan).  Wave h produces dQ columns of tiles dt = 2h,
+// 2h+1 and keeps that half of the transposed state.
 // ---------------------------------------------------------------------------
-template <int PHI, bool VEC>
-__global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
+constexpr int DQ_THREADS = 128;
+constexpr int DQ_STAGE = 5 * CHUNK + 16;   // phi(K), V, dnum, z_cache, Q rows + dden rows
+
+template <int PHI, bool VEC, bool FW>
+__global__ __launch_bounds__(DQ_THREADS) void lin_dq_kernel(
     const float* __restrict__ K, const float* __restrict__ V, const float* __restrict__ dnum,
     const float* __restrict__ dden, const float* __restrict__ zcache, const float* __restrict__ Q,
     float* __restrict__ dQ, const float* __restrict__ ws, int Bq, int S, int D, int E, int nseg,
     int L)
 {
-    __shared__ __attribute__((aligned(16))) float lds[LIN_WAVES * 2 * CHUNK];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float lds[2 * DQ_STAGE];
+    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int wid = blockIdx.x * LIN_WAVES + wave;
-    if (wid >= Bq * nseg)
-        return;
-    float* bK = lds + wave * 2 * CHUNK;
-    float* bV = bK + CHUNK;
+    const int wid = blockIdx.x;
     const int seq = wid / nseg, seg = wid - seq * nseg;
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
     constexpr bool HAS_Q = PHI != PHI_NONE;
 
-    // state transposed: StT[et][dt] lane (d = 16dt + l16), element r <-> e = 16et + 4g + r
-    f4 StT[4][4];
+    // transposed state slice, dt = 2h + j: StT[et][j] lane (d = 16dt + l16),
+    // element r <-> e = 16et + 4g + r
+    f4 StT[4][2];
     if (ws != nullptr) {
         const float* P = ws + (long)wid * LIN_WS;
 #pragma unroll
         for (int et = 0; et < 4; et++)
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-                StT[et][dt] = *reinterpret_cast<const f4*>(P + (16 * dt + l16) * 64 + 16 * et + 4 * g);
+            for (int j = 0; j < 2; j++)
+                StT[et][j] = *reinterpret_cast<const f4*>(P + (16 * (2 * h + j) + l16) * 64 + 16 * et + 4 * g);
     } else {
 #pragma unroll
         for (int et = 0; et < 4; et++)
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-                StT[et][dt] = f4zero();
+            for (int j = 0; j < 2; j++)
+                StT[et][j] = f4zero();
     }
 
-    f4 nk[4], nv[4], ndn[4], nzc[4], nq[4];
-    float ndd;
+    // wave 0 fetches K, V rows and dden, wave 1 dnum, z_cache and Q rows
+    f4 na[4], nb[4], nc[4];
+    float ndd = 0.0f;
     auto fetch = [&](int t0) {
-        const int t = t0 + l16;
-        ldR<VEC>(nk, K, D, rb, t, tlast, D, g);
-        ldR<VEC>(nv, V, E, rb, t, tlast, E, g);
-        ldR<VEC>(ndn, dnum, E, rb, t, tlast, E, g);
-        ldR<VEC>(nzc, zcache, D, rb, t, tlast, D, g);
-        if (HAS_Q)
-            ldR<VEC>(nq, Q, D, rb, t, tlast, D, g);
-        ndd = dden[rb + (t < tlast ? t : tlast)];
+        const int ro = min(l16, tlast - t0);
+        if (h == 0) {
+            ldR<VEC>(na, K + (rb + t0) * D, D, ro, D, g);
+            ldR<VEC>(nb, V + (rb + t0) * E, E, ro, E, g);
+            ndd = dden[rb + t0 + ro];
+        } else {
+            ldR<VEC>(na, dnum + (rb + t0) * E, E, ro, E, g);
+            ldR<VEC>(nb, zcache + (rb + t0) * D, D, ro, D, g);
+            if (HAS_Q)
+                ldR<VEC>(nc, Q + (rb + t0) * D, D, ro, D, g);
+        }
     };
     fetch(tbeg);
-    for (int t0 = tbeg; t0 < tend; t0 += 16) {
-        f4 k[4], v[4], dn[4], zc[4], q[4];
+    int c = 0;
+    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+        float* st = lds + (c & 1) * DQ_STAGE;
+        float* bK = st;
+        float* bV = st + CHUNK;
+        float* bN = st + 2 * CHUNK;
+        float* bZc = st + 3 * CHUNK;
+        float* bQ = st + 4 * CHUNK;
+        float* bd = st + 5 * CHUNK;
+        f4 a[4], b[4], cc[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            k[i] = nk[i];
-            v[i] = nv[i];
-            dn[i] = ndn[i];
-            zc[i] = nzc[i];
-            q[i] = HAS_Q ? nq[i] : f4zero();
+            a[i] = na[i];
+            b[i] = nb[i];
+            cc[i] = HAS_Q ? nc[i] : f4zero();
         }
         const float dd = ndd;
         if (t0 + 16 < tend)
             fetch(t0 + 16);
-        const long trow = rb + t0 + l16;
-        const bool rok = t0 + l16 < tend;
-        finR<PHI, true>(k, rok, D, g);
-        finR<PHI, false>(v, rok, E, g);
-        finR<PHI, false>(dn, rok, E, g);
-        putR(bK, k, l16, g);
-        putR(bV, v, l16, g);
-        f4 kC[4], vC[4];
-        getC(bK, kC, l16, g);
-        getC(bV, vC, l16, g);
+        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        if (h == 0) {
+            finR<PHI, true, FW>(a, full, rok, D, g);
+            finR<PHI, false, FW>(b, full, rok, E, g);
+            putR(bK, a, l16, g);
+            putR(bV, b, l16, g);
+            if (g == 0)
+                bd[l16] = dd;
+        } else {
+            finR<PHI, false, FW>(a, full, rok, E, g);
+            putR(bN, a, l16, g);
+            putR(bZc, b, l16, g);   // only rows that are stored get used
+            if (HAS_Q)
+                putR(bQ, cc, l16, g);
+        }
+        __syncthreads();
+        f4 v[4], dn[4];
+        getR(bV, v, l16, g);
+        getR(bN, dn, l16, g);
 
         // G^T[s][t] = V_s . dnum_t, lane t = l16, element r <-> s = 4g + r; keep s <= t
         f4 G = f4zero();
@@ -538,49 +657,63 @@ __global__ __launch_bounds__(LIN_THREADS) void lin_dq_kernel(
         for (int r = 0; r < 4; r++)
             G[r] = (4 * g + r <= l16) ? G[r] : 0.0f;
 
-        // dQ^T[d][t] = z_t[d] dden_t + sum_e S[d][e] dnum_t[e] + sum_s phi(K_s)[d] G^T[s][t]
+        f4 vC[4], kC[2];
+        getC(bV, vC, l16, g);
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            f4 acc = zc[dt] * dd;
+        for (int j = 0; j < 2; j++)
+            kC[j] = colC(bK, 2 * h + j, l16, g);
+        const float ddt = bd[l16];
+        // dQ^T[d][t] = z_t[d] dden_t + sum_e S[d][e] dnum_t[e] + sum_s phi(K_s)[d] G^T[s][t]
+        f4 dq[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int dt = 2 * h + j;
+            f4 acc = *reinterpret_cast<const f4*>(&bZc[l16 * CLD + 16 * dt + 4 * g]) * ddt;
 #pragma unroll
             for (int et = 0; et < 4; et++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(StT[et][dt][r], dn[et][r], acc);
+                    acc = mfma16(StT[et][j][r], dn[et][r], acc);
 #pragma unroll
             for (int r = 0; r < 4; r++)
-                acc = mfma16(kC[dt][r], G[r], acc);
+                acc = mfma16(kC[j][r], G[r], acc);
             if (HAS_Q) {
+                const f4 qv = *reinterpret_cast<const f4*>(&bQ[l16 * CLD + 16 * dt + 4 * g]);
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[i] *= Phi<PHI>::d(q[dt][i]);
+                    acc[i] *= Phi<PHI>::d(qv[i]);
             }
-            if (rok)
-                store4<VEC>(dQ + trow * D, 16 * dt + 4 * g, D, acc);
+            dq[j] = acc;
         }
-        // S^T += V^T phi(K)
+        // S^T += V^T phi(K) (this wave's columns)
 #pragma unroll
         for (int et = 0; et < 4; et++)
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                f4 acc = StT[et][dt];
+            for (int j = 0; j < 2; j++) {
+                f4 acc = StT[et][j];
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(vC[et][r], kC[dt][r], acc);
-                StT[et][dt] = acc;
+                    acc = mfma16(vC[et][r], kC[j][r], acc);
+                StT[et][j] = acc;
             }
+        if (full || rok) {
+            float* qrow = dQ + (rb + t0 + l16) * D;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                stR<VEC, FW>(qrow, 16 * (2 * h + j) + 4 * g, D, dq[j]);
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV (reverse-direction scan).  Two waves per segment share the staged
-// chunk through LDS: wave 0 holds S*[d][e] and produces dV, wave 1 holds
-// S*^T and z* and produces dK.
+// dK, dV (reverse-direction scan).  Four waves per segment: waves 0/1 hold
+// halves (by e columns) of S*[d][e] and produce dV, waves 2/3 hold halves (by
+// d columns) of S*^T and z* and produce dK.
 // ---------------------------------------------------------------------------
-constexpr int DKDV_THREADS = 128;
+constexpr int DKDV_THREADS = 256;
 constexpr int DKDV_STAGE = 4 * CHUNK + 16;   // phi(Q), phi(K), V, dnum chunks + dden rows
 
-template <int PHI, bool VEC>
+template <int PHI, bool VEC, bool FW>
 __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dnum, const float* __restrict__ dden, float* __restrict__ dK,
@@ -588,50 +721,52 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
     int L)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * DKDV_STAGE];   // double buffered
-    const int lane = threadIdx.x & 63, role = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
+    const bool isV = w < 2;
+    const int hh = w & 1;   // which 32-column half
     const int wid = blockIdx.x;   // segment
     const int seq = wid / nseg, seg = wid - seq * nseg;
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
 
-    // role 0: S[dt][et] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r   (dV product)
-    // role 1: S[et][dt] lane (d = 16dt + l16), element r <-> e = 16et + 4g + r   (dK product)
-    //         zs[dt] element r <-> d = 16dt + 4g + r
-    f4 Sm[4][4], zs[4];
+    // dV waves: Sm[dt][j] = S*[d][e], et = 2hh + j: lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
+    // dK waves: Sm[et][j] = S*[d][e], dt = 2hh + j: lane (d = 16dt + l16), element r <-> e = 16et + 4g + r
+    //           zs[j] element r <-> d = 16dt + 4g + r
+    f4 Sm[4][2], zs[2];
     {
         const float* P = ws != nullptr ? ws + (long)wid * LIN_WS : nullptr;
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
+        for (int a = 0; a < 4; a++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
+            for (int j = 0; j < 2; j++) {
+                const int half = 2 * hh + j;
                 if (P == nullptr) {
-                    Sm[a][c] = f4zero();
-                } else if (role == 0) {
+                    Sm[a][j] = f4zero();
+                } else if (isV) {
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        Sm[a][c][r] = P[(16 * a + 4 * g + r) * 64 + 16 * c + l16];
+                        Sm[a][j][r] = P[(16 * a + 4 * g + r) * 64 + 16 * half + l16];
                 } else {
-                    Sm[a][c] = *reinterpret_cast<const f4*>(P + (16 * c + l16) * 64 + 16 * a + 4 * g);
+                    Sm[a][j] = *reinterpret_cast<const f4*>(P + (16 * half + l16) * 64 + 16 * a + 4 * g);
                 }
             }
-            zs[a] = P != nullptr ? *reinterpret_cast<const f4*>(P + 4096 + 16 * a + 4 * g) : f4zero();
-        }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            zs[j] = (P != nullptr && !isV) ? *reinterpret_cast<const f4*>(P + 4096 + 16 * (2 * hh + j) + 4 * g)
+                                           : f4zero();
     }
 
-    // role 0 fetches Q and K rows, role 1 V and dnum rows (+ dden)
-    f4 na[4], nb[4];
+    // wave 0 fetches Q rows, wave 1 K, wave 2 V, wave 3 dnum (+ dden)
+    const float* src = w == 0 ? Q : (w == 1 ? K : (w == 2 ? V : dnum));
+    const int sld = w < 2 ? D : E;
+    f4 na[4];
     float ndd = 0.0f;
     auto fetch = [&](int t0) {
-        const int t = t0 + l16;
-        if (role == 0) {
-            ldR<VEC>(na, Q, D, rb, t, tlast, D, g);
-            ldR<VEC>(nb, K, D, rb, t, tlast, D, g);
-        } else {
-            ldR<VEC>(na, V, E, rb, t, tlast, E, g);
-            ldR<VEC>(nb, dnum, E, rb, t, tlast, E, g);
-            ndd = dden[rb + (t < tlast ? t : tlast)];
-        }
+        const int ro = min(l16, tlast - t0);
+        ldR<VEC>(na, src + (rb + t0) * sld, sld, ro, sld, g);
+        if (w == 3)
+            ndd = dden[rb + t0 + ro];
     };
     const int nchunk = (tend - tbeg + 15) / 16;
     fetch(tbeg + 16 * (nchunk - 1));
@@ -643,37 +778,25 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
         float* bV = st + 2 * CHUNK;
         float* bN = st + 3 * CHUNK;
         float* bd = st + 4 * CHUNK;
-        f4 a[4], b[4];
+        f4 a[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 4; i++)
             a[i] = na[i];
-            b[i] = nb[i];
-        }
         const float dd = ndd;
         if (c > 0)
             fetch(t0 - 16);
-        const long trow = rb + t0 + l16;
-        const bool rok = t0 + l16 < tend;
-        if (role == 0) {
-            finR<PHI, true>(a, rok, D, g);
-            finR<PHI, true>(b, rok, D, g);
-            putR(bQ, a, l16, g);
-            putR(bK, b, l16, g);
-        } else {
-            finR<PHI, false>(a, rok, E, g);
-            finR<PHI, false>(b, rok, E, g);
-            putR(bV, a, l16, g);
-            putR(bN, b, l16, g);
-            if (g == 0)
-                bd[l16] = rok ? dd : 0.0f;
-        }
+        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        if (w < 2)
+            finR<PHI, true, FW>(a, full, rok, D, g);
+        else
+            finR<PHI, false, FW>(a, full, rok, E, g);
+        putR(st + w * CHUNK, a, l16, g);
+        if (w == 3 && g == 0)
+            bd[l16] = rok ? dd : 0.0f;
         __syncthreads();
 
-        f4 qC[4], dnC[4];
-        getC(bQ, qC, l16, g);
-        getC(bN, dnC, l16, g);
-        if (role == 0) {
-            f4 qR[4], kR[4];
+        if (isV) {
+            f4 qR[4], kR[4], qC[4], dnC[2];
             getR(bQ, qR, l16, g);
             getR(bK, kR, l16, g);
             // M1^T[s][t] = phi(Q_s).phi(K_t); lane t = l16, element r <-> s = 4g + r; keep s >= t
@@ -686,37 +809,46 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 M1[r] = (4 * g + r >= l16) ? M1[r] : 0.0f;
-            // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_s dnum_s[e] M1^T[s][t]
+            getC(bQ, qC, l16, g);
 #pragma unroll
-            for (int et = 0; et < 4; et++) {
+            for (int j = 0; j < 2; j++)
+                dnC[j] = colC(bN, 2 * hh + j, l16, g);
+            // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_s dnum_s[e] M1^T[s][t]
+            f4 dv[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
                 f4 acc = f4zero();
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(Sm[dt][et][r], kR[dt][r], acc);
+                        acc = mfma16(Sm[dt][j][r], kR[dt][r], acc);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(dnC[et][r], M1[r], acc);
-                if (rok)
-                    store4<VEC>(dV + trow * E, 16 * et + 4 * g, E, acc);
+                    acc = mfma16(dnC[j][r], M1[r], acc);
+                dv[j] = acc;
             }
-            // S* += phi(Q)^T dnum
+            // S* += phi(Q)^T dnum (this wave's columns)
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-                for (int et = 0; et < 4; et++) {
-                    f4 acc = Sm[dt][et];
+                for (int j = 0; j < 2; j++) {
+                    f4 acc = Sm[dt][j];
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(qC[dt][r], dnC[et][r], acc);
-                    Sm[dt][et] = acc;
+                        acc = mfma16(qC[dt][r], dnC[j][r], acc);
+                    Sm[dt][j] = acc;
                 }
+            if (full || rok) {
+                float* vrow = dV + (rb + t0 + l16) * E;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    stR<VEC, FW>(vrow, 16 * (2 * hh + j) + 4 * g, E, dv[j]);
+            }
         } else {
-            f4 vR[4], dnR[4], kR[4];
+            f4 vR[4], dnR[4], dnC[4], qC[2];
             getR(bV, vR, l16, g);
             getR(bN, dnR, l16, g);
-            getR(bK, kR, l16, g);
             f4 ddC;
 #pragma unroll
             for (int r = 0; r < 4; r++)
@@ -731,43 +863,55 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 M2[r] = (4 * g + r >= l16) ? M2[r] + ddC[r] : 0.0f;
-            // dK^T[d][t] = (z*[d] + sum_e S*[d][e] V_t[e] + sum_s phi(Q_s)[d] M2^T[s][t]) phi'(K_t[d])
+            getC(bN, dnC, l16, g);
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                f4 acc = zs[dt];
+            for (int j = 0; j < 2; j++)
+                qC[j] = colC(bQ, 2 * hh + j, l16, g);
+            // dK^T[d][t] = (z*[d] + sum_e S*[d][e] V_t[e] + sum_s phi(Q_s)[d] M2^T[s][t]) phi'(K_t[d])
+            f4 dk[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int dt = 2 * hh + j;
+                f4 acc = zs[j];
 #pragma unroll
                 for (int et = 0; et < 4; et++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(Sm[et][dt][r], vR[et][r], acc);
+                        acc = mfma16(Sm[et][j][r], vR[et][r], acc);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(qC[dt][r], M2[r], acc);
+                    acc = mfma16(qC[j][r], M2[r], acc);
+                const f4 kv = *reinterpret_cast<const f4*>(&bK[l16 * CLD + 16 * dt + 4 * g]);
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[i] *= Phi<PHI>::d_from_f(kR[dt][i]);
-                if (rok)
-                    store4<VEC>(dK + trow * D, 16 * dt + 4 * g, D, acc);
+                    acc[i] *= Phi<PHI>::d_from_f(kv[i]);
+                dk[j] = acc;
             }
             // S*^T += dnum^T phi(Q); z* += phi(Q)^T dden (column sums, VALU)
 #pragma unroll
             for (int et = 0; et < 4; et++)
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    f4 acc = Sm[et][dt];
+                for (int j = 0; j < 2; j++) {
+                    f4 acc = Sm[et][j];
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(dnC[et][r], qC[dt][r], acc);
-                    Sm[et][dt] = acc;
+                        acc = mfma16(dnC[et][r], qC[j][r], acc);
+                    Sm[et][j] = acc;
                 }
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                float zp = qC[dt][0] * ddC[0] + qC[dt][1] * ddC[1] + qC[dt][2] * ddC[2] +
-                           qC[dt][3] * ddC[3];
+            for (int j = 0; j < 2; j++) {
+                float zp = qC[j][0] * ddC[0] + qC[j][1] * ddC[1] + qC[j][2] * ddC[2] +
+                           qC[j][3] * ddC[3];
                 zp = xrow_sum(zp);   // column total for d = 16dt + l16
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    zs[dt][i] += __shfl(zp, 4 * g + i, 64);
+                    zs[j][i] += __shfl(zp, 4 * g + i, 64);
+            }
+            if (full || rok) {
+                float* krow = dK + (rb + t0 + l16) * D;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    stR<VEC, FW>(krow, 16 * (2 * hh + j) + 4 * g, D, dk[j]);
             }
         }
     }
@@ -1042,21 +1186,27 @@ size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
     return (size_t)Bq * p.nseg * LIN_WS * sizeof(float);
 }
 
+// Fast-path kernel variant: 2 = D == E == 64 with 16-byte aligned rows, 1 = widths
+// multiple of 4 and aligned, 0 = anything else.
+static int lin_mode(bool vec, int D, int E) { return !vec ? 0 : (D == 64 && E == 64 ? 2 : 1); }
+
 template <int PHI>
 static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y, const float* w,
-                               float* ws, int Bq, int S, int D, int E, int reverse, bool vec,
+                               float* ws, int Bq, int S, int D, int E, int reverse, int mode,
                                hipStream_t st)
 {
-    const int nw = Bq * p.nseg;
-    dim3 grid((unsigned)((nw + LIN_WAVES - 1) / LIN_WAVES)), block(LIN_THREADS);
+    dim3 grid((unsigned)(Bq * p.nseg)), block(AGG_THREADS);
     {
         ProfScope ps(st, "lin_agg");
-        if (vec)
-            hipLaunchKernelGGL((lin_agg_kernel<PHI, true>), grid, block, 0, st, X, Y, w, ws, Bq,
-                               S, D, E, p.nseg, p.L);
+        if (mode == 2)
+            hipLaunchKernelGGL((lin_agg_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w, ws,
+                               Bq, S, D, E, p.nseg, p.L);
+        else if (mode == 1)
+            hipLaunchKernelGGL((lin_agg_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w, ws,
+                               Bq, S, D, E, p.nseg, p.L);
         else
-            hipLaunchKernelGGL((lin_agg_kernel<PHI, false>), grid, block, 0, st, X, Y, w, ws, Bq,
-                               S, D, E, p.nseg, p.L);
+            hipLaunchKernelGGL((lin_agg_kernel<PHI, false, false>), grid, block, 0, st, X, Y, w,
+                               ws, Bq, S, D, E, p.nseg, p.L);
     }
     {
         ProfScope ps(st, "lin_scan");
@@ -1090,22 +1240,25 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
     }
     const bool vec = (D % 4 == 0) && (E % 4 == 0) && al16(Q) && al16(K) && al16(V) && al16(O) &&
                      al16(zc);
+    const int mode = lin_mode(vec, D, E);
     float* wsf = (float*)ws;
     if (p.nseg > 1) {
-        hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, vec, st);
+        hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, mode, st);
         if (e != hipSuccess)
             return e;
     } else {
         wsf = nullptr;
     }
-    const int nw = Bq * p.nseg;
-    dim3 grid((unsigned)((nw + LIN_WAVES - 1) / LIN_WAVES)), block(LIN_THREADS);
+    dim3 grid((unsigned)(Bq * p.nseg)), block(FWD_THREADS);
     ProfScope ps(st, "lin_fwd");
-    if (vec)
-        hipLaunchKernelGGL((lin_fwd_kernel<PHI, true>), grid, block, 0, st, Q, K, V, O, den, zc,
+    if (mode == 2)
+        hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
+                           wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
+    else if (mode == 1)
+        hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
     else
-        hipLaunchKernelGGL((lin_fwd_kernel<PHI, false>), grid, block, 0, st, Q, K, V, O, den, zc,
+        hipLaunchKernelGGL((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
     return hipGetLastError();
 }
@@ -1150,22 +1303,25 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
     }
     const bool vec = (D % 4 == 0) && (E % 4 == 0) && al16(K) && al16(V) && al16(dnum) &&
                      al16(zc) && al16(Q) && al16(dQ);
+    const int mode = lin_mode(vec, D, E);
     float* wsf = (float*)ws;
     if (p.nseg > 1) {
-        hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, vec, st);
+        hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, mode, st);
         if (e != hipSuccess)
             return e;
     } else {
         wsf = nullptr;
     }
-    const int nw = Bq * p.nseg;
-    dim3 grid((unsigned)((nw + LIN_WAVES - 1) / LIN_WAVES)), block(LIN_THREADS);
+    dim3 grid((unsigned)(Bq * p.nseg)), block(DQ_THREADS);
     ProfScope ps(st, "lin_dq");
-    if (vec)
-        hipLaunchKernelGGL((lin_dq_kernel<PHI, true>), grid, block, 0, st, K, V, dnum, dden, zc,
+    if (mode == 2)
+        hipLaunchKernelGGL((lin_dq_kernel<PHI, true, true>), grid, block, 0, st, K, V, dnum, dden, zc,
+                           Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
+    else if (mode == 1)
+        hipLaunchKernelGGL((lin_dq_kernel<PHI, true, false>), grid, block, 0, st, K, V, dnum, dden, zc,
                            Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
     else
-        hipLaunchKernelGGL((lin_dq_kernel<PHI, false>), grid, block, 0, st, K, V, dnum, dden, zc,
+        hipLaunchKernelGGL((lin_dq_kernel<PHI, false, false>), grid, block, 0, st, K, V, dnum, dden, zc,
                            Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
     return hipGetLastError();
 }
@@ -1194,9 +1350,10 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
     }
     const bool vec = (D % 4 == 0) && (E % 4 == 0) && al16(Q) && al16(K) && al16(V) &&
                      al16(dnum) && al16(dK) && al16(dV);
+    const int mode = lin_mode(vec, D, E);
     float* wsf = (float*)ws;
     if (p.nseg > 1) {
-        hipError_t e = agg_and_scan<PHI>(p, Q, dnum, dden, wsf, Bq, S, D, E, 1, vec, st);
+        hipError_t e = agg_and_scan<PHI>(p, Q, dnum, dden, wsf, Bq, S, D, E, 1, mode, st);
         if (e != hipSuccess)
             return e;
     } else {
@@ -1204,11 +1361,14 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
     }
     dim3 grid((unsigned)(Bq * p.nseg)), block(DKDV_THREADS);
     ProfScope ps(st, "lin_dkdv");
-    if (vec)
-        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true>), grid, block, 0, st, Q, K, V, dnum, dden,
+    if (mode == 2)
+        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, dnum, dden,
+                           dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
+    else if (mode == 1)
+        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, dnum, dden,
                            dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
     else
-        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, false>), grid, block, 0, st, Q, K, V, dnum, dden,
+        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, dnum, dden,
                            dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
     return hipGetLastError();
 }
