@@ -102,8 +102,9 @@ struct FwdSmem {
     static constexpr int VS = MHA_BN + 4;   // Vt[d][key] row stride
     static constexpr int MS = DHP + 4;      // merge record: o[DHP], m, l
     static constexpr int TILES = MHA_BN * KS + DHP * VS;
+    static constexpr bool DB = DHP <= 64;    // double-buffered K/V tiles
     static constexpr int MERGE = (NSPLIT - 1) * MHA_BM * MS;
-    static constexpr int FLOATS = TILES > MERGE ? TILES : MERGE;
+    static constexpr int FLOATS = (DB ? 2 : 1) * TILES > MERGE ? (DB ? 2 : 1) * TILES : MERGE;
 };
 
 template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
@@ -118,8 +119,6 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     constexpr int NDT = DHP / 16;
     constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
-    float* Ks = smem;
-    float* Vt = smem + MHA_BN * KS;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -148,31 +147,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     float m_run = -1e30f, l_run = 0.0f;
 
     const int nkb = qb + 1;   // causal: key tiles 0..qb (MHA_BM == MHA_BN)
-    // K/V tiles: loaded into registers one tile ahead (DHP <= 128), stored to
-    // LDS at the top of the iteration that uses them.
-    constexpr bool PREFETCH = DHP <= 128;
-    TileRegs<DHP, MHA_BN, NT, VEC> kr, vr;
-    kr.load(K, base, rs, 0, S, Dh, tid);
-    if (WRITE_O)
-        vr.load(V, base, rs, 0, S, Dh, tid);
-    for (int kb = 0; kb < nkb; kb++) {
+    // One key tile of math on the tile in LDS (Ks, Vt).
+    auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vt, int kb) {
         const int k0 = kb * MHA_BN;
-        if (!PREFETCH && kb > 0) {
-            kr.load(K, base, rs, k0, S, Dh, tid);
-            if (WRITE_O)
-                vr.load(V, base, rs, k0, S, Dh, tid);
-        }
-        __syncthreads();
-        kr.template store<KS>(Ks, tid);
-        if (WRITE_O)
-            vr.template store_t<VS>(Vt, tid);
-        __syncthreads();
-        if (PREFETCH && kb + 1 < nkb) {
-            kr.load(K, base, rs, k0 + MHA_BN, S, Dh, tid);
-            if (WRITE_O)
-                vr.load(V, base, rs, k0 + MHA_BN, S, Dh, tid);
-        }
-
         // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
         f4 sacc[NKT];
 #pragma unroll
@@ -229,6 +206,62 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
                 }
                 oacc[dt] = acc;
             }
+        }
+    };
+    // K/V tiles are loaded into registers one tile ahead.  Narrow heads
+    // double-buffer the LDS tiles: tile kb+1 is written while tile kb is
+    // consumed, one barrier per tile; wider heads use one buffer (two
+    // barriers per tile, and no register prefetch for the widest).
+    TileRegs<DHP, MHA_BN, NT, VEC> kr, vr;
+    kr.load(K, base, rs, 0, S, Dh, tid);
+    if (WRITE_O)
+        vr.load(V, base, rs, 0, S, Dh, tid);
+    if constexpr (SM::DB) {
+        kr.template store<KS>(smem, tid);
+        if (WRITE_O)
+            vr.template store_t<VS>(smem + MHA_BN * KS, tid);
+        if (nkb > 1) {
+            kr.load(K, base, rs, MHA_BN, S, Dh, tid);
+            if (WRITE_O)
+                vr.load(V, base, rs, MHA_BN, S, Dh, tid);
+        }
+        __syncthreads();
+        for (int kb = 0; kb < nkb; kb++) {
+            const float* cur = smem + (kb & 1) * SM::TILES;
+            if (kb + 1 < nkb) {
+                float* nxt = smem + ((kb + 1) & 1) * SM::TILES;
+                kr.template store<KS>(nxt, tid);
+                if (WRITE_O)
+                    vr.template store_t<VS>(nxt + MHA_BN * KS, tid);
+                if (kb + 2 < nkb) {
+                    kr.load(K, base, rs, (kb + 2) * MHA_BN, S, Dh, tid);
+                    if (WRITE_O)
+                        vr.load(V, base, rs, (kb + 2) * MHA_BN, S, Dh, tid);
+                }
+            }
+            tile_math(cur, cur + MHA_BN * KS, kb);
+            __syncthreads();
+        }
+    } else {
+        constexpr bool PREFETCH = DHP <= 128;
+        for (int kb = 0; kb < nkb; kb++) {
+            const int k0 = kb * MHA_BN;
+            if (!PREFETCH && kb > 0) {
+                kr.load(K, base, rs, k0, S, Dh, tid);
+                if (WRITE_O)
+                    vr.load(V, base, rs, k0, S, Dh, tid);
+            }
+            __syncthreads();
+            kr.template store<KS>(smem, tid);
+            if (WRITE_O)
+                vr.template store_t<VS>(smem + MHA_BN * KS, tid);
+            __syncthreads();
+            if (PREFETCH && kb + 1 < nkb) {
+                kr.load(K, base, rs, k0 + MHA_BN, S, Dh, tid);
+                if (WRITE_O)
+                    vr.load(V, base, rs, k0 + MHA_BN, S, Dh, tid);
+            }
+            tile_math(smem, smem + MHA_BN * KS, kb);
         }
     }
     float l_tot = xrow_sum(l_run);
@@ -328,7 +361,12 @@ template <int DHP, int BM>
 struct BwdSmem {
     static constexpr int QS = DHP + 4;      // Qs/dOs [q][d] row stride
     static constexpr int TS = MHA_BN + 4;   // Kt [d][key] and dSs [q][key] row stride
-    static constexpr int FLOATS = 2 * BM * QS + DHP * TS + BM * TS + 2 * BM;
+    // Narrow heads double-buffer the query-side tiles (Q, dO, lse, Di, dS) so
+    // one barrier per query tile suffices.
+    static constexpr bool DB = DHP <= 64;
+    static constexpr int NB = DB ? 2 : 1;
+    static constexpr int STAGE = 2 * BM * QS + BM * TS + 2 * BM;   // Q, dO, dS, lse, Di
+    static constexpr int FLOATS = DHP * TS + NB * STAGE;
 };
 
 template <int DHP, int BM, int NSPLIT, bool VEC>
@@ -347,12 +385,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     constexpr int QS = SM::QS, TS = SM::TS;
     static_assert(NQW >= 1, "query split too fine for BM");
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
-    float* Qs = smem;
-    float* dOs = Qs + BM * QS;
-    float* Kt = dOs + BM * QS;
-    float* dSs = Kt + DHP * TS;
-    float* lse_s = dSs + BM * TS;
-    float* di_s = lse_s + BM;
+    float* Kt = smem;
+    // Stage i: Qs [BM][QS], dOs [BM][QS], dSs [BM][TS], lse_s [BM], di_s [BM].
+    auto stage = [&](int i) { return smem + DHP * TS + i * SM::STAGE; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -390,9 +425,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     }
 
     const int nqb = (S + BM - 1) / BM;
-    // Q/dO tiles and their lse/Di entries: loaded into registers one query
-    // tile ahead (DHP <= 128), stored to LDS at the top of the iteration.
-    constexpr bool PREFETCH = DHP <= 128;
+    // Q/dO tiles and their lse/Di entries pass through registers one query
+    // tile ahead of their store to LDS (DHP <= 128).
     TileRegs<DHP, BM, NT, VEC> qr, dor;
     float lse_r = 0.0f, di_r = 0.0f;
     auto load_q = [&](int q0) {
@@ -404,24 +438,23 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             di_r = Di[i];
         }
     };
-    const int qb0 = k0 / BM;
-    load_q(qb0 * BM);
-    for (int qb = qb0; qb < nqb; qb++) {
-        const int q0 = qb * BM;
-        if (!PREFETCH && qb > qb0)
-            load_q(q0);
-        __syncthreads();
-        qr.template store<QS>(Qs, tid);
-        dor.template store<QS>(dOs, tid);
+    auto store_q = [&](float* st) {
+        qr.template store<QS>(st, tid);
+        dor.template store<QS>(st + BM * QS, tid);
         if (tid < BM) {
-            lse_s[tid] = lse_r;
-            di_s[tid] = di_r;
+            st[2 * BM * QS + BM * TS + tid] = lse_r;
+            st[2 * BM * QS + BM * TS + BM + tid] = di_r;
         }
-        __syncthreads();
-        if (PREFETCH && qb + 1 < nqb)
-            load_q(q0 + BM);
-
-        // S = Q K^T and dP = dO V^T: lane holds key l16, queries 16qt + 4g + r.
+    };
+    // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
+    // l16, queries 16qt + 4g + r); dS goes to LDS for the dQ product, then
+    // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.
+    auto key_side = [&](float* st, int q0) {
+        const float* Qs = st;
+        const float* dOs = st + BM * QS;
+        float* dSs = st + 2 * BM * QS;
+        const float* lse_s = st + 2 * BM * QS + BM * TS;
+        const float* di_s = lse_s + BM;
         const bool diag = q0 < k0 + MHA_BN;   // tile touches the causal boundary
         f4 P[NQW], dS[NQW];
 #pragma unroll
@@ -450,7 +483,6 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
             }
         }
-        // dV^T += dO^T P and dK^T += Q^T dS (contraction over this wave's queries).
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             f4 av = dv[dt], ak = dk[dt];
@@ -467,9 +499,11 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             dv[dt] = av;
             dk[dt] = ak;
         }
-        __syncthreads();
-        // dQ tiles (qt, dt) of this query block, dealt round-robin to the waves:
-        // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.
+    };
+    // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
+    // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.
+    auto query_side = [&](const float* st, int q0) {
+        const float* dSs = st + 2 * BM * QS;
         for (int job = wave; job < NQT * NDT; job += NW) {
             const int qt = job % NQT, dt = job / NQT;
             f4 acc = f4zero();
@@ -489,13 +523,54 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
             }
         }
+    };
+
+    const int qb0 = k0 / BM;
+    load_q(qb0 * BM);
+    if constexpr (SM::DB) {
+        // Tile qb is in stage qb&1 when iteration qb starts.  Iteration qb
+        // writes tile qb+1 into the other stage (last read in iteration qb-1,
+        // before its barrier) and dS into its own stage, which the dQ jobs
+        // read after the barrier.
+        store_q(stage(qb0 & 1));
+        if (qb0 + 1 < nqb)
+            load_q((qb0 + 1) * BM);
+        __syncthreads();
+        for (int qb = qb0; qb < nqb; qb++) {
+            const int q0 = qb * BM;
+            float* cur = stage(qb & 1);
+            if (qb + 1 < nqb) {
+                store_q(stage((qb + 1) & 1));
+                if (qb + 2 < nqb)
+                    load_q(q0 + 2 * BM);
+            }
+            key_side(cur, q0);
+            __syncthreads();
+            query_side(cur, q0);
+        }
+    } else {
+        constexpr bool PREFETCH = DHP <= 128;
+        float* st = stage(0);
+        for (int qb = qb0; qb < nqb; qb++) {
+            const int q0 = qb * BM;
+            if (!PREFETCH && qb > qb0)
+                load_q(q0);
+            __syncthreads();
+            store_q(st);
+            __syncthreads();
+            if (PREFETCH && qb + 1 < nqb)
+                load_q(q0 + BM);
+            key_side(st, q0);
+            __syncthreads();
+            query_side(st, q0);
+        }
     }
 
     if (NSPLIT > 1) {
         // Sum the per-split partial dK^T/dV^T: splits qs > 0 publish through
         // LDS (reusing the Q/dO tiles), split 0 adds and stores.
         constexpr int RS = 2 * DHP + 4;   // record per (split, key): dk[DHP], dv[DHP]
-        static_assert((NSPLIT - 1) * MHA_BN * RS <= 2 * BM * QS + DHP * TS,
+        static_assert((NSPLIT - 1) * MHA_BN * RS <= SM::FLOATS,
                       "dK/dV reduction buffer does not fit");
         float* rb = smem;
         __syncthreads();   // every wave is done with the tiles
