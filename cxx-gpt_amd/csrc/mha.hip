@@ -99,9 +99,8 @@ struct TileRegs {
 template <int DHP, int NSPLIT>
 struct FwdSmem {
     static constexpr int KS = DHP + 4;      // Ks[key][d] row stride (floats)
-    static constexpr int VS = MHA_BN + 4;   // Vt[d][key] row stride
     static constexpr int MS = DHP + 4;      // merge record: o[DHP], m, l
-    static constexpr int TILES = MHA_BN * KS + DHP * VS;
+    static constexpr int TILES = 2 * MHA_BN * KS;   // Ks and Vs, both [key][d]
     static constexpr bool DB = DHP <= 64;    // double-buffered K/V tiles
     static constexpr int MERGE = (NSPLIT - 1) * MHA_BM * MS;
     static constexpr int FLOATS = (DB ? 2 : 1) * TILES > MERGE ? (DB ? 2 : 1) * TILES : MERGE;
@@ -115,7 +114,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
 {
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
-    constexpr int KS = SM::KS, VS = SM::VS, MS = SM::MS;
+    constexpr int KS = SM::KS, MS = SM::MS;
     constexpr int NDT = DHP / 16;
     constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
@@ -147,29 +146,33 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     float m_run = -1e30f, l_run = 0.0f;
 
     const int nkb = qb + 1;   // causal: key tiles 0..qb (MHA_BM == MHA_BN)
-    // One key tile of math on the tile in LDS (Ks, Vt).
-    auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vt, int kb) {
+    // One key tile of math on the tiles in LDS (Ks, Vs: [key][d], row stride KS).
+    auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
         const int k0 = kb * MHA_BN;
         // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
+        // The NKT key blocks run as interleaved accumulation chains.
         f4 sacc[NKT];
 #pragma unroll
-        for (int kk = 0; kk < NKT; kk++) {
-            const int kt = ks * NKT + kk;
-            f4 acc = f4zero();
+        for (int kk = 0; kk < NKT; kk++)
+            sacc[kk] = f4zero();
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
+        for (int dt = 0; dt < NDT; dt++) {
+#pragma unroll
+            for (int kk = 0; kk < NKT; kk++) {
+                const int kt = ks * NKT + kk;
                 const f4 kv = *reinterpret_cast<const f4*>(&Ks[(16 * kt + l16) * KS + 16 * dt + 4 * g]);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    acc = mfma16(kv[r], qreg[dt][r], acc);
+                    sacc[kk] = mfma16(kv[r], qreg[dt][r], sacc[kk]);
             }
-            if (kb == qb) {   // diagonal tile: causal mask key > query
+        }
+        if (kb == qb) {   // diagonal tile: causal mask key > query
+#pragma unroll
+            for (int kk = 0; kk < NKT; kk++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    if (k0 + 16 * kt + 4 * g + r > myq)
-                        acc[r] = -INFINITY;
-            }
-            sacc[kk] = acc;
+                    if (k0 + 16 * (ks * NKT + kk) + 4 * g + r > myq)
+                        sacc[kk][r] = -INFINITY;
         }
         float mloc = -INFINITY;
 #pragma unroll
@@ -192,75 +195,77 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
         l_run = l_run * alpha + psum;
         m_run = m_new;
         if (WRITE_O) {
-            // O^T += V^T P^T: A = V^T[d = 16dt + l16][key], B = P^T from sacc.
+            // O^T += V^T P^T: A = V^T[d = 16dt + l16][key = 16kt + 4g + r], read
+            // as single floats from the row-major V tile; B = P^T from sacc.
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
                 f4 acc = oacc[dt] * alpha;
 #pragma unroll
                 for (int kk = 0; kk < NKT; kk++) {
                     const int kt = ks * NKT + kk;
-                    const f4 vv = *reinterpret_cast<const f4*>(&Vt[(16 * dt + l16) * VS + 16 * kt + 4 * g]);
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        acc = mfma16(vv[r], sacc[kk][r], acc);
+                        acc = mfma16(Vs[(16 * kt + 4 * g + r) * KS + 16 * dt + l16], sacc[kk][r], acc);
                 }
                 oacc[dt] = acc;
             }
         }
     };
-    // K/V tiles are loaded into registers one tile ahead.  Narrow heads
-    // double-buffer the LDS tiles: tile kb+1 is written while tile kb is
-    // consumed, one barrier per tile; wider heads use one buffer (two
-    // barriers per tile, and no register prefetch for the widest).
+    // Narrow heads (DB) run a four-deep pipeline: two register stages, loaded
+    // from global memory three tiles ahead of use, feed two LDS buffers; tile
+    // kb+1 is written to LDS while tile kb is consumed, one barrier per tile.
+    // Wider heads use one LDS buffer (two barriers per tile) and one register
+    // stage (none for the widest).
     TileRegs<DHP, MHA_BN, NT, VEC> kr, vr;
-    kr.load(K, base, rs, 0, S, Dh, tid);
-    if (WRITE_O)
-        vr.load(V, base, rs, 0, S, Dh, tid);
-    if constexpr (SM::DB) {
-        kr.template store<KS>(smem, tid);
+    auto load_kv = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
+                       int kb) {
+        kx.load(K, base, rs, kb * MHA_BN, S, Dh, tid);
         if (WRITE_O)
-            vr.template store_t<VS>(smem + MHA_BN * KS, tid);
-        if (nkb > 1) {
-            kr.load(K, base, rs, MHA_BN, S, Dh, tid);
-            if (WRITE_O)
-                vr.load(V, base, rs, MHA_BN, S, Dh, tid);
-        }
+            vx.load(V, base, rs, kb * MHA_BN, S, Dh, tid);
+    };
+    auto store_kv = [&](const TileRegs<DHP, MHA_BN, NT, VEC>& kx,
+                        const TileRegs<DHP, MHA_BN, NT, VEC>& vx, float* buf) {
+        kx.template store<KS>(buf, tid);
+        if (WRITE_O)
+            vx.template store<KS>(buf + MHA_BN * KS, tid);
+    };
+    load_kv(kr, vr, 0);
+    if constexpr (SM::DB) {
+        TileRegs<DHP, MHA_BN, NT, VEC> kr1, vr1;
+        if (nkb > 1)
+            load_kv(kr1, vr1, 1);
+        store_kv(kr, vr, smem);
+        if (nkb > 2)
+            load_kv(kr, vr, 2);
         __syncthreads();
-        for (int kb = 0; kb < nkb; kb++) {
+        // Iteration kb: registers (kx, vx) hold tile kb+1; they go to LDS
+        // buffer (kb+1)&1 and are refilled with tile kb+3.
+        auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
+                        int kb) {
             const float* cur = smem + (kb & 1) * SM::TILES;
             if (kb + 1 < nkb) {
-                float* nxt = smem + ((kb + 1) & 1) * SM::TILES;
-                kr.template store<KS>(nxt, tid);
-                if (WRITE_O)
-                    vr.template store_t<VS>(nxt + MHA_BN * KS, tid);
-                if (kb + 2 < nkb) {
-                    kr.load(K, base, rs, (kb + 2) * MHA_BN, S, Dh, tid);
-                    if (WRITE_O)
-                        vr.load(V, base, rs, (kb + 2) * MHA_BN, S, Dh, tid);
-                }
+                store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
+                if (kb + 3 < nkb)
+                    load_kv(kx, vx, kb + 3);
             }
             tile_math(cur, cur + MHA_BN * KS, kb);
             __syncthreads();
+        };
+        for (int kb = 0; kb < nkb; kb += 2) {
+            step(kr1, vr1, kb);
+            if (kb + 1 < nkb)
+                step(kr, vr, kb + 1);
         }
     } else {
         constexpr bool PREFETCH = DHP <= 128;
         for (int kb = 0; kb < nkb; kb++) {
-            const int k0 = kb * MHA_BN;
-            if (!PREFETCH && kb > 0) {
-                kr.load(K, base, rs, k0, S, Dh, tid);
-                if (WRITE_O)
-                    vr.load(V, base, rs, k0, S, Dh, tid);
-            }
+            if (!PREFETCH && kb > 0)
+                load_kv(kr, vr, kb);
             __syncthreads();
-            kr.template store<KS>(smem, tid);
-            if (WRITE_O)
-                vr.template store_t<VS>(smem + MHA_BN * KS, tid);
+            store_kv(kr, vr, smem);
             __syncthreads();
-            if (PREFETCH && kb + 1 < nkb) {
-                kr.load(K, base, rs, k0 + MHA_BN, S, Dh, tid);
-                if (WRITE_O)
-                    vr.load(V, base, rs, k0 + MHA_BN, S, Dh, tid);
-            }
+            if (PREFETCH && kb + 1 < nkb)
+                load_kv(kr, vr, kb + 1);
             tile_math(smem, smem + MHA_BN * KS, kb);
         }
     }
@@ -410,11 +415,14 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             vreg[dt] = load4<VEC>(V + off, 16 * dt + 4 * g, Dh, kok);
         }
     }
-    // K^T tile for the dQ product.
-    {
-        TileRegs<DHP, MHA_BN, NT, VEC> kt;
-        kt.load(K, base, rs, k0, S, Dh, tid);
-        kt.template store_t<TS>(Kt, tid);
+    // K^T tile for the dQ product, written from the K operand registers by
+    // the waves of query split 0 (their key blocks kg cover the tile).
+    if (qs == 0) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                Kt[(16 * dt + 4 * g + r) * TS + kg * 16 + l16] = kreg[dt][r];
     }
 
     f4 dk[NDT], dv[NDT];
@@ -425,25 +433,27 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     }
 
     const int nqb = (S + BM - 1) / BM;
-    // Q/dO tiles and their lse/Di entries pass through registers one query
-    // tile ahead of their store to LDS (DHP <= 128).
-    TileRegs<DHP, BM, NT, VEC> qr, dor;
-    float lse_r = 0.0f, di_r = 0.0f;
-    auto load_q = [&](int q0) {
-        qr.load(Q, base, rs, q0, S, Dh, tid);
-        dor.load(dO, base, rs, q0, S, Dh, tid);
+    // A query tile in registers on its way to LDS: Q and dO rows, and the
+    // tile's lse and Di entries (lse is scaled by log2 e on its way to LDS).
+    struct QTile {
+        TileRegs<DHP, BM, NT, VEC> q, d;
+        float lse, di;
+    };
+    auto load_q = [&](QTile& t, int q0) {
+        t.q.load(Q, base, rs, q0, S, Dh, tid);
+        t.d.load(dO, base, rs, q0, S, Dh, tid);
         if (tid < BM) {   // rows past S repeat row S-1; their P is masked to 0
             const long i = (long)bh * S + min(q0 + tid, S - 1);
-            lse_r = lse[i] * kLog2e;
-            di_r = Di[i];
+            t.lse = lse[i];   // scaled at the LDS store: no use of loaded data here,
+            t.di = Di[i];     // so the loads stay in flight
         }
     };
-    auto store_q = [&](float* st) {
-        qr.template store<QS>(st, tid);
-        dor.template store<QS>(st + BM * QS, tid);
+    auto store_q = [&](const QTile& t, float* st) {
+        t.q.template store<QS>(st, tid);
+        t.d.template store<QS>(st + BM * QS, tid);
         if (tid < BM) {
-            st[2 * BM * QS + BM * TS + tid] = lse_r;
-            st[2 * BM * QS + BM * TS + BM + tid] = di_r;
+            st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
+            st[2 * BM * QS + BM * TS + BM + tid] = t.di;
         }
     };
     // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
@@ -456,31 +466,44 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         const float* lse_s = st + 2 * BM * QS + BM * TS;
         const float* di_s = lse_s + BM;
         const bool diag = q0 < k0 + MHA_BN;   // tile touches the causal boundary
+        // Query blocks are taken QI at a time so that 2*QI accumulation
+        // chains interleave on the MFMA pipe.
+        constexpr int QI = NQW <= 2 ? NQW : 1;
         f4 P[NQW], dS[NQW];
 #pragma unroll
-        for (int qq = 0; qq < NQW; qq++) {
-            const int qt = qs * NQW + qq;
-            f4 sa = f4zero(), da = f4zero();
+        for (int q1 = 0; q1 < NQW; q1 += QI) {
+            f4 sa[QI], da[QI];
+#pragma unroll
+            for (int j = 0; j < QI; j++)
+                sa[j] = da[j] = f4zero();
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
-                const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
-                const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    sa = mfma16(qa[r], kreg[dt][r], sa);
-                    da = mfma16(oa[r], vreg[dt][r], da);
+                for (int j = 0; j < QI; j++) {
+                    const int qt = qs * NQW + q1 + j;
+                    const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
+                    const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        sa[j] = mfma16(qa[r], kreg[dt][r], sa[j]);
+                        da[j] = mfma16(oa[r], vreg[dt][r], da[j]);
+                    }
                 }
             }
-            const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
-            const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int q = q0 + 16 * qt + 4 * g + r;
-                const bool ok = (!diag || mykey <= q) && q < S;
-                const float p = ok ? fast_exp2(sa[r] * c2 - l4[r]) : 0.0f;
-                P[qq][r] = p;
-                dS[qq][r] = p * (da[r] - d4[r]);
-                dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
+            for (int j = 0; j < QI; j++) {
+                const int qq = q1 + j, qt = qs * NQW + qq;
+                const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
+                const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int q = q0 + 16 * qt + 4 * g + r;
+                    const bool ok = (!diag || mykey <= q) && q < S;
+                    const float p = ok ? fast_exp2(sa[j][r] * c2 - l4[r]) : 0.0f;
+                    P[qq][r] = p;
+                    dS[qq][r] = p * (da[j][r] - d4[r]);
+                    dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
+                }
             }
         }
 #pragma unroll
@@ -501,52 +524,104 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         }
     };
     // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
-    // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.
+    // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
+    // wave's jobs share qt (NW is a multiple of NQT), so pairs of jobs run as
+    // two interleaved MFMA chains over one read of the dS operand.
+    constexpr int NJOB = NQT * NDT;
+    constexpr int NJ = (NJOB + NW - 1) / NW;   // jobs per wave (the last may be empty)
+    static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
+    auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
+        const int d = 16 * dt + l16;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int q = q0 + 16 * qt + 4 * g + r;
+            if (q < S && d < Dh)
+                atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
+        }
+    };
     auto query_side = [&](const float* st, int q0) {
         const float* dSs = st + 2 * BM * QS;
-        for (int job = wave; job < NQT * NDT; job += NW) {
-            const int qt = job % NQT, dt = job / NQT;
-            f4 acc = f4zero();
+        const int qt = wave % NQT;
+        const float* arow = dSs + (16 * qt + l16) * TS + 4 * g;
+        if constexpr (NJ % 2 == 0) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++) {
-                const f4 a = *reinterpret_cast<const f4*>(&dSs[(16 * qt + l16) * TS + 16 * kt + 4 * g]);
-                const f4 bb = *reinterpret_cast<const f4*>(&Kt[(16 * dt + l16) * TS + 16 * kt + 4 * g]);
+            for (int i = 0; i < NJ; i += 2) {
+                const int dt0 = (wave + i * NW) / NQT, dt1 = (wave + (i + 1) * NW) / NQT;
+                const float* b0 = Kt + (16 * dt0 + l16) * TS + 4 * g;
+                const float* b1 = Kt + (16 * dt1 + l16) * TS + 4 * g;
+                f4 acc0 = f4zero(), acc1 = f4zero();
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc = mfma16(a[r], bb[r], acc);
+                for (int kt = 0; kt < 4; kt++) {
+                    const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
+                    const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
+                    const f4 v = *reinterpret_cast<const f4*>(b1 + 16 * kt);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        acc0 = mfma16(a[r], u[r], acc0);
+                        acc1 = mfma16(a[r], v[r], acc1);
+                    }
+                }
+                dq_store(acc0, q0, qt, dt0);
+                dq_store(acc1, q0, qt, dt1);
             }
-            const int d = 16 * dt + l16;
+        } else {
+            for (int job = wave; job < NJOB; job += NW) {
+                const int dt = job / NQT;
+                const float* b0 = Kt + (16 * dt + l16) * TS + 4 * g;
+                f4 acc = f4zero();
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int q = q0 + 16 * qt + 4 * g + r;
-                if (q < S && d < Dh)
-                    atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
+                for (int kt = 0; kt < 4; kt++) {
+                    const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
+                    const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc = mfma16(a[r], u[r], acc);
+                }
+                dq_store(acc, q0, qt, dt);
             }
         }
     };
 
     const int qb0 = k0 / BM;
-    load_q(qb0 * BM);
+    QTile t0;
+    t0.lse = t0.di = 0.0f;
+    load_q(t0, qb0 * BM);
     if constexpr (SM::DB) {
-        // Tile qb is in stage qb&1 when iteration qb starts.  Iteration qb
-        // writes tile qb+1 into the other stage (last read in iteration qb-1,
-        // before its barrier) and dS into its own stage, which the dQ jobs
-        // read after the barrier.
-        store_q(stage(qb0 & 1));
+        // Four-deep pipeline: two register stages loaded three query tiles
+        // ahead of use, two LDS stages.  Tile qb is in stage qb&1 when
+        // iteration qb starts.  The iteration writes dS into its own stage
+        // (the dQ jobs read it after the barrier) and, once its own S/dP/dV/dK
+        // work is issued, tile qb+1 into the Q/dO/lse/Di part of the other
+        // stage: that part was last read before the previous barrier, and the
+        // dQ jobs of iteration qb-1 still running on other waves read only the
+        // other stage's dS part.  Writing the next tile after the key-side
+        // work, rather than at the top, leaves the dQ atomics and loads of the
+        // previous iteration time to drain before the wait for its registers.
+        QTile t1;
+        t1.lse = t1.di = 0.0f;
         if (qb0 + 1 < nqb)
-            load_q((qb0 + 1) * BM);
+            load_q(t1, (qb0 + 1) * BM);
+        store_q(t0, stage(qb0 & 1));
+        if (qb0 + 2 < nqb)
+            load_q(t0, (qb0 + 2) * BM);
         __syncthreads();
-        for (int qb = qb0; qb < nqb; qb++) {
+        // Iteration qb: registers tx hold tile qb+1 and are refilled with qb+3.
+        auto step = [&](QTile& tx, int qb) {
             const int q0 = qb * BM;
             float* cur = stage(qb & 1);
-            if (qb + 1 < nqb) {
-                store_q(stage((qb + 1) & 1));
-                if (qb + 2 < nqb)
-                    load_q(q0 + 2 * BM);
-            }
             key_side(cur, q0);
+            if (qb + 1 < nqb) {
+                store_q(tx, stage((qb + 1) & 1));
+                if (qb + 3 < nqb)
+                    load_q(tx, q0 + 3 * BM);
+            }
             __syncthreads();
             query_side(cur, q0);
+        };
+        for (int qb = qb0; qb < nqb; qb += 2) {
+            step(t1, qb);
+            if (qb + 1 < nqb)
+                step(t0, qb + 1);
         }
     } else {
         constexpr bool PREFETCH = DHP <= 128;
@@ -554,12 +629,12 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         for (int qb = qb0; qb < nqb; qb++) {
             const int q0 = qb * BM;
             if (!PREFETCH && qb > qb0)
-                load_q(q0);
+                load_q(t0, q0);
             __syncthreads();
-            store_q(st);
+            store_q(t0, st);
             __syncthreads();
             if (PREFETCH && qb + 1 < nqb)
-                load_q(q0 + BM);
+                load_q(t0, q0 + BM);
             key_side(st, q0);
             __syncthreads();
             query_side(st, q0);
