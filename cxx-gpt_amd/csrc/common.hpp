@@ -121,6 +121,17 @@ __device__ __forceinline__ f4 load4c(const float* __restrict__ row, int c, int n
     return v;
 }
 
+// Zero the lanes of a loaded f4 whose row is invalid (!ok) or whose columns
+// lie past n.  Applied apart from the (clamped, unconditional) load, once the
+// data is needed anyway, so that the load itself stays asynchronous.
+__device__ __forceinline__ f4 mask4(f4 v, int c, int n, bool ok)
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        v[i] = (ok && c + i < n) ? v[i] : 0.0f;
+    return v;
+}
+
 __device__ __forceinline__ void atomic_add_f32(float* p, float v)
 {
     unsafeAtomicAdd(p, v);

@@ -106,23 +106,42 @@ struct FwdSmem {
     static constexpr int FLOATS = (DB ? 2 : 1) * TILES > MERGE ? (DB ? 2 : 1) * TILES : MERGE;
 };
 
+// Persistent grids: workgroup w of G takes job r*G + w in even rounds r and
+// r*G + G-1-w in odd rounds.  Jobs are numbered heaviest first, so the
+// serpentine order pairs a workgroup's heavy early jobs with light late ones.
+__device__ __forceinline__ int snake_job(int r)
+{
+    const int G = gridDim.x, w = blockIdx.x;
+    return r * G + ((r & 1) ? G - 1 - w : w);
+}
+
+// threadIdx.x, re-read per job behind an empty asm so that the compiler does
+// not hoist the job body's thread-dependent address arithmetic out of the job
+// loop (holding it across jobs costs registers).
+__device__ __forceinline__ int job_tid()
+{
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// One forward job: query tile qb of head bh (job = qi*BH + bh, qb = nqb-1-qi).
 template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
-__global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
+__device__ __forceinline__ void mha_fwd_job(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
-    float qscale)
+    float qscale, int job, float* __restrict__ smem)
 {
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
     constexpr int KS = SM::KS, MS = SM::MS;
     constexpr int NDT = DHP / 16;
     constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
-    __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int qg = wave & 3, ks = wave >> 2;
-    const int qi = blockIdx.x / BH, bh = blockIdx.x - qi * BH;
+    const int qi = job / BH, bh = job - qi * BH;
     const int qb = nqb - 1 - qi;
     const int b = bh / H, h = bh - b * H;
     const long rs = (long)H * Dh;
@@ -132,12 +151,14 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     const bool qok = myq < S;
     // B operand of S^T = K Q^T: lane holds Q[myq][16*dt + 4*g + r], pre-scaled
     // by scale*log2(e) so scores land in the exp2 domain; zero past Dh.
+    // (Masking and scaling are applied once the first K/V tiles are
+    // requested, so the Q loads and the K/V loads are in flight together.)
     f4 qreg[NDT];
     {
         const float* qrow = Q + base + (long)(qok ? myq : 0) * rs;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = load4<VEC>(qrow, 16 * dt + 4 * g, Dh, qok) * qscale;
+            qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
     }
     f4 oacc[NDT];
 #pragma unroll
@@ -231,12 +252,16 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     };
     load_kv(kr, vr, 0);
     if constexpr (SM::DB) {
+        // The prologue's loads past the last key tile repeat it (clamped tile
+        // index), so its memory operations are the same on every path and the
+        // compiler's waits for them stay tight.
         TileRegs<DHP, MHA_BN, NT, VEC> kr1, vr1;
-        if (nkb > 1)
-            load_kv(kr1, vr1, 1);
+        load_kv(kr1, vr1, min(1, nkb - 1));
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
         store_kv(kr, vr, smem);
-        if (nkb > 2)
-            load_kv(kr, vr, 2);
+        load_kv(kr, vr, min(2, nkb - 1));
         __syncthreads();
         // Iteration kb: registers (kx, vx) hold tile kb+1; they go to LDS
         // buffer (kb+1)&1 and are refilled with tile kb+3.
@@ -245,6 +270,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             const float* cur = smem + (kb & 1) * SM::TILES;
             if (kb + 1 < nkb) {
                 store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
+                // Keep the refill below the LDS writes: issued earlier, the
+                // wait for the old data would include the new loads.
+                __builtin_amdgcn_sched_barrier(0);
                 if (kb + 3 < nkb)
                     load_kv(kx, vx, kb + 3);
             }
@@ -258,6 +286,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
         }
     } else {
         constexpr bool PREFETCH = DHP <= 128;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
         for (int kb = 0; kb < nkb; kb++) {
             if (!PREFETCH && kb > 0)
                 load_kv(kr, vr, kb);
@@ -326,6 +357,26 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     }
 }
 
+template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
+__global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
+    float qscale)
+{
+    __shared__ __attribute__((aligned(16))) float smem[FwdSmem<DHP, NSPLIT>::FLOATS];
+    const int njobs = nqb * BH;
+#pragma nounroll
+    for (int r = 0;; r++) {
+        const int job = snake_job(r);
+        if (job >= njobs)
+            break;
+        if (r > 0)
+            __syncthreads();   // the previous job's last LDS reads are done
+        mha_fwd_job<DHP, NSPLIT, VEC, WRITE_O>(Q, K, V, O, lse, S, H, Dh, BH, nqb, qscale, job,
+                                                smem);
+    }
+}
+
 // ----------------------------------------------------------------------------
 // backward pre-pass: Di = rowsum(dO * O) (the reference's gs, kernel_test.cpp:76-78)
 // and dQ = 0.  16 lanes per (row, head) segment.
@@ -374,6 +425,11 @@ struct BwdSmem {
     static constexpr int FLOATS = DHP * TS + NB * STAGE;
 };
 
+// Persistent backward kernel.  Job kb*BH + bh is key tile kb of head bh; a
+// workgroup takes jobs in serpentine order and, once the last query tile of a
+// job has been through its key-side work, requests the next job's K/V rows
+// and first query tiles, so that they arrive while the current job finishes
+// its dQ jobs and dK/dV reduction.
 template <int DHP, int BM, int NSPLIT, bool VEC>
 __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
@@ -394,290 +450,360 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     // Stage i: Qs [BM][QS], dOs [BM][QS], dSs [BM][TS], lse_s [BM], di_s [BM].
     auto stage = [&](int i) { return smem + DHP * TS + i * SM::STAGE; };
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, g = lane >> 4;
-    const int kg = wave & 3, qs = wave >> 2;
-    const int kb = blockIdx.x / BH, bh = blockIdx.x - kb * BH;
-    const int b = bh / H, h = bh - b * H;
-    const long rs = (long)H * Dh;
-    const long base = (long)b * S * rs + (long)h * Dh;
-    const int k0 = kb * MHA_BN;
-    const int mykey = k0 + kg * 16 + l16;
-    const bool kok = mykey < S;
-
-    // B operands for S = Q K^T and dP = dO V^T: K/V[mykey][16dt + 4g + r], zero past Dh.
-    f4 kreg[NDT], vreg[NDT];
-    {
-        const long off = base + (long)(kok ? mykey : 0) * rs;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            kreg[dt] = load4<VEC>(K + off, 16 * dt + 4 * g, Dh, kok);
-            vreg[dt] = load4<VEC>(V + off, 16 * dt + 4 * g, Dh, kok);
-        }
-    }
-    // K^T tile for the dQ product, written from the K operand registers by
-    // the waves of query split 0 (their key blocks kg cover the tile).
-    if (qs == 0) {
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                Kt[(16 * dt + 4 * g + r) * TS + kg * 16 + l16] = kreg[dt][r];
-    }
-
-    f4 dk[NDT], dv[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        dk[dt] = f4zero();
-        dv[dt] = f4zero();
-    }
-
+    const int njobs = nkb * BH;
     const int nqb = (S + BM - 1) / BM;
+    const long rs = (long)H * Dh;
+
+    // Job geometry.
+    struct Job {
+        int bh, k0, qb0;
+        long base;
+    };
+    auto job_of = [&](int job) {
+        Job j;
+        const int kb = job / BH;
+        j.bh = job - kb * BH;
+        const int b = j.bh / H, h = j.bh - b * H;
+        j.base = (long)b * S * rs + (long)h * Dh;
+        j.k0 = kb * MHA_BN;
+        j.qb0 = j.k0 / BM;
+        return j;
+    };
+
     // A query tile in registers on its way to LDS: Q and dO rows, and the
     // tile's lse and Di entries (lse is scaled by log2 e on its way to LDS).
     struct QTile {
         TileRegs<DHP, BM, NT, VEC> q, d;
         float lse, di;
     };
-    auto load_q = [&](QTile& t, int q0) {
-        t.q.load(Q, base, rs, q0, S, Dh, tid);
-        t.d.load(dO, base, rs, q0, S, Dh, tid);
-        if (tid < BM) {   // rows past S repeat row S-1; their P is masked to 0
-            const long i = (long)bh * S + min(q0 + tid, S - 1);
-            t.lse = lse[i];   // scaled at the LDS store: no use of loaded data here,
-            t.di = Di[i];     // so the loads stay in flight
-        }
+    auto load_q = [&](QTile& t, const Job& j, int q0) {
+        const int tid = job_tid();
+        t.q.load(Q, j.base, rs, q0, S, Dh, tid);
+        t.d.load(dO, j.base, rs, q0, S, Dh, tid);
+        // Every thread loads (rows past S repeat row S-1, their P is masked to
+        // 0); threads tid < BM store.  No use of the loaded data here (lse is
+        // scaled at the LDS store), so the loads stay in flight.
+        const long i = (long)j.bh * S + min(q0 + (tid & (BM - 1)), S - 1);
+        t.lse = lse[i];
+        t.di = Di[i];
     };
-    auto store_q = [&](const QTile& t, float* st) {
-        t.q.template store<QS>(st, tid);
-        t.d.template store<QS>(st + BM * QS, tid);
-        if (tid < BM) {
-            st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
-            st[2 * BM * QS + BM * TS + BM + tid] = t.di;
-        }
-    };
-    // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
-    // l16, queries 16qt + 4g + r); dS goes to LDS for the dQ product, then
-    // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.
-    auto key_side = [&](float* st, int q0) {
-        const float* Qs = st;
-        const float* dOs = st + BM * QS;
-        float* dSs = st + 2 * BM * QS;
-        const float* lse_s = st + 2 * BM * QS + BM * TS;
-        const float* di_s = lse_s + BM;
-        const bool diag = q0 < k0 + MHA_BN;   // tile touches the causal boundary
-        // Query blocks are taken QI at a time so that 2*QI accumulation
-        // chains interleave on the MFMA pipe.
-        constexpr int QI = NQW <= 2 ? NQW : 1;
-        f4 P[NQW], dS[NQW];
-#pragma unroll
-        for (int q1 = 0; q1 < NQW; q1 += QI) {
-            f4 sa[QI], da[QI];
-#pragma unroll
-            for (int j = 0; j < QI; j++)
-                sa[j] = da[j] = f4zero();
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-#pragma unroll
-                for (int j = 0; j < QI; j++) {
-                    const int qt = qs * NQW + q1 + j;
-                    const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
-                    const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        sa[j] = mfma16(qa[r], kreg[dt][r], sa[j]);
-                        da[j] = mfma16(oa[r], vreg[dt][r], da[j]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < QI; j++) {
-                const int qq = q1 + j, qt = qs * NQW + qq;
-                const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
-                const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int q = q0 + 16 * qt + 4 * g + r;
-                    const bool ok = (!diag || mykey <= q) && q < S;
-                    const float p = ok ? fast_exp2(sa[j][r] * c2 - l4[r]) : 0.0f;
-                    P[qq][r] = p;
-                    dS[qq][r] = p * (da[j][r] - d4[r]);
-                    dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
-                }
-            }
-        }
+    // Loads past the last query tile repeat it (clamped tile index), so the
+    // job prologue issues the same memory operations on every path and the
+    // compiler's waits for its register stages stay tight.
+    auto tile_q0 = [&](int qb) { return min(qb, nqb - 1) * BM; };
+
+    // B operands for S = Q K^T and dP = dO V^T: K/V[key][16dt + 4g + r] for the
+    // lane's key (zeroed past S and Dh at the start of the job); and the
+    // first two query tiles.
+    f4 kreg[NDT], vreg[NDT];
+    QTile t0, t1;
+    auto load_kv = [&](const Job& j) {
+        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int l16 = lane & 15, g = lane >> 4, kg = wave & 3;
+        const int key = min(j.k0 + kg * 16 + l16, S - 1);   // masked at job start
+        const long off = j.base + (long)key * rs;
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            f4 av = dv[dt], ak = dk[dt];
+            kreg[dt] = load4c<VEC>(K + off, 16 * dt + 4 * g, Dh);
+            vreg[dt] = load4c<VEC>(V + off, 16 * dt + 4 * g, Dh);
+        }
+    };
+    auto load_first_q = [&](const Job& j) {
+        load_q(t0, j, j.qb0 * BM);
+        if (SM::DB)
+            load_q(t1, j, tile_q0(j.qb0 + 1));
+    };
+
+    Job jc = job_of(snake_job(0));   // the grid never exceeds the job count
+    load_kv(jc);
+    load_first_q(jc);
+#pragma nounroll
+    for (int r = 0;; r++) {
+        const int jn = snake_job(r + 1);
+        const bool more = jn < njobs;
+        const Job jnext = job_of(more ? jn : 0);
+
+        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int l16 = lane & 15, g = lane >> 4;
+        const int kg = wave & 3, qs = wave >> 2;
+        const long base = jc.base;
+        const int k0 = jc.k0, qb0 = jc.qb0;
+        const int mykey = k0 + kg * 16 + l16;
+        const bool kok = mykey < S;
+
+        f4 dk[NDT], dv[NDT];
 #pragma unroll
-            for (int qq = 0; qq < NQW; qq++) {
-                const int qt = qs * NQW + qq;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = (16 * qt + 4 * g + r) * QS + 16 * dt + l16;
-                    av = mfma16(dOs[row], P[qq][r], av);
-                    ak = mfma16(Qs[row], dS[qq][r], ak);
-                }
+        for (int dt = 0; dt < NDT; dt++) {
+            dk[dt] = f4zero();
+            dv[dt] = f4zero();
+        }
+        auto store_q = [&](const QTile& t, float* st) {
+            t.q.template store<QS>(st, tid);
+            t.d.template store<QS>(st + BM * QS, tid);
+            if (tid < BM) {
+                st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
+                st[2 * BM * QS + BM * TS + BM + tid] = t.di;
             }
-            dv[dt] = av;
-            dk[dt] = ak;
-        }
-    };
-    // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
-    // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
-    // wave's jobs share qt (NW is a multiple of NQT), so pairs of jobs run as
-    // two interleaved MFMA chains over one read of the dS operand.
-    constexpr int NJOB = NQT * NDT;
-    constexpr int NJ = (NJOB + NW - 1) / NW;   // jobs per wave (the last may be empty)
-    static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
-    auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
-        const int d = 16 * dt + l16;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int q = q0 + 16 * qt + 4 * g + r;
-            if (q < S && d < Dh)
-                atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
-        }
-    };
-    auto query_side = [&](const float* st, int q0) {
-        const float* dSs = st + 2 * BM * QS;
-        const int qt = wave % NQT;
-        const float* arow = dSs + (16 * qt + l16) * TS + 4 * g;
-        if constexpr (NJ % 2 == 0) {
-#pragma unroll
-            for (int i = 0; i < NJ; i += 2) {
-                const int dt0 = (wave + i * NW) / NQT, dt1 = (wave + (i + 1) * NW) / NQT;
-                const float* b0 = Kt + (16 * dt0 + l16) * TS + 4 * g;
-                const float* b1 = Kt + (16 * dt1 + l16) * TS + 4 * g;
-                f4 acc0 = f4zero(), acc1 = f4zero();
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++) {
-                    const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
-                    const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
-                    const f4 v = *reinterpret_cast<const f4*>(b1 + 16 * kt);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        acc0 = mfma16(a[r], u[r], acc0);
-                        acc1 = mfma16(a[r], v[r], acc1);
+        };
+        // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
+        // l16, queries 16qt + 4g + r); dS goes to LDS for the dQ product, then
+        // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.
+        auto key_side = [&](float* st, int q0) {
+            const float* Qs = st;
+            const float* dOs = st + BM * QS;
+            float* dSs = st + 2 * BM * QS;
+            const float* lse_s = st + 2 * BM * QS + BM * TS;
+            const float* di_s = lse_s + BM;
+            const bool diag = q0 < k0 + MHA_BN;   // tile touches the causal boundary
+            // Query blocks are taken QI at a time so that 2*QI accumulation
+            // chains interleave on the MFMA pipe.
+            constexpr int QI = NQW <= 2 ? NQW : 1;
+            f4 P[NQW], dS[NQW];
+    #pragma unroll
+            for (int q1 = 0; q1 < NQW; q1 += QI) {
+                f4 sa[QI], da[QI];
+    #pragma unroll
+                for (int j = 0; j < QI; j++)
+                    sa[j] = da[j] = f4zero();
+    #pragma unroll
+                for (int dt = 0; dt < NDT; dt++) {
+    #pragma unroll
+                    for (int j = 0; j < QI; j++) {
+                        const int qt = qs * NQW + q1 + j;
+                        const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
+                        const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
+    #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            sa[j] = mfma16(qa[r], kreg[dt][r], sa[j]);
+                            da[j] = mfma16(oa[r], vreg[dt][r], da[j]);
+                        }
                     }
                 }
-                dq_store(acc0, q0, qt, dt0);
-                dq_store(acc1, q0, qt, dt1);
+    #pragma unroll
+                for (int j = 0; j < QI; j++) {
+                    const int qq = q1 + j, qt = qs * NQW + qq;
+                    const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
+                    const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
+    #pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int q = q0 + 16 * qt + 4 * g + r;
+                        const bool ok = (!diag || mykey <= q) && q < S;
+                        const float p = ok ? fast_exp2(sa[j][r] * c2 - l4[r]) : 0.0f;
+                        P[qq][r] = p;
+                        dS[qq][r] = p * (da[j][r] - d4[r]);
+                        dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
+                    }
+                }
+            }
+    #pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                f4 av = dv[dt], ak = dk[dt];
+    #pragma unroll
+                for (int qq = 0; qq < NQW; qq++) {
+                    const int qt = qs * NQW + qq;
+    #pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int row = (16 * qt + 4 * g + r) * QS + 16 * dt + l16;
+                        av = mfma16(dOs[row], P[qq][r], av);
+                        ak = mfma16(Qs[row], dS[qq][r], ak);
+                    }
+                }
+                dv[dt] = av;
+                dk[dt] = ak;
+            }
+        };
+        // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
+        // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
+        // wave's jobs share qt (NW is a multiple of NQT), so pairs of jobs run as
+        // two interleaved MFMA chains over one read of the dS operand.
+        constexpr int NJOB = NQT * NDT;
+        constexpr int NJ = (NJOB + NW - 1) / NW;   // jobs per wave (the last may be empty)
+        static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
+        auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
+            const int d = 16 * dt + l16;
+    #pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int q = q0 + 16 * qt + 4 * g + r;
+                if (q < S && d < Dh)
+                    atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
+            }
+        };
+        auto query_side = [&](const float* st, int q0) {
+            const float* dSs = st + 2 * BM * QS;
+            const int qt = wave % NQT;
+            const float* arow = dSs + (16 * qt + l16) * TS + 4 * g;
+            if constexpr (NJ % 2 == 0) {
+    #pragma unroll
+                for (int i = 0; i < NJ; i += 2) {
+                    const int dt0 = (wave + i * NW) / NQT, dt1 = (wave + (i + 1) * NW) / NQT;
+                    const float* b0 = Kt + (16 * dt0 + l16) * TS + 4 * g;
+                    const float* b1 = Kt + (16 * dt1 + l16) * TS + 4 * g;
+                    f4 acc0 = f4zero(), acc1 = f4zero();
+    #pragma unroll
+                    for (int kt = 0; kt < 4; kt++) {
+                        const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
+                        const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
+                        const f4 v = *reinterpret_cast<const f4*>(b1 + 16 * kt);
+    #pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            acc0 = mfma16(a[r], u[r], acc0);
+                            acc1 = mfma16(a[r], v[r], acc1);
+                        }
+                    }
+                    dq_store(acc0, q0, qt, dt0);
+                    dq_store(acc1, q0, qt, dt1);
+                }
+            } else {
+                for (int jq = wave; jq < NJOB; jq += NW) {
+                    const int dt = jq / NQT;
+                    const float* b0 = Kt + (16 * dt + l16) * TS + 4 * g;
+                    f4 acc = f4zero();
+    #pragma unroll
+                    for (int kt = 0; kt < 4; kt++) {
+                        const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
+                        const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
+    #pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            acc = mfma16(a[r], u[r], acc);
+                    }
+                    dq_store(acc, q0, qt, dt);
+                }
+            }
+        };
+
+        // Zero the K/V operands past S and Dh (their loads were clamped).
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            kreg[dt] = mask4(kreg[dt], 16 * dt + 4 * g, Dh, kok);
+            vreg[dt] = mask4(vreg[dt], 16 * dt + 4 * g, Dh, kok);
+        }
+        // K^T tile for the dQ product, written from the K operand registers by
+        // the waves of query split 0 (their key blocks kg cover the tile).
+        if (qs == 0) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; r4++)
+                    Kt[(16 * dt + 4 * g + r4) * TS + kg * 16 + l16] = kreg[dt][r4];
+        }
+        if constexpr (SM::DB) {
+            // Four-deep pipeline: two register stages loaded three query tiles
+            // ahead of use, two LDS stages.  Tile qb is in stage qb&1 when
+            // iteration qb starts.  The iteration writes dS into its own stage
+            // (the dQ jobs read it after the barrier) and, once its own
+            // S/dP/dV/dK work is issued, tile qb+1 into the Q/dO/lse/Di part of
+            // the other stage: that part was last read before the previous
+            // barrier, and the dQ jobs of iteration qb-1 still running on other
+            // waves read only the other stage's dS part.  Writing the next tile
+            // after the key-side work, rather than at the top, leaves the dQ
+            // atomics and loads of the previous iteration time to drain before
+            // the wait for its registers.
+            store_q(t0, stage(qb0 & 1));
+            load_q(t0, jc, tile_q0(qb0 + 2));
+            __syncthreads();
+            // Iteration qb < nqb-1: registers tx hold tile qb+1 and are
+            // refilled with qb+3.
+            auto step = [&](QTile& tx, int qb) {
+                const int q0 = qb * BM;
+                float* cur = stage(qb & 1);
+                key_side(cur, q0);
+                store_q(tx, stage((qb + 1) & 1));
+                // Keep the refill below the LDS writes: issued earlier, the
+                // wait for the old data would include the new loads.
+                __builtin_amdgcn_sched_barrier(0);
+                if (qb + 3 < nqb)
+                    load_q(tx, jc, q0 + 3 * BM);
+                __syncthreads();
+                query_side(cur, q0);
+            };
+            int qb = qb0;
+            for (; qb + 2 < nqb; qb += 2) {
+                step(t1, qb);
+                step(t0, qb + 1);
+            }
+            if (qb + 1 < nqb)
+                step(t1, qb++);
+            // The last query tile: once its key-side work is issued the next
+            // job's K/V rows and first query tiles are requested (all register
+            // stages are free by then), ahead of this tile's dQ atomics.
+            {
+                const int q0 = qb * BM;
+                float* cur = stage(qb & 1);
+                key_side(cur, q0);
+                // Not above the key-side work: the loads overwrite its operands.
+                __builtin_amdgcn_sched_barrier(0);
+                if (more) {
+                    load_kv(jnext);
+                    load_first_q(jnext);
+                }
+                __syncthreads();
+                query_side(cur, q0);
             }
         } else {
-            for (int job = wave; job < NJOB; job += NW) {
-                const int dt = job / NQT;
-                const float* b0 = Kt + (16 * dt + l16) * TS + 4 * g;
-                f4 acc = f4zero();
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++) {
-                    const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
-                    const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        acc = mfma16(a[r], u[r], acc);
+            constexpr bool PREFETCH = DHP <= 128;
+            float* st = stage(0);
+            for (int qb = qb0; qb < nqb; qb++) {
+                const int q0 = qb * BM;
+                if (!PREFETCH && qb > qb0)
+                    load_q(t0, jc, q0);
+                __syncthreads();
+                store_q(t0, st);
+                __syncthreads();
+                if (PREFETCH && qb + 1 < nqb)
+                    load_q(t0, jc, q0 + BM);
+                key_side(st, q0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (qb + 1 == nqb && more) {   // next job's loads, as above
+                    load_kv(jnext);
+                    load_first_q(jnext);
                 }
-                dq_store(acc, q0, qt, dt);
+                __syncthreads();
+                query_side(st, q0);
             }
         }
-    };
 
-    const int qb0 = k0 / BM;
-    QTile t0;
-    t0.lse = t0.di = 0.0f;
-    load_q(t0, qb0 * BM);
-    if constexpr (SM::DB) {
-        // Four-deep pipeline: two register stages loaded three query tiles
-        // ahead of use, two LDS stages.  Tile qb is in stage qb&1 when
-        // iteration qb starts.  The iteration writes dS into its own stage
-        // (the dQ jobs read it after the barrier) and, once its own S/dP/dV/dK
-        // work is issued, tile qb+1 into the Q/dO/lse/Di part of the other
-        // stage: that part was last read before the previous barrier, and the
-        // dQ jobs of iteration qb-1 still running on other waves read only the
-        // other stage's dS part.  Writing the next tile after the key-side
-        // work, rather than at the top, leaves the dQ atomics and loads of the
-        // previous iteration time to drain before the wait for its registers.
-        QTile t1;
-        t1.lse = t1.di = 0.0f;
-        if (qb0 + 1 < nqb)
-            load_q(t1, (qb0 + 1) * BM);
-        store_q(t0, stage(qb0 & 1));
-        if (qb0 + 2 < nqb)
-            load_q(t0, (qb0 + 2) * BM);
-        __syncthreads();
-        // Iteration qb: registers tx hold tile qb+1 and are refilled with qb+3.
-        auto step = [&](QTile& tx, int qb) {
-            const int q0 = qb * BM;
-            float* cur = stage(qb & 1);
-            key_side(cur, q0);
-            if (qb + 1 < nqb) {
-                store_q(tx, stage((qb + 1) & 1));
-                if (qb + 3 < nqb)
-                    load_q(tx, q0 + 3 * BM);
+        if (NSPLIT > 1) {
+            // Sum the per-split partial dK^T/dV^T: splits qs > 0 publish
+            // through LDS (reusing the Q/dO tiles), split 0 adds and stores.
+            constexpr int RS = 2 * DHP + 4;   // record per (split, key): dk[DHP], dv[DHP]
+            static_assert((NSPLIT - 1) * MHA_BN * RS <= SM::FLOATS,
+                          "dK/dV reduction buffer does not fit");
+            float* rb = smem;
+            __syncthreads();   // every wave is done with the tiles
+            const int krow = kg * 16 + l16;
+            if (qs > 0) {
+                float* rec = rb + ((qs - 1) * MHA_BN + krow) * RS;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) {
+                    *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = dk[dt];
+                    *reinterpret_cast<f4*>(&rec[DHP + 16 * dt + 4 * g]) = dv[dt];
+                }
             }
             __syncthreads();
-            query_side(cur, q0);
-        };
-        for (int qb = qb0; qb < nqb; qb += 2) {
-            step(t1, qb);
-            if (qb + 1 < nqb)
-                step(t0, qb + 1);
+            if (qs == 0) {
+#pragma unroll
+                for (int j = 1; j < NSPLIT; j++) {
+                    const float* rec = rb + ((j - 1) * MHA_BN + krow) * RS;
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt++) {
+                        dk[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]);
+                        dv[dt] += *reinterpret_cast<const f4*>(&rec[DHP + 16 * dt + 4 * g]);
+                    }
+                }
+            }
         }
-    } else {
-        constexpr bool PREFETCH = DHP <= 128;
-        float* st = stage(0);
-        for (int qb = qb0; qb < nqb; qb++) {
-            const int q0 = qb * BM;
-            if (!PREFETCH && qb > qb0)
-                load_q(t0, q0);
-            __syncthreads();
-            store_q(t0, st);
-            __syncthreads();
-            if (PREFETCH && qb + 1 < nqb)
-                load_q(t0, q0 + BM);
-            key_side(st, q0);
-            __syncthreads();
-            query_side(st, q0);
-        }
-    }
-
-    if (NSPLIT > 1) {
-        // Sum the per-split partial dK^T/dV^T: splits qs > 0 publish through
-        // LDS (reusing the Q/dO tiles), split 0 adds and stores.
-        constexpr int RS = 2 * DHP + 4;   // record per (split, key): dk[DHP], dv[DHP]
-        static_assert((NSPLIT - 1) * MHA_BN * RS <= SM::FLOATS,
-                      "dK/dV reduction buffer does not fit");
-        float* rb = smem;
-        __syncthreads();   // every wave is done with the tiles
-        const int krow = kg * 16 + l16;
-        if (qs > 0) {
-            float* rec = rb + ((qs - 1) * MHA_BN + krow) * RS;
+        if (qs == 0 && kok) {
+            const long off = base + (long)mykey * rs;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
-                *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = dk[dt];
-                *reinterpret_cast<f4*>(&rec[DHP + 16 * dt + 4 * g]) = dv[dt];
+                store4<VEC>(dK + off, 16 * dt + 4 * g, Dh, dk[dt] * scale);
+                store4<VEC>(dV + off, 16 * dt + 4 * g, Dh, dv[dt]);
             }
         }
-        __syncthreads();
-        if (qs > 0)
-            return;
-#pragma unroll
-        for (int j = 1; j < NSPLIT; j++) {
-            const float* rec = rb + ((j - 1) * MHA_BN + krow) * RS;
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-                dk[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]);
-                dv[dt] += *reinterpret_cast<const f4*>(&rec[DHP + 16 * dt + 4 * g]);
-            }
-        }
-    }
-    if (kok) {
-        const long off = base + (long)mykey * rs;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            store4<VEC>(dK + off, 16 * dt + 4 * g, Dh, dk[dt] * scale);
-            store4<VEC>(dV + off, 16 * dt + 4 * g, Dh, dv[dt]);
-        }
+        if (!more)
+            break;
+        jc = jnext;
+        __syncthreads();   // the reduction records and K^T tile are consumed
     }
 }
 
@@ -686,12 +812,40 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
 // ----------------------------------------------------------------------------
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Compute units of the current device (cached per device).
+static int device_cus()
+{
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (cached[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// Persistent grid size: `per_cu` resident workgroups per compute unit, never
+// more workgroups than jobs.
+static unsigned persistent_grid(long njobs, int per_cu)
+{
+    const long g = (long)device_cus() * per_cu;
+    return (unsigned)(njobs < g ? njobs : g);
+}
+
 // Wave groups per workgroup: two per SIMD wherever registers allow.
 template <int DHP>
 struct MhaSplits {
     static constexpr int FWD = DHP <= 128 ? 2 : 1;
     static constexpr int BWD = DHP <= 64 ? 2 : 1;
     static constexpr int BWD_BM = DHP <= 128 ? 64 : 32;
+    // Resident workgroups per CU for the persistent grids.
+    static constexpr int FWD_PER_CU = 1;
+    static constexpr int BWD_PER_CU = 1;
 };
 
 template <int DHP, bool VEC>
@@ -702,7 +856,7 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     const int BH = B * H;
     const int nqb = (S + MHA_BM - 1) / MHA_BM;
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid((unsigned)(nqb * BH)), block(256 * NS);
+    dim3 grid(persistent_grid((long)nqb * BH, MhaSplits<DHP>::FWD_PER_CU)), block(256 * NS);
     if (O != nullptr) {
         ProfScope ps(st, "mha_fwd");
         hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true>), grid, block, 0, st, Q, K, V, O,
@@ -765,7 +919,7 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
     const int BH = B * H;
     const int nkb = (S + MHA_BN - 1) / MHA_BN;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid((unsigned)(nkb * BH)), block(256 * NS);
+    dim3 grid(persistent_grid((long)nkb * BH, MhaSplits<DHP>::BWD_PER_CU)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, "mha_bwd");
