@@ -125,255 +125,280 @@ __device__ __forceinline__ int job_tid()
     return t;
 }
 
-// One forward job: query tile qb of head bh (job = qi*BH + bh, qb = nqb-1-qi).
-template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
-__device__ __forceinline__ void mha_fwd_job(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
-    float qscale, int job, float* __restrict__ smem)
-{
-    using SM = FwdSmem<DHP, NSPLIT>;
-    constexpr int NT = 256 * NSPLIT;
-    constexpr int KS = SM::KS, MS = SM::MS;
-    constexpr int NDT = DHP / 16;
-    constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
-
-    const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, g = lane >> 4;
-    const int qg = wave & 3, ks = wave >> 2;
-    const int qi = job / BH, bh = job - qi * BH;
-    const int qb = nqb - 1 - qi;
-    const int b = bh / H, h = bh - b * H;
-    const long rs = (long)H * Dh;
-    const long base = (long)b * S * rs + (long)h * Dh;
-
-    const int myq = qb * MHA_BM + qg * 16 + l16;
-    const bool qok = myq < S;
-    // B operand of S^T = K Q^T: lane holds Q[myq][16*dt + 4*g + r], pre-scaled
-    // by scale*log2(e) so scores land in the exp2 domain; zero past Dh.
-    // (Masking and scaling are applied once the first K/V tiles are
-    // requested, so the Q loads and the K/V loads are in flight together.)
-    f4 qreg[NDT];
-    {
-        const float* qrow = Q + base + (long)(qok ? myq : 0) * rs;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
-    }
-    f4 oacc[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++)
-        oacc[dt] = f4zero();
-    float m_run = -1e30f, l_run = 0.0f;
-
-    const int nkb = qb + 1;   // causal: key tiles 0..qb (MHA_BM == MHA_BN)
-    // One key tile of math on the tiles in LDS (Ks, Vs: [key][d], row stride KS).
-    auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
-        const int k0 = kb * MHA_BN;
-        // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
-        // The NKT key blocks run as interleaved accumulation chains.
-        f4 sacc[NKT];
-#pragma unroll
-        for (int kk = 0; kk < NKT; kk++)
-            sacc[kk] = f4zero();
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-#pragma unroll
-            for (int kk = 0; kk < NKT; kk++) {
-                const int kt = ks * NKT + kk;
-                const f4 kv = *reinterpret_cast<const f4*>(&Ks[(16 * kt + l16) * KS + 16 * dt + 4 * g]);
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    sacc[kk] = mfma16(kv[r], qreg[dt][r], sacc[kk]);
-            }
-        }
-        if (kb == qb) {   // diagonal tile: causal mask key > query
-#pragma unroll
-            for (int kk = 0; kk < NKT; kk++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    if (k0 + 16 * (ks * NKT + kk) + 4 * g + r > myq)
-                        sacc[kk][r] = -INFINITY;
-        }
-        float mloc = -INFINITY;
-#pragma unroll
-        for (int kk = 0; kk < NKT; kk++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                mloc = fmaxf(mloc, sacc[kk][r]);
-        mloc = xrow_max(mloc);
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = fast_exp2(m_run - m_new);
-        float psum = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < NKT; kk++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float p = fast_exp2(sacc[kk][r] - m_new);
-                sacc[kk][r] = p;
-                psum += p;
-            }
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (WRITE_O) {
-            // O^T += V^T P^T: A = V^T[d = 16dt + l16][key = 16kt + 4g + r], read
-            // as single floats from the row-major V tile; B = P^T from sacc.
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++) {
-                f4 acc = oacc[dt] * alpha;
-#pragma unroll
-                for (int kk = 0; kk < NKT; kk++) {
-                    const int kt = ks * NKT + kk;
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        acc = mfma16(Vs[(16 * kt + 4 * g + r) * KS + 16 * dt + l16], sacc[kk][r], acc);
-                }
-                oacc[dt] = acc;
-            }
-        }
-    };
-    // Narrow heads (DB) run a four-deep pipeline: two register stages, loaded
-    // from global memory three tiles ahead of use, feed two LDS buffers; tile
-    // kb+1 is written to LDS while tile kb is consumed, one barrier per tile.
-    // Wider heads use one LDS buffer (two barriers per tile) and one register
-    // stage (none for the widest).
-    TileRegs<DHP, MHA_BN, NT, VEC> kr, vr;
-    auto load_kv = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
-                       int kb) {
-        kx.load(K, base, rs, kb * MHA_BN, S, Dh, tid);
-        if (WRITE_O)
-            vx.load(V, base, rs, kb * MHA_BN, S, Dh, tid);
-    };
-    auto store_kv = [&](const TileRegs<DHP, MHA_BN, NT, VEC>& kx,
-                        const TileRegs<DHP, MHA_BN, NT, VEC>& vx, float* buf) {
-        kx.template store<KS>(buf, tid);
-        if (WRITE_O)
-            vx.template store<KS>(buf + MHA_BN * KS, tid);
-    };
-    load_kv(kr, vr, 0);
-    if constexpr (SM::DB) {
-        // The prologue's loads past the last key tile repeat it (clamped tile
-        // index), so its memory operations are the same on every path and the
-        // compiler's waits for them stay tight.
-        TileRegs<DHP, MHA_BN, NT, VEC> kr1, vr1;
-        load_kv(kr1, vr1, min(1, nkb - 1));
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
-        store_kv(kr, vr, smem);
-        load_kv(kr, vr, min(2, nkb - 1));
-        __syncthreads();
-        // Iteration kb: registers (kx, vx) hold tile kb+1; they go to LDS
-        // buffer (kb+1)&1 and are refilled with tile kb+3.
-        auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
-                        int kb) {
-            const float* cur = smem + (kb & 1) * SM::TILES;
-            if (kb + 1 < nkb) {
-                store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
-                // Keep the refill below the LDS writes: issued earlier, the
-                // wait for the old data would include the new loads.
-                __builtin_amdgcn_sched_barrier(0);
-                if (kb + 3 < nkb)
-                    load_kv(kx, vx, kb + 3);
-            }
-            tile_math(cur, cur + MHA_BN * KS, kb);
-            __syncthreads();
-        };
-        for (int kb = 0; kb < nkb; kb += 2) {
-            step(kr1, vr1, kb);
-            if (kb + 1 < nkb)
-                step(kr, vr, kb + 1);
-        }
-    } else {
-        constexpr bool PREFETCH = DHP <= 128;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
-        for (int kb = 0; kb < nkb; kb++) {
-            if (!PREFETCH && kb > 0)
-                load_kv(kr, vr, kb);
-            __syncthreads();
-            store_kv(kr, vr, smem);
-            __syncthreads();
-            if (PREFETCH && kb + 1 < nkb)
-                load_kv(kr, vr, kb + 1);
-            tile_math(smem, smem + MHA_BN * KS, kb);
-        }
-    }
-    float l_tot = xrow_sum(l_run);
-
-    if (NSPLIT > 1) {
-        // Merge the key splits: split ks > 0 publishes (o, m, l) per query row,
-        // split 0 rescales everything to the common maximum.
-        float* mb = smem;
-        __syncthreads();   // every wave is done with the K/V tiles
-        const int qrow = qg * 16 + l16;
-        if (ks > 0) {
-            float* rec = mb + ((ks - 1) * MHA_BM + qrow) * MS;
-            if (WRITE_O)
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++)
-                    *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = oacc[dt];
-            if (g == 0) {
-                rec[DHP] = m_run;
-                rec[DHP + 1] = l_tot;
-            }
-        }
-        __syncthreads();
-        if (ks > 0)
-            return;
-        float m_all = m_run;
-#pragma unroll
-        for (int j = 1; j < NSPLIT; j++)
-            m_all = fmaxf(m_all, mb[((j - 1) * MHA_BM + qrow) * MS + DHP]);
-        const float a0 = fast_exp2(m_run - m_all);
-        l_tot *= a0;
-        if (WRITE_O)
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-                oacc[dt] = oacc[dt] * a0;
-#pragma unroll
-        for (int j = 1; j < NSPLIT; j++) {
-            const float* rec = mb + ((j - 1) * MHA_BM + qrow) * MS;
-            const float aj = fast_exp2(rec[DHP] - m_all);
-            l_tot += rec[DHP + 1] * aj;
-            if (WRITE_O)
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++)
-                    oacc[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]) * aj;
-        }
-        m_run = m_all;
-    }
-    if (qok) {
-        if (WRITE_O) {
-            const float inv = 1.0f / l_tot;
-            float* orow = O + base + (long)myq * rs;
-#pragma unroll
-            for (int dt = 0; dt < NDT; dt++)
-                store4<VEC>(orow, 16 * dt + 4 * g, Dh, oacc[dt] * inv);
-        }
-        if (lse != nullptr && g == 0)
-            lse[(long)bh * S + myq] = (m_run + fast_log2(l_tot)) * kLn2;
-    }
-}
-
+// Persistent forward kernel.  Job qi*BH + bh is query tile qb = nqb-1-qi of
+// head bh (longest first); a workgroup takes jobs in serpentine order and,
+// once the last key tile of a job has been through its math, requests the
+// next job's Q rows and first two K/V tiles, so that they arrive while the
+// current job merges its key splits and writes O.
 template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
 __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
     float qscale)
 {
-    __shared__ __attribute__((aligned(16))) float smem[FwdSmem<DHP, NSPLIT>::FLOATS];
+    using SM = FwdSmem<DHP, NSPLIT>;
+    constexpr int NT = 256 * NSPLIT;
+    constexpr int KS = SM::KS, MS = SM::MS;
+    constexpr int NDT = DHP / 16;
+    constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
+    __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
+
     const int njobs = nqb * BH;
+    const long rs = (long)H * Dh;
+    struct Job {
+        int bh, qb;
+        long base;
+    };
+    auto job_of = [&](int job) {
+        Job j;
+        const int qi = job / BH;
+        j.bh = job - qi * BH;
+        j.qb = nqb - 1 - qi;
+        const int b = j.bh / H, h = j.bh - b * H;
+        j.base = (long)b * S * rs + (long)h * Dh;
+        return j;
+    };
+
+    // B operand of S^T = K Q^T: lane holds Q[myq][16*dt + 4*g + r], pre-scaled
+    // by scale*log2(e) so scores land in the exp2 domain; zero past Dh.  The
+    // rows are loaded raw (clamped) and masked and scaled at the start of the
+    // job, so that the loads stay in flight with the K/V loads.
+    f4 qreg[NDT];
+    // Narrow heads (DB) run a four-deep pipeline: two register stages, loaded
+    // from global memory three tiles ahead of use, feed two LDS buffers; tile
+    // kb+1 is written to LDS while tile kb is consumed, one barrier per tile.
+    // Wider heads use one LDS buffer (two barriers per tile) and one register
+    // stage (none for the widest).
+    TileRegs<DHP, MHA_BN, NT, VEC> kr, vr, kr1, vr1;
+    auto load_kv = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
+                       const Job& j, int kb) {
+        const int tid = job_tid();
+        kx.load(K, j.base, rs, kb * MHA_BN, S, Dh, tid);
+        if (WRITE_O)
+            vx.load(V, j.base, rs, kb * MHA_BN, S, Dh, tid);
+    };
+    // A job's first loads: Q rows and key tiles 0 and 1.  Loads past the last
+    // key tile repeat it (clamped tile index), so these memory operations are
+    // the same on every path and the compiler's waits for them stay tight.
+    auto load_first = [&](const Job& j) {
+        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int l16 = lane & 15, g = lane >> 4, qg = wave & 3;
+        const int q = min(j.qb * MHA_BM + qg * 16 + l16, S - 1);
+        const float* qrow = Q + j.base + (long)q * rs;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
+        load_kv(kr, vr, j, 0);
+        if (SM::DB)
+            load_kv(kr1, vr1, j, min(1, j.qb));
+    };
+
+    Job jc = job_of(snake_job(0));   // the grid never exceeds the job count
+    load_first(jc);
 #pragma nounroll
     for (int r = 0;; r++) {
-        const int job = snake_job(r);
-        if (job >= njobs)
+        const int jn = snake_job(r + 1);
+        const bool more = jn < njobs;
+        const Job jnext = job_of(more ? jn : 0);
+
+        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int l16 = lane & 15, g = lane >> 4;
+        const int qg = wave & 3, ks = wave >> 2;
+        const int qb = jc.qb, bh = jc.bh;
+        const long base = jc.base;
+        const int myq = qb * MHA_BM + qg * 16 + l16;
+        const bool qok = myq < S;
+        const int nkb = qb + 1;   // causal: key tiles 0..qb (MHA_BM == MHA_BN)
+
+        f4 oacc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            oacc[dt] = f4zero();
+        float m_run = -1e30f, l_run = 0.0f;
+        auto store_kv = [&](const TileRegs<DHP, MHA_BN, NT, VEC>& kx,
+                            const TileRegs<DHP, MHA_BN, NT, VEC>& vx, float* buf) {
+            kx.template store<KS>(buf, tid);
+            if (WRITE_O)
+                vx.template store<KS>(buf + MHA_BN * KS, tid);
+        };
+        // One key tile of math on the tiles in LDS (Ks, Vs: [key][d], row stride KS).
+        auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
+            const int k0 = kb * MHA_BN;
+            // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
+            // The NKT key blocks run as interleaved accumulation chains.
+            f4 sacc[NKT];
+    #pragma unroll
+            for (int kk = 0; kk < NKT; kk++)
+                sacc[kk] = f4zero();
+    #pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+    #pragma unroll
+                for (int kk = 0; kk < NKT; kk++) {
+                    const int kt = ks * NKT + kk;
+                    const f4 kv = *reinterpret_cast<const f4*>(&Ks[(16 * kt + l16) * KS + 16 * dt + 4 * g]);
+    #pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        sacc[kk] = mfma16(kv[r], qreg[dt][r], sacc[kk]);
+                }
+            }
+            if (kb == qb) {   // diagonal tile: causal mask key > query
+    #pragma unroll
+                for (int kk = 0; kk < NKT; kk++)
+    #pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (k0 + 16 * (ks * NKT + kk) + 4 * g + r > myq)
+                            sacc[kk][r] = -INFINITY;
+            }
+            float mloc = -INFINITY;
+    #pragma unroll
+            for (int kk = 0; kk < NKT; kk++)
+    #pragma unroll
+                for (int r = 0; r < 4; r++)
+                    mloc = fmaxf(mloc, sacc[kk][r]);
+            mloc = xrow_max(mloc);
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = fast_exp2(m_run - m_new);
+            float psum = 0.0f;
+    #pragma unroll
+            for (int kk = 0; kk < NKT; kk++)
+    #pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = fast_exp2(sacc[kk][r] - m_new);
+                    sacc[kk][r] = p;
+                    psum += p;
+                }
+            l_run = l_run * alpha + psum;
+            m_run = m_new;
+            if (WRITE_O) {
+                // O^T += V^T P^T: A = V^T[d = 16dt + l16][key = 16kt + 4g + r], read
+                // as single floats from the row-major V tile; B = P^T from sacc.
+    #pragma unroll
+                for (int dt = 0; dt < NDT; dt++) {
+                    f4 acc = oacc[dt] * alpha;
+    #pragma unroll
+                    for (int kk = 0; kk < NKT; kk++) {
+                        const int kt = ks * NKT + kk;
+    #pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            acc = mfma16(Vs[(16 * kt + 4 * g + r) * KS + 16 * dt + l16], sacc[kk][r], acc);
+                    }
+                    oacc[dt] = acc;
+                }
+            }
+        };
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
+        if constexpr (SM::DB) {
+            store_kv(kr, vr, smem);
+            __builtin_amdgcn_sched_barrier(0);
+            load_kv(kr, vr, jc, min(2, nkb - 1));
+            __syncthreads();
+            // Iteration kb < nkb-1: registers (kx, vx) hold tile kb+1; they go
+            // to LDS buffer (kb+1)&1 and are refilled with tile kb+3.
+            auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx,
+                            TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) {
+                const float* cur = smem + (kb & 1) * SM::TILES;
+                store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
+                // Keep the refill below the LDS writes: issued earlier, the
+                // wait for the old data would include the new loads.
+                __builtin_amdgcn_sched_barrier(0);
+                if (kb + 3 < nkb)
+                    load_kv(kx, vx, jc, kb + 3);
+                tile_math(cur, cur + MHA_BN * KS, kb);
+                __syncthreads();
+            };
+            int kb = 0;
+            for (; kb + 2 < nkb; kb += 2) {
+                step(kr1, vr1, kb);
+                step(kr, vr, kb + 1);
+            }
+            if (kb + 1 < nkb)
+                step(kr1, vr1, kb++);
+            // The last key tile; then the next job's first loads (all register
+            // stages are free by then).
+            const float* cur = smem + (kb & 1) * SM::TILES;
+            tile_math(cur, cur + MHA_BN * KS, kb);
+            __builtin_amdgcn_sched_barrier(0);   // not above the math: it reads qreg
+            if (more)
+                load_first(jnext);
+            __syncthreads();
+        } else {
+            constexpr bool PREFETCH = DHP <= 128;
+            for (int kb = 0; kb < nkb; kb++) {
+                if (!PREFETCH && kb > 0)
+                    load_kv(kr, vr, jc, kb);
+                __syncthreads();
+                store_kv(kr, vr, smem);
+                __syncthreads();
+                if (PREFETCH && kb + 1 < nkb)
+                    load_kv(kr, vr, jc, kb + 1);
+                tile_math(smem, smem + MHA_BN * KS, kb);
+                if (kb + 1 == nkb && more) {   // next job's first loads, as above
+                    __builtin_amdgcn_sched_barrier(0);
+                    load_first(jnext);
+                }
+            }
+        }
+        float l_tot = xrow_sum(l_run);
+
+        if (NSPLIT > 1) {
+            // Merge the key splits: split ks > 0 publishes (o, m, l) per query row,
+            // split 0 rescales everything to the common maximum.
+            float* mb = smem;
+            __syncthreads();   // every wave is done with the K/V tiles
+            const int qrow = qg * 16 + l16;
+            if (ks > 0) {
+                float* rec = mb + ((ks - 1) * MHA_BM + qrow) * MS;
+                if (WRITE_O)
+    #pragma unroll
+                    for (int dt = 0; dt < NDT; dt++)
+                        *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = oacc[dt];
+                if (g == 0) {
+                    rec[DHP] = m_run;
+                    rec[DHP + 1] = l_tot;
+                }
+            }
+            __syncthreads();
+            if (ks == 0) {
+            float m_all = m_run;
+    #pragma unroll
+            for (int j = 1; j < NSPLIT; j++)
+                m_all = fmaxf(m_all, mb[((j - 1) * MHA_BM + qrow) * MS + DHP]);
+            const float a0 = fast_exp2(m_run - m_all);
+            l_tot *= a0;
+            if (WRITE_O)
+    #pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+                    oacc[dt] = oacc[dt] * a0;
+    #pragma unroll
+            for (int j = 1; j < NSPLIT; j++) {
+                const float* rec = mb + ((j - 1) * MHA_BM + qrow) * MS;
+                const float aj = fast_exp2(rec[DHP] - m_all);
+                l_tot += rec[DHP + 1] * aj;
+                if (WRITE_O)
+    #pragma unroll
+                    for (int dt = 0; dt < NDT; dt++)
+                        oacc[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]) * aj;
+            }
+            m_run = m_all;
+            }
+        }
+        if (ks == 0 && qok) {
+            if (WRITE_O) {
+                const float inv = 1.0f / l_tot;
+                float* orow = O + base + (long)myq * rs;
+    #pragma unroll
+                for (int dt = 0; dt < NDT; dt++)
+                    store4<VEC>(orow, 16 * dt + 4 * g, Dh, oacc[dt] * inv);
+            }
+            if (lse != nullptr && g == 0)
+                lse[(long)bh * S + myq] = (m_run + fast_log2(l_tot)) * kLn2;
+        }
+        if (!more)
             break;
-        if (r > 0)
-            __syncthreads();   // the previous job's last LDS reads are done
-        mha_fwd_job<DHP, NSPLIT, VEC, WRITE_O>(Q, K, V, O, lse, S, H, Dh, BH, nqb, qscale, job,
-                                                smem);
+        jc = jnext;
+        __syncthreads();   // the merge records are consumed
     }
 }
 
@@ -829,12 +854,20 @@ static int device_cus()
     return cached[dev];
 }
 
-// Persistent grid size: `per_cu` resident workgroups per compute unit, never
-// more workgroups than jobs.
-static unsigned persistent_grid(long njobs, int per_cu)
+// Grid size for the job-loop kernels: a persistent grid (`per_cu` resident
+// workgroups per compute unit) with serpentine job order, or one workgroup
+// per job under the hardware's dynamic dispatch.  The serpentine order
+// balances heavy-first triangular job lists over pairs of rounds (two rounds
+// sum to nearly the same work on every workgroup), so it is used for up to
+// two rounds, and, where `even_rounds` allows, for any even number of rounds.
+// Persistent workgroups also prefetch their next job.
+static unsigned job_grid(long njobs, int per_cu, bool even_rounds)
 {
     const long g = (long)device_cus() * per_cu;
-    return (unsigned)(njobs < g ? njobs : g);
+    const long rounds = (njobs + g - 1) / g;
+    if (rounds <= 2 || (even_rounds && rounds % 2 == 0))
+        return (unsigned)(njobs < g ? njobs : g);
+    return (unsigned)njobs;
 }
 
 // Wave groups per workgroup: two per SIMD wherever registers allow.
@@ -843,7 +876,7 @@ struct MhaSplits {
     static constexpr int FWD = DHP <= 128 ? 2 : 1;
     static constexpr int BWD = DHP <= 64 ? 2 : 1;
     static constexpr int BWD_BM = DHP <= 128 ? 64 : 32;
-    // Resident workgroups per CU for the persistent grids.
+    // Resident workgroups per CU assumed for the persistent grids.
     static constexpr int FWD_PER_CU = 1;
     static constexpr int BWD_PER_CU = 1;
 };
@@ -856,7 +889,7 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     const int BH = B * H;
     const int nqb = (S + MHA_BM - 1) / MHA_BM;
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid(persistent_grid((long)nqb * BH, MhaSplits<DHP>::FWD_PER_CU)), block(256 * NS);
+    dim3 grid(job_grid((long)nqb * BH, MhaSplits<DHP>::FWD_PER_CU, false)), block(256 * NS);
     if (O != nullptr) {
         ProfScope ps(st, "mha_fwd");
         hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true>), grid, block, 0, st, Q, K, V, O,
@@ -919,7 +952,7 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
     const int BH = B * H;
     const int nkb = (S + MHA_BN - 1) / MHA_BN;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid(persistent_grid((long)nkb * BH, MhaSplits<DHP>::BWD_PER_CU)), block(256 * NS);
+    dim3 grid(job_grid((long)nkb * BH, MhaSplits<DHP>::BWD_PER_CU, true)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, "mha_bwd");
