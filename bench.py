@@ -20,6 +20,7 @@ them can be made the reported workload with --workload NAME):
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
+  copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
 resident in HBM before timing starts.  Timing: W warmup steps, then K steps
@@ -279,7 +280,33 @@ def _hexp(c, name, Bq, S, seed, steps, warmup):
                 frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
 
+def _copy(c, steps, warmup):
+    """Calibration workload: a plain device-to-device copy of a 256 MiB fp32
+    tensor (torch's copy kernel).  Its rocprofv3 FETCH_SIZE / WRITE_SIZE
+    readings against the known 256 MiB read + 256 MiB write give the scale
+    factor for the counters of the attention kernels (profiles/)."""
+    n = 64 << 20
+    src, dst = c.empty(n), c.empty(n)
+    src.fill_(1.0)
+
+    def step():
+        dst.copy_(src)
+    ms = timed(step, steps, warmup, c.stream)
+    nbytes = 2 * n * 4
+    value = nbytes / (ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": "copy", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4), "traffic": nbytes,
+            "bytes_per_launch": nbytes}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": "copy: 256 MiB fp32 device-to-device copy (HBM "
+                                    "calibration, not an attention workload)",
+                        "bytes_per_step": nbytes},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=None)
+
+
 def run_workload(c, name, steps, warmup):
+    if name == "copy":
+        return _copy(c, steps, warmup)
     if name == "c2":
         return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
     if name == "c2legacy":
@@ -346,7 +373,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5"])
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
