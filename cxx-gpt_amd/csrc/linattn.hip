@@ -124,6 +124,49 @@ __device__ __forceinline__ void putR(float* __restrict__ buf, const f4 (&v)[4], 
         *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]) = v[ct];
 }
 
+// The same for a part of a chunk: column tiles ct0 .. ct0+NCT-1.  The waves
+// of a segment stage the chunk's inputs by column tiles, so each wave loads
+// and transforms (phi) an equal share.
+template <bool VEC, int NCT>
+__device__ __forceinline__ void ldRp(f4 (&v)[NCT], const float* __restrict__ base, int ld, int ro,
+                                     int ncol, int g, int ct0)
+{
+    const float* p = base + ro * ld;
+#pragma unroll
+    for (int i = 0; i < NCT; i++)
+        v[i] = load4c<VEC>(p, 16 * (ct0 + i) + 4 * g, ncol);
+}
+
+template <int PHI, bool APPLY, bool FW, int NCT>
+__device__ __forceinline__ void finRp(f4 (&v)[NCT], bool full, bool rok, int ncol, int g, int ct0)
+{
+    if (APPLY && PHI != PHI_NONE)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v[i][e] = Phi<PHI>::f(v[i][e]);
+    if (!FW)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v[i][e] = (16 * (ct0 + i) + 4 * g + e < ncol) ? v[i][e] : 0.0f;
+    if (!full)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+            v[i] = rok ? v[i] : f4zero();
+}
+
+template <int NCT>
+__device__ __forceinline__ void putRp(float* __restrict__ buf, const f4 (&v)[NCT], int l16, int g,
+                                      int ct0)
+{
+#pragma unroll
+    for (int i = 0; i < NCT; i++)
+        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * (ct0 + i) + 4 * g]) = v[i];
+}
+
 __device__ __forceinline__ void getR(const float* __restrict__ buf, f4 (&v)[4], int l16, int g)
 {
 #pragma unroll
@@ -197,7 +240,7 @@ constexpr int AGG_THREADS = 128;
 constexpr int AGG_STAGE = 2 * CHUNK + 16;
 
 template <int PHI, bool VEC, bool FW>
-__global__ __launch_bounds__(AGG_THREADS) void lin_agg_kernel(
+__global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void lin_agg_kernel(
     const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ w,
     float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L)
 {
@@ -217,17 +260,15 @@ __global__ __launch_bounds__(AGG_THREADS) void lin_agg_kernel(
             St[a][j] = f4zero();
     float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    f4 na[4];
+    // wave h stages column tiles 2h, 2h+1 of X and Y; wave 0 also w
+    f4 nx[2], ny[2];
     float nw = 1.0f;
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        if (h == 0) {
-            ldR<VEC>(na, X + (rb + t0) * D, D, ro, D, g);
-            if (w != nullptr)
-                nw = w[rb + t0 + ro];
-        } else {
-            ldR<VEC>(na, Y + (rb + t0) * E, E, ro, E, g);
-        }
+        ldRp<VEC, 2>(nx, X + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(ny, Y + (rb + t0) * E, E, ro, E, g, 2 * h);
+        if (h == 0 && w != nullptr)
+            nw = w[rb + t0 + ro];
     };
     fetch(tbeg);
     int c = 0;
@@ -236,23 +277,22 @@ __global__ __launch_bounds__(AGG_THREADS) void lin_agg_kernel(
         float* bX = st;
         float* bY = st + CHUNK;
         float* bw = st + 2 * CHUNK;
-        f4 a[4];
+        f4 ax[2], ay[2];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            a[i] = na[i];
+        for (int i = 0; i < 2; i++) {
+            ax[i] = nx[i];
+            ay[i] = ny[i];
+        }
         const float wv = nw;
         if (t0 + 16 < tend)
             fetch(t0 + 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
-        if (h == 0) {
-            finR<PHI, true, FW>(a, full, rok, D, g);
-            putR(bX, a, l16, g);
-            if (g == 0)
-                bw[l16] = wv;
-        } else {
-            finR<PHI, false, FW>(a, full, rok, E, g);
-            putR(bY, a, l16, g);
-        }
+        finRp<PHI, true, FW, 2>(ax, full, rok, D, g, 2 * h);
+        finRp<PHI, false, FW, 2>(ay, full, rok, E, g, 2 * h);
+        putRp(bX, ax, l16, g, 2 * h);
+        putRp(bY, ay, l16, g, 2 * h);
+        if (h == 0 && g == 0)
+            bw[l16] = wv;
         __syncthreads();
         f4 xC[4], yC[2];
         getC(bX, xC, l16, g);
@@ -306,13 +346,28 @@ __global__ __launch_bounds__(256) void lin_scan_kernel(float* __restrict__ ws, i
     if (j >= (long)Bq * LIN_WS)
         return;
     const long seq = j / LIN_WS, e = j - seq * LIN_WS;
+    // Batches of SB segments: all loads of a batch are issued before its
+    // stores, so the loop costs one memory round trip per batch rather than
+    // one per segment.
+    constexpr int SB = 8;
     float run = 0.0f;
-    for (int k = 0; k < nseg; k++) {
-        const int s = reverse ? nseg - 1 - k : k;
-        const long idx = (seq * nseg + s) * LIN_WS + e;
-        const float tmp = ws[idx];
-        ws[idx] = run;
-        run += tmp;
+    for (int k0 = 0; k0 < nseg; k0 += SB) {
+        float v[SB];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int k = min(k0 + u, nseg - 1);
+            const int s = reverse ? nseg - 1 - k : k;
+            v[u] = ws[(seq * nseg + s) * LIN_WS + e];
+        }
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            if (k0 + u < nseg) {
+                const int k = k0 + u;
+                const int s = reverse ? nseg - 1 - k : k;
+                ws[(seq * nseg + s) * LIN_WS + e] = run;
+                run += v[u];
+            }
+        }
     }
 }
 
@@ -324,7 +379,7 @@ constexpr int FWD_THREADS = 128;
 constexpr int FWD_STAGE = 3 * CHUNK;   // phi(Q), phi(K), V
 
 template <int PHI, bool VEC, bool FW>
-__global__ __launch_bounds__(FWD_THREADS) void lin_fwd_kernel(
+__global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void lin_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zcache,
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
@@ -366,19 +421,13 @@ __global__ __launch_bounds__(FWD_THREADS) void lin_fwd_kernel(
         }
     }
 
-    // wave 0 fetches Q and K rows, wave 1 V rows
-    f4 na[4], nb[4];
+    // wave h stages column tiles 2h, 2h+1 of Q, K and V
+    f4 nq[2], nk[2], nv[2];
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        if (h == 0) {
-            ldR<VEC>(na, Q + (rb + t0) * D, D, ro, D, g);
-            ldR<VEC>(nb, K + (rb + t0) * D, D, ro, D, g);
-        } else {
-            ldR<VEC>(na, V + (rb + t0) * E, E, ro, E, g);
-#pragma unroll
-            for (int i = 0; i < 4; i++)   // keeps nb defined on both paths (no stack copy)
-                nb[i] = na[i];
-        }
+        ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(nv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
     };
     fetch(tbeg);
     int c = 0;
@@ -387,24 +436,22 @@ __global__ __launch_bounds__(FWD_THREADS) void lin_fwd_kernel(
         float* bQ = st;
         float* bK = st + CHUNK;
         float* bV = st + 2 * CHUNK;
-        f4 a[4], b[4];
+        f4 aq[2], ak[2], av[2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            a[i] = na[i];
-            b[i] = nb[i];
+        for (int i = 0; i < 2; i++) {
+            aq[i] = nq[i];
+            ak[i] = nk[i];
+            av[i] = nv[i];
         }
         if (t0 + 16 < tend)   // next chunk's rows, in flight during this chunk
             fetch(t0 + 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
-        if (h == 0) {
-            finR<PHI, true, FW>(a, full, rok, D, g);
-            finR<PHI, true, FW>(b, full, rok, D, g);
-            putR(bQ, a, l16, g);
-            putR(bK, b, l16, g);
-        } else {
-            finR<PHI, false, FW>(a, full, rok, E, g);
-            putR(bV, a, l16, g);
-        }
+        finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
+        finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
+        finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
+        putRp(bQ, aq, l16, g, 2 * h);
+        putRp(bK, ak, l16, g, 2 * h);
+        putRp(bV, av, l16, g, 2 * h);
         __syncthreads();
         f4 q[4], k[4];
         getR(bQ, q, l16, g);
@@ -557,7 +604,7 @@ constexpr int DQ_THREADS = 128;
 constexpr int DQ_STAGE = 5 * CHUNK + 16;   // phi(K), V, dnum, z_cache, Q rows + dden rows
 
 template <int PHI, bool VEC, bool FW>
-__global__ __launch_bounds__(DQ_THREADS) void lin_dq_kernel(
+__global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void lin_dq_kernel(
     const float* __restrict__ K, const float* __restrict__ V, const float* __restrict__ dnum,
     const float* __restrict__ dden, const float* __restrict__ zcache, const float* __restrict__ Q,
     float* __restrict__ dQ, const float* __restrict__ ws, int Bq, int S, int D, int E, int nseg,
@@ -590,21 +637,20 @@ __global__ __launch_bounds__(DQ_THREADS) void lin_dq_kernel(
                 StT[et][j] = f4zero();
     }
 
-    // wave 0 fetches K, V rows and dden, wave 1 dnum, z_cache and Q rows
-    f4 na[4], nb[4], nc[4];
+    // wave h stages column tiles 2h, 2h+1 of K, V, dnum, z_cache and Q; wave 0
+    // also dden
+    f4 nk[2], nv[2], nn[2], nz[2], nq[2];
     float ndd = 0.0f;
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        if (h == 0) {
-            ldR<VEC>(na, K + (rb + t0) * D, D, ro, D, g);
-            ldR<VEC>(nb, V + (rb + t0) * E, E, ro, E, g);
+        ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(nv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
+        ldRp<VEC, 2>(nn, dnum + (rb + t0) * E, E, ro, E, g, 2 * h);
+        ldRp<VEC, 2>(nz, zcache + (rb + t0) * D, D, ro, D, g, 2 * h);
+        if (HAS_Q)
+            ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+        if (h == 0)
             ndd = dden[rb + t0 + ro];
-        } else {
-            ldR<VEC>(na, dnum + (rb + t0) * E, E, ro, E, g);
-            ldR<VEC>(nb, zcache + (rb + t0) * D, D, ro, D, g);
-            if (HAS_Q)
-                ldR<VEC>(nc, Q + (rb + t0) * D, D, ro, D, g);
-        }
     };
     fetch(tbeg);
     int c = 0;
@@ -616,31 +662,30 @@ __global__ __launch_bounds__(DQ_THREADS) void lin_dq_kernel(
         float* bZc = st + 3 * CHUNK;
         float* bQ = st + 4 * CHUNK;
         float* bd = st + 5 * CHUNK;
-        f4 a[4], b[4], cc[4];
+        f4 ak[2], av[2], an[2], az[2], aq[2];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            a[i] = na[i];
-            b[i] = nb[i];
-            cc[i] = HAS_Q ? nc[i] : f4zero();
+        for (int i = 0; i < 2; i++) {
+            ak[i] = nk[i];
+            av[i] = nv[i];
+            an[i] = nn[i];
+            az[i] = nz[i];
+            aq[i] = HAS_Q ? nq[i] : f4zero();
         }
         const float dd = ndd;
         if (t0 + 16 < tend)
             fetch(t0 + 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
-        if (h == 0) {
-            finR<PHI, true, FW>(a, full, rok, D, g);
-            finR<PHI, false, FW>(b, full, rok, E, g);
-            putR(bK, a, l16, g);
-            putR(bV, b, l16, g);
-            if (g == 0)
-                bd[l16] = dd;
-        } else {
-            finR<PHI, false, FW>(a, full, rok, E, g);
-            putR(bN, a, l16, g);
-            putR(bZc, b, l16, g);   // only rows that are stored get used
-            if (HAS_Q)
-                putR(bQ, cc, l16, g);
-        }
+        finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
+        finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
+        finRp<PHI, false, FW, 2>(an, full, rok, E, g, 2 * h);
+        putRp(bK, ak, l16, g, 2 * h);
+        putRp(bV, av, l16, g, 2 * h);
+        putRp(bN, an, l16, g, 2 * h);
+        putRp(bZc, az, l16, g, 2 * h);   // only rows that are stored get used
+        if (HAS_Q)
+            putRp(bQ, aq, l16, g, 2 * h);
+        if (h == 0 && g == 0)
+            bd[l16] = dd;
         __syncthreads();
         f4 v[4], dn[4];
         getR(bV, v, l16, g);
@@ -714,7 +759,7 @@ constexpr int DKDV_THREADS = 256;
 constexpr int DKDV_STAGE = 4 * CHUNK + 16;   // phi(Q), phi(K), V, dnum chunks + dden rows
 
 template <int PHI, bool VEC, bool FW>
-__global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
+__global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void lin_dkdv_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dnum, const float* __restrict__ dden, float* __restrict__ dK,
     float* __restrict__ dV, const float* __restrict__ ws, int Bq, int S, int D, int E, int nseg,
@@ -757,14 +802,15 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
                                            : f4zero();
     }
 
-    // wave 0 fetches Q rows, wave 1 K, wave 2 V, wave 3 dnum (+ dden)
-    const float* src = w == 0 ? Q : (w == 1 ? K : (w == 2 ? V : dnum));
-    const int sld = w < 2 ? D : E;
-    f4 na[4];
+    // wave w stages column tile w of Q, K, V and dnum; wave 3 also dden
+    f4 nq[1], nk[1], nv[1], nn[1];
     float ndd = 0.0f;
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        ldR<VEC>(na, src + (rb + t0) * sld, sld, ro, sld, g);
+        ldRp<VEC, 1>(nq, Q + (rb + t0) * D, D, ro, D, g, w);
+        ldRp<VEC, 1>(nk, K + (rb + t0) * D, D, ro, D, g, w);
+        ldRp<VEC, 1>(nv, V + (rb + t0) * E, E, ro, E, g, w);
+        ldRp<VEC, 1>(nn, dnum + (rb + t0) * E, E, ro, E, g, w);
         if (w == 3)
             ndd = dden[rb + t0 + ro];
     };
@@ -778,19 +824,19 @@ __global__ __launch_bounds__(DKDV_THREADS) void lin_dkdv_kernel(
         float* bV = st + 2 * CHUNK;
         float* bN = st + 3 * CHUNK;
         float* bd = st + 4 * CHUNK;
-        f4 a[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            a[i] = na[i];
+        f4 aq[1] = {nq[0]}, ak[1] = {nk[0]}, av[1] = {nv[0]}, an[1] = {nn[0]};
         const float dd = ndd;
         if (c > 0)
             fetch(t0 - 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
-        if (w < 2)
-            finR<PHI, true, FW>(a, full, rok, D, g);
-        else
-            finR<PHI, false, FW>(a, full, rok, E, g);
-        putR(st + w * CHUNK, a, l16, g);
+        finRp<PHI, true, FW, 1>(aq, full, rok, D, g, w);
+        finRp<PHI, true, FW, 1>(ak, full, rok, D, g, w);
+        finRp<PHI, false, FW, 1>(av, full, rok, E, g, w);
+        finRp<PHI, false, FW, 1>(an, full, rok, E, g, w);
+        putRp(bQ, aq, l16, g, w);
+        putRp(bK, ak, l16, g, w);
+        putRp(bV, av, l16, g, w);
+        putRp(bN, an, l16, g, w);
         if (w == 3 && g == 0)
             bd[l16] = rok ? dd : 0.0f;
         __syncthreads();
