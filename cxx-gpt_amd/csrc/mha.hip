@@ -227,41 +227,41 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
             // The NKT key blocks run as interleaved accumulation chains.
             f4 sacc[NKT];
-    #pragma unroll
+#pragma unroll
             for (int kk = 0; kk < NKT; kk++)
                 sacc[kk] = f4zero();
-    #pragma unroll
+#pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
-    #pragma unroll
+#pragma unroll
                 for (int kk = 0; kk < NKT; kk++) {
                     const int kt = ks * NKT + kk;
                     const f4 kv = *reinterpret_cast<const f4*>(&Ks[(16 * kt + l16) * KS + 16 * dt + 4 * g]);
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 4; r++)
                         sacc[kk] = mfma16(kv[r], qreg[dt][r], sacc[kk]);
                 }
             }
             if (kb == qb) {   // diagonal tile: causal mask key > query
-    #pragma unroll
+#pragma unroll
                 for (int kk = 0; kk < NKT; kk++)
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 4; r++)
                         if (k0 + 16 * (ks * NKT + kk) + 4 * g + r > myq)
                             sacc[kk][r] = -INFINITY;
             }
             float mloc = -INFINITY;
-    #pragma unroll
+#pragma unroll
             for (int kk = 0; kk < NKT; kk++)
-    #pragma unroll
+#pragma unroll
                 for (int r = 0; r < 4; r++)
                     mloc = fmaxf(mloc, sacc[kk][r]);
             mloc = xrow_max(mloc);
             const float m_new = fmaxf(m_run, mloc);
             const float alpha = fast_exp2(m_run - m_new);
             float psum = 0.0f;
-    #pragma unroll
+#pragma unroll
             for (int kk = 0; kk < NKT; kk++)
-    #pragma unroll
+#pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float p = fast_exp2(sacc[kk][r] - m_new);
                     sacc[kk][r] = p;
@@ -272,13 +272,13 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             if (WRITE_O) {
                 // O^T += V^T P^T: A = V^T[d = 16dt + l16][key = 16kt + 4g + r], read
                 // as single floats from the row-major V tile; B = P^T from sacc.
-    #pragma unroll
+#pragma unroll
                 for (int dt = 0; dt < NDT; dt++) {
                     f4 acc = oacc[dt] * alpha;
-    #pragma unroll
+#pragma unroll
                     for (int kk = 0; kk < NKT; kk++) {
                         const int kt = ks * NKT + kk;
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; r++)
                             acc = mfma16(Vs[(16 * kt + 4 * g + r) * KS + 16 * dt + l16], sacc[kk][r], acc);
                     }
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             if (ks > 0) {
                 float* rec = mb + ((ks - 1) * MHA_BM + qrow) * MS;
                 if (WRITE_O)
-    #pragma unroll
+#pragma unroll
                     for (int dt = 0; dt < NDT; dt++)
                         *reinterpret_cast<f4*>(&rec[16 * dt + 4 * g]) = oacc[dt];
                 if (g == 0) {
@@ -362,22 +362,22 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             __syncthreads();
             if (ks == 0) {
             float m_all = m_run;
-    #pragma unroll
+#pragma unroll
             for (int j = 1; j < NSPLIT; j++)
                 m_all = fmaxf(m_all, mb[((j - 1) * MHA_BM + qrow) * MS + DHP]);
             const float a0 = fast_exp2(m_run - m_all);
             l_tot *= a0;
             if (WRITE_O)
-    #pragma unroll
+#pragma unroll
                 for (int dt = 0; dt < NDT; dt++)
                     oacc[dt] = oacc[dt] * a0;
-    #pragma unroll
+#pragma unroll
             for (int j = 1; j < NSPLIT; j++) {
                 const float* rec = mb + ((j - 1) * MHA_BM + qrow) * MS;
                 const float aj = fast_exp2(rec[DHP] - m_all);
                 l_tot += rec[DHP + 1] * aj;
                 if (WRITE_O)
-    #pragma unroll
+#pragma unroll
                     for (int dt = 0; dt < NDT; dt++)
                         oacc[dt] += *reinterpret_cast<const f4*>(&rec[16 * dt + 4 * g]) * aj;
             }
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             if (WRITE_O) {
                 const float inv = 1.0f / l_tot;
                 float* orow = O + base + (long)myq * rs;
-    #pragma unroll
+#pragma unroll
                 for (int dt = 0; dt < NDT; dt++)
                     store4<VEC>(orow, 16 * dt + 4 * g, Dh, oacc[dt] * inv);
             }
@@ -574,6 +574,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // l16, queries 16qt + 4g + r); dS goes to LDS for the dQ product, then
         // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.
         auto key_side = [&](float* st, int q0) {
+            // Raised issue priority for this MFMA-dense section: the other
+            // wave of the SIMD fills its stalls instead of interleaving.
+            __builtin_amdgcn_s_setprio(1);
             const float* Qs = st;
             const float* dOs = st + BM * QS;
             float* dSs = st + 2 * BM * QS;
@@ -584,32 +587,32 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             // chains interleave on the MFMA pipe.
             constexpr int QI = NQW <= 2 ? NQW : 1;
             f4 P[NQW], dS[NQW];
-    #pragma unroll
+#pragma unroll
             for (int q1 = 0; q1 < NQW; q1 += QI) {
                 f4 sa[QI], da[QI];
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < QI; j++)
                     sa[j] = da[j] = f4zero();
-    #pragma unroll
+#pragma unroll
                 for (int dt = 0; dt < NDT; dt++) {
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < QI; j++) {
                         const int qt = qs * NQW + q1 + j;
                         const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
                         const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; r++) {
                             sa[j] = mfma16(qa[r], kreg[dt][r], sa[j]);
                             da[j] = mfma16(oa[r], vreg[dt][r], da[j]);
                         }
                     }
                 }
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < QI; j++) {
                     const int qq = q1 + j, qt = qs * NQW + qq;
                     const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
                     const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int q = q0 + 16 * qt + 4 * g + r;
                         const bool ok = (!diag || mykey <= q) && q < S;
@@ -620,13 +623,13 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     }
                 }
             }
-    #pragma unroll
+#pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
                 f4 av = dv[dt], ak = dk[dt];
-    #pragma unroll
+#pragma unroll
                 for (int qq = 0; qq < NQW; qq++) {
                     const int qt = qs * NQW + qq;
-    #pragma unroll
+#pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int row = (16 * qt + 4 * g + r) * QS + 16 * dt + l16;
                         av = mfma16(dOs[row], P[qq][r], av);
@@ -636,6 +639,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 dv[dt] = av;
                 dk[dt] = ak;
             }
+            __builtin_amdgcn_s_setprio(0);
         };
         // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
         // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
@@ -646,7 +650,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
         auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
             const int d = 16 * dt + l16;
-    #pragma unroll
+#pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int q = q0 + 16 * qt + 4 * g + r;
                 if (q < S && d < Dh)
@@ -658,18 +662,18 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             const int qt = wave % NQT;
             const float* arow = dSs + (16 * qt + l16) * TS + 4 * g;
             if constexpr (NJ % 2 == 0) {
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < NJ; i += 2) {
                     const int dt0 = (wave + i * NW) / NQT, dt1 = (wave + (i + 1) * NW) / NQT;
                     const float* b0 = Kt + (16 * dt0 + l16) * TS + 4 * g;
                     const float* b1 = Kt + (16 * dt1 + l16) * TS + 4 * g;
                     f4 acc0 = f4zero(), acc1 = f4zero();
-    #pragma unroll
+#pragma unroll
                     for (int kt = 0; kt < 4; kt++) {
                         const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
                         const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
                         const f4 v = *reinterpret_cast<const f4*>(b1 + 16 * kt);
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; r++) {
                             acc0 = mfma16(a[r], u[r], acc0);
                             acc1 = mfma16(a[r], v[r], acc1);
@@ -683,11 +687,11 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     const int dt = jq / NQT;
                     const float* b0 = Kt + (16 * dt + l16) * TS + 4 * g;
                     f4 acc = f4zero();
-    #pragma unroll
+#pragma unroll
                     for (int kt = 0; kt < 4; kt++) {
                         const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
                         const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
-    #pragma unroll
+#pragma unroll
                         for (int r = 0; r < 4; r++)
                             acc = mfma16(a[r], u[r], acc);
                     }
