@@ -1210,12 +1210,16 @@ LinPlan lin_plan(int Bq, int S, int D, int E)
     p.L = S;
     if (p.fast) {
         const int nchunk = (S + 15) / 16;
-        // enough waves to cover the chip a few times, segments of >= 1 chunk
-        int want = (2048 + Bq - 1) / Bq;
+        // Segments per sequence (measured on MI355X at B' = 96): long
+        // sequences want ~2048 segment workgroups in all (two rounds of
+        // resident workgroups), shorter ones (<= 64 chunks) ~768 (one round,
+        // shorter agg/scan passes); at least two chunks per segment.
+        const int target = nchunk > 64 ? 2048 : 768;
+        int want = (target + Bq - 1) / Bq;
+        if (want > nchunk / 2)
+            want = nchunk / 2;
         if (want < 1)
             want = 1;
-        if (want > nchunk)
-            want = nchunk;
         const int cps = (nchunk + want - 1) / want;   // chunks per segment
         p.L = 16 * cps;
         p.nseg = (S + p.L - 1) / p.L;
