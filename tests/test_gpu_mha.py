@@ -126,6 +126,31 @@ def test_ragged_shapes(dev, B, S, H, Dh):
     assert_close(dV, rV, "dV")
 
 
+@pytest.mark.parametrize("B,S,H,Dh", [
+    (4, 200, 20, 32),    # 320 jobs: two persistent rounds, next-job prefetch
+    (2, 300, 40, 128),   # 400 jobs: two rounds at the 128 head width
+    (2, 129, 70, 256),   # 420 jobs: two rounds at 256 (one wave group backward)
+    (5, 130, 50, 16),    # 750 jobs: three rounds, one workgroup per job
+    (3, 130, 100, 7),    # 900 jobs, scalar loads: four rounds (persistent backward)
+    (2, 520, 30, 64),    # 540 jobs: three rounds at 64 with a ragged last tile
+])
+def test_multi_round_jobs(dev, B, S, H, Dh):
+    """Job counts beyond one workgroup per compute unit: persistent grids that
+    carry a workgroup through several (query or key) tiles of different heads
+    with the next job prefetched, and the one-workgroup-per-job grids used for
+    odd round counts.  Every head is checked against the oracle."""
+    Q, K, V, dO = normal_inputs((B * S, H * Dh), (B * S, H * Dh), 11 * S + Dh)
+    O, lse = _run_fwd(dev, Q, K, V, B, S, H, Dh, want_lse=True)
+    rO, rlse = orc.mha_fwd(Q, K, V, B, S, H, Dh, nthreads=8, want_lse=True)
+    assert_close(O, rO, "fwd")
+    assert_close(lse, rlse, "lse")
+    rQ, rK, rV = orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=8)
+    dQ, dK, dV = _run_bwd(dev, Q, K, V, O, dO, B, S, H, Dh, lse=lse)
+    assert_close(dQ, rQ, "dQ")
+    assert_close(dK, rK, "dK")
+    assert_close(dV, rV, "dV")
+
+
 def test_causality_and_first_row(dev):
     """Permuting future keys/values leaves earlier outputs bit-identical;
     row 0 equals V row 0 exactly."""
