@@ -14,9 +14,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace cxg {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Compile-time integer argument for generic lambdas (a lambda body
+// instantiated once per value).
+template <int N>
+using ic = std::integral_constant<int, N>;
 
 __device__ __forceinline__ f4 mfma16(float a, float b, f4 c)
 {

@@ -26,9 +26,13 @@
 //             accumulates partial dK^T/dV^T in registers (summed over the
 //             splits through LDS at the end) and adds dQ = dS K into the
 //             zero-initialised dQ with float atomics.
-// The flat grid index is (tile * B*H + bh): heavy causal tiles dispatch first,
-// and when B*H is a multiple of 8 all tiles of a head share an XCD (and its
-// L2), since workgroups are dealt to the 8 XCDs round-robin.
+// In both, the second split numbers its 16-row groups in reverse (waves w and
+// w+4 share a SIMD), and 16x16 blocks that lie wholly above the causal
+// diagonal are skipped, so a diagonal tile costs each SIMD at most 3 of the 4
+// block-columns of work a full tile does.
+// Jobs are numbered (tile * B*H + bh): heavy causal tiles first, and when B*H
+// is a multiple of 8 all tiles of a head share an XCD (and its L2), since
+// workgroups are dealt to the 8 XCDs round-robin.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -115,6 +119,24 @@ __device__ __forceinline__ int snake_job(int r)
     return r * G + ((r & 1) ? G - 1 - w : w);
 }
 
+// Row (or key) group of wave `wave` in a workgroup of 4 or 8 waves.  The
+// waves of a workgroup are dealt to the compute unit's four SIMDs
+// round-robin, so waves w and w+4 share a SIMD; the second four take the
+// 16-row groups in reverse order, so that in a tile on the causal diagonal,
+// where a group's share of unmasked blocks grows with its index, the SIMDs
+// get nearly equal work (3, 3, 2, 2 of the 10 unmasked 16x16 blocks).
+__device__ __forceinline__ int pair_group(int wave)
+{
+    return (wave & 4) ? 3 - (wave & 3) : (wave & 3);
+}
+
+// Wave index as a scalar (wave-uniform) value, so that branches on it are
+// uniform branches.
+__device__ __forceinline__ int wave_id(int tid)
+{
+    return __builtin_amdgcn_readfirstlane(tid >> 6);
+}
+
 // threadIdx.x, re-read per job behind an empty asm so that the compiler does
 // not hoist the job body's thread-dependent address arithmetic out of the job
 // loop (holding it across jobs costs registers).
@@ -181,8 +203,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
     // key tile repeat it (clamped tile index), so these memory operations are
     // the same on every path and the compiler's waits for them stay tight.
     auto load_first = [&](const Job& j) {
-        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
-        const int l16 = lane & 15, g = lane >> 4, qg = wave & 3;
+        const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
+        const int l16 = lane & 15, g = lane >> 4, qg = pair_group(wave);
         const int q = min(j.qb * MHA_BM + qg * 16 + l16, S - 1);
         const float* qrow = Q + j.base + (long)q * rs;
 #pragma unroll
@@ -201,9 +223,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
         const bool more = jn < njobs;
         const Job jnext = job_of(more ? jn : 0);
 
-        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4;
-        const int qg = wave & 3, ks = wave >> 2;
+        const int qg = pair_group(wave), ks = wave >> 2;
         const int qb = jc.qb, bh = jc.bh;
         const long base = jc.base;
         const int myq = qb * MHA_BM + qg * 16 + l16;
@@ -221,19 +243,23 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             if (WRITE_O)
                 vx.template store<KS>(buf + MHA_BN * KS, tid);
         };
-        // One key tile of math on the tiles in LDS (Ks, Vs: [key][d], row stride KS).
-        auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
+        // One key tile of math on the tiles in LDS (Ks, Vs: [key][d], row stride
+        // KS), over the first NA of the wave's NKT key blocks (the others lie
+        // wholly above the causal diagonal).
+        auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb,
+                             auto na) {
+            constexpr int NA = decltype(na)::value;
             const int k0 = kb * MHA_BN;
             // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
-            // The NKT key blocks run as interleaved accumulation chains.
-            f4 sacc[NKT];
+            // The NA key blocks run as interleaved accumulation chains.
+            f4 sacc[NA];
 #pragma unroll
-            for (int kk = 0; kk < NKT; kk++)
+            for (int kk = 0; kk < NA; kk++)
                 sacc[kk] = f4zero();
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
-                for (int kk = 0; kk < NKT; kk++) {
+                for (int kk = 0; kk < NA; kk++) {
                     const int kt = ks * NKT + kk;
                     const f4 kv = *reinterpret_cast<const f4*>(&Ks[(16 * kt + l16) * KS + 16 * dt + 4 * g]);
 #pragma unroll
@@ -243,7 +269,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             }
             if (kb == qb) {   // diagonal tile: causal mask key > query
 #pragma unroll
-                for (int kk = 0; kk < NKT; kk++)
+                for (int kk = 0; kk < NA; kk++)
 #pragma unroll
                     for (int r = 0; r < 4; r++)
                         if (k0 + 16 * (ks * NKT + kk) + 4 * g + r > myq)
@@ -251,7 +277,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             }
             float mloc = -INFINITY;
 #pragma unroll
-            for (int kk = 0; kk < NKT; kk++)
+            for (int kk = 0; kk < NA; kk++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     mloc = fmaxf(mloc, sacc[kk][r]);
@@ -260,7 +286,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             const float alpha = fast_exp2(m_run - m_new);
             float psum = 0.0f;
 #pragma unroll
-            for (int kk = 0; kk < NKT; kk++)
+            for (int kk = 0; kk < NA; kk++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float p = fast_exp2(sacc[kk][r] - m_new);
@@ -276,7 +302,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
                 for (int dt = 0; dt < NDT; dt++) {
                     f4 acc = oacc[dt] * alpha;
 #pragma unroll
-                    for (int kk = 0; kk < NKT; kk++) {
+                    for (int kk = 0; kk < NA; kk++) {
                         const int kt = ks * NKT + kk;
 #pragma unroll
                         for (int r = 0; r < 4; r++)
@@ -284,6 +310,22 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
                     }
                     oacc[dt] = acc;
                 }
+            }
+        };
+        // A key tile: off the diagonal every block is live; on it (two key
+        // splits) key block kt = ks*NKT + kk is live for kt <= qg, a prefix of
+        // the wave's blocks, and the rest are skipped (a block of scores that
+        // are all masked leaves the online-softmax state unchanged), down to
+        // the whole tile.
+        auto tile = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
+            if (NSPLIT == 1 || kb != qb) {
+                tile_math(Ks, Vs, kb, ic<NKT>{});
+            } else {
+                const int na = qg - ks * NKT + 1;
+                if (na >= NKT)
+                    tile_math(Ks, Vs, kb, ic<NKT>{});
+                else if (na == 1)
+                    tile_math(Ks, Vs, kb, ic<1>{});
             }
         };
 #pragma unroll
@@ -305,7 +347,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
                 __builtin_amdgcn_sched_barrier(0);
                 if (kb + 3 < nkb)
                     load_kv(kx, vx, jc, kb + 3);
-                tile_math(cur, cur + MHA_BN * KS, kb);
+                tile(cur, cur + MHA_BN * KS, kb);
                 __syncthreads();
             };
             int kb = 0;
@@ -318,7 +360,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             // The last key tile; then the next job's first loads (all register
             // stages are free by then).
             const float* cur = smem + (kb & 1) * SM::TILES;
-            tile_math(cur, cur + MHA_BN * KS, kb);
+            tile(cur, cur + MHA_BN * KS, kb);
             __builtin_amdgcn_sched_barrier(0);   // not above the math: it reads qreg
             if (more)
                 load_first(jnext);
@@ -333,7 +375,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
                 __syncthreads();
                 if (PREFETCH && kb + 1 < nkb)
                     load_kv(kr, vr, jc, kb + 1);
-                tile_math(smem, smem + MHA_BN * KS, kb);
+                tile(smem, smem + MHA_BN * KS, kb);
                 if (kb + 1 == nkb && more) {   // next job's first loads, as above
                     __builtin_amdgcn_sched_barrier(0);
                     load_first(jnext);
@@ -470,6 +512,10 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     constexpr int NQW = NQT / NSPLIT;   // ... per wave
     constexpr int QS = SM::QS, TS = SM::TS;
     static_assert(NQW >= 1, "query split too fine for BM");
+    // Eight waves over four query blocks (two per wave): query/key blocks on
+    // the far side of the causal diagonal are skipped in the key-side and dQ
+    // products, and the dQ blocks are paired across SIMDs.
+    constexpr bool SKIP = NW == 8 && NQT == 4;
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
     float* Kt = smem;
     // Stage i: Qs [BM][QS], dOs [BM][QS], dSs [BM][TS], lse_s [BM], di_s [BM].
@@ -523,8 +569,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     f4 kreg[NDT], vreg[NDT];
     QTile t0, t1;
     auto load_kv = [&](const Job& j) {
-        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
-        const int l16 = lane & 15, g = lane >> 4, kg = wave & 3;
+        const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
+        const int l16 = lane & 15, g = lane >> 4, kg = pair_group(wave);
         const int key = min(j.k0 + kg * 16 + l16, S - 1);   // masked at job start
         const long off = j.base + (long)key * rs;
 #pragma unroll
@@ -548,9 +594,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         const bool more = jn < njobs;
         const Job jnext = job_of(more ? jn : 0);
 
-        const int tid = job_tid(), lane = tid & 63, wave = tid >> 6;
+        const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4;
-        const int kg = wave & 3, qs = wave >> 2;
+        const int kg = pair_group(wave), qs = wave >> 2;
         const long base = jc.base;
         const int k0 = jc.k0, qb0 = jc.qb0;
         const int mykey = k0 + kg * 16 + l16;
@@ -572,8 +618,12 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         };
         // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
         // l16, queries 16qt + 4g + r); dS goes to LDS for the dQ product, then
-        // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.
-        auto key_side = [&](float* st, int q0) {
+        // dV^T += dO^T P and dK^T += Q^T dS accumulate in registers.  The
+        // first F of the wave's NQW query blocks lie wholly before its key
+        // block (all masked: P = dS = 0) and are skipped; the dQ product never
+        // reads their dS.
+        auto key_side_f = [&](float* st, int q0, auto first) {
+            constexpr int F = decltype(first)::value;
             // Raised issue priority for this MFMA-dense section: the other
             // wave of the SIMD fills its stalls instead of interleaving.
             __builtin_amdgcn_s_setprio(1);
@@ -597,6 +647,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
                     for (int j = 0; j < QI; j++) {
+                        if (q1 + j < F)
+                            continue;
                         const int qt = qs * NQW + q1 + j;
                         const f4 qa = *reinterpret_cast<const f4*>(&Qs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
                         const f4 oa = *reinterpret_cast<const f4*>(&dOs[(16 * qt + l16) * QS + 16 * dt + 4 * g]);
@@ -610,6 +662,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
 #pragma unroll
                 for (int j = 0; j < QI; j++) {
                     const int qq = q1 + j, qt = qs * NQW + qq;
+                    if (qq < F)
+                        continue;
                     const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
                     const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
 #pragma unroll
@@ -627,7 +681,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             for (int dt = 0; dt < NDT; dt++) {
                 f4 av = dv[dt], ak = dk[dt];
 #pragma unroll
-                for (int qq = 0; qq < NQW; qq++) {
+                for (int qq = F; qq < NQW; qq++) {
                     const int qt = qs * NQW + qq;
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
@@ -641,10 +695,25 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             }
             __builtin_amdgcn_s_setprio(0);
         };
+        auto key_side = [&](float* st, int q0) {
+            // Leading query blocks of the wave that end before its first key.
+            int f = 0;
+#pragma unroll
+            for (int qq = 0; qq < NQW; qq++)
+                if (q0 + 16 * (qs * NQW + qq) + 15 < k0 + 16 * kg)
+                    f = qq + 1;
+            if (!SKIP || f == 0)
+                key_side_f(st, q0, ic<0>{});
+            else if (f == 1)
+                key_side_f(st, q0, ic<1>{});
+        };
         // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
         // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
         // wave's jobs share qt (NW is a multiple of NQT), so pairs of jobs run as
-        // two interleaved MFMA chains over one read of the dS operand.
+        // two interleaved MFMA chains over one read of the dS operand.  With
+        // eight waves and four query blocks, waves w and w+4 (one SIMD) take
+        // blocks qt and 3-qt; a block's key blocks past its last query are
+        // masked out and skipped.
         constexpr int NJOB = NQT * NDT;
         constexpr int NJ = (NJOB + NW - 1) / NW;   // jobs per wave (the last may be empty)
         static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
@@ -657,9 +726,12 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
             }
         };
-        auto query_side = [&](const float* st, int q0) {
+        const int dq_qt = SKIP ? pair_group(wave) : wave % NQT;
+        // FULL: all four key blocks are live; otherwise those before kend.
+        auto query_side_f = [&](const float* st, int q0, int kend, auto full) {
+            constexpr bool FULL = decltype(full)::value;
             const float* dSs = st + 2 * BM * QS;
-            const int qt = wave % NQT;
+            const int qt = dq_qt;
             const float* arow = dSs + (16 * qt + l16) * TS + 4 * g;
             if constexpr (NJ % 2 == 0) {
 #pragma unroll
@@ -670,6 +742,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     f4 acc0 = f4zero(), acc1 = f4zero();
 #pragma unroll
                     for (int kt = 0; kt < 4; kt++) {
+                        if (!FULL && kt >= kend)
+                            break;
                         const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
                         const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
                         const f4 v = *reinterpret_cast<const f4*>(b1 + 16 * kt);
@@ -689,6 +763,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     f4 acc = f4zero();
 #pragma unroll
                     for (int kt = 0; kt < 4; kt++) {
+                        if (!FULL && kt >= kend)
+                            break;
                         const f4 a = *reinterpret_cast<const f4*>(arow + 16 * kt);
                         const f4 u = *reinterpret_cast<const f4*>(b0 + 16 * kt);
 #pragma unroll
@@ -698,6 +774,14 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     dq_store(acc, q0, qt, dt);
                 }
             }
+        };
+        auto query_side = [&](const float* st, int q0) {
+            // Key blocks kt with a key at or before the block's last query.
+            const int kend = (q0 + 16 * dq_qt + 15 - k0) / 16 + 1;
+            if (!SKIP || kend >= 4)
+                query_side_f(st, q0, 4, std::true_type{});
+            else
+                query_side_f(st, q0, kend, std::false_type{});
         };
 
         // Zero the K/V operands past S and Dh (their loads were clamped).
