@@ -119,6 +119,21 @@ __device__ __forceinline__ int snake_job(int r)
     return r * G + ((r & 1) ? G - 1 - w : w);
 }
 
+// Job of workgroup w in a grid of one job per workgroup, N jobs on C compute
+// units holding two workgroups each (C < N <= 2C).  Workgroup w + C is
+// placed on the compute unit of workgroup w (the dispatcher fills every
+// compute unit once before it doubles up), so the P = N - C compute units
+// that receive two workgroups take a heavy and a light job each (indices
+// summing to a constant) and the other C - P take the C - P heaviest jobs
+// alone.  Two resident jobs overlap one another's load and merge phases.
+__device__ __forceinline__ int paired_job(int w, int N, int C)
+{
+    const int P = N - C;
+    if (w >= C)
+        return N - 1 - (w - C);
+    return w >= P ? w - P : (C - P) + w;
+}
+
 // Row (or key) group of wave `wave` in a workgroup of 4 or 8 waves.  The
 // waves of a workgroup are dealt to the compute unit's four SIMDs
 // round-robin, so waves w and w+4 share a SIMD; the second four take the
@@ -153,10 +168,10 @@ __device__ __forceinline__ int job_tid()
 // next job's Q rows and first two K/V tiles, so that they arrive while the
 // current job merges its key splits and writes O.
 template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
-__global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
+__global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
-    float qscale)
+    float qscale, int pair_cus)
 {
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
@@ -215,7 +230,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_fwd_kernel(
             load_kv(kr1, vr1, j, min(1, j.qb));
     };
 
-    Job jc = job_of(snake_job(0));   // the grid never exceeds the job count
+    // The grid never exceeds the job count.  pair_cus > 0: one job per
+    // workgroup, two workgroups per compute unit (paired_job).
+    Job jc = job_of(pair_cus > 0 ? paired_job(blockIdx.x, njobs, pair_cus) : snake_job(0));
     load_first(jc);
 #pragma nounroll
     for (int r = 0;; r++) {
@@ -967,6 +984,10 @@ struct MhaSplits {
     // Resident workgroups per CU assumed for the persistent grids.
     static constexpr int FWD_PER_CU = 1;
     static constexpr int BWD_PER_CU = 1;
+    // Two forward workgroups fit one compute unit (at most 128 VGPRs under
+    // the kernel's launch bound, 2 x 68 KB of LDS): job counts between one
+    // and two per compute unit run as one paired round (paired_job).
+    static constexpr bool FWD_PAIR = DHP <= 64;
 };
 
 template <int DHP, bool VEC>
@@ -977,15 +998,22 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     const int BH = B * H;
     const int nqb = (S + MHA_BM - 1) / MHA_BM;
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid(job_grid((long)nqb * BH, MhaSplits<DHP>::FWD_PER_CU, false)), block(256 * NS);
+    const long njobs = (long)nqb * BH;
+    const int cus = device_cus();
+    int pair = 0;
+    dim3 grid(job_grid(njobs, MhaSplits<DHP>::FWD_PER_CU, false)), block(256 * NS);
+    if (MhaSplits<DHP>::FWD_PAIR && njobs > cus && njobs <= 2L * cus) {
+        pair = cus;
+        grid.x = (unsigned)njobs;
+    }
     if (O != nullptr) {
         ProfScope ps(st, "mha_fwd");
         hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true>), grid, block, 0, st, Q, K, V, O,
-                           lse, S, H, Dh, BH, nqb, qscale);
+                           lse, S, H, Dh, BH, nqb, qscale, pair);
     } else {
         ProfScope ps(st, "mha_stats");
         hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, false>), grid, block, 0, st, Q, K, V, O,
-                           lse, S, H, Dh, BH, nqb, qscale);
+                           lse, S, H, Dh, BH, nqb, qscale, pair);
     }
     return hipGetLastError();
 }
