@@ -214,9 +214,10 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         if (WRITE_O)
             vx.load(V, j.base, rs, kb * MHA_BN, S, Dh, tid);
     };
-    // A job's first loads: Q rows and key tiles 0 and 1.  Loads past the last
-    // key tile repeat it (clamped tile index), so these memory operations are
-    // the same on every path and the compiler's waits for them stay tight.
+    // A job's first loads: Q rows and key tile 0 (and, for the single-stage
+    // pipeline, nothing more; the double-buffered one requests tiles 1 and 2
+    // once tile 0 is in LDS, so that every workgroup's first tile arrives
+    // ahead of the later ones).
     auto load_first = [&](const Job& j) {
         const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4, qg = pair_group(wave);
@@ -226,8 +227,6 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         for (int dt = 0; dt < NDT; dt++)
             qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
         load_kv(kr, vr, j, 0);
-        if (SM::DB)
-            load_kv(kr1, vr1, j, min(1, j.qb));
     };
 
     // The grid never exceeds the job count.  pair_cus > 0: one job per
@@ -351,20 +350,25 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         if constexpr (SM::DB) {
             store_kv(kr, vr, smem);
             __builtin_amdgcn_sched_barrier(0);
+            // Tiles past the last one repeat it (clamped index), so these
+            // loads are the same on every path and the waits stay tight.
+            load_kv(kr1, vr1, jc, min(1, nkb - 1));
             load_kv(kr, vr, jc, min(2, nkb - 1));
             __syncthreads();
-            // Iteration kb < nkb-1: registers (kx, vx) hold tile kb+1; they go
-            // to LDS buffer (kb+1)&1 and are refilled with tile kb+3.
+            // Iteration kb < nkb-1: the math of tile kb (LDS buffer kb&1),
+            // then registers (kx, vx), holding tile kb+1, go to buffer
+            // (kb+1)&1 (last read in iteration kb-1) and are refilled with
+            // tile kb+3.
             auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx,
                             TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) {
                 const float* cur = smem + (kb & 1) * SM::TILES;
+                tile(cur, cur + MHA_BN * KS, kb);
                 store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
                 // Keep the refill below the LDS writes: issued earlier, the
                 // wait for the old data would include the new loads.
                 __builtin_amdgcn_sched_barrier(0);
                 if (kb + 3 < nkb)
                     load_kv(kx, vx, jc, kb + 3);
-                tile(cur, cur + MHA_BN * KS, kb);
                 __syncthreads();
             };
             int kb = 0;
