@@ -144,4 +144,23 @@ __device__ __forceinline__ void atomic_add_f32(float* p, float v)
     unsafeAtomicAdd(p, v);
 }
 
+// Float atomic adds through a raw buffer descriptor over [base, base + 2 GiB):
+// a lane whose byte offset is kDropOffset (past the descriptor's range) is
+// dropped by the hardware bounds check.  Masked lanes therefore need no
+// branch, and every path issues the same number of memory instructions, which
+// keeps the compiler's waits on earlier loads exact.
+constexpr unsigned kDropOffset = 0x7ffffff0u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t atomic_rsrc(float* base)
+{
+    // Raw (stride 0) buffer; 0x00020000: 32-bit data format, the gfx9 raw layout.
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)kDropOffset, 0x00020000);
+}
+
+__device__ __forceinline__ void buffer_atomic_add_f32(__amdgpu_buffer_rsrc_t r, unsigned off,
+                                                      float v)
+{
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)off, 0, 0);
+}
+
 } // namespace cxg

@@ -738,13 +738,19 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         constexpr int NJOB = NQT * NDT;
         constexpr int NJ = (NJOB + NW - 1) / NW;   // jobs per wave (the last may be empty)
         static_assert(NW % NQT == 0, "dQ jobs of a wave must share their query block");
+        // dQ adds through a buffer descriptor based at the tile's first row;
+        // rows past S and columns past Dh are dropped by the descriptor's
+        // bounds check rather than by a branch (byte offsets of a 64-row tile
+        // stay below 2 GiB for H*Dh < 8M).
         auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
             const int d = 16 * dt + l16;
+            const __amdgpu_buffer_rsrc_t rq = atomic_rsrc(dQ + base + (long)q0 * rs);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int q = q0 + 16 * qt + 4 * g + r;
-                if (q < S && d < Dh)
-                    atomic_add_f32(dQ + base + (long)q * rs + d, acc[r] * scale);
+                const int qi = 16 * qt + 4 * g + r;
+                const unsigned off = (q0 + qi < S && d < Dh) ? (unsigned)(qi * rs + d) * 4u
+                                                             : kDropOffset;
+                buffer_atomic_add_f32(rq, off, acc[r] * scale);
             }
         };
         const int dq_qt = SKIP ? pair_group(wave) : wave % NQT;
