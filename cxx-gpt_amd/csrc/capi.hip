@@ -245,7 +245,7 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
     if (!Q || !K || !V || !O || !den || !zc)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
-    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_FWD);
     Scratch ws;
     st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
     if (st != CXG_OK)
@@ -280,7 +280,7 @@ static int lin_dq_common(int phi, const float* K, const float* V, const float* d
     if (!K || !V || !dnum || !dden || !zc || !dQ || (phi == PHI_ELU1 && !Q))
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
-    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_DQ);
     Scratch ws;
     st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
     if (st != CXG_OK)
@@ -300,7 +300,7 @@ static int lin_dkdv_common(int phi, const float* Q, const float* K, const float*
     if (!Q || !K || !V || !dnum || !dden || !dK || !dV)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
-    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E);
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_DKDV);
     Scratch ws;
     st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
     if (st != CXG_OK)

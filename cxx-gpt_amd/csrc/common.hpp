@@ -144,23 +144,45 @@ __device__ __forceinline__ void atomic_add_f32(float* p, float v)
     unsafeAtomicAdd(p, v);
 }
 
-// Float atomic adds through a raw buffer descriptor over [base, base + 2 GiB):
-// a lane whose byte offset is kDropOffset (past the descriptor's range) is
-// dropped by the hardware bounds check.  Masked lanes therefore need no
+// Stores and float atomic adds through a raw buffer descriptor over
+// [base, base + 2 GiB): a lane whose byte offset is kDropOffset (past the
+// descriptor's range) is dropped by the hardware bounds check, as is every
+// lane of a descriptor built with no records.  Masked lanes therefore need no
 // branch, and every path issues the same number of memory instructions, which
-// keeps the compiler's waits on earlier loads exact.
+// keeps the compiler's waits on earlier loads exact (a branch around a store
+// or atomic makes it wait for all of them).
 constexpr unsigned kDropOffset = 0x7ffffff0u;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t atomic_rsrc(float* base)
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+
+// Raw (stride 0) buffer; 0x00020000: 32-bit data format, the gfx9 raw layout.
+// base == nullptr gives a descriptor that drops every access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const float* base)
 {
-    // Raw (stride 0) buffer; 0x00020000: 32-bit data format, the gfx9 raw layout.
-    return __builtin_amdgcn_make_buffer_rsrc(base, 0, (int)kDropOffset, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0,
+                                             base != nullptr ? (int)kDropOffset : 0, 0x00020000);
 }
 
 __device__ __forceinline__ void buffer_atomic_add_f32(__amdgpu_buffer_rsrc_t r, unsigned off,
                                                       float v)
 {
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ void buffer_store_f4(__amdgpu_buffer_rsrc_t r, unsigned off, f4 v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, (int)off, 0, 0);
+}
+
+__device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t r, unsigned off, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)off, 0, 0);
+}
+
+// Load through a buffer descriptor: out-of-range lanes read 0.
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, unsigned off)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
 
 } // namespace cxg

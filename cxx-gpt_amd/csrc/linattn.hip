@@ -42,8 +42,6 @@
 
 namespace cxg {
 
-constexpr int LIN_THREADS = 256;
-constexpr int LIN_WAVES = LIN_THREADS / 64;
 constexpr int CLD = 68;             // LDS row stride of a staged 16 x 64 chunk
 constexpr int CHUNK = 16 * CLD;     // floats per staged chunk matrix
 
@@ -260,39 +258,40 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
             St[a][j] = f4zero();
     float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    // wave h stages column tiles 2h, 2h+1 of X and Y; wave 0 also w
-    f4 nx[2], ny[2];
-    float nw = 1.0f;
-    auto fetch = [&](int t0) {
+    // Wave h stages column tiles 2h, 2h+1 of X and Y (and every lane loads
+    // its row's w).  Two register sets, loaded two chunks ahead of use; loads
+    // past the last chunk repeat it (clamped) and the w load goes through a
+    // buffer descriptor (none when w is null: 0 is read), so every path
+    // issues the same loads and the waits for each set stay exact.
+    const int nch = (tend - tbeg + 15) / 16;
+    const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w != nullptr ? w + rb : nullptr);
+    f4 xa[2], ya[2], xb[2], yb[2];
+    float wa, wb;
+    auto fetch = [&](f4 (&fx)[2], f4 (&fy)[2], float& fw, int t0) {
         const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 2>(nx, X + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(ny, Y + (rb + t0) * E, E, ro, E, g, 2 * h);
-        if (h == 0 && w != nullptr)
-            nw = w[rb + t0 + ro];
+        ldRp<VEC, 2>(fx, X + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(fy, Y + (rb + t0) * E, E, ro, E, g, 2 * h);
+        fw = buffer_load_f32(rw, (unsigned)(t0 + ro) * 4u);
     };
-    fetch(tbeg);
-    int c = 0;
-    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+    fetch(xa, ya, wa, tbeg);
+    fetch(xb, yb, wb, min(tbeg + 16, tlc));
+    auto chunk = [&](f4 (&ax)[2], f4 (&ay)[2], float& aw, int c) __attribute__((always_inline)) {
+        const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * AGG_STAGE;
         float* bX = st;
         float* bY = st + CHUNK;
         float* bw = st + 2 * CHUNK;
-        f4 ax[2], ay[2];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            ax[i] = nx[i];
-            ay[i] = ny[i];
-        }
-        const float wv = nw;
-        if (t0 + 16 < tend)
-            fetch(t0 + 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 2>(ax, full, rok, D, g, 2 * h);
         finRp<PHI, false, FW, 2>(ay, full, rok, E, g, 2 * h);
         putRp(bX, ax, l16, g, 2 * h);
         putRp(bY, ay, l16, g, 2 * h);
         if (h == 0 && g == 0)
-            bw[l16] = wv;
+            bw[l16] = w != nullptr ? aw : 1.0f;
+        // Below the LDS writes, which read the set: refill it with chunk c+2.
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(ax, ay, aw, min(t0 + 32, tlc));
         __syncthreads();
         f4 xC[4], yC[2];
         getC(bX, xC, l16, g);
@@ -320,7 +319,15 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
                 for (int r = 0; r < 4; r++)
                     zp[dt] += wc[r] * xC[dt][r];   // rows past the segment hold xC = 0
         }
+    };
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        chunk(xa, ya, wa, c);
+        chunk(xb, yb, wb, c + 1);
     }
+    if (c < nch)
+        chunk(xa, ya, wa, c);
+
     float* P = ws + (long)wid * LIN_WS;
 #pragma unroll
     for (int dt = 0; dt < 4; dt++) {
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const int seq = wid / nseg, seg = wid - seq * nseg;
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
-    float* bZ = lds + 2 * FWD_STAGE;   // wave 0: z rows for the z_cache store
+    float* bZ = lds + 2 * FWD_STAGE;   // z rows for the z_cache store (each wave its tiles)
 
     // state slice S[d][e], et = 2h + j: St[dt][j] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
     // z (prefix of phi(K) before the chunk): zC[dt] = z[16dt + l16], zR[dt][i] = z[16dt + 4g + i]
@@ -421,30 +428,29 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         }
     }
 
-    // wave h stages column tiles 2h, 2h+1 of Q, K and V
-    f4 nq[2], nk[2], nv[2];
-    auto fetch = [&](int t0) {
+    // Wave h stages column tiles 2h, 2h+1 of Q, K and V.  Two register sets,
+    // loaded two chunks ahead of use: the set holding chunk c is written to
+    // LDS at the start of chunk c and refilled with chunk c+2.  Loads past the
+    // last chunk repeat it (clamped), and the stores are branch-free (buffer
+    // descriptors, masked lanes dropped), so every path issues the same memory
+    // instructions and the waits for each set stay exact.
+    const int nch = (tend - tbeg + 15) / 16;
+    const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
+    f4 qa[2], ka[2], va[2], qb[2], kb[2], vb[2];
+    auto fetch = [&](f4 (&fq)[2], f4 (&fk)[2], f4 (&fv)[2], int t0) {
         const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(nv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
+        ldRp<VEC, 2>(fq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(fk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+        ldRp<VEC, 2>(fv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
     };
-    fetch(tbeg);
-    int c = 0;
-    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+    fetch(qa, ka, va, tbeg);
+    fetch(qb, kb, vb, min(tbeg + 16, tlc));
+    auto chunk = [&](f4 (&aq)[2], f4 (&ak)[2], f4 (&av)[2], int c) __attribute__((always_inline)) {
+        const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * FWD_STAGE;
         float* bQ = st;
         float* bK = st + CHUNK;
         float* bV = st + 2 * CHUNK;
-        f4 aq[2], ak[2], av[2];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            aq[i] = nq[i];
-            ak[i] = nk[i];
-            av[i] = nv[i];
-        }
-        if (t0 + 16 < tend)   // next chunk's rows, in flight during this chunk
-            fetch(t0 + 16);
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
         finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
@@ -452,6 +458,9 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         putRp(bQ, aq, l16, g, 2 * h);
         putRp(bK, ak, l16, g, 2 * h);
         putRp(bV, av, l16, g, 2 * h);
+        // Below the LDS writes, which read the set: refill it with chunk c+2.
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(aq, ak, av, min(t0 + 32, tlc));
         __syncthreads();
         f4 q[4], k[4];
         getR(bQ, q, l16, g);
@@ -484,16 +493,21 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         for (int j = 0; j < 2; j++)
             vC[j] = colC(bV, 2 * h + j, l16, g);
         // z_t = z_prev + inclusive prefix of phi(K) over the chunk (column
-        // layout); wave 0 turns it into rows through LDS for 16-byte stores
+        // layout); each wave turns its two column tiles into rows through
+        // LDS for 16-byte stores
+        f4 zp[4];
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
             float tot;
-            const f4 pz = col_prefix16(kC[dt], tot, lane);
-            if (h == 0)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    bZ[(4 * g + r) * CLD + 16 * dt + l16] = zC[dt] + pz[r];
+            zp[dt] = col_prefix16(kC[dt], tot, lane) + zC[dt];
             zC[dt] += tot;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const f4 zw = h ? zp[2 + j] : zp[j];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                bZ[(4 * g + r) * CLD + 16 * (2 * h + j) + l16] = zw[r];
         }
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
@@ -527,26 +541,49 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                     acc = mfma16(kC[dt][r], vC[j][r], acc);
                 St[dt][j] = acc;
             }
-        // outputs of row t0 + l16
-        if (full || rok) {
+        // outputs of row t0 + l16: O and z_cache columns of this wave's two
+        // tiles; den from wave 0
+        const bool ok = full || rok;
+        f4 zrow[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            zrow[j] = *reinterpret_cast<const f4*>(&bZ[l16 * CLD + 16 * (2 * h + j) + 4 * g]);
+        const float dval = den_incl_eps ? dn + 1e-8f : dn;
+        if constexpr (FW) {
+            const __amdgpu_buffer_rsrc_t ro_ = buf_rsrc(O + (rb + t0) * E);
+            const __amdgpu_buffer_rsrc_t rz_ = buf_rsrc(zcache != nullptr ? zcache + (rb + t0) * D
+                                                                          : nullptr);
+            const __amdgpu_buffer_rsrc_t rd_ = buf_rsrc(den + rb + t0);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const unsigned col = 16 * (2 * h + j) + 4 * g;
+                buffer_store_f4(ro_, ok ? (unsigned)(l16 * E + col) * 4u : kDropOffset, o[j]);
+                buffer_store_f4(rz_, ok ? (unsigned)(l16 * D + col) * 4u : kDropOffset, zrow[j]);
+            }
+            buffer_store_f32(rd_, (ok && h == 0 && g == 0) ? (unsigned)l16 * 4u : kDropOffset,
+                             dval);
+        } else if (ok) {
             float* orow = O + (rb + t0 + l16) * E;
 #pragma unroll
             for (int j = 0; j < 2; j++)
                 stR<VEC, FW>(orow, 16 * (2 * h + j) + 4 * g, E, o[j]);
-            if (h == 0) {
-                if (zcache != nullptr) {
-                    f4 zrow[4];
-                    getR(bZ, zrow, l16, g);
-                    float* zrw = zcache + (rb + t0 + l16) * D;
+            if (zcache != nullptr) {
+                float* zrw = zcache + (rb + t0 + l16) * D;
 #pragma unroll
-                    for (int ct = 0; ct < 4; ct++)
-                        stR<VEC, FW>(zrw, 16 * ct + 4 * g, D, zrow[ct]);
-                }
-                if (g == 0)
-                    den[rb + t0 + l16] = den_incl_eps ? dn + 1e-8f : dn;
+                for (int j = 0; j < 2; j++)
+                    stR<VEC, FW>(zrw, 16 * (2 * h + j) + 4 * g, D, zrow[j]);
             }
+            if (h == 0 && g == 0)
+                den[rb + t0 + l16] = dval;
         }
+    };
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        chunk(qa, ka, va, c);
+        chunk(qb, kb, vb, c + 1);
     }
+    if (c < nch)
+        chunk(qa, ka, va, c);
 
     if (Sfin != nullptr && seg == nseg - 1) {
         // final state of the sequence: [d][e] (linear_cuda) or [e][d] (two_stage)
@@ -1202,7 +1239,46 @@ __global__ __launch_bounds__(256) void phi_hexp_bwd_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 static inline bool al16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
-LinPlan lin_plan(int Bq, int S, int D, int E)
+// Compute units of the current device (cached per device).
+static int lin_cus()
+{
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Workgroups of a pass's main kernel resident at once on the current device
+// (occupancy of the D = E = 64 variant times the compute units), cached.
+static int lin_slots(int pass)
+{
+    static int per_cu[3];
+    if (per_cu[pass] <= 0) {
+        int n = 0;
+        hipError_t e = hipErrorInvalidValue;
+        if (pass == LIN_PASS_FWD)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)lin_fwd_kernel<PHI_ELU1, true, true>, FWD_THREADS, 0);
+        else if (pass == LIN_PASS_DQ)
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)lin_dq_kernel<PHI_ELU1, true, true>, DQ_THREADS, 0);
+        else
+            e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)lin_dkdv_kernel<PHI_ELU1, true, true>, DKDV_THREADS, 0);
+        per_cu[pass] = (e == hipSuccess && n > 0) ? n : 4;
+    }
+    return per_cu[pass] * lin_cus();
+}
+
+LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 {
     LinPlan p;
     p.fast = (D <= 64 && E <= 64);
@@ -1211,11 +1287,13 @@ LinPlan lin_plan(int Bq, int S, int D, int E)
     if (p.fast) {
         const int nchunk = (S + 15) / 16;
         // Segments per sequence (measured on MI355X at B' = 96): long
-        // sequences want ~2048 segment workgroups in all (two rounds of
-        // resident workgroups), shorter ones (<= 64 chunks) ~768 (one round,
-        // shorter agg/scan passes); at least two chunks per segment.
-        const int target = nchunk > 64 ? 2048 : 768;
-        int want = (target + Bq - 1) / Bq;
+        // sequences (> 64 chunks) want up to two rounds of the main kernel's
+        // resident workgroups (rounding up past a round boundary leaves a
+        // round that runs almost empty), shorter ones about three segment
+        // workgroups per compute unit (shorter agg/scan passes); at least
+        // two chunks per segment.
+        const int target = nchunk > 64 ? 2 * lin_slots(pass) : 3 * lin_cus();
+        int want = target / Bq;
         if (want > nchunk / 2)
             want = nchunk / 2;
         if (want < 1)
@@ -1272,7 +1350,7 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
                            float* zc, float* Sfin, float* zfin, int sfin_de, int den_eps, int Bq,
                            int S, int D, int E, void* ws, hipStream_t st)
 {
-    const LinPlan p = lin_plan(Bq, S, D, E);
+    const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
     if (!p.fast) {
         float* state = (float*)ws;
         const size_t sm = (size_t)(3 * D + 256) * sizeof(float);
@@ -1344,7 +1422,7 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
                           const float* zc, const float* Q, float* dQ, int Bq, int S, int D, int E,
                           void* ws, hipStream_t st)
 {
-    const LinPlan p = lin_plan(Bq, S, D, E);
+    const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DQ);
     if (!p.fast) {
         ProfScope ps(st, "lin_dq_generic");
         hipLaunchKernelGGL((lin_dq_generic_kernel<PHI>), dim3(Bq), dim3(256), 0, st, K, V, dnum,
@@ -1390,7 +1468,7 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
                             const float* dden, float* dK, float* dV, int Bq, int S, int D, int E,
                             void* ws, hipStream_t st)
 {
-    const LinPlan p = lin_plan(Bq, S, D, E);
+    const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DKDV);
     if (!p.fast) {
         ProfScope ps(st, "lin_dkdv_generic");
         hipLaunchKernelGGL((lin_dkdv_generic_kernel<PHI>), dim3(Bq), dim3(256),

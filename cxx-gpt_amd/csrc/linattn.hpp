@@ -17,7 +17,11 @@ struct LinPlan {
     int L;       // rows per segment (multiple of 16)
 };
 
-LinPlan lin_plan(int Bq, int S, int D, int E);
+// The scan pass a plan is for: each sizes its segments to its own main
+// kernel's resident workgroups.
+enum LinPass { LIN_PASS_FWD = 0, LIN_PASS_DQ = 1, LIN_PASS_DKDV = 2 };
+
+LinPlan lin_plan(int Bq, int S, int D, int E, int pass);
 // device scratch (bytes) the fwd / dQ / dKdV launchers need for this plan
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E);
 

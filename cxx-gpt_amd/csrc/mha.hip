@@ -744,7 +744,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // stay below 2 GiB for H*Dh < 8M).
         auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
             const int d = 16 * dt + l16;
-            const __amdgpu_buffer_rsrc_t rq = atomic_rsrc(dQ + base + (long)q0 * rs);
+            const __amdgpu_buffer_rsrc_t rq = buf_rsrc(dQ + base + (long)q0 * rs);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int qi = 16 * qt + 4 * g + r;
