@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256) void lin_step1_kernel(
 // 2h+1 and keeps that half of the transposed state.
 // ---------------------------------------------------------------------------
 constexpr int DQ_THREADS = 128;
-constexpr int DQ_STAGE = 5 * CHUNK + 16;   // phi(K), V, dnum, z_cache, Q rows + dden rows
+constexpr int DQ_STAGE = 3 * CHUNK + 16;   // phi(K), V, dnum chunks + dden rows
 
 template <int PHI, bool VEC, bool FW>
 __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void lin_dq_kernel(
@@ -674,8 +674,15 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                 StT[et][j] = f4zero();
     }
 
-    // wave h stages column tiles 2h, 2h+1 of K, V, dnum, z_cache and Q; wave 0
-    // also dden
+    // Wave h loads column tiles 2h, 2h+1 of K, V, dnum, z_cache and Q (every
+    // lane also its row's dden).  K, V and dnum go through LDS; z_cache and Q
+    // are only needed in the row layout they are loaded in (row l16, the
+    // wave's own column tiles), so they stay in registers.  The next chunk's
+    // loads are issued unconditionally (clamped past the last chunk) and the
+    // dQ stores are branch-free (buffer descriptor, masked lanes dropped), so
+    // the waits for them stay exact.
+    const int nch = (tend - tbeg + 15) / 16;
+    const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
     f4 nk[2], nv[2], nn[2], nz[2], nq[2];
     float ndd = 0.0f;
     auto fetch = [&](int t0) {
@@ -686,19 +693,16 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         ldRp<VEC, 2>(nz, zcache + (rb + t0) * D, D, ro, D, g, 2 * h);
         if (HAS_Q)
             ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
-        if (h == 0)
-            ndd = dden[rb + t0 + ro];
+        ndd = dden[rb + t0 + ro];
     };
     fetch(tbeg);
-    int c = 0;
-    for (int t0 = tbeg; t0 < tend; t0 += 16, c++) {
+    for (int c = 0; c < nch; c++) {
+        const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * DQ_STAGE;
         float* bK = st;
         float* bV = st + CHUNK;
         float* bN = st + 2 * CHUNK;
-        float* bZc = st + 3 * CHUNK;
-        float* bQ = st + 4 * CHUNK;
-        float* bd = st + 5 * CHUNK;
+        float* bd = st + 3 * CHUNK;
         f4 ak[2], av[2], an[2], az[2], aq[2];
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -709,8 +713,7 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
             aq[i] = HAS_Q ? nq[i] : f4zero();
         }
         const float dd = ndd;
-        if (t0 + 16 < tend)
-            fetch(t0 + 16);
+        fetch(min(t0 + 16, tlc));
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
         finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
@@ -718,9 +721,6 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         putRp(bK, ak, l16, g, 2 * h);
         putRp(bV, av, l16, g, 2 * h);
         putRp(bN, an, l16, g, 2 * h);
-        putRp(bZc, az, l16, g, 2 * h);   // only rows that are stored get used
-        if (HAS_Q)
-            putRp(bQ, aq, l16, g, 2 * h);
         if (h == 0 && g == 0)
             bd[l16] = dd;
         __syncthreads();
@@ -749,8 +749,7 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         f4 dq[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int dt = 2 * h + j;
-            f4 acc = *reinterpret_cast<const f4*>(&bZc[l16 * CLD + 16 * dt + 4 * g]) * ddt;
+            f4 acc = az[j] * ddt;
 #pragma unroll
             for (int et = 0; et < 4; et++)
 #pragma unroll
@@ -759,12 +758,10 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 acc = mfma16(kC[j][r], G[r], acc);
-            if (HAS_Q) {
-                const f4 qv = *reinterpret_cast<const f4*>(&bQ[l16 * CLD + 16 * dt + 4 * g]);
+            if (HAS_Q)
 #pragma unroll
                 for (int i = 0; i < 4; i++)
-                    acc[i] *= Phi<PHI>::d(qv[i]);
-            }
+                    acc[i] *= Phi<PHI>::d(aq[j][i]);
             dq[j] = acc;
         }
         // S^T += V^T phi(K) (this wave's columns)
@@ -778,7 +775,14 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
                     acc = mfma16(vC[et][r], kC[j][r], acc);
                 StT[et][j] = acc;
             }
-        if (full || rok) {
+        const bool ok = full || rok;
+        if constexpr (FW) {
+            const __amdgpu_buffer_rsrc_t rq = buf_rsrc(dQ + (rb + t0) * D);
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                buffer_store_f4(rq, ok ? (unsigned)(l16 * D + 16 * (2 * h + j) + 4 * g) * 4u
+                                       : kDropOffset, dq[j]);
+        } else if (ok) {
             float* qrow = dQ + (rb + t0 + l16) * D;
 #pragma unroll
             for (int j = 0; j < 2; j++)
@@ -1287,12 +1291,12 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
     if (p.fast) {
         const int nchunk = (S + 15) / 16;
         // Segments per sequence (measured on MI355X at B' = 96): long
-        // sequences (> 64 chunks) want up to two rounds of the main kernel's
-        // resident workgroups (rounding up past a round boundary leaves a
-        // round that runs almost empty), shorter ones about three segment
-        // workgroups per compute unit (shorter agg/scan passes); at least
-        // two chunks per segment.
-        const int target = nchunk > 64 ? 2 * lin_slots(pass) : 3 * lin_cus();
+        // sequences (> 64 chunks) want one round of the main kernel's
+        // resident workgroups (rounding up past it leaves a round that runs
+        // almost empty; two rounds cost more in agg/scan and segment start-up
+        // than they gain), shorter ones about three segment workgroups per
+        // compute unit; at least two chunks per segment.
+        const int target = nchunk > 64 ? lin_slots(pass) : 3 * lin_cus();
         int want = target / Bq;
         if (want > nchunk / 2)
             want = nchunk / 2;
