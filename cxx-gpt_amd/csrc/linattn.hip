@@ -232,9 +232,12 @@ __device__ __forceinline__ f4 colC(const float* __restrict__ buf, int ct, int l1
 // per-segment aggregates: dS = sum_s phi(X_s)^T Y_s (64 x 64), dz = sum_s w_s phi(X_s)
 // (w = 1 when null).  Forward direction: X = K, Y = V.  Reverse: X = Q, Y = dnum,
 // w = dden.  Written row-major [d][e] followed by z[d], LIN_WS floats per segment.
-// Wave h accumulates columns e of tiles et = 2h, 2h+1.
+// Four waves: wave (h, half) accumulates columns e of tiles et = 2h, 2h+1 over
+// one half of the segment's chunks (the two halves run side by side, which
+// halves the chain of dependent chunk steps), and the halves are summed
+// through LDS at the end.
 // ---------------------------------------------------------------------------
-constexpr int AGG_THREADS = 128;
+constexpr int AGG_THREADS = 256;
 constexpr int AGG_STAGE = 2 * CHUNK + 16;
 
 template <int PHI, bool VEC, bool FW>
@@ -242,12 +245,20 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ w,
     float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L)
 {
-    __shared__ __attribute__((aligned(16))) float lds[2 * AGG_STAGE];
-    const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
+    __shared__ __attribute__((aligned(16))) float lds[4 * AGG_STAGE];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int h = wv & 1, half = wv >> 1;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x;
     const int seq = wid / nseg, seg = wid - seq * nseg;
-    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
+    const int sbeg = seg * L, send = min(S, sbeg + L);
+    const int nch_all = (send - sbeg + 15) / 16;
+    const int nh = (nch_all + 1) / 2;   // chunks of the first half (the second has nh or nh-1)
+    // this half's rows [tbeg, tend); the second half of a one-chunk segment is empty
+    const int tbeg = min(sbeg + 16 * nh * half, send);
+    const int tend = half ? send : min(send, sbeg + 16 * nh);
+    // clamp target for row loads: the half's last row, or the segment's for an empty half
+    const int tlast = (tend > tbeg ? tend : send) - 1;
     const long rb = (long)seq * S;
 
     f4 St[4][2];
@@ -258,40 +269,58 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
             St[a][j] = f4zero();
     float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Wave h stages column tiles 2h, 2h+1 of X and Y (and every lane loads
-    // its row's w).  Two register sets, loaded two chunks ahead of use; loads
-    // past the last chunk repeat it (clamped) and the w load goes through a
-    // buffer descriptor (none when w is null: 0 is read), so every path
-    // issues the same loads and the waits for each set stay exact.
-    const int nch = (tend - tbeg + 15) / 16;
-    const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
+    // Wave (h, half) stages column tiles 2h, 2h+1 of X and Y for its half's
+    // chunks (and every lane loads its row's w).  Two register sets, loaded
+    // two chunks ahead of use; loads past the last chunk repeat it (clamped;
+    // rows outside the half are masked to zero) and the w load goes through a
+    // buffer descriptor (none when w is null: 0 is read), so every path issues
+    // the same loads and the waits for each set stay exact.  Both halves step
+    // through nh chunks (one barrier per step); a half with fewer chunks steps
+    // through an empty one.
+    const int tlc = tbeg + 16 * max(nh - 1, 0);
+    const int tlcl = min(tlc, tlast);   // clamped fetch rows stay in the segment
     const __amdgpu_buffer_rsrc_t rw = buf_rsrc(w != nullptr ? w + rb : nullptr);
     f4 xa[2], ya[2], xb[2], yb[2];
     float wa, wb;
+    // Row loads are coalesced: wave h of the half takes chunk rows
+    // 8h + 4i + l/16 (i = 0, 1), columns 4(l%16) .. +3, so each instruction
+    // reads four whole rows.
+    const int crow = 8 * h + (lane >> 4), ccol = 4 * (lane & 15);
     auto fetch = [&](f4 (&fx)[2], f4 (&fy)[2], float& fw, int t0) {
-        const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 2>(fx, X + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(fy, Y + (rb + t0) * E, E, ro, E, g, 2 * h);
-        fw = buffer_load_f32(rw, (unsigned)(t0 + ro) * 4u);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const long r = rb + min(t0 + crow + 4 * i, tlast);
+            fx[i] = load4c<VEC>(X + r * D, ccol, D);
+            fy[i] = load4c<VEC>(Y + r * E, ccol, E);
+        }
+        fw = buffer_load_f32(rw, (unsigned)min(t0 + l16, tlast) * 4u);
     };
-    fetch(xa, ya, wa, tbeg);
-    fetch(xb, yb, wb, min(tbeg + 16, tlc));
+    fetch(xa, ya, wa, min(tbeg, tlcl));
+    fetch(xb, yb, wb, min(tbeg + 16, tlcl));
+    float* stg = lds + half * 2 * AGG_STAGE;
     auto chunk = [&](f4 (&ax)[2], f4 (&ay)[2], float& aw, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
-        float* st = lds + (c & 1) * AGG_STAGE;
+        float* st = stg + (c & 1) * AGG_STAGE;
         float* bX = st;
         float* bY = st + CHUNK;
         float* bw = st + 2 * CHUNK;
-        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
-        finRp<PHI, true, FW, 2>(ax, full, rok, D, g, 2 * h);
-        finRp<PHI, false, FW, 2>(ay, full, rok, E, g, 2 * h);
-        putRp(bX, ax, l16, g, 2 * h);
-        putRp(bY, ay, l16, g, 2 * h);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const bool ok = t0 + crow + 4 * i < tend;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float xv = Phi<PHI>::f(ax[i][e]);
+                ax[i][e] = (ok && (FW || ccol + e < D)) ? xv : 0.0f;
+                ay[i][e] = (ok && (FW || ccol + e < E)) ? ay[i][e] : 0.0f;
+            }
+            *reinterpret_cast<f4*>(&bX[(crow + 4 * i) * CLD + ccol]) = ax[i];
+            *reinterpret_cast<f4*>(&bY[(crow + 4 * i) * CLD + ccol]) = ay[i];
+        }
         if (h == 0 && g == 0)
             bw[l16] = w != nullptr ? aw : 1.0f;
         // Below the LDS writes, which read the set: refill it with chunk c+2.
         __builtin_amdgcn_sched_barrier(0);
-        fetch(ax, ay, aw, min(t0 + 32, tlc));
+        fetch(ax, ay, aw, min(t0 + 32, tlcl));
         __syncthreads();
         f4 xC[4], yC[2];
         getC(bX, xC, l16, g);
@@ -317,29 +346,62 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    zp[dt] += wc[r] * xC[dt][r];   // rows past the segment hold xC = 0
+                    zp[dt] += wc[r] * xC[dt][r];   // rows past the half hold xC = 0
         }
     };
     int c = 0;
-    for (; c + 1 < nch; c += 2) {
+    for (; c + 1 < nh; c += 2) {
         chunk(xa, ya, wa, c);
         chunk(xb, yb, wb, c + 1);
     }
-    if (c < nch)
+    if (c < nh)
         chunk(xa, ya, wa, c);
 
-    float* P = ws + (long)wid * LIN_WS;
+    // Sum the halves: the second publishes its state slice (and z partials)
+    // through LDS, the first adds and writes the record.
+    __syncthreads();   // every wave is done with the stages
+    float* red = lds + h * (64 * 33);   // [lane][33]: 32 state values + z
+    if (half == 1) {
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) {
+        for (int dt = 0; dt < 4; dt++) {
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                P[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16] = St[dt][j][r];
-        if (h == 0) {
-            const float z = xrow_sum(zp[dt]);
-            if (g == 0)
-                P[4096 + 16 * dt + l16] = z;
+                for (int r = 0; r < 4; r++)
+                    red[lane * 33 + (dt * 2 + j) * 4 + r] = St[dt][j][r];
+        }
+        if (h == 0)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                red[64 * 66 + lane * 4 + dt] = zp[dt];
+    }
+    __syncthreads();
+    if (half == 0) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    St[dt][j][r] += red[lane * 33 + (dt * 2 + j) * 4 + r];
+        }
+        if (h == 0)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                zp[dt] += red[64 * 66 + lane * 4 + dt];
+        float* P = ws + (long)wid * LIN_WS;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    P[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16] = St[dt][j][r];
+            if (h == 0) {
+                const float z = xrow_sum(zp[dt]);
+                if (g == 0)
+                    P[4096 + 16 * dt + l16] = z;
+            }
         }
     }
 }
