@@ -905,7 +905,11 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
                                            : f4zero();
     }
 
-    // wave w stages column tile w of Q, K, V and dnum; wave 3 also dden
+    // Wave w stages column tile w of Q, K, V and dnum (every lane also loads
+    // its row's dden).  The next chunk's loads are issued unconditionally
+    // (clamped to the first chunk) and the dK/dV stores are branch-free
+    // (buffer descriptors, masked lanes dropped), so the waits for the loads
+    // stay exact.
     f4 nq[1], nk[1], nv[1], nn[1];
     float ndd = 0.0f;
     auto fetch = [&](int t0) {
@@ -914,8 +918,7 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
         ldRp<VEC, 1>(nk, K + (rb + t0) * D, D, ro, D, g, w);
         ldRp<VEC, 1>(nv, V + (rb + t0) * E, E, ro, E, g, w);
         ldRp<VEC, 1>(nn, dnum + (rb + t0) * E, E, ro, E, g, w);
-        if (w == 3)
-            ndd = dden[rb + t0 + ro];
+        ndd = dden[rb + t0 + ro];
     };
     const int nchunk = (tend - tbeg + 15) / 16;
     fetch(tbeg + 16 * (nchunk - 1));
@@ -929,8 +932,7 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
         float* bd = st + 4 * CHUNK;
         f4 aq[1] = {nq[0]}, ak[1] = {nk[0]}, av[1] = {nv[0]}, an[1] = {nn[0]};
         const float dd = ndd;
-        if (c > 0)
-            fetch(t0 - 16);
+        fetch(max(t0 - 16, tbeg));
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 1>(aq, full, rok, D, g, w);
         finRp<PHI, true, FW, 1>(ak, full, rok, D, g, w);
@@ -988,7 +990,14 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
                         acc = mfma16(qC[dt][r], dnC[j][r], acc);
                     Sm[dt][j] = acc;
                 }
-            if (full || rok) {
+            const bool ok = full || rok;
+            if constexpr (FW) {
+                const __amdgpu_buffer_rsrc_t rv = buf_rsrc(dV + (rb + t0) * E);
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    buffer_store_f4(rv, ok ? (unsigned)(l16 * E + 16 * (2 * hh + j) + 4 * g) * 4u
+                                           : kDropOffset, dv[j]);
+            } else if (ok) {
                 float* vrow = dV + (rb + t0 + l16) * E;
 #pragma unroll
                 for (int j = 0; j < 2; j++)
@@ -1056,7 +1065,14 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
                 for (int i = 0; i < 4; i++)
                     zs[j][i] += __shfl(zp, 4 * g + i, 64);
             }
-            if (full || rok) {
+            const bool ok = full || rok;
+            if constexpr (FW) {
+                const __amdgpu_buffer_rsrc_t rk = buf_rsrc(dK + (rb + t0) * D);
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    buffer_store_f4(rk, ok ? (unsigned)(l16 * D + 16 * (2 * hh + j) + 4 * g) * 4u
+                                           : kDropOffset, dk[j]);
+            } else if (ok) {
                 float* krow = dK + (rb + t0 + l16) * D;
 #pragma unroll
                 for (int j = 0; j < 2; j++)
