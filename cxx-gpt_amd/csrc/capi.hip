@@ -434,6 +434,38 @@ int cxg_phi_hexp_bwd(const float* dphi, const float* x, float* dx, size_t N, siz
 }
 
 // ---------------------------------------------------------------------------
+// rotary position embedding
+// ---------------------------------------------------------------------------
+static int rope_common(float* Q, float* K, size_t B, size_t S, size_t D, size_t head_dim,
+                       float sign, cxg_stream_t stream)
+{
+    if (head_dim < 2 || head_dim % 2 != 0 || head_dim > (size_t)ROPE_MAX_HEAD_DIM ||
+        D % head_dim != 0)
+        return CXG_ERR_DIMS;
+    if (B == 0 || S == 0 || D == 0)
+        return CXG_OK;
+    if (!fits_int(S) || !fits_int(D) || B > ((size_t)1 << 40) / S ||
+        B * S > ((size_t)1 << 42) / D)
+        return CXG_ERR_DIMS;
+    if (!Q && !K)
+        return CXG_ERR_NULL;
+    return hip_status(rope_launch(Q, K, (long)B, (int)S, (int)D, (int)head_dim, sign,
+                                  (hipStream_t)stream));
+}
+
+int cxg_rope_fwd(float* Q, float* K, size_t B, size_t S, size_t D, size_t head_dim,
+                 cxg_stream_t stream)
+{
+    return rope_common(Q, K, B, S, D, head_dim, 1.0f, stream);
+}
+
+int cxg_rope_bwd(float* dQ, float* dK, size_t B, size_t S, size_t D, size_t head_dim,
+                 cxg_stream_t stream)
+{
+    return rope_common(dQ, dK, B, S, D, head_dim, -1.0f, stream);
+}
+
+// ---------------------------------------------------------------------------
 // timing hook
 // ---------------------------------------------------------------------------
 void cxg_prof_enable(int on)

@@ -46,4 +46,15 @@ hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
                                float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,
                                hipStream_t st);
 
+// Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
+// may be null, and they may be one buffer).  Frequencies of pairs 0 ..
+// head_dim/2-1 travel in the kernel arguments.
+constexpr int ROPE_MAX_HEAD_DIM = 1024;
+struct RopeFreqs {
+    float w[ROPE_MAX_HEAD_DIM / 2];
+};
+void rope_freqs(int head_dim, RopeFreqs* fr);
+hipError_t rope_launch(float* Q, float* K, long B, int S, int D, int head_dim, float sign,
+                       hipStream_t st);
+
 } // namespace cxg

@@ -43,6 +43,8 @@ SIGNATURES = {
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_rope_fwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
+    "cxg_rope_bwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_prof_enable": [ctypes.c_int],
     "cxg_prof_reset": [],
     "cxg_prof_query": [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
@@ -188,6 +190,15 @@ def phi_hexp_fwd(x, phi, N, D, E, stream=None):
 
 def phi_hexp_bwd(dphi, x, dx, N, D, E, stream=None):
     _call("cxg_phi_hexp_bwd", _ptr(dphi), _ptr(x), _ptr(dx), N, D, E, _stream(stream))
+
+
+# ------------------------------------------------------------------ RoPE
+def rope_fwd(Q, K, B, S, D, head_dim, stream=None):
+    _call("cxg_rope_fwd", _ptr(Q), _ptr(K), B, S, D, head_dim, _stream(stream))
+
+
+def rope_bwd(dQ, dK, B, S, D, head_dim, stream=None):
+    _call("cxg_rope_bwd", _ptr(dQ), _ptr(dK), B, S, D, head_dim, _stream(stream))
 
 
 # ------------------------------------------------------------------ timing hook

@@ -150,6 +150,18 @@ int cxg_phi_hexp_fwd(const float *x, float *phi, size_t N, size_t D, size_t E,
 int cxg_phi_hexp_bwd(const float *dphi, const float *x, float *dx, size_t N, size_t D,
                      size_t E, cxg_stream_t stream);
 
+/* ===================== rotary position embedding =====================
+ * two_stage_cuda::rope_fwd / rope_bwd (two_stage_cuda_kernels.cuh:72-76,
+ * two_stage_cuda_kernels.cu:1810-1878), in place on (B*S, D) rows: pair i of
+ * each head of width head_dim in a row at position p = row % S rotates by
+ * +-p * 10000^(-2i/head_dim) (fwd +, bwd - = the inverse).  Either pointer
+ * may be NULL (that tensor is skipped); Q == K rotates the buffer twice, as
+ * the reference does.  head_dim even, 2..1024, D % head_dim == 0. */
+int cxg_rope_fwd(float *Q, float *K, size_t B, size_t S, size_t D, size_t head_dim,
+                 cxg_stream_t stream);
+int cxg_rope_bwd(float *dQ, float *dK, size_t B, size_t S, size_t D, size_t head_dim,
+                 cxg_stream_t stream);
+
 /* ===================== per-kernel timing hook =====================
  * Off by default.  When on, each kernel launch is bracketed by HIP events on
  * its stream; cxg_prof_query synchronises them and returns the summed device

@@ -123,6 +123,21 @@ void kernel_attn_bwd_dKdV(const CT& Q, const CT& K, const CT& V, const CT& dnum,
           "kernel_attn_bwd_dKdV");
 }
 
+// two_stage_cuda_kernels.cuh:72-76 (in place; Q and K may be one tensor)
+template <class CT>
+void rope_fwd(CT& Q, CT& K, size_t B, size_t S, size_t D, size_t head_dim)
+{
+    using namespace cxg_dropin;
+    check(cxg_rope_fwd(mptr(Q), mptr(K), B, S, D, head_dim, nullptr), "rope_fwd");
+}
+
+template <class CT>
+void rope_bwd(CT& dQ, CT& dK, size_t B, size_t S, size_t D, size_t head_dim)
+{
+    using namespace cxg_dropin;
+    check(cxg_rope_bwd(mptr(dQ), mptr(dK), B, S, D, head_dim, nullptr), "rope_bwd");
+}
+
 } // namespace two_stage_cuda
 
 namespace linear_cuda {

@@ -754,3 +754,26 @@ void orc_phi_hexp_backward(const float *dphi, const float *x, float *dx,
             }
         }
 }
+
+/* ---------------- rotary position embedding ----------------
+ * kernel_test.cpp:451-459 (rope_one) and :460-471 (ref_rope): the same float
+ * expressions (powf of a float exponent, the angle as a float product, cosf
+ * / sinf of it), rows in order. */
+void orc_rope(float *X, size_t B, size_t S, size_t D, size_t head_dim, float sign)
+{
+    const float base = 10000.0f;
+    const size_t rows = B * S;
+    for (size_t r = 0; r < rows; r++) {
+        const size_t p = r % S;
+        for (size_t h = 0; h < D / head_dim; h++)
+            for (size_t i = 0; i < head_dim / 2; i++) {
+                const float w = powf(base, -2.0f * (float)i / (float)head_dim);
+                const float ang = sign * (float)p * w;
+                const float c = cosf(ang), s = sinf(ang);
+                float *x = X + r * D + h * head_dim + 2 * i;
+                const float a = x[0], b = x[1];
+                x[0] = a * c - b * s;
+                x[1] = a * s + b * c;
+            }
+    }
+}

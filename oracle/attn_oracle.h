@@ -149,6 +149,15 @@ void orc_phi_hexp_forward(const float *x, float *phi, size_t N, size_t D, size_t
 void orc_phi_hexp_backward(const float *dphi, const float *x, float *dx,
                            size_t N, size_t D, size_t E);
 
+/* ---------------- rotary position embedding ----------------
+ * src/TwoStage/kernel_test.cpp:451-471 (ref_rope / rope_one): X (B*S, D),
+ * heads of width head_dim; row r has position p = r % S; pair i of a head
+ * rotates by sign * p * w_i, w_i = powf(10000, -2i/head_dim), all in float:
+ *   x'_2i = x_2i cos - x_2i+1 sin,   x'_2i+1 = x_2i sin + x_2i+1 cos.
+ * sign = +1: two_stage_cuda::rope_fwd; -1: rope_bwd (the inverse rotation).
+ * In place. */
+void orc_rope(float *X, size_t B, size_t S, size_t D, size_t head_dim, float sign);
+
 #ifdef __cplusplus
 }
 #endif

@@ -248,3 +248,10 @@ def phi_hexp_backward(dphi, x, D, E):
     dx = _z(N, E)
     lib().orc_phi_hexp_backward(_p(dphi), _p(x), _p(dx), _sz(N), _sz(D), _sz(E))
     return dx
+
+
+def rope(X, B, S, D, head_dim, sign):
+    """kernel_test.cpp:451-471 ref_rope: returns the rotated copy of X (B*S, D)."""
+    Y = np.array(X, dtype=np.float32, copy=True, order="C")
+    lib().orc_rope(_p(Y), _sz(B), _sz(S), _sz(D), _sz(head_dim), ctypes.c_float(sign))
+    return Y

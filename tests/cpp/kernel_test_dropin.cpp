@@ -1,5 +1,5 @@
 // kernel_test_dropin.cpp -- the reference's kernel-level test
-// (src/TwoStage/kernel_test.cpp:210-441) rebuilt on this library's C++
+// (src/TwoStage/kernel_test.cpp:210-499) rebuilt on this library's C++
 // drop-in wrappers (include/cxxgpt_dropin.hpp) and the HIP-backed TensorN
 // stand-in, so the call sites read exactly as the reference's do.
 //
@@ -169,6 +169,36 @@ static void linear_gpt_block(size_t B, size_t S, size_t E)
     expect("lgpt phi_elu_backward", t2v(dxq.toTensor()), rdxq);
 }
 
+// kernel_test.cpp:443-499: RoPE forward and backward against ref_rope, then
+// the round trip with Q and K one tensor (rotated twice each way).
+static void rope_block()
+{
+    const size_t B = 2, S = 6, D = 16, hd = 8, dim = B * S;
+    auto Q = draw(dim * D);
+    auto K = draw(dim * D);
+    const auto Q0 = Q;
+    auto cQ = up(Q, {dim, D});
+    auto cK = up(K, {dim, D});
+    two_stage_cuda::rope_fwd(cQ, cK, B, S, D, hd);
+    orc_rope(Q.data(), B, S, D, hd, 1.0f);
+    orc_rope(K.data(), B, S, D, hd, 1.0f);
+    expect("rope fwd Q", t2v(cQ.toTensor()), Q);
+    expect("rope fwd K", t2v(cK.toTensor()), K);
+    auto dQ = draw(dim * D);
+    auto dK = draw(dim * D);
+    auto cdQ = up(dQ, {dim, D});
+    auto cdK = up(dK, {dim, D});
+    two_stage_cuda::rope_bwd(cdQ, cdK, B, S, D, hd);
+    orc_rope(dQ.data(), B, S, D, hd, -1.0f);
+    orc_rope(dK.data(), B, S, D, hd, -1.0f);
+    expect("rope bwd dQ", t2v(cdQ.toTensor()), dQ);
+    expect("rope bwd dK", t2v(cdK.toTensor()), dK);
+    auto cQ2 = up(Q0, {dim, D});
+    two_stage_cuda::rope_fwd(cQ2, cQ2, B, S, D, hd);
+    two_stage_cuda::rope_bwd(cQ2, cQ2, B, S, D, hd);
+    expect("rope roundtrip", t2v(cQ2.toTensor()), Q0);
+}
+
 int main()
 {
     orc_mt_seed(&g_rng, 1234);   // kernel_test.cpp:12
@@ -179,6 +209,7 @@ int main()
     lin_block("flat", 2, 5, 7, 6);
     mha_block("big S=256", 2, 256, 2, 64);
     lin_block("chunk", 2, 32, 256, 256);
+    rope_block();
     // LinearGPT's path, which the reference's kernel test does not cover
     linear_gpt_block(2, 40, 48);
     hipError_t e = hipDeviceSynchronize();

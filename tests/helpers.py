@@ -62,6 +62,13 @@ def kernel_test_inputs():
     lin_block("flat", 2, 5, 7, 6)          # :335-374
     mha_block("bigS", 2, 256, 2, 64)       # :377-409
     lin_block("chunk", 2, 32, 256, 256)    # :410-441
+    # :443-489 RoPE: Q, K then dQ, dK, each (B*S, D)
+    B, S, D, hd = 2, 6, 16, 8
+    n = B * S * D
+    out["rope"] = dict(Q=g.frand(n).reshape(B * S, D), K=g.frand(n).reshape(B * S, D),
+                       B=B, S=S, D=D, hd=hd)
+    out["rope"]["dQ"] = g.frand(n).reshape(B * S, D)
+    out["rope"]["dK"] = g.frand(n).reshape(B * S, D)
     return out
 
 

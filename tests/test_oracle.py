@@ -343,3 +343,69 @@ def test_planted_mistakes_are_caught(kt):
                                   transpose_state=True), gold)  # state [d][e] read as [e][d]
     # eps placement: den + 1 would be caught; den + 1e-8 vs none is below the bar by design
     assert _rejects(_np_kattn_fwd(c["Q"], c["K"], c["V"], B, S, D, E, 1.0), gold)
+
+
+# ------------------------------------------------------------------ RoPE
+def _np_rope64(X, S, D, hd, sign, freq_exp=-2.0, swap=False):
+    """Independent float64 restatement of the rotation (complex-number form):
+    pair (x_2i, x_2i+1) of each head is x_2i + j x_2i+1 times exp(j sign p w_i),
+    w_i = 10000^(freq_exp i / hd).  `freq_exp` and `swap` plant mistakes."""
+    rows = X.shape[0]
+    p = (np.arange(rows) % S).astype(np.float64)[:, None]
+    i = np.arange(hd // 2, dtype=np.float64)
+    w = 10000.0 ** (freq_exp * i / hd)
+    x = X.astype(np.float64).reshape(rows, D // hd, hd // 2, 2)
+    z = x[..., 0] + 1j * x[..., 1]
+    if swap:
+        z = x[..., 1] + 1j * x[..., 0]
+    z = z * np.exp(1j * sign * p[:, :, None] * w[None, None, :])
+    out = np.stack([z.real, z.imag], axis=-1)
+    return out.reshape(rows, D)
+
+
+def test_rope_oracle_vs_complex_form(kt):
+    """kernel_test.cpp:443-489 block (and a wider one): the float oracle agrees
+    with the float64 complex-rotation form, forward and backward."""
+    r = kt["rope"]
+    B, S, D, hd = r["B"], r["S"], r["D"], r["hd"]
+    for X, sign in ((r["Q"], 1.0), (r["K"], 1.0), (r["dQ"], -1.0), (r["dK"], -1.0)):
+        assert_close(orc.rope(X, B, S, D, hd, sign), _np_rope64(X, S, D, hd, sign), "rope")
+    rng = np.random.default_rng(4)
+    X = rng.standard_normal((3 * 40, 96)).astype(np.float32)
+    for hd in (96, 32, 2):
+        assert_close(orc.rope(X, 3, 40, 96, hd, 1.0), _np_rope64(X, 40, 96, hd, 1.0),
+                     f"rope hd={hd}")
+
+
+def test_rope_invariants():
+    rng = np.random.default_rng(5)
+    B, S, D, hd = 2, 33, 64, 16
+    X = rng.standard_normal((B * S, D)).astype(np.float32)
+    Y = orc.rope(X, B, S, D, hd, 1.0)
+    # position 0 of every sequence is left exactly as it was (cos 0 = 1, sin 0 = 0)
+    np.testing.assert_array_equal(Y[0::S], X[0::S])
+    # rotations preserve each pair's length
+    n0 = np.hypot(X[:, 0::2].astype(np.float64), X[:, 1::2])
+    n1 = np.hypot(Y[:, 0::2].astype(np.float64), Y[:, 1::2])
+    assert np.max(np.abs(n0 - n1)) < 1e-5
+    # the backward is the inverse rotation
+    assert_close(orc.rope(Y, B, S, D, hd, -1.0), X, "rope round trip")
+    # pair 0 has w = 1: (1, 0) at position p becomes (cos p, sin p)
+    E = np.zeros((S, 2), dtype=np.float32)
+    E[:, 0] = 1.0
+    R = orc.rope(E, 1, S, 2, 2, 1.0)
+    p = np.arange(S)
+    assert np.max(np.abs(R[:, 0] - np.cos(p))) < 1e-6
+    assert np.max(np.abs(R[:, 1] - np.sin(p))) < 1e-6
+
+
+def test_rope_planted_mistakes_are_caught(kt):
+    r = kt["rope"]
+    B, S, D, hd = r["B"], r["S"], r["D"], r["hd"]
+    X = r["Q"]
+    got = orc.rope(X, B, S, D, hd, 1.0)
+    assert not _rejects(got, _np_rope64(X, S, D, hd, 1.0))
+    assert _rejects(got, _np_rope64(X, S, D, hd, -1.0))                  # wrong sign
+    assert _rejects(got, _np_rope64(X, S, D, hd, 1.0, freq_exp=-1.0))    # wrong frequencies
+    assert _rejects(got, _np_rope64(X, S, D, hd, 1.0, swap=True))        # pair order swapped
+    assert _rejects(got, _np_rope64(X, S + 1, D, hd, 1.0))               # wrong positions
