@@ -20,6 +20,8 @@ them can be made the reported workload with --workload NAME):
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
+  rope      RoPE fwd + bwd on the stage-1 q/k heads at the C2 shape (in place),
+            GB/s of compulsory I/O (each tensor read and written once)
   copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
@@ -121,7 +123,8 @@ def attribute(cx, step, steps):
     cx.prof_enable(False)
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
-              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "phi_hexp_fwd", "phi_hexp_bwd"):
+              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "phi_hexp_fwd", "phi_hexp_bwd",
+              "rope_fwd", "rope_bwd"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)
@@ -304,9 +307,43 @@ def _copy(c, steps, warmup):
                 frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
 
+def _rope(c, name, B, S, H, Dh, seed, steps, warmup):
+    """RoPE on the stage-1 q/k heads of two_stage_gpt.hpp (:102 forward, :174
+    backward) at the C2 shape: cxg_rope_fwd on (Q, K) then cxg_rope_bwd on
+    (dQ, dK), all (B*S, H*Dh), in place.  Compulsory I/O: each tensor read and
+    written once per call."""
+    g = c.gen(seed)
+    shp = (B * S, H * Dh)
+    Q, K, dQ, dK = [c.randn(g, *shp) for _ in range(4)]
+    P = _ptr
+    D = H * Dh
+    step = Stepper(c.cx.lib(), [
+        ("cxg_rope_fwd", (P(Q), P(K), B, S, D, Dh, c.sp)),
+        ("cxg_rope_bwd", (P(dQ), P(dK), B, S, D, Dh, c.sp)),
+    ])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    per_call = 2 * 2 * B * S * D * 4        # two tensors, read + write
+    total = 2 * per_call
+    value = total / (ms * 1e-3) / 1e9
+    dom = max(att, key=lambda k: att[k][0])
+    ach = per_call / (att[dom][0] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": per_call,
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: RoPE forward + backward on the stage-1 q/k heads "
+                                    f"(two_stage_cuda::rope_fwd/rope_bwd), in place",
+                        "B": B, "S": S, "H": H, "Dh": Dh, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=[Q, K, dQ, dK, B, S, D, Dh])
+
+
 def run_workload(c, name, steps, warmup):
     if name == "copy":
         return _copy(c, steps, warmup)
+    if name == "rope":
+        return _rope(c, name, 8, 256, 12, 64, 81, steps, warmup)
     if name == "c2":
         return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
     if name == "c2legacy":
@@ -335,7 +372,11 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
     dims = inputs[4:]
     reps, t0 = 0, time.perf_counter()
     while True:
-        if name.startswith("c2") or name == "c5":
+        if name == "rope":
+            B, S, D, hd = dims
+            for X, sign in ((Q, 1.0), (K, 1.0), (V, -1.0), (dO, -1.0)):
+                orc.rope(X, B, S, D, hd, sign)
+        elif name.startswith("c2") or name == "c5":
             B, S, H, Dh = dims
             O = orc.mha_fwd(Q, K, V, B, S, H, Dh, nthreads=nthreads)
             orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=nthreads)
@@ -350,6 +391,13 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
         if el >= budget_s or reps >= 1000:
             break
     per = el / reps
+    if name == "rope":
+        B, S, D, hd = dims
+        return dict(value=round(2 * 2 * 2 * B * S * D * 4 / per / 1e9, 4), unit="GB/s", cores=1,
+                    kind="port",
+                    sample=f"{reps} rope fwd+bwd passes (B{B} S{S} D{D} head_dim {hd}) through "
+                           f"the C oracle's ref_rope restatement, one thread; {el:.1f} s wall, "
+                           f"{per * 1e3:.1f} ms/pass")
     if name.startswith("c2") or name == "c5":
         B, S, H, Dh = dims
         return dict(value=round(mha_flops(B, S, H, Dh) / per / 1e12, 6), unit="TFLOP/s",
@@ -373,7 +421,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "copy"])
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "rope", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -414,7 +462,7 @@ def main():
     }
     sec = {}
     if not args.no_secondary and args.workload == "c2":
-        for name in ("c2legacy", "c3", "c3s256", "c4", "c5"):
+        for name in ("c2legacy", "c3", "c3s256", "c4", "c5", "rope"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),
