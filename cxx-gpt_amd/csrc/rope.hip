@@ -25,7 +25,7 @@
 namespace cxg {
 
 constexpr int ROPE_THREADS = 256;
-constexpr int ROPE_ROWS = 4;
+constexpr int ROPE_ROWS = 2;
 
 // VEC: rows of Q and K 8-byte aligned (pairs move as float2).  Q and K may be
 // one buffer (ALIAS), so they are not declared restrict.
