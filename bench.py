@@ -22,6 +22,8 @@ them can be made the reported workload with --workload NAME):
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
   rope      RoPE fwd + bwd on the stage-1 q/k heads at the C2 shape (in place),
             GB/s of compulsory I/O (each tensor read and written once)
+  c2rope    C2 with RoPE fused into the MHA kernels (cxg_mha_rope_fwd/bwd)
+  c2ropesep C2 with RoPE as separate passes, the reference's call sequence
   copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
@@ -124,7 +126,7 @@ def attribute(cx, step, steps):
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "phi_hexp_fwd", "phi_hexp_bwd",
-              "rope_fwd", "rope_bwd"):
+              "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)
@@ -171,7 +173,10 @@ class Ctx:
         return self.torch.empty(*shape, device=self.dev)
 
 
-def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup):
+def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
+    """rope: None (plain MHA), "fused" (cxg_mha_rope_fwd/bwd) or "separate"
+    (cxg_rope_fwd, cxg_mha_fwd, cxg_mha_bwd, cxg_rope_bwd: the reference's call
+    sequence at two_stage_gpt.hpp:102-106, :171-174)."""
     g = c.gen(seed)
     shp = (B * S, H * Dh)
     Q, K, V, dO = [c.randn(g, *shp) for _ in range(4)]
@@ -180,17 +185,25 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup):
     ws_bytes = c.cx.mha_bwd_workspace_size(B, S, H, Dh)
     ws = c.empty(max(1, ws_bytes // 4))
     P = _ptr
-    step = Stepper(c.cx.lib(), [
-        ("cxg_mha_fwd", (P(Q), P(K), P(V), P(O), P(lse), B, S, H, Dh, c.sp)),
-        ("cxg_mha_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(lse), P(dQ), P(dK), P(dV),
-                         B, S, H, Dh, P(ws), ws_bytes, c.sp)),
-    ])
+    fwd, bwd = ("cxg_mha_rope_fwd", "cxg_mha_rope_bwd") if rope == "fused" else \
+        ("cxg_mha_fwd", "cxg_mha_bwd")
+    calls = [
+        (fwd, (P(Q), P(K), P(V), P(O), P(lse), B, S, H, Dh, c.sp)),
+        (bwd, (P(Q), P(K), P(V), P(O), P(dO), P(lse), P(dQ), P(dK), P(dV),
+               B, S, H, Dh, P(ws), ws_bytes, c.sp)),
+    ]
+    if rope == "separate":
+        calls = [("cxg_rope_fwd", (P(Q), P(K), B, S, H * Dh, Dh, c.sp))] + calls + \
+                [("cxg_rope_bwd", (P(dQ), P(dK), B, S, H * Dh, Dh, c.sp))]
+    step = Stepper(c.cx.lib(), calls)
     ms = timed(step, steps, warmup, c.stream)
     att = attribute(c.cx, step, max(10, min(steps, 100)))
     flops = mha_flops(B, S, H, Dh)
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
-              "mha_bwd": mha_flops(B, S, H, Dh, fwd=False)}
+              "mha_bwd": mha_flops(B, S, H, Dh, fwd=False),
+              "mha_rope_fwd": mha_flops(B, S, H, Dh, bwd=False),
+              "mha_rope_bwd": mha_flops(B, S, H, Dh, fwd=False)}
     dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
     ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
     roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
@@ -201,8 +214,13 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup):
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: causal softmax MHA fwd+bwd ("
-                                    + ("cxg_mha_fwd with lse -> cxg_mha_bwd" if use_lse else
-                                       "legacy signatures, no lse") + ")",
+                                    + {None: ("cxg_mha_fwd with lse -> cxg_mha_bwd" if use_lse
+                                              else "legacy signatures, no lse"),
+                                       "fused": "RoPE fused: cxg_mha_rope_fwd -> "
+                                                "cxg_mha_rope_bwd",
+                                       "separate": "RoPE as separate passes: cxg_rope_fwd, "
+                                                   "cxg_mha_fwd, cxg_mha_bwd, cxg_rope_bwd"}[rope]
+                                    + ")",
                         "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops},
                 frac=value / FP32_MFMA_PEAK_TFLOPS,
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
@@ -344,6 +362,10 @@ def run_workload(c, name, steps, warmup):
         return _copy(c, steps, warmup)
     if name == "rope":
         return _rope(c, name, 8, 256, 12, 64, 81, steps, warmup)
+    if name == "c2rope":
+        return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup, rope="fused")
+    if name == "c2ropesep":
+        return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup, rope="separate")
     if name == "c2":
         return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
     if name == "c2legacy":
@@ -421,7 +443,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "rope", "copy"])
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "rope", "c2rope",
+                             "c2ropesep", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -462,7 +485,7 @@ def main():
     }
     sec = {}
     if not args.no_secondary and args.workload == "c2":
-        for name in ("c2legacy", "c3", "c3s256", "c4", "c5", "rope"):
+        for name in ("c2legacy", "c3", "c3s256", "c4", "c5", "rope", "c2rope", "c2ropesep"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

@@ -172,6 +172,23 @@ int cxg_mha_fwd(const float* Q, const float* K, const float* V, float* O, float*
                                      (hipStream_t)stream));
 }
 
+int cxg_mha_rope_fwd(const float* Q, const float* K, const float* V, float* O, float* lse,
+                     size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream)
+{
+    bool empty;
+    int st = mha_check(B, S, H, Dh, &empty);
+    if (st == CXG_OK && Dh % 2 != 0)
+        st = CXG_ERR_DIMS;
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O)
+        return CXG_ERR_NULL;
+    MhaRope rope;
+    mha_rope_freqs((int)Dh, &rope);
+    return hip_status(mha_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)H, (int)Dh,
+                                     (hipStream_t)stream, &rope));
+}
+
 size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh)
 {
     (void)Dh;
@@ -179,15 +196,23 @@ size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh)
     return 2 * round_up(rows * sizeof(float), 256);
 }
 
-int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
-                const float* dO, const float* lse, float* dQ, float* dK, float* dV,
-                size_t B, size_t S, size_t H, size_t Dh, void* workspace,
-                size_t workspace_bytes, cxg_stream_t stream)
+static int mha_bwd_common(const float* Q, const float* K, const float* V, const float* O,
+                          const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                          size_t B, size_t S, size_t H, size_t Dh, void* workspace,
+                          size_t workspace_bytes, cxg_stream_t stream, bool with_rope)
 {
     bool empty;
     int st = mha_check(B, S, H, Dh, &empty);
+    if (st == CXG_OK && with_rope && Dh % 2 != 0)
+        st = CXG_ERR_DIMS;
     if (st != CXG_OK || empty)
         return st;
+    MhaRope rope_freq;
+    const MhaRope* rope = nullptr;
+    if (with_rope) {
+        mha_rope_freqs((int)Dh, &rope_freq);
+        rope = &rope_freq;
+    }
     if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
@@ -202,7 +227,7 @@ int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
     hipError_t e;
     if (lse == nullptr) {
         // statistics-only forward pass (the reference recomputes them too)
-        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s);
+        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s, rope);
         if (e != hipSuccess)
             return hip_status(e);
         lse = lse_ws;
@@ -210,8 +235,26 @@ int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
     e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
     if (e != hipSuccess)
         return hip_status(e);
-    e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s);
+    e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s, rope);
     return hip_status(e);
+}
+
+int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
+                const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                size_t B, size_t S, size_t H, size_t Dh, void* workspace,
+                size_t workspace_bytes, cxg_stream_t stream)
+{
+    return mha_bwd_common(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, workspace,
+                          workspace_bytes, stream, false);
+}
+
+int cxg_mha_rope_bwd(const float* Q, const float* K, const float* V, const float* O,
+                     const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                     size_t B, size_t S, size_t H, size_t Dh, void* workspace,
+                     size_t workspace_bytes, cxg_stream_t stream)
+{
+    return mha_bwd_common(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, workspace,
+                          workspace_bytes, stream, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -37,14 +37,23 @@ struct ProfScope {
 // ---- launchers (defined next to their kernels) -----------------------------
 // Softmax MHA.  Layout (B*S, H*Dh) row-major.  lse is [B*H][S] (natural log of
 // the softmax denominator of the scaled scores, max included).
+// Rotary embedding fused into the MHA kernels (rope != nullptr): Q and K are
+// read unrotated and rotated per head (head_dim = Dh) as they are loaded, and
+// the backward's dQ, dK are the gradients with respect to the unrotated
+// inputs.  w[i] = 10000^(-2i/Dh), i < Dh/2.
+struct MhaRope {
+    float w[128];
+};
+void mha_rope_freqs(int Dh, MhaRope* r);
 hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float* O,
-                          float* lse, int B, int S, int H, int Dh, hipStream_t st);
+                          float* lse, int B, int S, int H, int Dh, hipStream_t st,
+                          const MhaRope* rope = nullptr);
 hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ,
                                int B, int S, int H, int Dh, hipStream_t st);
 hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
                                const float* dO, const float* lse, const float* Di,
                                float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,
-                               hipStream_t st);
+                               hipStream_t st, const MhaRope* rope = nullptr);
 
 // Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
 // may be null, and they may be one buffer).  Frequencies of pairs 0 ..

@@ -43,6 +43,50 @@ namespace cxg {
 constexpr int MHA_BM = 64;   // query rows per tile
 constexpr int MHA_BN = 64;   // key rows per tile
 
+// Rotary embedding of one f4 of a row at position pos, columns c .. c+3 of a
+// head (c a multiple of 4): pairs (c, c+1) and (c+2, c+3) rotate by
+// sign * pos * w[pair] (sign -1: the inverse, for gradients).
+// sin and cos of a float angle a (radians, |a| < 2^20): reduced to [-pi, pi]
+// in double precision (k = rint(a / 2pi), r = a - 2pi k: error below 1e-10 at
+// these magnitudes), then evaluated on r / 2pi revolutions by the hardware
+// v_sin_f32 / v_cos_f32 (max abs error 1.3e-7 over [-0.5, 0.5] revolutions,
+// measured on MI355X against double).  About ten instructions, against the
+// general-argument library routine's hundred.
+__device__ __forceinline__ void sincos_rev(float a, float* s, float* c)
+{
+    constexpr double kInv2Pi = 0.15915494309189535;
+    constexpr double k2Pi = 6.283185307179586;
+    const double ad = (double)a;
+    const double k = rint(ad * kInv2Pi);
+    const float x = (float)(fma(-k, k2Pi, ad) * kInv2Pi);
+    *s = __builtin_amdgcn_sinf(x);
+    *c = __builtin_amdgcn_cosf(x);
+}
+
+// w: the frequency table (LDS copy of MhaRope::w).
+__device__ __forceinline__ f4 rope4(f4 v, int pos, int c, const float* w, float sign)
+{
+    float s0, c0, s1, c1;
+    sincos_rev(sign * (float)pos * w[c >> 1], &s0, &c0);
+    sincos_rev(sign * (float)pos * w[(c >> 1) + 1], &s1, &c1);
+    f4 o;
+    o[0] = v[0] * c0 - v[1] * s0;
+    o[1] = v[0] * s0 + v[1] * c0;
+    o[2] = v[2] * c1 - v[3] * s1;
+    o[3] = v[2] * s1 + v[3] * c1;
+    return o;
+}
+
+// Copy the rotary frequencies into LDS (by one lane, with uniform indices so
+// the kernel argument is read with scalar loads); the caller synchronises.
+__device__ __forceinline__ void rope_table(float* __restrict__ w, const MhaRope& rp)
+{
+    if (threadIdx.x == 0)
+#pragma unroll
+        for (int i = 0; i < 128; i++)
+            w[i] = rp.w[i];
+}
+
 // ROWS x DHP fp32 tile of one head, held in registers between its global load
 // and its LDS store (so the next tile's loads overlap the current tile's math).
 // Thread tid of NT owns f4 units u = tid + i*NT: row u / (DHP/4), column
@@ -76,6 +120,23 @@ struct TileRegs {
             if (NU % NT == 0 || u < NU) {
                 const int row = u / CPR, c = 4 * (u - row * CPR);
                 *reinterpret_cast<f4*>(&T[row * LD + c]) = r[i];
+            }
+        }
+    }
+    // row-major like store(), each row rotated (positions row0 + row, clamped
+    // to S-1 as the load was; columns past Dh hold zeros or repeats that the
+    // consumers mask)
+    template <int LD>
+    __device__ __forceinline__ void store_rope(float* __restrict__ T, int tid, int row0, int S,
+                                               const float* rw) const
+    {
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = tid + i * NT;
+            if (NU % NT == 0 || u < NU) {
+                const int row = u / CPR, c = 4 * (u - row * CPR);
+                *reinterpret_cast<f4*>(&T[row * LD + c]) =
+                    rope4(r[i], min(row0 + row, S - 1), c, rw, 1.0f);
             }
         }
     }
@@ -167,11 +228,11 @@ __device__ __forceinline__ int job_tid()
 // once the last key tile of a job has been through its math, requests the
 // next job's Q rows and first two K/V tiles, so that they arrive while the
 // current job merges its key splits and writes O.
-template <int DHP, int NSPLIT, bool VEC, bool WRITE_O>
+template <int DHP, int NSPLIT, bool VEC, bool WRITE_O, bool ROPE>
 __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
-    float qscale, int pair_cus)
+    float qscale, int pair_cus, const MhaRope rope)
 {
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
@@ -179,6 +240,11 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
     constexpr int NDT = DHP / 16;
     constexpr int NKT = 4 / NSPLIT;   // 16-key blocks per wave per tile
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
+    __shared__ float rope_w[ROPE ? 128 : 1];
+    if constexpr (ROPE) {
+        rope_table(rope_w, rope);
+        __syncthreads();
+    }
 
     const int njobs = nqb * BH;
     const long rs = (long)H * Dh;
@@ -253,9 +319,14 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         for (int dt = 0; dt < NDT; dt++)
             oacc[dt] = f4zero();
         float m_run = -1e30f, l_run = 0.0f;
+        // kb: the key tile held in (kx, vx); K is rotated on its way to LDS
+        // under ROPE.
         auto store_kv = [&](const TileRegs<DHP, MHA_BN, NT, VEC>& kx,
-                            const TileRegs<DHP, MHA_BN, NT, VEC>& vx, float* buf) {
-            kx.template store<KS>(buf, tid);
+                            const TileRegs<DHP, MHA_BN, NT, VEC>& vx, float* buf, int kb) {
+            if constexpr (ROPE)
+                kx.template store_rope<KS>(buf, tid, kb * MHA_BN, S, rope_w);
+            else
+                kx.template store<KS>(buf, tid);
             if (WRITE_O)
                 vx.template store<KS>(buf + MHA_BN * KS, tid);
         };
@@ -345,10 +416,14 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             }
         };
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok) * qscale;
+        for (int dt = 0; dt < NDT; dt++) {
+            f4 q = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok);
+            if constexpr (ROPE)
+                q = rope4(q, min(myq, S - 1), 16 * dt + 4 * g, rope_w, 1.0f);
+            qreg[dt] = q * qscale;
+        }
         if constexpr (SM::DB) {
-            store_kv(kr, vr, smem);
+            store_kv(kr, vr, smem, 0);
             __builtin_amdgcn_sched_barrier(0);
             // Tiles past the last one repeat it (clamped index), so these
             // loads are the same on every path and the waits stay tight.
@@ -363,7 +438,7 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
                             TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) {
                 const float* cur = smem + (kb & 1) * SM::TILES;
                 tile(cur, cur + MHA_BN * KS, kb);
-                store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES);
+                store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES, kb + 1);
                 // Keep the refill below the LDS writes: issued earlier, the
                 // wait for the old data would include the new loads.
                 __builtin_amdgcn_sched_barrier(0);
@@ -392,7 +467,7 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
                 if (!PREFETCH && kb > 0)
                     load_kv(kr, vr, jc, kb);
                 __syncthreads();
-                store_kv(kr, vr, smem);
+                store_kv(kr, vr, smem, kb);
                 __syncthreads();
                 if (PREFETCH && kb + 1 < nkb)
                     load_kv(kr, vr, jc, kb + 1);
@@ -518,12 +593,12 @@ struct BwdSmem {
 // job has been through its key-side work, requests the next job's K/V rows
 // and first query tiles, so that they arrive while the current job finishes
 // its dQ jobs and dK/dV reduction.
-template <int DHP, int BM, int NSPLIT, bool VEC>
+template <int DHP, int BM, int NSPLIT, bool VEC, bool ROPE>
 __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
-    int BH, int nkb, float scale, float c2)
+    int BH, int nkb, float scale, float c2, const MhaRope rope)
 {
     using SM = BwdSmem<DHP, BM>;
     constexpr int NT = 256 * NSPLIT;
@@ -538,6 +613,11 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     // products, and the dQ blocks are paired across SIMDs.
     constexpr bool SKIP = NW == 8 && NQT == 4;
     __shared__ __attribute__((aligned(16))) float smem[SM::FLOATS];
+    __shared__ float rope_w[ROPE ? 128 : 1];
+    if constexpr (ROPE) {
+        rope_table(rope_w, rope);
+        __syncthreads();
+    }
     float* Kt = smem;
     // Stage i: Qs [BM][QS], dOs [BM][QS], dSs [BM][TS], lse_s [BM], di_s [BM].
     auto stage = [&](int i) { return smem + DHP * TS + i * SM::STAGE; };
@@ -629,8 +709,12 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             dk[dt] = f4zero();
             dv[dt] = f4zero();
         }
-        auto store_q = [&](const QTile& t, float* st) {
-            t.q.template store<QS>(st, tid);
+        // q0: the tile's first row (its Q rows are rotated on the way under ROPE)
+        auto store_q = [&](const QTile& t, float* st, int q0) __attribute__((always_inline)) {
+            if constexpr (ROPE)
+                t.q.template store_rope<QS>(st, tid, q0, S, rope_w);
+            else
+                t.q.template store<QS>(st, tid);
             t.d.template store<QS>(st + BM * QS, tid);
             if (tid < BM) {
                 st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
@@ -643,7 +727,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // first F of the wave's NQW query blocks lie wholly before its key
         // block (all masked: P = dS = 0) and are skipped; the dQ product never
         // reads their dS.
-        auto key_side_f = [&](float* st, int q0, auto first) {
+        auto key_side_f = [&](float* st, int q0, auto first) __attribute__((always_inline)) {
             constexpr int F = decltype(first)::value;
             // Raised issue priority for this MFMA-dense section: the other
             // wave of the SIMD fills its stalls instead of interleaving.
@@ -716,7 +800,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             }
             __builtin_amdgcn_s_setprio(0);
         };
-        auto key_side = [&](float* st, int q0) {
+        auto key_side = [&](float* st, int q0) __attribute__((always_inline)) {
             // Leading query blocks of the wave that end before its first key.
             int f = 0;
 #pragma unroll
@@ -742,8 +826,24 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // rows past S and columns past Dh are dropped by the descriptor's
         // bounds check rather than by a branch (byte offsets of a 64-row tile
         // stay below 2 GiB for H*Dh < 8M).
-        auto dq_store = [&](const f4& acc, int q0, int qt, int dt) {
+        auto dq_store = [&](f4 acc, int q0, int qt, int dt) __attribute__((always_inline)) {
             const int d = 16 * dt + l16;
+            if constexpr (ROPE) {
+                // Gradient w.r.t. the unrotated Q: rotate this contribution by
+                // -pos*w (linear, so the sum of rotated contributions is the
+                // rotated sum).  Columns d and d^1 form a pair; they sit in
+                // lanes l16 and l16^1.
+                const float wv = rope_w[d >> 1];
+                const bool odd = (l16 & 1) != 0;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int q = min(q0 + 16 * qt + 4 * g + r, S - 1);
+                    float sn, cs;
+                    sincos_rev(-(float)q * wv, &sn, &cs);
+                    const float other = __shfl_xor(acc[r], 1, 64);
+                    acc[r] = odd ? other * sn + acc[r] * cs : acc[r] * cs - other * sn;
+                }
+            }
             const __amdgpu_buffer_rsrc_t rq = buf_rsrc(dQ + base + (long)q0 * rs);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
@@ -755,7 +855,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         };
         const int dq_qt = SKIP ? pair_group(wave) : wave % NQT;
         // FULL: all four key blocks are live; otherwise those before kend.
-        auto query_side_f = [&](const float* st, int q0, int kend, auto full) {
+        auto query_side_f = [&](const float* st, int q0, int kend, auto full) __attribute__((always_inline)) {
             constexpr bool FULL = decltype(full)::value;
             const float* dSs = st + 2 * BM * QS;
             const int qt = dq_qt;
@@ -802,7 +902,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 }
             }
         };
-        auto query_side = [&](const float* st, int q0) {
+        auto query_side = [&](const float* st, int q0) __attribute__((always_inline)) {
             // Key blocks kt with a key at or before the block's last query.
             const int kend = (q0 + 16 * dq_qt + 15 - k0) / 16 + 1;
             if (!SKIP || kend >= 4)
@@ -815,6 +915,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             kreg[dt] = mask4(kreg[dt], 16 * dt + 4 * g, Dh, kok);
+            if constexpr (ROPE)
+                kreg[dt] = rope4(kreg[dt], min(mykey, S - 1), 16 * dt + 4 * g, rope_w, 1.0f);
             vreg[dt] = mask4(vreg[dt], 16 * dt + 4 * g, Dh, kok);
         }
         // K^T tile for the dQ product, written from the K operand registers by
@@ -838,7 +940,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             // after the key-side work, rather than at the top, leaves the dQ
             // atomics and loads of the previous iteration time to drain before
             // the wait for its registers.
-            store_q(t0, stage(qb0 & 1));
+            store_q(t0, stage(qb0 & 1), qb0 * BM);
             load_q(t0, jc, tile_q0(qb0 + 2));
             __syncthreads();
             // Iteration qb < nqb-1: registers tx hold tile qb+1 and are
@@ -847,7 +949,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 const int q0 = qb * BM;
                 float* cur = stage(qb & 1);
                 key_side(cur, q0);
-                store_q(tx, stage((qb + 1) & 1));
+                store_q(tx, stage((qb + 1) & 1), (qb + 1) * BM);
                 // Keep the refill below the LDS writes: issued earlier, the
                 // wait for the old data would include the new loads.
                 __builtin_amdgcn_sched_barrier(0);
@@ -887,7 +989,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 if (!PREFETCH && qb > qb0)
                     load_q(t0, jc, q0);
                 __syncthreads();
-                store_q(t0, st);
+                store_q(t0, st, q0);
                 __syncthreads();
                 if (PREFETCH && qb + 1 < nqb)
                     load_q(t0, jc, q0 + BM);
@@ -936,6 +1038,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             const long off = base + (long)mykey * rs;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
+                if constexpr (ROPE)   // gradient w.r.t. the unrotated K: the inverse rotation
+                    dk[dt] = rope4(dk[dt], mykey, 16 * dt + 4 * g, rope_w, -1.0f);
                 store4<VEC>(dK + off, 16 * dt + 4 * g, Dh, dk[dt] * scale);
                 store4<VEC>(dV + off, 16 * dt + 4 * g, Dh, dv[dt]);
             }
@@ -1000,9 +1104,10 @@ struct MhaSplits {
     static constexpr bool FWD_PAIR = DHP <= 64;
 };
 
-template <int DHP, bool VEC>
+template <int DHP, bool VEC, bool ROPE>
 static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, float* O,
-                                float* lse, int B, int S, int H, int Dh, hipStream_t st)
+                                float* lse, int B, int S, int H, int Dh, hipStream_t st,
+                                const MhaRope& rope)
 {
     constexpr int NS = MhaSplits<DHP>::FWD;
     const int BH = B * H;
@@ -1017,40 +1122,54 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
         grid.x = (unsigned)njobs;
     }
     if (O != nullptr) {
-        ProfScope ps(st, "mha_fwd");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true>), grid, block, 0, st, Q, K, V, O,
-                           lse, S, H, Dh, BH, nqb, qscale, pair);
+        ProfScope ps(st, ROPE ? "mha_rope_fwd" : "mha_fwd");
+        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true, ROPE>), grid, block, 0, st, Q, K,
+                           V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
     } else {
         ProfScope ps(st, "mha_stats");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, false>), grid, block, 0, st, Q, K, V, O,
-                           lse, S, H, Dh, BH, nqb, qscale, pair);
+        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, false, ROPE>), grid, block, 0, st, Q, K,
+                           V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
     }
     return hipGetLastError();
 }
 
 template <int DHP>
 static hipError_t fwd_dispatch(const float* Q, const float* K, const float* V, float* O,
-                               float* lse, int B, int S, int H, int Dh, hipStream_t st)
+                               float* lse, int B, int S, int H, int Dh, hipStream_t st,
+                               const MhaRope* rope)
 {
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      (O == nullptr || aligned16(O));
+    if (rope != nullptr) {
+        if (vec)
+            return fwd_dispatch2<DHP, true, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope);
+        return fwd_dispatch2<DHP, false, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope);
+    }
+    const MhaRope none{};
     if (vec)
-        return fwd_dispatch2<DHP, true>(Q, K, V, O, lse, B, S, H, Dh, st);
-    return fwd_dispatch2<DHP, false>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return fwd_dispatch2<DHP, true, false>(Q, K, V, O, lse, B, S, H, Dh, st, none);
+    return fwd_dispatch2<DHP, false, false>(Q, K, V, O, lse, B, S, H, Dh, st, none);
+}
+
+void mha_rope_freqs(int Dh, MhaRope* r)
+{
+    // kernel_test.cpp:453 (the reference's CPU RoPE): powf of the same float exponent
+    for (int i = 0; i < 128; i++)
+        r->w[i] = i < Dh / 2 ? powf(10000.0f, -2.0f * (float)i / (float)Dh) : 0.0f;
 }
 
 hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float* O, float* lse,
-                          int B, int S, int H, int Dh, hipStream_t st)
+                          int B, int S, int H, int Dh, hipStream_t st, const MhaRope* rope)
 {
     if (Dh <= 16)
-        return fwd_dispatch<16>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return fwd_dispatch<16>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     if (Dh <= 32)
-        return fwd_dispatch<32>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return fwd_dispatch<32>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     if (Dh <= 64)
-        return fwd_dispatch<64>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return fwd_dispatch<64>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     if (Dh <= 128)
-        return fwd_dispatch<128>(Q, K, V, O, lse, B, S, H, Dh, st);
-    return fwd_dispatch<256>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return fwd_dispatch<128>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
+    return fwd_dispatch<256>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
 }
 
 hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ, int B,
@@ -1069,10 +1188,11 @@ hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float
     return hipGetLastError();
 }
 
-template <int DHP>
+template <int DHP, bool ROPE>
 static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
-                               float* dV, int B, int S, int H, int Dh, hipStream_t st)
+                               float* dV, int B, int S, int H, int Dh, hipStream_t st,
+                               const MhaRope& rope)
 {
     constexpr int NS = MhaSplits<DHP>::BWD, BM = MhaSplits<DHP>::BWD_BM;
     const int BH = B * H;
@@ -1081,29 +1201,37 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
     dim3 grid(job_grid((long)nkb * BH, MhaSplits<DHP>::BWD_PER_CU, true)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
-    ProfScope ps(st, "mha_bwd");
+    ProfScope ps(st, ROPE ? "mha_rope_bwd" : "mha_bwd");
     if (vec)
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, true>), grid, block, 0, st, Q, K, V, dO,
-                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
+        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, true, ROPE>), grid, block, 0, st, Q, K, V, dO,
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
     else
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, false>), grid, block, 0, st, Q, K, V, dO,
-                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e);
+        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, false, ROPE>), grid, block, 0, st, Q, K, V, dO,
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
     return hipGetLastError();
 }
 
 hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
-                               float* dV, int B, int S, int H, int Dh, hipStream_t st)
+                               float* dV, int B, int S, int H, int Dh, hipStream_t st,
+                               const MhaRope* rope)
 {
+    const MhaRope none{};
+    const MhaRope& rp = rope != nullptr ? *rope : none;
+#define CXG_BWD(D)                                                                            \
+    return rope != nullptr                                                                    \
+               ? bwd_dispatch<D, true>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp)  \
+               : bwd_dispatch<D, false>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp)
     if (Dh <= 16)
-        return bwd_dispatch<16>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        CXG_BWD(16);
     if (Dh <= 32)
-        return bwd_dispatch<32>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        CXG_BWD(32);
     if (Dh <= 64)
-        return bwd_dispatch<64>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        CXG_BWD(64);
     if (Dh <= 128)
-        return bwd_dispatch<128>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
-    return bwd_dispatch<256>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st);
+        CXG_BWD(128);
+    CXG_BWD(256);
+#undef CXG_BWD
 }
 
 } // namespace cxg

@@ -31,6 +31,9 @@ SIGNATURES = {
     "cxg_mha_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz,
                     _vp],
     "cxg_mha_bwd_workspace_size": [_sz, _sz, _sz, _sz],
+    "cxg_mha_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
+    "cxg_mha_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp,
+                         _sz, _vp],
     "cxg_kattn_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_kattn_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_kattn_bwd_dQ": [_vp] * 8 + [_sz] * 4 + [_vp],
@@ -128,6 +131,19 @@ def mha_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, workspace=None, s
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _call("cxg_mha_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
           _ptr(dK), _ptr(dV), B, S, H, Dh, _ptr(workspace), ws_bytes, _stream(stream))
+
+
+def mha_rope_fwd(Q, K, V, O, B, S, H, Dh, lse=None, stream=None):
+    _call("cxg_mha_rope_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(lse), B, S, H, Dh,
+          _stream(stream))
+
+
+def mha_rope_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, workspace=None,
+                 stream=None):
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _call("cxg_mha_rope_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse),
+          _ptr(dQ), _ptr(dK), _ptr(dV), B, S, H, Dh, _ptr(workspace), ws_bytes,
+          _stream(stream))
 
 
 def mha_bwd_workspace_size(B, S, H, Dh):

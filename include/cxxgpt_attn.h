@@ -70,6 +70,21 @@ int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
                 size_t workspace_bytes, cxg_stream_t stream);
 size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh);
 
+/* RoPE fused into the MHA kernels.  No single counterpart in the reference:
+ * cxg_mha_rope_fwd(Q, K, ...) computes what two_stage_gpt.hpp:102-106 does
+ * with rope_fwd(Q, K, B, S, H*Dh, Dh) followed by fused_mha_fwd, reading Q
+ * and K unrotated and leaving them unchanged (they are rotated as they are
+ * loaded).  cxg_mha_rope_bwd takes the same unrotated Q, K and returns dQ,
+ * dK with respect to them: fused_mha_bwd on the rotated tensors followed by
+ * rope_bwd(dQ, dK) (two_stage_gpt.hpp:171-174).  Dh even; otherwise as
+ * cxg_mha_fwd / cxg_mha_bwd (lse from cxg_mha_rope_fwd, same workspace). */
+int cxg_mha_rope_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
+                     size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream);
+int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float *O,
+                     const float *dO, const float *lse, float *dQ, float *dK, float *dV,
+                     size_t B, size_t S, size_t H, size_t Dh, void *workspace,
+                     size_t workspace_bytes, cxg_stream_t stream);
+
 /* ============ ELU+1 linear "kernel" attention, two_stage_cuda API ============
  * phi(x) = x > 0 ? x + 1 : exp(x), fused.  Q/K (B*S, D), V/O (B*S, E); one
  * sequence per b (multi-head callers pass B = batch*heads, head-major rows).

@@ -109,3 +109,58 @@ def test_error_paths(dev):
                        ((None, None, 1, 2, 32, 8), cx.CXG_ERR_NULL),
                        ((None, None, 0, 2, 32, 8), cx.CXG_OK)):          # empty: nothing to do
         assert cx.call_status("cxg_rope_fwd", *args, st) == want, args
+
+
+# ---------------------------------------------------------------- RoPE fused into MHA
+def _fused_refs(Q, K, V, B, S, H, Dh):
+    D = H * Dh
+    Qr = orc.rope(Q, B, S, D, Dh, 1.0)
+    Kr = orc.rope(K, B, S, D, Dh, 1.0)
+    O, lse = orc.mha_fwd(Qr, Kr, V, B, S, H, Dh, nthreads=8, want_lse=True)
+    return Qr, Kr, O, lse
+
+
+@pytest.mark.parametrize("B,S,H,Dh", [
+    (8, 256, 12, 64),    # the C2 shape (stage-1 heads of two_stage_gpt.hpp)
+    (1, 1000, 2, 64),    # positions up to 999
+    (2, 65, 2, 16), (1, 100, 3, 32), (1, 130, 2, 128), (1, 70, 1, 256), (3, 7, 2, 8),
+])
+def test_fused_mha_rope(dev, B, S, H, Dh):
+    """cxg_mha_rope_fwd/bwd == rope_fwd; fused_mha_fwd; fused_mha_bwd; rope_bwd
+    (two_stage_gpt.hpp:102-106, :171-174), on the C oracle."""
+    import torch
+    import cxxgpt_attn as cx
+    D = H * Dh
+    Q, K, V, dO = normal_inputs((B * S, D), (B * S, D), 31 * S + Dh)
+    Qr, Kr, rO, rlse = _fused_refs(Q, K, V, B, S, H, Dh)
+    tQ, tK, tV, tdO = (_t(a, dev) for a in (Q, K, V, dO))
+    tO = torch.full_like(tQ, float("nan"))
+    tl = torch.full((B * H * S,), float("nan"), device=dev)
+    cx.mha_rope_fwd(tQ, tK, tV, tO, B, S, H, Dh, lse=tl)
+    torch.cuda.synchronize()
+    O = tO.cpu().numpy()
+    assert_close(O, rO, "fused fwd O")
+    assert_close(tl.cpu().numpy(), rlse, "fused fwd lse")
+    np.testing.assert_array_equal(tQ.cpu().numpy(), Q)   # inputs are left unrotated
+    np.testing.assert_array_equal(tK.cpu().numpy(), K)
+    gQ, gK, gV = orc.mha_bwd(Qr, Kr, V, O, dO, B, S, H, Dh, nthreads=8)
+    rdQ = orc.rope(gQ, B, S, D, Dh, -1.0)
+    rdK = orc.rope(gK, B, S, D, Dh, -1.0)
+    for use_lse in (True, False):
+        outs = [torch.full_like(tQ, float("nan")) for _ in range(3)]
+        cx.mha_rope_bwd(tQ, tK, tV, tO, tdO, *outs, B, S, H, Dh, lse=tl if use_lse else None)
+        torch.cuda.synchronize()
+        dQ, dK, dV = (o.cpu().numpy() for o in outs)
+        assert_close(dQ, rdQ, f"fused dQ lse={use_lse}")
+        assert_close(dK, rdK, f"fused dK lse={use_lse}")
+        assert_close(dV, gV, f"fused dV lse={use_lse}")
+
+
+def test_fused_mha_rope_rejects_odd_head_dim(dev):
+    import torch
+    import cxxgpt_attn as cx
+    t = torch.zeros(64, device=dev)
+    P = cx._ptr
+    st = cx.call_status("cxg_mha_rope_fwd", P(t), P(t), P(t), P(t), None, 1, 2, 1, 7,
+                        cx._stream(None))
+    assert st == cx.CXG_ERR_DIMS
