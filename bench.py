@@ -17,6 +17,8 @@ them can be made the reported workload with --workload NAME):
             two_stage API chain kernel_attn_fwd -> bwd_step1 -> bwd_dQ ->
             bwd_dKdV; GB/s of compulsory I/O, (12*S*D + 2*S)*4 bytes/sequence
   c3s256    the same at S=256
+  c3fused   c3 with the one-call backward: kernel_attn_fwd without z_cache ->
+            cxg_kattn_bwd (step1 + dQ + dKdV fused); c3fuseds256 at S=256
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
@@ -70,10 +72,14 @@ def lin_bytes(Bq, S, D):
     return (12 * S * D + 2 * S) * 4 * Bq
 
 
-def lin_kernel_bytes(Bq, S, D):
+def lin_kernel_bytes(Bq, S, D, fused=False):
     """Per-launch bytes each linear-attention entry point must move through its
-    own (legacy, split) signature: inputs read once, outputs written once."""
+    own signature: inputs read once, outputs written once.  fused: the forward
+    without z_cache and the one-call backward."""
     T, r = Bq * S * D * 4, Bq * S * 4   # one (rows x 64) tensor, one per-row vector
+    if fused:
+        return {"lin_fwd": 3 * T + T + r,        # Q,K,V -> O, den
+                "lin_bwd": 5 * T + r + 3 * T}    # Q,K,V,O,dO, den -> dQ, dK, dV
     return {"lin_fwd": 3 * T + 2 * T + r,        # Q,K,V -> O, z_cache, den
             "lin_step1": 2 * T + r + T + r,      # O, dO, den -> dnum, dden
             "lin_dq": 5 * T + r + T,             # K, V, dnum, z_cache, Q, dden -> dQ
@@ -125,7 +131,8 @@ def attribute(cx, step, steps):
     cx.prof_enable(False)
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
-              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "phi_hexp_fwd", "phi_hexp_bwd",
+              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
+              "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd"):
         tot, cnt = cx.prof_query(n)
         if cnt:
@@ -226,27 +233,38 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
 
 
-def _kattn(c, name, Bq, S, D, seed, steps, warmup):
+def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
+    """fused: kernel_attn_fwd without z_cache, then the one-call backward
+    (cxg_kattn_bwd); otherwise the reference's four-call chain."""
     g = c.gen(seed)
     E, N = D, Bq * S
     Q, K, V, dO = c.randn(g, N, D), c.randn(g, N, D), c.randn(g, N, E), c.randn(g, N, E)
-    O, den, zc = c.empty(N, E), c.empty(N), c.empty(N, D)
-    dnum, dden = c.empty(N, E), c.empty(N)
+    O, den = c.empty(N, E), c.empty(N)
     dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
     P = _ptr
-    step = Stepper(c.cx.lib(), [
-        ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E, c.sp)),
-        ("cxg_kattn_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, c.sp)),
-        ("cxg_kattn_bwd_dQ", (P(K), P(V), P(dnum), P(dden), P(zc), P(Q), P(dQ), None,
-                              Bq, S, D, E, c.sp)),
-        ("cxg_kattn_bwd_dKdV", (P(Q), P(K), P(V), P(dnum), P(dden), P(dK), P(dV),
-                                Bq, S, D, E, c.sp)),
-    ])
+    if fused:
+        step = Stepper(c.cx.lib(), [
+            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), None, None, None, Bq, S, D, E,
+                               c.sp)),
+            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(dQ), P(dK), P(dV),
+                               Bq, S, D, E, c.sp)),
+        ])
+    else:
+        zc, dnum, dden = c.empty(N, D), c.empty(N, E), c.empty(N)
+        step = Stepper(c.cx.lib(), [
+            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E,
+                               c.sp)),
+            ("cxg_kattn_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, c.sp)),
+            ("cxg_kattn_bwd_dQ", (P(K), P(V), P(dnum), P(dden), P(zc), P(Q), P(dQ), None,
+                                  Bq, S, D, E, c.sp)),
+            ("cxg_kattn_bwd_dKdV", (P(Q), P(K), P(V), P(dnum), P(dden), P(dK), P(dV),
+                                    Bq, S, D, E, c.sp)),
+        ])
     ms = timed(step, steps, warmup, c.stream)
     att = attribute(c.cx, step, max(10, min(steps, 50)))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
-    kb = lin_kernel_bytes(Bq, S, D)
+    kb = lin_kernel_bytes(Bq, S, D, fused)
     dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
     ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
@@ -254,8 +272,9 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup):
             "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
-                config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, two_stage API "
-                                    "chain (fwd, step1, dQ, dKdV)",
+                config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, " + (
+                            "fused backward (cxg_kattn_fwd without z_cache -> cxg_kattn_bwd)"
+                            if fused else "two_stage API chain (fwd, step1, dQ, dKdV)"),
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
@@ -377,6 +396,11 @@ def run_workload(c, name, steps, warmup):
         return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2))
     if name == "c3s256":
         return _kattn(c, name, 96, 256, 64, 78, steps, warmup)
+    if name == "c3fused":
+        return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2),
+                      fused=True)
+    if name == "c3fuseds256":
+        return _kattn(c, name, 96, 256, 64, 78, steps, warmup, fused=True)
     if name == "c4":
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
     raise ValueError(f"unknown workload {name}")
@@ -443,8 +467,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c4", "c5", "rope", "c2rope",
-                             "c2ropesep", "copy"])
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c4",
+                             "c5", "rope", "c2rope", "c2ropesep", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -485,7 +509,8 @@ def main():
     }
     sec = {}
     if not args.no_secondary and args.workload == "c2":
-        for name in ("c2legacy", "c3", "c3s256", "c4", "c5", "rope", "c2rope", "c2ropesep"):
+        for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c4", "c5", "rope",
+                     "c2rope", "c2ropesep"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

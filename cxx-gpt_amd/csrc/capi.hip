@@ -285,7 +285,7 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
     int st = lin_check(B, S, D, E, &empty);
     if (st != CXG_OK || empty)
         return st;
-    if (!Q || !K || !V || !O || !den || !zc)
+    if (!Q || !K || !V || !O || !den)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
     const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_FWD);
@@ -352,6 +352,37 @@ static int lin_dkdv_common(int phi, const float* Q, const float* K, const float*
                                       (int)E, ws.p, s));
 }
 
+static int lin_bwd_common(int phi, const float* Q, const float* K, const float* V,
+                          const float* O, const float* dO, const float* den, float* dQ,
+                          float* dK, float* dV, size_t B, size_t S, size_t D, size_t E,
+                          cxg_stream_t stream)
+{
+    bool empty;
+    int st = lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O || !dO || !den || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    Scratch ws;
+    if (!lin_bwd_fused_ok((int)D, (int)E)) {
+        // wide heads: the split kernels, intermediates in stream-ordered scratch
+        if (B * S > ((size_t)1 << 34) / (D + E + 1))
+            return CXG_ERR_DIMS;
+        st = ws.acquire(nullptr, 0, lin_bwd_split_ws_bytes((int)B, (int)S, (int)D, (int)E), s);
+        if (st != CXG_OK)
+            return st;
+        return hip_status(lin_bwd_split_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B,
+                                               (int)S, (int)D, (int)E, ws.p, s));
+    }
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_BWD);
+    st = ws.acquire(nullptr, 0, lin_bwd_ws_bytes(p, (int)B, (int)S), s);
+    if (st != CXG_OK)
+        return st;
+    return hip_status(lin_bwd_fused_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B, (int)S,
+                                           (int)D, (int)E, ws.p, s));
+}
+
 int cxg_kattn_fwd(const float* Q, const float* K, const float* V, float* O, float* den_cache,
                   float* z_cache, float* S_buf, float* z_buf, size_t B, size_t S, size_t D,
                   size_t E, cxg_stream_t stream)
@@ -379,6 +410,13 @@ int cxg_kattn_bwd_dKdV(const float* Q, const float* K, const float* V, const flo
                        size_t E, cxg_stream_t stream)
 {
     return lin_dkdv_common(PHI_ELU1, Q, K, V, dnum, dden, dK, dV, B, S, D, E, stream);
+}
+
+int cxg_kattn_bwd(const float* Q, const float* K, const float* V, const float* O,
+                  const float* dO, const float* den_cache, float* dQ, float* dK, float* dV,
+                  size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
+{
+    return lin_bwd_common(PHI_ELU1, Q, K, V, O, dO, den_cache, dQ, dK, dV, B, S, D, E, stream);
 }
 
 int cxg_lin_fwd(const float* Q_phi, const float* K_phi, const float* V, float* O,
@@ -410,6 +448,14 @@ int cxg_lin_bwd_dKdV(const float* Q_phi, const float* K_phi, const float* V, con
 {
     return lin_dkdv_common(PHI_NONE, Q_phi, K_phi, V, dnum, dden, dK_phi, dV, B, S, D, E,
                            stream);
+}
+
+int cxg_lin_bwd(const float* Q_phi, const float* K_phi, const float* V, const float* O,
+                const float* dO, const float* den_cache, float* dQ_phi, float* dK_phi,
+                float* dV, size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
+{
+    return lin_bwd_common(PHI_NONE, Q_phi, K_phi, V, O, dO, den_cache, dQ_phi, dK_phi, dV, B, S,
+                          D, E, stream);
 }
 
 static int phi_check(size_t N, size_t D, size_t E, bool hexp, bool* empty)

@@ -39,177 +39,9 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "linattn.hpp"
+#include "linattn_dev.hpp"
 
 namespace cxg {
-
-constexpr int CLD = 68;             // LDS row stride of a staged 16 x 64 chunk
-constexpr int CHUNK = 16 * CLD;     // floats per staged chunk matrix
-
-template <int PHI>
-struct Phi;
-template <>
-struct Phi<PHI_ELU1> {
-    // two_stage_cuda_kernels.cu:1027-1031 / kernel_test.cpp:16-17
-    static __device__ __forceinline__ float f(float x) { return x > 0.0f ? x + 1.0f : __expf(x); }
-    static __device__ __forceinline__ float d(float x) { return x > 0.0f ? 1.0f : __expf(x); }
-    // phi'(x) from phi(x): phi(x) = x+1 > 1 for x > 0 and exp(x) <= 1 otherwise
-    static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
-};
-template <>
-struct Phi<PHI_NONE> {
-    static __device__ __forceinline__ float f(float x) { return x; }
-    static __device__ __forceinline__ float d(float) { return 1.0f; }
-    static __device__ __forceinline__ float d_from_f(float) { return 1.0f; }
-};
-
-// ---------------------------------------------------------------------------
-// chunk staging helpers
-// ---------------------------------------------------------------------------
-// Template flags of the fast-path kernels: VEC = widths multiple of 4 and
-// 16-byte aligned rows (16-byte loads / stores), FW = D == E == 64 (no column
-// masks at all).  Row addresses are a wave-uniform chunk base plus a 32-bit
-// per-lane offset.
-
-// Raw R-layout registers of a chunk: lane (l16, g) holds chunk row `ro` (the
-// caller clamps it into the segment), columns 16ct + 4g .. +3 (clamped to ncol).
-template <bool VEC>
-__device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ base, int ld, int ro,
-                                    int ncol, int g)
-{
-    const float* p = base + ro * ld;
-#pragma unroll
-    for (int ct = 0; ct < 4; ct++)
-        v[ct] = load4c<VEC>(p, 16 * ct + 4 * g, ncol);
-}
-
-// Apply phi, then zero the entries outside the valid columns (unless the
-// width is full) and rows (only in a partial chunk; `full` is wave-uniform).
-template <int PHI, bool APPLY, bool FW>
-__device__ __forceinline__ void finR(f4 (&v)[4], bool full, bool rok, int ncol, int g)
-{
-    if (APPLY && PHI != PHI_NONE)
-#pragma unroll
-        for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                v[ct][i] = Phi<PHI>::f(v[ct][i]);
-    if (!FW)
-#pragma unroll
-        for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                v[ct][i] = (16 * ct + 4 * g + i < ncol) ? v[ct][i] : 0.0f;
-    if (!full)
-#pragma unroll
-        for (int ct = 0; ct < 4; ct++)
-            v[ct] = rok ? v[ct] : f4zero();
-}
-
-// Store an R-layout f4 of one row: no guard for a full width.
-template <bool VEC, bool FW>
-__device__ __forceinline__ void stR(float* __restrict__ row, int c, int n, f4 v)
-{
-    if (FW)
-        *reinterpret_cast<f4*>(row + c) = v;
-    else
-        store4<VEC>(row, c, n, v);
-}
-
-__device__ __forceinline__ void putR(float* __restrict__ buf, const f4 (&v)[4], int l16, int g)
-{
-#pragma unroll
-    for (int ct = 0; ct < 4; ct++)
-        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]) = v[ct];
-}
-
-// The same for a part of a chunk: column tiles ct0 .. ct0+NCT-1.  The waves
-// of a segment stage the chunk's inputs by column tiles, so each wave loads
-// and transforms (phi) an equal share.
-template <bool VEC, int NCT>
-__device__ __forceinline__ void ldRp(f4 (&v)[NCT], const float* __restrict__ base, int ld, int ro,
-                                     int ncol, int g, int ct0)
-{
-    const float* p = base + ro * ld;
-#pragma unroll
-    for (int i = 0; i < NCT; i++)
-        v[i] = load4c<VEC>(p, 16 * (ct0 + i) + 4 * g, ncol);
-}
-
-template <int PHI, bool APPLY, bool FW, int NCT>
-__device__ __forceinline__ void finRp(f4 (&v)[NCT], bool full, bool rok, int ncol, int g, int ct0)
-{
-    if (APPLY && PHI != PHI_NONE)
-#pragma unroll
-        for (int i = 0; i < NCT; i++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                v[i][e] = Phi<PHI>::f(v[i][e]);
-    if (!FW)
-#pragma unroll
-        for (int i = 0; i < NCT; i++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                v[i][e] = (16 * (ct0 + i) + 4 * g + e < ncol) ? v[i][e] : 0.0f;
-    if (!full)
-#pragma unroll
-        for (int i = 0; i < NCT; i++)
-            v[i] = rok ? v[i] : f4zero();
-}
-
-template <int NCT>
-__device__ __forceinline__ void putRp(float* __restrict__ buf, const f4 (&v)[NCT], int l16, int g,
-                                      int ct0)
-{
-#pragma unroll
-    for (int i = 0; i < NCT; i++)
-        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * (ct0 + i) + 4 * g]) = v[i];
-}
-
-__device__ __forceinline__ void getR(const float* __restrict__ buf, f4 (&v)[4], int l16, int g)
-{
-#pragma unroll
-    for (int ct = 0; ct < 4; ct++)
-        v[ct] = *reinterpret_cast<const f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]);
-}
-
-__device__ __forceinline__ void getC(const float* __restrict__ buf, f4 (&c)[4], int l16, int g)
-{
-#pragma unroll
-    for (int ct = 0; ct < 4; ct++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-            c[ct][r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
-}
-
-// Per-row scalars of chunk rows 4g+r (row offsets clamped to rmax), column layout.
-__device__ __forceinline__ f4 ldRowsC(const float* __restrict__ w, int rmax, int g)
-{
-    f4 v;
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-        v[r] = w[min(4 * g + r, rmax)];
-    return v;
-}
-
-// Inclusive prefix sum over the 16 chunk rows of a column-layout value
-// (rows 4g+r of column l16); returns the prefixes and the column total.
-__device__ __forceinline__ f4 col_prefix16(f4 c, float& total, int lane)
-{
-    const int g = lane >> 4;
-    f4 p;
-    p[0] = c[0];
-    p[1] = p[0] + c[1];
-    p[2] = p[1] + c[2];
-    p[3] = p[2] + c[3];
-    float x = p[3];
-    float y = __shfl_up(x, 16, 64);
-    x = g >= 1 ? x + y : x;
-    y = __shfl_up(x, 32, 64);
-    x = g >= 2 ? x + y : x;   // inclusive prefix of the 4-row totals over g
-    const float excl = x - p[3];
-    total = __shfl(x, 48 + (lane & 15), 64);
-    return p + excl;
-}
 
 // ---------------------------------------------------------------------------
 // Segment kernels.  A workgroup of NW waves owns one segment; the 64x64
@@ -219,16 +51,7 @@ __device__ __forceinline__ f4 col_prefix16(f4 c, float& total, int lane)
 // double-buffered LDS stage; one barrier per chunk publishes the stage to
 // the other waves.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ f4 colC(const float* __restrict__ buf, int ct, int l16, int g)
-{
-    f4 c;
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-        c[r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
-    return c;
-}
 
-// ---------------------------------------------------------------------------
 // per-segment aggregates: dS = sum_s phi(X_s)^T Y_s (64 x 64), dz = sum_s w_s phi(X_s)
 // (w = 1 when null).  Forward direction: X = K, Y = V.  Reverse: X = Q, Y = dnum,
 // w = dden.  Written row-major [d][e] followed by z[d], LIN_WS floats per segment.
@@ -1218,6 +1041,24 @@ __global__ __launch_bounds__(256) void lin_dkdv_generic_kernel(
 }
 
 // Copy a [d][e] state to the caller's layout ([d][e] or [e][d]).
+// z_cache for wide heads in the one-call backward (which receives no z_cache):
+// z_t = sum_{s<=t} phi(K_s), row by row in fp32 as the forward forms it.  One
+// thread per column of a sequence.
+template <int PHI>
+__global__ __launch_bounds__(256) void lin_zc_kernel(const float* __restrict__ K,
+                                                    float* __restrict__ zc, int S, int D)
+{
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= D)
+        return;
+    const long base = (long)blockIdx.y * S * D + d;
+    float z = 0.0f;
+    for (int t = 0; t < S; t++) {
+        z += Phi<PHI>::f(K[base + (long)t * D]);
+        zc[base + (long)t * D] = z;
+    }
+}
+
 __global__ void lin_state_copy_kernel(const float* __restrict__ src, float* __restrict__ dst,
                                       long Bq, int D, int E, int de)
 {
@@ -1342,7 +1183,9 @@ static int lin_cus()
 // (occupancy of the D = E = 64 variant times the compute units), cached.
 static int lin_slots(int pass)
 {
-    static int per_cu[3];
+    static int per_cu[4];
+    if (pass == LIN_PASS_BWD)
+        return lin_bwd_slots() * lin_cus();
     if (per_cu[pass] <= 0) {
         int n = 0;
         hipError_t e = hipErrorInvalidValue;
@@ -1590,6 +1433,48 @@ hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float*
     if (phi == PHI_ELU1)
         return dkdv_impl<PHI_ELU1>(Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, ws, st);
     return dkdv_impl<PHI_NONE>(Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, ws, st);
+}
+
+// One-call backward for heads wider than the fused kernels take: z_cache, step
+// 1, dQ and dK/dV through the split kernels, with the intermediates in the
+// workspace: zc (N x D), dnum (N x E), dden (N), then the scan scratch.
+static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
+size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E)
+{
+    const size_t N = (size_t)Bq * S;
+    const size_t a = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DQ), Bq, D, E);
+    const size_t b = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DKDV), Bq, D, E);
+    return al256(N * D * 4) + al256(N * E * 4) + al256(N * 4) + (a > b ? a : b);
+}
+
+hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const float* V,
+                                const float* O, const float* dO, const float* den, float* dQ,
+                                float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
+                                hipStream_t st)
+{
+    const size_t N = (size_t)Bq * S;
+    char* p = (char*)ws;
+    float* zc = (float*)p;
+    p += al256(N * D * 4);
+    float* dnum = (float*)p;
+    p += al256(N * E * 4);
+    float* dden = (float*)p;
+    p += al256(N * 4);
+    {
+        ProfScope ps(st, "lin_zc");
+        dim3 grid((unsigned)((D + 255) / 256), (unsigned)Bq);
+        if (phi == PHI_ELU1)
+            hipLaunchKernelGGL(lin_zc_kernel<PHI_ELU1>, grid, dim3(256), 0, st, K, zc, S, D);
+        else
+            hipLaunchKernelGGL(lin_zc_kernel<PHI_NONE>, grid, dim3(256), 0, st, K, zc, S, D);
+    }
+    hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);
+    if (e == hipSuccess)
+        e = lin_dq_launch(phi, K, V, dnum, dden, zc, Q, dQ, Bq, S, D, E, p, st);
+    if (e == hipSuccess)
+        e = lin_dkdv_launch(phi, Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, p, st);
+    return e;
 }
 
 hipError_t phi_elu_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st)

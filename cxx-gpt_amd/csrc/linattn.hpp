@@ -19,7 +19,7 @@ struct LinPlan {
 
 // The scan pass a plan is for: each sizes its segments to its own main
 // kernel's resident workgroups.
-enum LinPass { LIN_PASS_FWD = 0, LIN_PASS_DQ = 1, LIN_PASS_DKDV = 2 };
+enum LinPass { LIN_PASS_FWD = 0, LIN_PASS_DQ = 1, LIN_PASS_DKDV = 2, LIN_PASS_BWD = 3 };
 
 LinPlan lin_plan(int Bq, int S, int D, int E, int pass);
 // device scratch (bytes) the fwd / dQ / dKdV launchers need for this plan
@@ -39,6 +39,22 @@ hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* d
 hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float* V,
                            const float* dnum, const float* dden, float* dK, float* dV, int Bq,
                            int S, int D, int E, void* ws, hipStream_t st);
+// Fused backward (step 1 + dQ + dK/dV, linbwd.hip) for D, E <= 64.  den is the
+// forward's den_cache; dnum = dO / den and dden = -(dO . O) / den as in step 1.
+bool lin_bwd_fused_ok(int D, int E);
+int lin_bwd_slots();   // resident fused-backward workgroups per compute unit
+size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S);
+hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const float* V,
+                                const float* O, const float* dO, const float* den, float* dQ,
+                                float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
+                                hipStream_t st);
+// The same for other widths, through the split kernels (workspace: zc, dnum,
+// dden and the scan scratch).
+size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E);
+hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const float* V,
+                                const float* O, const float* dO, const float* den, float* dQ,
+                                float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
+                                hipStream_t st);
 hipError_t phi_elu_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st);
 hipError_t phi_elu_bwd_launch(const float* dphi, const float* x, float* dx, long N, int D, int E,
                               hipStream_t st);

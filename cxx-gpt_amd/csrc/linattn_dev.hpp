@@ -1,0 +1,193 @@
+// linattn_dev.hpp -- device helpers shared by the linear-attention kernels
+// (linattn.hip: forward, split backward; linbwd.hip: fused backward): the
+// feature map, the LDS chunk stage layout and its register views.
+//
+// Register layouts of a 16-row chunk (lane l, l16 = l%16, g = l/16, f4 element r):
+//   R-layout:  v[ct][r] = M[t0 + l16][16ct + 4g + r]   (row per lane)
+//   C-layout:  v[ct][r] = M[t0 + 4g + r][16ct + l16]   (column per lane)
+#pragma once
+
+#include "common.hpp"
+#include "linattn.hpp"
+
+namespace cxg {
+
+constexpr int CLD = 68;             // LDS row stride of a staged 16 x 64 chunk
+constexpr int CHUNK = 16 * CLD;     // floats per staged chunk matrix
+
+template <int PHI>
+struct Phi;
+template <>
+struct Phi<PHI_ELU1> {
+    // two_stage_cuda_kernels.cu:1027-1031 / kernel_test.cpp:16-17
+    static __device__ __forceinline__ float f(float x) { return x > 0.0f ? x + 1.0f : __expf(x); }
+    static __device__ __forceinline__ float d(float x) { return x > 0.0f ? 1.0f : __expf(x); }
+    // phi'(x) from phi(x): phi(x) = x+1 > 1 for x > 0 and exp(x) <= 1 otherwise
+    static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
+};
+template <>
+struct Phi<PHI_NONE> {
+    static __device__ __forceinline__ float f(float x) { return x; }
+    static __device__ __forceinline__ float d(float) { return 1.0f; }
+    static __device__ __forceinline__ float d_from_f(float) { return 1.0f; }
+};
+
+// ---------------------------------------------------------------------------
+// chunk staging helpers
+// ---------------------------------------------------------------------------
+// Template flags of the fast-path kernels: VEC = widths multiple of 4 and
+// 16-byte aligned rows (16-byte loads / stores), FW = D == E == 64 (no column
+// masks at all).  Row addresses are a wave-uniform chunk base plus a 32-bit
+// per-lane offset.
+
+// Raw R-layout registers of a chunk: lane (l16, g) holds chunk row `ro` (the
+// caller clamps it into the segment), columns 16ct + 4g .. +3 (clamped to ncol).
+template <bool VEC>
+__device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ base, int ld, int ro,
+                                    int ncol, int g)
+{
+    const float* p = base + ro * ld;
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+        v[ct] = load4c<VEC>(p, 16 * ct + 4 * g, ncol);
+}
+
+// Apply phi, then zero the entries outside the valid columns (unless the
+// width is full) and rows (only in a partial chunk; `full` is wave-uniform).
+template <int PHI, bool APPLY, bool FW>
+__device__ __forceinline__ void finR(f4 (&v)[4], bool full, bool rok, int ncol, int g)
+{
+    if (APPLY && PHI != PHI_NONE)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[ct][i] = Phi<PHI>::f(v[ct][i]);
+    if (!FW)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                v[ct][i] = (16 * ct + 4 * g + i < ncol) ? v[ct][i] : 0.0f;
+    if (!full)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+            v[ct] = rok ? v[ct] : f4zero();
+}
+
+// Store an R-layout f4 of one row: no guard for a full width.
+template <bool VEC, bool FW>
+__device__ __forceinline__ void stR(float* __restrict__ row, int c, int n, f4 v)
+{
+    if (FW)
+        *reinterpret_cast<f4*>(row + c) = v;
+    else
+        store4<VEC>(row, c, n, v);
+}
+
+__device__ __forceinline__ void putR(float* __restrict__ buf, const f4 (&v)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]) = v[ct];
+}
+
+// The same for a part of a chunk: column tiles ct0 .. ct0+NCT-1.  The waves
+// of a segment stage the chunk's inputs by column tiles, so each wave loads
+// and transforms (phi) an equal share.
+template <bool VEC, int NCT>
+__device__ __forceinline__ void ldRp(f4 (&v)[NCT], const float* __restrict__ base, int ld, int ro,
+                                     int ncol, int g, int ct0)
+{
+    const float* p = base + ro * ld;
+#pragma unroll
+    for (int i = 0; i < NCT; i++)
+        v[i] = load4c<VEC>(p, 16 * (ct0 + i) + 4 * g, ncol);
+}
+
+template <int PHI, bool APPLY, bool FW, int NCT>
+__device__ __forceinline__ void finRp(f4 (&v)[NCT], bool full, bool rok, int ncol, int g, int ct0)
+{
+    if (APPLY && PHI != PHI_NONE)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v[i][e] = Phi<PHI>::f(v[i][e]);
+    if (!FW)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v[i][e] = (16 * (ct0 + i) + 4 * g + e < ncol) ? v[i][e] : 0.0f;
+    if (!full)
+#pragma unroll
+        for (int i = 0; i < NCT; i++)
+            v[i] = rok ? v[i] : f4zero();
+}
+
+template <int NCT>
+__device__ __forceinline__ void putRp(float* __restrict__ buf, const f4 (&v)[NCT], int l16, int g,
+                                      int ct0)
+{
+#pragma unroll
+    for (int i = 0; i < NCT; i++)
+        *reinterpret_cast<f4*>(&buf[l16 * CLD + 16 * (ct0 + i) + 4 * g]) = v[i];
+}
+
+__device__ __forceinline__ void getR(const float* __restrict__ buf, f4 (&v)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+        v[ct] = *reinterpret_cast<const f4*>(&buf[l16 * CLD + 16 * ct + 4 * g]);
+}
+
+__device__ __forceinline__ void getC(const float* __restrict__ buf, f4 (&c)[4], int l16, int g)
+{
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            c[ct][r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
+}
+
+// Per-row scalars of chunk rows 4g+r (row offsets clamped to rmax), column layout.
+__device__ __forceinline__ f4 ldRowsC(const float* __restrict__ w, int rmax, int g)
+{
+    f4 v;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        v[r] = w[min(4 * g + r, rmax)];
+    return v;
+}
+
+// Inclusive prefix sum over the 16 chunk rows of a column-layout value
+// (rows 4g+r of column l16); returns the prefixes and the column total.
+__device__ __forceinline__ f4 col_prefix16(f4 c, float& total, int lane)
+{
+    const int g = lane >> 4;
+    f4 p;
+    p[0] = c[0];
+    p[1] = p[0] + c[1];
+    p[2] = p[1] + c[2];
+    p[3] = p[2] + c[3];
+    float x = p[3];
+    float y = __shfl_up(x, 16, 64);
+    x = g >= 1 ? x + y : x;
+    y = __shfl_up(x, 32, 64);
+    x = g >= 2 ? x + y : x;   // inclusive prefix of the 4-row totals over g
+    const float excl = x - p[3];
+    total = __shfl(x, 48 + (lane & 15), 64);
+    return p + excl;
+}
+
+__device__ __forceinline__ f4 colC(const float* __restrict__ buf, int ct, int l16, int g)
+{
+    f4 c;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        c[r] = buf[(4 * g + r) * CLD + 16 * ct + l16];
+    return c;
+}
+
+} // namespace cxg

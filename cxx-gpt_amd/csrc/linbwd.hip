@@ -1,0 +1,615 @@
+// linbwd.hip -- fused backward of causal linear attention (gfx950, FP32 MFMA):
+// step 1, dQ and dK/dV in one pass over each segment.
+//
+// Replaces the three-call backward of the reference's callers
+//   kernel_attn_bwd_step1 -> _bwd_dQ -> _bwd_dKdV      (two_stage_gpt.hpp:149-157,
+//     two_stage_cuda_kernels.cu:1190-1809, phi = ELU+1 fused)
+//   causal_linear_attention_bwd_step1 -> _dQ -> _dKdV  (linear_gpt.hpp:154-167,
+//     linear_cuda_kernels.cu:101-298, phi applied outside)
+// for callers that can issue one call.  Q, K, V, O, dO and den are read once and
+// dQ, dK, dV written once; dnum = dO / den and dden = -(dO . O) / den (the step-1
+// outputs, two_stage_cuda_kernels.cu:1190-1248) never leave the chip, and no
+// z_cache is needed.
+//
+// Per sequence (Q/K rows of width D, V/O rows of width E, D, E <= 64):
+//   dQ_t = (z_t dden_t + S_t dnum_t) * phi'(Q_t)
+//          S_t = sum_{s<=t} phi(K_s) V_s^T,  z_t = sum_{s<=t} phi(K_s)
+//   dV_t = S*_t^T phi(K_t),  dK_t = (z*_t + S*_t V_t) * phi'(K_t)
+//          S*_t = sum_{s>=t} phi(Q_s) dnum_s^T,  z*_t = sum_{s>=t} dden_s phi(Q_s)
+//
+// Structure.  Segments of L rows (16-row chunks), as in the split kernels.
+//  * lin_bagg: per segment, the aggregate of phi(K)^T V and phi(K) (every
+//    segment) and of phi(Q)^T dnum and dden phi(Q) (segments 1..), plus for
+//    every chunk the exclusive within-segment prefix of phi(K) (the z table).
+//  * lin_bscan: over the segments of a sequence, the first aggregate becomes an
+//    inclusive prefix (its z part an exclusive one), the second an exclusive
+//    suffix.
+//  * lin_bwd: walks each segment's chunks from last to first.  S* and z* start
+//    at the suffix of later segments and take in each chunk after its dK/dV
+//    are formed.  S starts at the inclusive prefix at the segment end and gives
+//    up each chunk's phi(K)^T V before that chunk's dQ is formed, so every row
+//    is read once.  z is not recovered by subtraction (cancellation near a
+//    segment start would reach ~1e-4 relative): a chunk's starting z is the
+//    segment's exclusive prefix plus its z table entry, both forward sums.
+//    The S subtraction keeps dQ within a tenth of the parity tolerance at
+//    S = 4096 (its error is relative to |S| at the segment end, which stays
+//    within a small factor of |S_t| away from the sequence start).
+#include "common.hpp"
+#include "launch.hpp"
+#include "linattn.hpp"
+#include "linattn_dev.hpp"
+
+namespace cxg {
+
+// Row-coalesced chunk loads: wave w of a 4-wave workgroup takes chunk rows
+// 4w + lane/16, columns 4(lane%16) .. +3, so one instruction reads four whole
+// 256-byte rows.  Rows past the segment are clamped (and zeroed after the
+// load); columns past the width read a clamped copy and are zeroed too.
+template <bool VEC, bool FW>
+__device__ __forceinline__ f4 ld_row4(const float* __restrict__ base, long row, int ld, int col,
+                                      int ncol)
+{
+    const f4 v = load4c<VEC>(base + row * ld, col, ncol);
+    return FW ? v : mask4(v, col, ncol, true);
+}
+
+// ---------------------------------------------------------------------------
+// lin_bagg: per-segment aggregates.  Workgroups [0, Bq*nseg) form the prefix
+// records (X = phi(K), Y = V, w = 1, z table); workgroups after that the
+// suffix records of segments 1.. (X = phi(Q), Y = dnum, w = dden; segment 0's
+// suffix aggregate is never used).  Records are row-major [d][e] plus z[d],
+// LIN_WS floats.  Wave w accumulates output columns e of tile w over the
+// segment's chunks, in forward order.
+// ---------------------------------------------------------------------------
+constexpr int BAGG_THREADS = 256;
+constexpr int BAGG_STAGE = 2 * CHUNK + 16;
+
+// One instance per workgroup kind: SUF is uniform over the workgroup, and each
+// instance is straight-line code (no branch around its loads, so the waits on
+// the loads in flight stay exact).
+template <int PHI, bool VEC, bool FW, bool SUF>
+__device__ __attribute__((always_inline)) inline void bagg_body(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
+    float* __restrict__ rec, float* __restrict__ ztab_seg, float* __restrict__ lds, int seq,
+    int seg, int S, int D, int E, int L)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
+    const int nch = (tend - tbeg + 15) / 16;
+    const int tlc = tbeg + 16 * (nch - 1);
+    const long rb = (long)seq * S;
+    const int lrow = 4 * w + g, lcol = 4 * l16;
+    // z table entries of this segment's chunks (prefix records only)
+    const __amdgpu_buffer_rsrc_t rz = buf_rsrc(SUF ? nullptr : ztab_seg);
+
+    f4 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+        acc[dt] = f4zero();
+    float zrun = 0.0f;   // column total of w * X for d = 16w + l16
+
+    // raw rows: prefix records load K, V; suffix records Q, O, dO and den
+    struct Set {
+        f4 a, b, c;
+        float dn;
+    };
+    auto fetch = [&](Set& s, int t0) {
+        const long r = rb + min(t0 + lrow, tlast);
+        if constexpr (!SUF) {
+            s.a = ld_row4<VEC, FW>(K, r, D, lcol, D);
+            s.b = ld_row4<VEC, FW>(V, r, E, lcol, E);
+        } else {
+            s.a = ld_row4<VEC, FW>(Q, r, D, lcol, D);
+            s.b = ld_row4<VEC, FW>(O, r, E, lcol, E);
+            s.c = ld_row4<VEC, FW>(dO, r, E, lcol, E);
+            s.dn = den[r];
+        }
+    };
+    Set sa, sb;
+    fetch(sa, tbeg);
+    fetch(sb, min(tbeg + 16, tlc));
+    auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
+        const int t0 = tbeg + 16 * c;
+        float* st = lds + (c & 1) * BAGG_STAGE;
+        float* bX = st;
+        float* bY = st + CHUNK;
+        float* bw = st + 2 * CHUNK;
+        const bool ok = t0 + lrow < tend;
+        f4 x, y;
+        float wv;
+        if constexpr (!SUF) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[i] = ok ? Phi<PHI>::f(s.a[i]) : 0.0f;
+                y[i] = ok ? s.b[i] : 0.0f;
+            }
+            wv = 1.0f;
+        } else {
+            const float inv = ok ? 1.0f / s.dn : 0.0f;
+            const float dot = row16_sum(s.c[0] * s.b[0] + s.c[1] * s.b[1] + s.c[2] * s.b[2] +
+                                        s.c[3] * s.b[3]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                x[i] = ok ? Phi<PHI>::f(s.a[i]) : 0.0f;
+                y[i] = s.c[i] * inv;
+            }
+            wv = -dot * inv;
+        }
+        if (!FW)
+            x = mask4(x, lcol, D, true);   // phi(0) != 0: re-zero the padded columns
+        *reinterpret_cast<f4*>(&bX[lrow * CLD + lcol]) = x;
+        *reinterpret_cast<f4*>(&bY[lrow * CLD + lcol]) = y;
+        bw[lrow] = wv;   // the row's 16 lanes store the same value
+        // Below the LDS writes, which read the set: refill it with chunk c+2.
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(s, min(t0 + 32, tlc));
+        __syncthreads();
+        f4 xC[4];
+        getC(bX, xC, l16, g);
+        const f4 yC = colC(bY, w, l16, g);
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            f4 a = acc[dt];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                a = mfma16(xC[dt][r], yC[r], a);
+            acc[dt] = a;
+        }
+        // column total of w * X over the chunk for d = 16w + l16
+        const f4 xw = colC(bX, w, l16, g);
+        float zp = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            zp += SUF ? xw[r] * bw[4 * g + r] : xw[r];
+        zp = xrow_sum(zp);
+        // z table: the exclusive prefix before this chunk (one lane per column)
+        buffer_store_f32(rz, g == 0 ? (unsigned)(c * 64 + 16 * w + l16) * 4u : kDropOffset, zrun);
+        zrun += zp;
+    };
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        chunk(sa, c);
+        chunk(sb, c + 1);
+    }
+    if (c < nch)
+        chunk(sa, c);
+
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            rec[(16 * dt + 4 * g + r) * 64 + 16 * w + l16] = acc[dt][r];
+    if (g == 0)
+        rec[4096 + 16 * w + l16] = zrun;
+}
+
+template <int PHI, bool VEC, bool FW>
+__global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
+    float* __restrict__ wsP, float* __restrict__ wsB, float* __restrict__ ztab, int Bq, int S,
+    int D, int E, int nseg, int L, int nchs)
+{
+    __shared__ __attribute__((aligned(16))) float lds[2 * BAGG_STAGE];
+    const int nP = Bq * nseg;
+    if ((int)blockIdx.x < nP) {
+        const int seq = blockIdx.x / nseg, seg = blockIdx.x - seq * nseg;
+        bagg_body<PHI, VEC, FW, false>(Q, K, V, O, dO, den, wsP + (long)blockIdx.x * LIN_WS,
+                                       ztab + ((long)seq * nchs + seg * (L / 16)) * 64, lds, seq,
+                                       seg, S, D, E, L);
+    } else {
+        const int b = blockIdx.x - nP;
+        const int seq = b / (nseg - 1), seg = 1 + (b - seq * (nseg - 1));
+        bagg_body<PHI, VEC, FW, true>(Q, K, V, O, dO, den,
+                                      wsB + ((long)seq * nseg + seg) * LIN_WS, nullptr, lds, seq,
+                                      seg, S, D, E, L);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// lin_bscan: per sequence and record element, over the segments.  Prefix
+// records: inclusive for the state (the backward walk starts at the segment
+// end), exclusive for z.  Suffix records: exclusive from the end (segment 0's
+// record is only written).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void lin_bscan_kernel(float* __restrict__ wsP,
+                                                       float* __restrict__ wsB, int Bq, int nseg)
+{
+    const long j = (long)blockIdx.x * 256 + threadIdx.x;
+    const long n = (long)Bq * LIN_WS;
+    if (j >= 2 * n)
+        return;
+    const bool suf = j >= n;
+    const long k = suf ? j - n : j;
+    const long seq = k / LIN_WS, e = k - seq * LIN_WS;
+    float* base = (suf ? wsB : wsP) + seq * nseg * LIN_WS + e;
+    const bool incl = !suf && e < 4096;
+    // Batches of SB segments: all loads of a batch are issued before its stores.
+    constexpr int SB = 8;
+    const int cnt = suf ? nseg - 1 : nseg;   // records read
+    float run = 0.0f;
+    for (int k0 = 0; k0 < cnt; k0 += SB) {
+        float v[SB];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const int q = min(k0 + u, cnt - 1);
+            const int s = suf ? nseg - 1 - q : q;
+            v[u] = base[(long)s * LIN_WS];
+        }
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            if (k0 + u < cnt) {
+                const int q = k0 + u;
+                const int s = suf ? nseg - 1 - q : q;
+                const float nx = run + v[u];
+                base[(long)s * LIN_WS] = incl ? nx : run;
+                run = nx;
+            }
+        }
+    }
+    if (suf)
+        base[0] = run;   // segment 0: the suffix of every later segment
+}
+
+// ---------------------------------------------------------------------------
+// lin_bwd: the fused pass.  Four waves per segment; wave w owns
+//   column tile w of S* (e = 16w..): forms dV columns e of tile w,
+//   column tile w of S^T (d = 16w..): forms dQ columns d of tile w,
+//   and dK columns d of tile w from S* rows d of tile w, which the waves
+//   publish through LDS (each wave writes its updated S* slice at the start of
+//   the next chunk, after the barrier that ends every read of the old one).
+// The chunk's 16x16 products phi(Q)phi(K)^T and dnum V^T are split over the
+// waves by 16-wide slices of the contraction and summed through LDS.
+// ---------------------------------------------------------------------------
+constexpr int BWD_THREADS = 256;
+constexpr int BWD_STAGE = 4 * CHUNK + 16;   // phi(Q), phi(K), V, dnum chunks + dden rows
+constexpr int SLD = 68;                     // row stride of the S* copy [d][e]
+constexpr int BWD_LDS = 2 * BWD_STAGE + 64 * SLD + 4 * 2 * 256;
+
+template <int PHI, bool VEC, bool FW>
+__global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))) void lin_bwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
+    const float* __restrict__ wsP, const float* __restrict__ wsB, const float* __restrict__ ztab,
+    int S, int D, int E, int nseg, int L, int nchs)
+{
+    __shared__ __attribute__((aligned(16))) float lds[BWD_LDS];
+    float* sS = lds + 2 * BWD_STAGE;   // S* [d][e]
+    float* sP = sS + 64 * SLD;         // partial products [wave][2][lane * 4 + r]
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int wid = blockIdx.x;
+    const int seq = wid / nseg, seg = wid - seq * nseg;
+    const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
+    const long rb = (long)seq * S;
+    const int lrow = 4 * w + g, lcol = 4 * l16;
+
+    // StT[et]: lane (d = 16w + l16), element r <-> e = 16et + 4g + r of S^T (inclusive
+    //          prefix at the segment end, then S before the current chunk)
+    // Sm[dt]:  lane (e = 16w + l16), element r <-> d = 16dt + 4g + r of S* (suffix
+    //          of the chunks after the current one)
+    // zs, pz:  element r <-> d = 16w + 4g + r of z* and of z before the segment
+    f4 StT[4], Sm[4];
+    const float* RP = wsP + (long)wid * LIN_WS;
+    const float* RB = wsB + (long)wid * LIN_WS;
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        StT[a] = *reinterpret_cast<const f4*>(RP + (16 * w + l16) * 64 + 16 * a + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            Sm[a][r] = RB[(16 * a + 4 * g + r) * 64 + 16 * w + l16];
+    }
+    f4 zs = *reinterpret_cast<const f4*>(RB + 4096 + 16 * w + 4 * g);
+    const f4 pz = *reinterpret_cast<const f4*>(RP + 4096 + 16 * w + 4 * g);
+
+    const int nch = (tend - tbeg + 15) / 16;
+    const float* zt0 = ztab + ((long)seq * nchs + tbeg / 16) * 64 + 16 * w + 4 * g;
+    struct Set {
+        f4 q, k, v, o, d, zt;
+        float dn;
+    };
+    auto fetch = [&](Set& s, int c) {
+        const long r = rb + min(tbeg + 16 * c + lrow, tlast);
+        s.q = ld_row4<VEC, FW>(Q, r, D, lcol, D);
+        s.k = ld_row4<VEC, FW>(K, r, D, lcol, D);
+        s.v = ld_row4<VEC, FW>(V, r, E, lcol, E);
+        s.o = ld_row4<VEC, FW>(O, r, E, lcol, E);
+        s.d = ld_row4<VEC, FW>(dO, r, E, lcol, E);
+        s.dn = den[r];
+        s.zt = *reinterpret_cast<const f4*>(zt0 + (long)c * 64);
+    };
+    Set sa, sb;
+    fetch(sa, nch - 1);
+    fetch(sb, max(nch - 2, 0));
+    auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
+        const int t0 = tbeg + 16 * c;
+        float* st = lds + (c & 1) * BWD_STAGE;
+        float* bQ = st;
+        float* bK = st + CHUNK;
+        float* bV = st + 2 * CHUNK;
+        float* bN = st + 3 * CHUNK;
+        float* bd = st + 4 * CHUNK;
+        {
+            // step 1 for this wave's four rows, phi, row masks; stage the chunk
+            const bool ok = t0 + lrow < tend;
+            const float inv = ok ? 1.0f / s.dn : 0.0f;
+            const float dot = row16_sum(s.d[0] * s.o[0] + s.d[1] * s.o[1] + s.d[2] * s.o[2] +
+                                        s.d[3] * s.o[3]);
+            f4 q, k, v;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                q[i] = ok ? Phi<PHI>::f(s.q[i]) : 0.0f;
+                k[i] = ok ? Phi<PHI>::f(s.k[i]) : 0.0f;
+                v[i] = ok ? s.v[i] : 0.0f;
+            }
+            if (!FW) {
+                q = mask4(q, lcol, D, true);
+                k = mask4(k, lcol, D, true);
+            }
+            *reinterpret_cast<f4*>(&bQ[lrow * CLD + lcol]) = q;
+            *reinterpret_cast<f4*>(&bK[lrow * CLD + lcol]) = k;
+            *reinterpret_cast<f4*>(&bV[lrow * CLD + lcol]) = v;
+            *reinterpret_cast<f4*>(&bN[lrow * CLD + lcol]) = s.d * inv;
+            bd[lrow] = -dot * inv;   // the row's 16 lanes store the same value
+        }
+        const f4 zb = pz + s.zt;   // z before the chunk, columns d of tile w
+        // Below the LDS writes, which read the set: refill it with chunk c-2.
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(s, max(c - 2, 0));
+        __syncthreads();
+
+        // partial products over the contraction slice of tile w:
+        //   M1[s][t] = phi(Q_s).phi(K_t),  X[s][t] = dnum_s.V_t
+        {
+            const f4 qRw = *reinterpret_cast<const f4*>(&bQ[l16 * CLD + 16 * w + 4 * g]);
+            const f4 kRw = *reinterpret_cast<const f4*>(&bK[l16 * CLD + 16 * w + 4 * g]);
+            const f4 nRw = *reinterpret_cast<const f4*>(&bN[l16 * CLD + 16 * w + 4 * g]);
+            const f4 vRw = *reinterpret_cast<const f4*>(&bV[l16 * CLD + 16 * w + 4 * g]);
+            f4 m1 = f4zero(), x = f4zero();
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                m1 = mfma16(qRw[r], kRw[r], m1);
+                x = mfma16(nRw[r], vRw[r], x);
+            }
+            *reinterpret_cast<f4*>(&sP[(2 * w) * 256 + lane * 4]) = m1;
+            *reinterpret_cast<f4*>(&sP[(2 * w + 1) * 256 + lane * 4]) = x;
+        }
+        // This wave's S* slice (it took in chunk c+1 last step) for the dK of
+        // chunk c: written after the barrier above, which every wave passes only
+        // once its reads of the previous copy (dK of chunk c+1) are done.
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                sS[(16 * dt + 4 * g + r) * SLD + 16 * w + l16] = Sm[dt][r];
+        __syncthreads();
+        // lane t = l16, element r <-> s = 4g + r:
+        //   M1 (keep s >= t), M2 = X + dden_s (s >= t), G = X^T + dden_t (s <= t)
+        f4 M1 = f4zero(), X = f4zero(), Xt = f4zero();
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            M1 += *reinterpret_cast<const f4*>(&sP[(2 * u) * 256 + lane * 4]);
+            X += *reinterpret_cast<const f4*>(&sP[(2 * u + 1) * 256 + lane * 4]);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                Xt[r] += sP[(2 * u + 1) * 256 + ((l16 >> 2) * 16 + 4 * g + r) * 4 + (l16 & 3)];
+        }
+        const f4 ddS = *reinterpret_cast<const f4*>(&bd[4 * g]);
+        const float ddT = bd[l16];
+        f4 M2, G;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int sr = 4 * g + r;
+            M1[r] = sr >= l16 ? M1[r] : 0.0f;
+            M2[r] = sr >= l16 ? X[r] + ddS[r] : 0.0f;
+            G[r] = sr <= l16 ? Xt[r] + ddT : 0.0f;
+        }
+        const bool okt = t0 + l16 < tend;
+        const unsigned soff = (unsigned)(l16 * 64 + 16 * w + 4 * g);   // FW store offsets
+
+        // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_{s>=t} dnum_s[e] M1[s][t]
+        f4 kR[4];
+        getR(bK, kR, l16, g);
+        const f4 nCw = colC(bN, w, l16, g);
+        {
+            f4 dv = f4zero();
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    dv = mfma16(Sm[dt][r], kR[dt][r], dv);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                dv = mfma16(nCw[r], M1[r], dv);
+            if constexpr (FW) {
+                buffer_store_f4(buf_rsrc(dV + (rb + t0) * E), okt ? soff * 4u : kDropOffset, dv);
+            } else if (okt) {
+                store4<VEC>(dV + (rb + t0 + l16) * E, 16 * w + 4 * g, E, dv);
+            }
+        }
+        // dK^T[d][t] = (z*[d] + sum_e S*[d][e] V_t[e] + sum_{s>=t} phi(Q_s)[d] M2[s][t]) phi'(K_t[d])
+        const f4 qCw = colC(bQ, w, l16, g);
+        {
+            f4 vR[4];
+            getR(bV, vR, l16, g);
+            f4 dk = zs;
+#pragma unroll
+            for (int et = 0; et < 4; et++) {
+                const f4 sT = *reinterpret_cast<const f4*>(&sS[(16 * w + l16) * SLD + 16 * et + 4 * g]);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    dk = mfma16(sT[r], vR[et][r], dk);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                dk = mfma16(qCw[r], M2[r], dk);
+            const f4 kRw = *reinterpret_cast<const f4*>(&bK[l16 * CLD + 16 * w + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dk[i] *= Phi<PHI>::d_from_f(kRw[i]);
+            if constexpr (FW) {
+                buffer_store_f4(buf_rsrc(dK + (rb + t0) * D), okt ? soff * 4u : kDropOffset, dk);
+            } else if (okt) {
+                store4<VEC>(dK + (rb + t0 + l16) * D, 16 * w + 4 * g, D, dk);
+            }
+        }
+        // S^T gives up the chunk: S^T[e][d] -= sum_t V_t[e] phi(K_t)[d]
+        const f4 kCw = colC(bK, w, l16, g);
+        {
+            f4 vC[4];
+            getC(bV, vC, l16, g);
+            const f4 nk = -kCw;
+#pragma unroll
+            for (int et = 0; et < 4; et++) {
+                f4 a = StT[et];
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    a = mfma16(vC[et][r], nk[r], a);
+                StT[et] = a;
+            }
+        }
+        // dQ^T[d][t] = (z_t[d] dden_t + sum_e S[d][e] dnum_t[e]) phi'(Q_t[d]), with
+        // z_t = zb + sum_{s<=t} phi(K_s) and S_t = S + sum_{s<=t} phi(K_s) V_s^T:
+        //   = (zb[d] dden_t + sum_e S[d][e] dnum_t[e] + sum_{s<=t} phi(K_s)[d] G[s][t]) phi'
+        {
+            f4 nR[4];
+            getR(bN, nR, l16, g);
+            f4 dq = zb * ddT;
+#pragma unroll
+            for (int et = 0; et < 4; et++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    dq = mfma16(StT[et][r], nR[et][r], dq);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                dq = mfma16(kCw[r], G[r], dq);
+            const f4 qRw = *reinterpret_cast<const f4*>(&bQ[l16 * CLD + 16 * w + 4 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                dq[i] *= Phi<PHI>::d_from_f(qRw[i]);
+            if constexpr (FW) {
+                buffer_store_f4(buf_rsrc(dQ + (rb + t0) * D), okt ? soff * 4u : kDropOffset, dq);
+            } else if (okt) {
+                store4<VEC>(dQ + (rb + t0 + l16) * D, 16 * w + 4 * g, D, dq);
+            }
+        }
+        // S* += phi(Q)^T dnum (columns e of tile w); z* += phi(Q)^T dden (columns d of tile w)
+        {
+            f4 qC[4];
+            getC(bQ, qC, l16, g);
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                f4 a = Sm[dt];
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    a = mfma16(qC[dt][r], nCw[r], a);
+                Sm[dt] = a;
+            }
+            float zp = qCw[0] * ddS[0] + qCw[1] * ddS[1] + qCw[2] * ddS[2] + qCw[3] * ddS[3];
+            zp = xrow_sum(zp);   // column total for d = 16w + l16
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                zs[i] += __shfl(zp, 4 * g + i, 64);
+        }
+    };
+    int c = nch - 1;
+    for (; c >= 1; c -= 2) {
+        chunk(sa, c);
+        chunk(sb, c - 1);
+    }
+    if (c == 0)
+        chunk(sa, 0);
+}
+
+// ---------------------------------------------------------------------------
+// launcher
+// ---------------------------------------------------------------------------
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool lin_bwd_fused_ok(int D, int E) { return D >= 1 && E >= 1 && D <= 64 && E <= 64; }
+
+int lin_bwd_slots()
+{
+    static int per_cu = 0;
+    if (per_cu <= 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)lin_bwd_kernel<PHI_ELU1, true, true>, BWD_THREADS, 0) !=
+                hipSuccess ||
+            n <= 0)
+            n = 2;
+        per_cu = n;
+    }
+    return per_cu;
+}
+
+size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S)
+{
+    const long nchs = (S + 15) / 16;
+    return ((size_t)2 * Bq * p.nseg * LIN_WS + (size_t)Bq * nchs * 64) * sizeof(float);
+}
+
+template <int PHI, bool VEC, bool FW>
+static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const float* V,
+                         const float* O, const float* dO, const float* den, float* dQ, float* dK,
+                         float* dV, float* wsP, float* wsB, float* zt, int Bq, int S, int D, int E,
+                         hipStream_t st)
+{
+    const int nchs = (S + 15) / 16;
+    {
+        ProfScope ps(st, "lin_bagg");
+        const unsigned nb = (unsigned)(Bq * p.nseg + Bq * (p.nseg - 1));
+        hipLaunchKernelGGL((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
+                           Q, K, V, O, dO, den, wsP, wsB, zt, Bq, S, D, E, p.nseg, p.L, nchs);
+    }
+    {
+        ProfScope ps(st, "lin_bscan");
+        const long n = 2L * Bq * LIN_WS;
+        hipLaunchKernelGGL(lin_bscan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           wsP, wsB, Bq, p.nseg);
+    }
+    ProfScope ps(st, "lin_bwd");
+    hipLaunchKernelGGL((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
+                       dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt,
+                       S, D, E, p.nseg, p.L, nchs);
+}
+
+template <int PHI>
+static void bwd_dispatch(const LinPlan& p, const float* Q, const float* K, const float* V,
+                         const float* O, const float* dO, const float* den, float* dQ, float* dK,
+                         float* dV, float* wsP, float* wsB, float* zt, int Bq, int S, int D, int E,
+                         hipStream_t st)
+{
+    const bool vec = D % 4 == 0 && E % 4 == 0 && al16(Q) && al16(K) && al16(V) && al16(O) &&
+                     al16(dO) && al16(dQ) && al16(dK) && al16(dV);
+    if (vec && D == 64 && E == 64)
+        bwd_launch_t<PHI, true, true>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D,
+                                      E, st);
+    else if (vec)
+        bwd_launch_t<PHI, true, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S,
+                                       D, E, st);
+    else
+        bwd_launch_t<PHI, false, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S,
+                                        D, E, st);
+}
+
+hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const float* V,
+                                const float* O, const float* dO, const float* den, float* dQ,
+                                float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
+                                hipStream_t st)
+{
+    const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_BWD);
+    float* wsP = (float*)ws;
+    float* wsB = wsP + (size_t)Bq * p.nseg * LIN_WS;
+    float* zt = wsB + (size_t)Bq * p.nseg * LIN_WS;
+    if (phi == PHI_ELU1)
+        bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D, E, st);
+    else
+        bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D, E, st);
+    return hipGetLastError();
+}
+
+} // namespace cxg

@@ -38,10 +38,12 @@ SIGNATURES = {
     "cxg_kattn_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_kattn_bwd_dQ": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_kattn_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
+    "cxg_kattn_bwd": [_vp] * 9 + [_sz] * 4 + [_vp],
     "cxg_lin_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_lin_bwd_dQ": [_vp] * 7 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
+    "cxg_lin_bwd": [_vp] * 9 + [_sz] * 4 + [_vp],
     "cxg_phi_elu_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
@@ -171,6 +173,12 @@ def kattn_bwd_dKdV(Q, K, V, dnum, dden, dK, dV, B, S, D, E, stream=None):
           _ptr(dV), B, S, D, E, _stream(stream))
 
 
+def kattn_bwd(Q, K, V, O, dO, den, dQ, dK, dV, B, S, D, E, stream=None):
+    """Fused step1 + dQ + dKdV (no z_cache, no dnum/dden round trip)."""
+    _call("cxg_kattn_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(dQ),
+          _ptr(dK), _ptr(dV), B, S, D, E, _stream(stream))
+
+
 # ------------------------------------------------------------------ linear_cuda API
 def lin_fwd(Qp, Kp, V, O, den, zc, S_buf, z_buf, B, S, D, E, stream=None):
     _call("cxg_lin_fwd", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(den), _ptr(zc),
@@ -190,6 +198,12 @@ def lin_bwd_dQ(Kp, V, dnum, dden, zc, dQp, S_buf, B, S, D, E, stream=None):
 def lin_bwd_dKdV(Qp, Kp, V, dnum, dden, dKp, dV, B, S, D, E, stream=None):
     _call("cxg_lin_bwd_dKdV", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(dnum), _ptr(dden), _ptr(dKp),
           _ptr(dV), B, S, D, E, _stream(stream))
+
+
+def lin_bwd(Qp, Kp, V, O, dO, den, dQp, dKp, dV, B, S, D, E, stream=None):
+    """Fused step1 + dQ + dKdV of the linear_cuda API."""
+    _call("cxg_lin_bwd", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(dQp),
+          _ptr(dKp), _ptr(dV), B, S, D, E, _stream(stream))
 
 
 def phi_elu_fwd(x, phi, N, D, E, stream=None):

@@ -93,8 +93,9 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
 
 /* two_stage_cuda::kernel_attn_fwd (two_stage_cuda_kernels.cuh:39-44,
  * two_stage_cuda_kernels.cu:1133-1185).  z_cache (B*S, D): inclusive cumsum of
- * phi(K).  S_buf (B*E, D) and z_buf (B, D): scratch, contents unspecified
- * after the call (may be NULL). */
+ * phi(K); may be NULL (not written) when the backward is cxg_kattn_bwd, which
+ * does not read it.  S_buf (B*E, D) and z_buf (B, D): scratch, contents
+ * unspecified after the call (may be NULL). */
 int cxg_kattn_fwd(const float *Q, const float *K, const float *V, float *O,
                   float *den_cache, float *z_cache, float *S_buf, float *z_buf,
                   size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
@@ -118,6 +119,18 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
                        const float *dnum, const float *dden, float *dK, float *dV,
                        size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
 
+/* Fused backward: kernel_attn_bwd_step1 + kernel_attn_bwd_dQ +
+ * kernel_attn_bwd_dKdV in one call, as two_stage_gpt.hpp:149-157 issues them
+ * (two_stage_cuda_kernels.cuh:46-61).  No single counterpart in the reference.
+ * Reads Q, K, V, O, dO and den_cache once and writes dQ, dK, dV; the step-1
+ * intermediates (dnum = dO/den, dden = -sum_e dO*O/den) stay on chip and no
+ * z_cache is needed.  D <= 64 and E <= 64 take the fused kernels; wider heads
+ * run the split kernels inside the call (z_cache, dnum, dden in stream-ordered
+ * scratch). */
+int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O,
+                  const float *dO, const float *den_cache, float *dQ, float *dK, float *dV,
+                  size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
 /* ============ causal linear attention, linear_cuda API (phi outside) ==========
  * Inputs are feature-mapped already: Q_phi/K_phi (B*S, D), V/O (B*S, E).
  * State layout [d][e]; den_cache includes eps (den = phiQ.z + 1e-8).
@@ -129,6 +142,15 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
 int cxg_lin_fwd(const float *Q_phi, const float *K_phi, const float *V, float *O,
                 float *den_cache, float *z_cache, float *S_buf, float *z_buf,
                 size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+
+/* Fused backward of the linear_cuda API: causal_linear_attention_bwd_step1 +
+ * _bwd_dQ + _bwd_dKdV in one call, as linear_gpt.hpp:154-167 issues them.  No
+ * single counterpart in the reference.  den_cache as written by cxg_lin_fwd
+ * (eps included); widths as cxg_kattn_bwd.  z_cache of cxg_lin_fwd may be
+ * NULL when this backward is used. */
+int cxg_lin_bwd(const float *Q_phi, const float *K_phi, const float *V, const float *O,
+                const float *dO, const float *den_cache, float *dQ_phi, float *dK_phi,
+                float *dV, size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
 
 /* linear_cuda::causal_linear_attention_bwd_step1 (linear_cuda_kernels.cuh:18-22,
  * linear_cuda_kernels.cu:101-150). */

@@ -1,0 +1,201 @@
+"""GPU parity tests of the fused linear-attention backward (cxg_kattn_bwd, cxg_lin_bwd).
+
+The fused entry does what the reference's callers do with three calls
+(two_stage_gpt.hpp:149-157: kernel_attn_bwd_step1 -> _bwd_dQ -> _bwd_dKdV;
+linear_gpt.hpp:154-167: the linear_cuda counterparts).  Each test runs the
+GPU forward (z_cache not written, as a caller of the fused backward would),
+then the fused backward on the GPU's own O and den, and checks dQ, dK, dV
+against the oracle chain step1 -> dQ -> dKdV on the same O and den
+(kernel_test.cpp:276-292 feeds its backward oracle the kernel's O the same
+way), and against the reference's literal backward oracle
+(kernel_test.cpp:128-193) where the shape is small.
+"""
+import numpy as np
+import pytest
+
+import oracle as orc
+from helpers import assert_close, kernel_test_inputs, normal_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+
+def _nan(dev, *shape):
+    import torch
+    return torch.full(shape, float("nan"), device=dev)
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+def fused_kattn(dev, Q, K, V, dO, B, S, D, E):
+    import torch
+    import cxxgpt_attn as cx
+    N = B * S
+    tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
+    O, den = _nan(dev, N, E), _nan(dev, N)
+    cx.kattn_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+    dQ, dK, dV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
+    cx.kattn_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E)
+    torch.cuda.synchronize()
+    return dict(O=_np(O), den=_np(den), dQ=_np(dQ), dK=_np(dK), dV=_np(dV))
+
+
+def check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=False, tag=""):
+    g = fused_kattn(dev, Q, K, V, dO, B, S, D, E)
+    rO, rden, rzc = orc.kattn_fwd(Q, K, V, B, S, D, E, nthreads=8)
+    assert_close(g["O"], rO, f"{tag} O")
+    assert_close(g["den"], rden, f"{tag} den")
+    dnum, dden = orc.kattn_bwd_step1(g["O"], dO, g["den"], B * S, E)
+    rdQ = orc.kattn_bwd_dQ(K, V, dnum, dden, rzc, Q, B, S, D, E, nthreads=8)
+    rdK, rdV = orc.kattn_bwd_dKdV(Q, K, V, dnum, dden, B, S, D, E, nthreads=8)
+    assert_close(g["dQ"], rdQ, f"{tag} dQ")
+    assert_close(g["dK"], rdK, f"{tag} dK")
+    assert_close(g["dV"], rdV, f"{tag} dV")
+    if literal:
+        lQ, lK, lV = orc.kattn_bwd_literal(Q, K, V, g["O"], dO, rden, B, S, D, E)
+        assert_close(g["dQ"], lQ, f"{tag} dQ literal")
+        assert_close(g["dK"], lK, f"{tag} dK literal")
+        assert_close(g["dV"], lV, f"{tag} dV literal")
+
+
+@pytest.mark.parametrize("block", ["stage2", "flat", "chunk"])
+def test_kernel_test_blocks(dev, block):
+    blk = kernel_test_inputs()[block]
+    check_fused_kattn(dev, blk["Q"], blk["K"], blk["V"], blk["dO"], blk["B"], blk["S"],
+                      blk["D"], blk["E"], literal=True, tag=block)
+
+
+@pytest.mark.parametrize("S", [256, 4096])
+def test_config3_elu(dev, S):
+    """C3 (B' = 96, D = E = 64): several segments per sequence at S4096."""
+    B, D, E = 96, 64, 64
+    Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 300 + S)
+    check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"fused C3 S{S}")
+
+
+@pytest.mark.parametrize("B,S,D,E", [
+    (1, 1, 64, 64), (3, 15, 64, 64), (2, 17, 32, 48), (2, 100, 64, 64), (1, 1000, 64, 64),
+    (5, 333, 16, 8), (2, 40, 64, 1), (300, 16, 64, 64), (1, 4099, 64, 64), (2, 3000, 60, 64),
+    (1, 50, 128, 64), (2, 20, 64, 96),   # wider than 64: the split kernels inside the call
+])
+def test_ragged_shapes(dev, B, S, D, E):
+    """Partial last chunks, one and many segments, narrow and non-multiple-of-4 widths."""
+    Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 17 * S + D + E)
+    check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=(S <= 40), tag=f"B{B}S{S}D{D}E{E}")
+
+
+def test_unaligned_rows(dev):
+    """Tensors starting 4 bytes past a 16-byte boundary take the scalar-load variant."""
+    import torch
+    import cxxgpt_attn as cx
+    B, S, D, E = 2, 300, 64, 64
+    N = B * S
+    Q, K, V, dO = normal_inputs((N, D), (N, E), 5)
+
+    def off(a):
+        buf = torch.zeros(a.size + 1, device=dev)
+        buf[1:] = _t(a, dev).reshape(-1)
+        return buf[1:]
+
+    def offz(n):
+        return torch.full((n + 1,), float("nan"), device=dev)[1:]
+
+    tQ, tK, tV, tdO = off(Q), off(K), off(V), off(dO)
+    O, den = offz(N * E), offz(N)
+    cx.kattn_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+    dQ, dK, dV = offz(N * D), offz(N * D), offz(N * E)
+    cx.kattn_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E)
+    torch.cuda.synchronize()
+    gO, gden = _np(O).reshape(N, E), _np(den)
+    _, _, rzc = orc.kattn_fwd(Q, K, V, B, S, D, E, nthreads=8)
+    dnum, dden = orc.kattn_bwd_step1(gO, dO, gden, N, E)
+    assert_close(_np(dQ).reshape(N, D), orc.kattn_bwd_dQ(K, V, dnum, dden, rzc, Q, B, S, D, E),
+                 "unaligned dQ")
+    rdK, rdV = orc.kattn_bwd_dKdV(Q, K, V, dnum, dden, B, S, D, E)
+    assert_close(_np(dK).reshape(N, D), rdK, "unaligned dK")
+    assert_close(_np(dV).reshape(N, E), rdV, "unaligned dV")
+
+
+def test_matches_split_chain(dev):
+    """The fused backward and the three-call chain agree on the same forward outputs."""
+    import torch
+    import cxxgpt_attn as cx
+    B, S, D, E = 8, 2048, 64, 64
+    N = B * S
+    Q, K, V, dO = normal_inputs((N, D), (N, E), 77)
+    tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
+    O, den, zc = _nan(dev, N, E), _nan(dev, N), _nan(dev, N, D)
+    cx.kattn_fwd(tQ, tK, tV, O, den, zc, None, None, B, S, D, E)
+    dnum, dden = _nan(dev, N, E), _nan(dev, N)
+    cx.kattn_bwd_step1(O, tdO, den, dnum, dden, N, E)
+    sQ, sK, sV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
+    cx.kattn_bwd_dQ(tK, tV, dnum, dden, zc, tQ, sQ, None, B, S, D, E)
+    cx.kattn_bwd_dKdV(tQ, tK, tV, dnum, dden, sK, sV, B, S, D, E)
+    fQ, fK, fV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
+    cx.kattn_bwd(tQ, tK, tV, O, tdO, den, fQ, fK, fV, B, S, D, E)
+    torch.cuda.synchronize()
+    assert_close(_np(fQ), _np(sQ), "dQ fused vs split")
+    assert_close(_np(fK), _np(sK), "dK fused vs split")
+    assert_close(_np(fV), _np(sV), "dV fused vs split")
+
+
+def fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag):
+    import torch
+    import cxxgpt_attn as cx
+    N = B * S
+    tQ, tK, tV, tdO = _t(Qp, dev), _t(Kp, dev), _t(V, dev), _t(dO, dev)
+    O, den = _nan(dev, N, E), _nan(dev, N)
+    cx.lin_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+    dQ, dK, dV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
+    cx.lin_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E)
+    torch.cuda.synchronize()
+    rO, rden, rzc, _, _ = orc.lcu_fwd(Qp, Kp, V, B, S, D, E, nthreads=8)
+    assert_close(_np(O), rO, f"{tag} O")
+    assert_close(_np(den), rden, f"{tag} den_cache")
+    dnum, dden = orc.lcu_bwd_step1(_np(O), dO, _np(den), N, E)
+    assert_close(_np(dQ), orc.lcu_bwd_dQ(Kp, V, dnum, dden, rzc, B, S, D, E, nthreads=8),
+                 f"{tag} dQ_phi")
+    rdK, rdV = orc.lcu_bwd_dKdV(Qp, Kp, V, dnum, dden, B, S, D, E, nthreads=8)
+    assert_close(_np(dK), rdK, f"{tag} dK_phi")
+    assert_close(_np(dV), rdV, f"{tag} dV")
+
+
+@pytest.mark.parametrize("B,S,E", [(2, 64, 64), (3, 77, 48), (2, 500, 20)])
+def test_linear_cuda_elu(dev, B, S, E):
+    """LinearGPT's path with phi outside (D = next_pow2(E), zero-padded columns)."""
+    D = 1 << (E - 1).bit_length()
+    Xq, Xk, V, dO = normal_inputs((B * S, E), (B * S, E), 7 + E)
+    Qp, Kp = orc.phi_elu_forward(Xq, D, E), orc.phi_elu_forward(Xk, D, E)
+    fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu fused E{E}")
+
+
+@pytest.mark.parametrize("B,S", [(96, 1024), (3, 100)])
+def test_config4_hadamard_exp(dev, B, S):
+    """C4: Hadamard+Exp features (phi outside), Q, K ~ N(0, 0.25), V, dO ~ N(0, 1)."""
+    D = E = 64
+    N = B * S
+    Q, K, _, _ = normal_inputs((N, D), (N, E), 400, q_std=0.5)
+    _, _, V, dO = normal_inputs((N, D), (N, E), 400)
+    Qp, Kp = orc.phi_hexp_forward(Q, D, D), orc.phi_hexp_forward(K, D, D)
+    fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag="C4 fused")
+
+
+def test_error_paths(dev):
+    import torch
+    import cxxgpt_attn as cx
+    t = torch.zeros(64, device=dev)
+    P = cx._ptr
+    st = cx._stream(None)
+    p9 = [P(t)] * 9
+    for fn in ("cxg_kattn_bwd", "cxg_lin_bwd"):
+        assert cx.call_status(fn, *p9, 1, 4, 0, 8, st) == cx.CXG_ERR_DIMS
+        assert cx.call_status(fn, *p9, 1, 4, 8, 0, st) == cx.CXG_ERR_DIMS
+        assert cx.call_status(fn, *([None] + p9[1:]), 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
+        assert cx.call_status(fn, *p9[:5], None, *p9[6:], 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
+        assert cx.call_status(fn, *([None] * 9), 0, 4, 8, 8, st) == cx.CXG_OK   # empty
