@@ -365,8 +365,10 @@ static int lin_bwd_common(int phi, const float* Q, const float* K, const float* 
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
     Scratch ws;
-    if (!lin_bwd_fused_ok((int)D, (int)E)) {
-        // wide heads: the split kernels, intermediates in stream-ordered scratch
+    // the fused kernels address a sequence's rows with 32-bit byte offsets
+    if (!lin_bwd_fused_ok((int)D, (int)E) || S >= ((size_t)1 << 22)) {
+        // wide heads (or very long sequences): the split kernels, intermediates in
+        // stream-ordered scratch
         if (B * S > ((size_t)1 << 34) / (D + E + 1))
             return CXG_ERR_DIMS;
         st = ws.acquire(nullptr, 0, lin_bwd_split_ws_bytes((int)B, (int)S, (int)D, (int)E), s);

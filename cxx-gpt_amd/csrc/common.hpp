@@ -62,13 +62,23 @@ __device__ __forceinline__ float xrow_max(float v)
     v = fmaxf(v, __shfl_xor(v, 32, 64));
     return v;
 }
-// Sum over the 16 lanes of one row (lanes sharing l / 16).
+// Lane exchange within a 16-lane row through DPP (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of one row (lanes sharing l / 16): rotations by 8
+// and 4 within the row, then the quad swaps 2 and 1.  Each lane adds the same
+// pairs as an xor-8/4/2/1 butterfly, so the result is that butterfly's.
 __device__ __forceinline__ float row16_sum(float v)
 {
-    v += __shfl_xor(v, 8, 64);
-    v += __shfl_xor(v, 4, 64);
-    v += __shfl_xor(v, 2, 64);
-    v += __shfl_xor(v, 1, 64);
+    v += dpp_f<0x128>(v);   // row_ror:8
+    v += dpp_f<0x124>(v);   // row_ror:4
+    v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
     return v;
 }
 
@@ -183,6 +193,11 @@ __device__ __forceinline__ void buffer_store_f32(__amdgpu_buffer_rsrc_t r, unsig
 __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, unsigned off)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ f4 buffer_load_f4(__amdgpu_buffer_rsrc_t r, unsigned off)
+{
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
 } // namespace cxg
