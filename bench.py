@@ -17,8 +17,9 @@ them can be made the reported workload with --workload NAME):
             two_stage API chain kernel_attn_fwd -> bwd_step1 -> bwd_dQ ->
             bwd_dKdV; GB/s of compulsory I/O, (12*S*D + 2*S)*4 bytes/sequence
   c3s256    the same at S=256
-  c3fused   c3 with the one-call backward: kernel_attn_fwd without z_cache ->
-            cxg_kattn_bwd (step1 + dQ + dKdV fused); c3fuseds256 at S=256
+  c3fused   c3 through the fused pair: cxg_kattn_fwd_ctx (O, den and a segment-
+            state context instead of z_cache) -> cxg_kattn_bwd (step1 + dQ + dKdV
+            in one pass, prefix state from the context); c3fuseds256 at S=256
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
@@ -243,11 +244,13 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
     dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
     P = _ptr
     if fused:
+        nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+        ctx = c.empty(max(1, nctx // 4))
         step = Stepper(c.cx.lib(), [
-            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), None, None, None, Bq, S, D, E,
-                               c.sp)),
-            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(dQ), P(dK), P(dV),
-                               Bq, S, D, E, c.sp)),
+            ("cxg_kattn_fwd_ctx", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, D, E,
+                                   c.sp)),
+            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ), P(dK),
+                               P(dV), Bq, S, D, E, c.sp)),
         ])
     else:
         zc, dnum, dden = c.empty(N, D), c.empty(N, E), c.empty(N)
@@ -273,7 +276,7 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, " + (
-                            "fused backward (cxg_kattn_fwd without z_cache -> cxg_kattn_bwd)"
+                            "fused pair (cxg_kattn_fwd_ctx -> cxg_kattn_bwd with the context)"
                             if fused else "two_stage API chain (fwd, step1, dQ, dKdV)"),
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))

@@ -279,7 +279,7 @@ static int lin_check(size_t B, size_t S, size_t D, size_t E, bool* empty)
 static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, const float* K,
                           const float* V, float* O, float* den, float* zc, float* S_buf,
                           float* z_buf, size_t B, size_t S, size_t D, size_t E,
-                          cxg_stream_t stream)
+                          cxg_stream_t stream, void* ctx = nullptr, size_t ctx_bytes = 0)
 {
     bool empty;
     int st = lin_check(B, S, D, E, &empty);
@@ -289,6 +289,20 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
     const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_FWD);
+    // context for the fused backward (shapes the fused kernels take): the
+    // segment records are the scan workspace itself
+    const size_t need = ctx_bytes > 0 || ctx != nullptr
+                            ? lin_ctx_bytes((int)B, (int)S, (int)D, (int)E) : 0;
+    if (need > 0) {
+        if (ctx == nullptr)
+            return CXG_ERR_NULL;
+        if (ctx_bytes < need)
+            return CXG_ERR_WORKSPACE;
+        const LinCtx c = lin_ctx_split(ctx, (int)B, (int)S, (int)D, (int)E);
+        return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de,
+                                         den_eps, (int)B, (int)S, (int)D, (int)E, c.rec, s, c.tot,
+                                         c.zt));
+    }
     Scratch ws;
     st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
     if (st != CXG_OK)
@@ -353,8 +367,8 @@ static int lin_dkdv_common(int phi, const float* Q, const float* K, const float*
 }
 
 static int lin_bwd_common(int phi, const float* Q, const float* K, const float* V,
-                          const float* O, const float* dO, const float* den, float* dQ,
-                          float* dK, float* dV, size_t B, size_t S, size_t D, size_t E,
+                          const float* O, const float* dO, const float* den, const void* ctx,
+                          float* dQ, float* dK, float* dV, size_t B, size_t S, size_t D, size_t E,
                           cxg_stream_t stream)
 {
     bool empty;
@@ -365,8 +379,7 @@ static int lin_bwd_common(int phi, const float* Q, const float* K, const float* 
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
     Scratch ws;
-    // the fused kernels address a sequence's rows with 32-bit byte offsets
-    if (!lin_bwd_fused_ok((int)D, (int)E) || S >= ((size_t)1 << 22)) {
+    if (!lin_bwd_fused_ok((int)D, (int)E, (long)S)) {
         // wide heads (or very long sequences): the split kernels, intermediates in
         // stream-ordered scratch
         if (B * S > ((size_t)1 << 34) / (D + E + 1))
@@ -377,12 +390,12 @@ static int lin_bwd_common(int phi, const float* Q, const float* K, const float* 
         return hip_status(lin_bwd_split_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B,
                                                (int)S, (int)D, (int)E, ws.p, s));
     }
-    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_BWD);
-    st = ws.acquire(nullptr, 0, lin_bwd_ws_bytes(p, (int)B, (int)S), s);
+    st = ws.acquire(nullptr, 0,
+                    lin_bwd_fused_ws_bytes((int)B, (int)S, (int)D, (int)E, ctx != nullptr), s);
     if (st != CXG_OK)
         return st;
     return hip_status(lin_bwd_fused_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B, (int)S,
-                                           (int)D, (int)E, ws.p, s));
+                                           (int)D, (int)E, ws.p, s, ctx));
 }
 
 int cxg_kattn_fwd(const float* Q, const float* K, const float* V, float* O, float* den_cache,
@@ -415,10 +428,35 @@ int cxg_kattn_bwd_dKdV(const float* Q, const float* K, const float* V, const flo
 }
 
 int cxg_kattn_bwd(const float* Q, const float* K, const float* V, const float* O,
-                  const float* dO, const float* den_cache, float* dQ, float* dK, float* dV,
-                  size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
+                  const float* dO, const float* den_cache, const void* ctx, float* dQ, float* dK,
+                  float* dV, size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
 {
-    return lin_bwd_common(PHI_ELU1, Q, K, V, O, dO, den_cache, dQ, dK, dV, B, S, D, E, stream);
+    return lin_bwd_common(PHI_ELU1, Q, K, V, O, dO, den_cache, ctx, dQ, dK, dV, B, S, D, E,
+                          stream);
+}
+
+size_t cxg_lin_ctx_size(size_t B, size_t S, size_t D, size_t E)
+{
+    bool empty;
+    if (lin_check(B, S, D, E, &empty) != CXG_OK || empty)
+        return 0;
+    return lin_ctx_bytes((int)B, (int)S, (int)D, (int)E);
+}
+
+int cxg_kattn_fwd_ctx(const float* Q, const float* K, const float* V, float* O,
+                      float* den_cache, void* ctx, size_t ctx_bytes, size_t B, size_t S,
+                      size_t D, size_t E, cxg_stream_t stream)
+{
+    return lin_fwd_common(PHI_ELU1, 0, 0, Q, K, V, O, den_cache, nullptr, nullptr, nullptr, B, S,
+                          D, E, stream, ctx, ctx_bytes);
+}
+
+int cxg_lin_fwd_ctx(const float* Q_phi, const float* K_phi, const float* V, float* O,
+                    float* den_cache, void* ctx, size_t ctx_bytes, size_t B, size_t S, size_t D,
+                    size_t E, cxg_stream_t stream)
+{
+    return lin_fwd_common(PHI_NONE, 1, 1, Q_phi, K_phi, V, O, den_cache, nullptr, nullptr,
+                          nullptr, B, S, D, E, stream, ctx, ctx_bytes);
 }
 
 int cxg_lin_fwd(const float* Q_phi, const float* K_phi, const float* V, float* O,
@@ -453,11 +491,12 @@ int cxg_lin_bwd_dKdV(const float* Q_phi, const float* K_phi, const float* V, con
 }
 
 int cxg_lin_bwd(const float* Q_phi, const float* K_phi, const float* V, const float* O,
-                const float* dO, const float* den_cache, float* dQ_phi, float* dK_phi,
-                float* dV, size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream)
+                const float* dO, const float* den_cache, const void* ctx, float* dQ_phi,
+                float* dK_phi, float* dV, size_t B, size_t S, size_t D, size_t E,
+                cxg_stream_t stream)
 {
-    return lin_bwd_common(PHI_NONE, Q_phi, K_phi, V, O, dO, den_cache, dQ_phi, dK_phi, dV, B, S,
-                          D, E, stream);
+    return lin_bwd_common(PHI_NONE, Q_phi, K_phi, V, O, dO, den_cache, ctx, dQ_phi, dK_phi, dV,
+                          B, S, D, E, stream);
 }
 
 static int phi_check(size_t N, size_t D, size_t E, bool hexp, bool* empty)

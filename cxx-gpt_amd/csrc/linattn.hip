@@ -275,7 +275,8 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zcache,
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
-    int sfin_de, int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L)
+    float* __restrict__ ctot, float* __restrict__ ztab, int sfin_de, int den_incl_eps, int Bq,
+    int S, int D, int E, int nseg, int L)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * FWD_STAGE + CHUNK];
     const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
@@ -285,6 +286,9 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const int tbeg = seg * L, tend = min(S, tbeg + L), tlast = tend - 1;
     const long rb = (long)seq * S;
     float* bZ = lds + 2 * FWD_STAGE;   // z rows for the z_cache store (each wave its tiles)
+    // context for the fused backward (nullable): z before every chunk, [chunk][64]
+    const __amdgpu_buffer_rsrc_t rzt =
+        buf_rsrc(ztab != nullptr ? ztab + ((long)seq * ((S + 15) / 16) + tbeg / 16) * 64 : nullptr);
 
     // state slice S[d][e], et = 2h + j: St[dt][j] lane (e = 16et + l16), element r <-> d = 16dt + 4g + r
     // z (prefix of phi(K) before the chunk): zC[dt] = z[16dt + l16], zR[dt][i] = z[16dt + 4g + i]
@@ -337,6 +341,12 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         float* bK = st + CHUNK;
         float* bV = st + 2 * CHUNK;
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        // context: z before the chunk (lanes l16 = 0 of wave 0 store, others dropped)
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            buffer_store_f4(rzt, (h == 0 && l16 == 0) ? (unsigned)(c * 64 + 16 * dt + 4 * g) * 4u
+                                                      : kDropOffset,
+                            zR[dt]);
         finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
         finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
         finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
@@ -488,6 +498,21 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             for (int dt = 0; dt < 4; dt++)
                 if (16 * dt + l16 < D)
                     zfin[(long)seq * D + 16 * dt + l16] = zC[dt];
+    }
+    if (ctot != nullptr && seg == nseg - 1) {
+        // context: the sequence's final state as a segment record, [d][e] then z
+        float* R = ctot + (long)seq * LIN_WS;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    R[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16] = St[dt][j][r];
+        if (h == 0 && g == 0)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                R[4096 + 16 * dt + l16] = zC[dt];
     }
 }
 
@@ -1272,8 +1297,9 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
 
 template <int PHI>
 static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float* O, float* den,
-                           float* zc, float* Sfin, float* zfin, int sfin_de, int den_eps, int Bq,
-                           int S, int D, int E, void* ws, hipStream_t st)
+                           float* zc, float* Sfin, float* zfin, float* ctot, float* ztab,
+                           int sfin_de, int den_eps, int Bq, int S, int D, int E, void* ws,
+                           hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
     if (!p.fast) {
@@ -1306,25 +1332,29 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
     ProfScope ps(st, "lin_fwd");
     if (mode == 2)
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
+                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           p.L);
     else if (mode == 1)
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
+                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           p.L);
     else
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, p.nseg, p.L);
+                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           p.L);
     return hipGetLastError();
 }
 
 hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                           float* den, float* zc, float* Sfin, float* zfin, int sfin_de,
-                          int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st)
+                          int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st,
+                          float* ctot, float* ztab)
 {
     if (phi == PHI_ELU1)
-        return fwd_impl<PHI_ELU1>(Q, K, V, O, den, zc, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E,
-                                  ws, st);
-    return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, sfin_de, den_eps, Bq, S, D, E, ws,
-                              st);
+        return fwd_impl<PHI_ELU1>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps,
+                                  Bq, S, D, E, ws, st);
+    return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq,
+                              S, D, E, ws, st);
 }
 
 hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, float* dnum,

@@ -28,9 +28,13 @@ size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E);
 // den_eps: 1 stores den + 1e-8 (linear_cuda), 0 stores den (two_stage).  O is
 // num / (den + 1e-8) either way.  Sfin/zfin (nullable) receive the final state,
 // sfin_de selecting [d][e] (1) or [e][d] (0) layout.
+// ctot / ztab (nullable, fast path only): the context for the fused backward:
+// each sequence's final state as a segment record, and z before every 16-row
+// chunk ([S / 16][64] per sequence).  ws then holds the segment prefix records.
 hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                           float* den, float* zc, float* Sfin, float* zfin, int sfin_de,
-                          int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st);
+                          int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st,
+                          float* ctot = nullptr, float* ztab = nullptr);
 hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, float* dnum,
                             float* dden, long N, int E, hipStream_t st);
 hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* dnum,
@@ -41,13 +45,25 @@ hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float*
                            int S, int D, int E, void* ws, hipStream_t st);
 // Fused backward (step 1 + dQ + dK/dV, linbwd.hip) for D, E <= 64.  den is the
 // forward's den_cache; dnum = dO / den and dden = -(dO . O) / den as in step 1.
-bool lin_bwd_fused_ok(int D, int E);
+bool lin_bwd_fused_ok(int D, int E, long S);
 int lin_bwd_slots();   // resident fused-backward workgroups per compute unit
 size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S);
+size_t lin_bwd_fused_ws_bytes(int Bq, int S, int D, int E, bool with_ctx);
+// Forward-to-backward context of the fused pair: the forward's segment prefix
+// records, each sequence's final-state record and the z table.
+struct LinCtx {
+    float* rec;   // Bq * nseg_fwd records (the forward's scan workspace)
+    float* tot;   // Bq records
+    float* zt;    // Bq * ceil(S / 16) * 64
+};
+size_t lin_ctx_bytes(int Bq, int S, int D, int E);   // 0: shapes the fused kernels do not take
+LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E);
+// ctx (nullable): as written by the forward with the same dimensions; the
+// backward then takes the prefix state and z from it instead of recomputing them.
 hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const float* V,
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
-                                hipStream_t st);
+                                hipStream_t st, const void* ctx);
 // The same for other widths, through the split kernels (workspace: zc, dnum,
 // dden and the scan scratch).
 size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E);

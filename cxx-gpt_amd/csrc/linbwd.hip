@@ -55,9 +55,10 @@ __device__ __forceinline__ f4 ld_row4(const float* __restrict__ base, long row, 
 
 // ---------------------------------------------------------------------------
 // lin_bagg: per-segment aggregates.  Workgroups [0, Bq*nseg) form the prefix
-// records (X = phi(K), Y = V, w = 1, z table); workgroups after that the
-// suffix records of segments 1.. (X = phi(Q), Y = dnum, w = dden; segment 0's
-// suffix aggregate is never used).  Records are row-major [d][e] plus z[d],
+// records (X = phi(K), Y = V, w = 1, z table; skipped when the forward's
+// context supplies them); workgroups after that the suffix records of
+// segments 1.. (X = phi(Q), Y = dnum, w = dden; segment 0's suffix aggregate
+// is never used).  Records are row-major [d][e] plus z[d],
 // LIN_WS floats.  Wave w accumulates output columns e of tile w over the
 // segment's chunks, in forward order.
 // ---------------------------------------------------------------------------
@@ -191,10 +192,10 @@ __global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
     float* __restrict__ wsP, float* __restrict__ wsB, float* __restrict__ ztab, int Bq, int S,
-    int D, int E, int nseg, int L, int nchs)
+    int D, int E, int nseg, int L, int nchs, int with_prefix)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * BAGG_STAGE];
-    const int nP = Bq * nseg;
+    const int nP = with_prefix ? Bq * nseg : 0;
     if ((int)blockIdx.x < nP) {
         const int seq = blockIdx.x / nseg, seg = blockIdx.x - seq * nseg;
         bagg_body<PHI, VEC, FW, false>(Q, K, V, O, dO, den, wsP + (long)blockIdx.x * LIN_WS,
@@ -216,10 +217,11 @@ __global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
 // record is only written).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void lin_bscan_kernel(float* __restrict__ wsP,
-                                                       float* __restrict__ wsB, int Bq, int nseg)
+                                                       float* __restrict__ wsB, int Bq, int nseg,
+                                                       int with_prefix)
 {
-    const long j = (long)blockIdx.x * 256 + threadIdx.x;
     const long n = (long)Bq * LIN_WS;
+    const long j = (long)blockIdx.x * 256 + threadIdx.x + (with_prefix ? 0 : n);
     if (j >= 2 * n)
         return;
     const bool suf = j >= n;
@@ -275,7 +277,8 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ wsP, const float* __restrict__ wsB, const float* __restrict__ ztab,
-    int S, int D, int E, int nseg, int L, int nchs)
+    const float* __restrict__ crec, const float* __restrict__ ctot, int mf, int nsegf, int S, int D,
+    int E, int nseg, int L, int nchs)
 {
     __shared__ __attribute__((aligned(16))) float lds[BWD_LDS];
     float* sS = lds + 2 * BWD_STAGE;   // S* [d][e]
@@ -293,8 +296,17 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     // Sm[dt]:  lane (e = 16w + l16), element r <-> d = 16dt + 4g + r of S* (suffix
     //          of the chunks after the current one)
     // zs, pz:  element r <-> d = 16w + 4g + r of z* and of z before the segment
+    // With the forward's context (ctot != null) the segment-end state is the
+    // record at the forward's segment boundary mf * (seg + 1) (or the final
+    // state) and ztab holds absolute z, so the segment prefix of z is not added.
     f4 StT[4], Sm[4];
-    const float* RP = wsP + (long)wid * LIN_WS;
+    const float* RP;
+    if (ctot != nullptr) {
+        const int e = min(mf * (seg + 1), nsegf);
+        RP = e < nsegf ? crec + ((long)seq * nsegf + e) * LIN_WS : ctot + (long)seq * LIN_WS;
+    } else {
+        RP = wsP + (long)wid * LIN_WS;
+    }
     const float* RB = wsB + (long)wid * LIN_WS;
 #pragma unroll
     for (int a = 0; a < 4; a++) {
@@ -304,7 +316,8 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             Sm[a][r] = RB[(16 * a + 4 * g + r) * 64 + 16 * w + l16];
     }
     f4 zs = *reinterpret_cast<const f4*>(RB + 4096 + 16 * w + 4 * g);
-    const f4 pz = *reinterpret_cast<const f4*>(RP + 4096 + 16 * w + 4 * g);
+    const f4 pz = ctot != nullptr ? f4zero()
+                                  : *reinterpret_cast<const f4*>(RP + 4096 + 16 * w + 4 * g);
 
     const int nch = (tend - tbeg + 15) / 16;
     const float* zt0 = ztab + ((long)seq * nchs + tbeg / 16) * 64 + 16 * w + 4 * g;
@@ -556,7 +569,12 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
 // ---------------------------------------------------------------------------
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-bool lin_bwd_fused_ok(int D, int E) { return D >= 1 && E >= 1 && D <= 64 && E <= 64; }
+// The fused kernels take D, E <= 64 and address a sequence's rows with 32-bit
+// byte offsets.
+bool lin_bwd_fused_ok(int D, int E, long S)
+{
+    return D >= 1 && E >= 1 && D <= 64 && E <= 64 && S >= 1 && S < (1L << 22);
+}
 
 int lin_bwd_slots()
 {
@@ -579,64 +597,117 @@ size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S)
     return ((size_t)2 * Bq * p.nseg * LIN_WS + (size_t)Bq * nchs * 64) * sizeof(float);
 }
 
+size_t lin_ctx_bytes(int Bq, int S, int D, int E)
+{
+    if (!lin_bwd_fused_ok(D, E, S))
+        return 0;
+    const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
+    const long nchs = (S + 15) / 16;
+    return ((size_t)Bq * (pf.nseg + 1) * LIN_WS + (size_t)Bq * nchs * 64) * sizeof(float);
+}
+
+LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E)
+{
+    const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
+    LinCtx c;
+    c.rec = (float*)ctx;
+    c.tot = c.rec + (size_t)Bq * pf.nseg * LIN_WS;
+    c.zt = c.tot + (size_t)Bq * LIN_WS;
+    return c;
+}
+
+// Launch context: with the forward's context (c.tot != null) the prefix
+// records and the z table come from it and only the suffix aggregates are
+// formed; mf forward segments make one backward segment.
+struct BwdArgs {
+    float *wsP, *wsB, *zt;
+    LinCtx c;
+    int mf, nsegf;
+};
+
 template <int PHI, bool VEC, bool FW>
 static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const float* V,
                          const float* O, const float* dO, const float* den, float* dQ, float* dK,
-                         float* dV, float* wsP, float* wsB, float* zt, int Bq, int S, int D, int E,
-                         hipStream_t st)
+                         float* dV, const BwdArgs& a, int Bq, int S, int D, int E, hipStream_t st)
 {
     const int nchs = (S + 15) / 16;
-    {
+    const bool pre = a.c.tot == nullptr;
+    const unsigned nb = (unsigned)((pre ? Bq * p.nseg : 0) + Bq * (p.nseg - 1));
+    if (nb > 0) {
         ProfScope ps(st, "lin_bagg");
-        const unsigned nb = (unsigned)(Bq * p.nseg + Bq * (p.nseg - 1));
         hipLaunchKernelGGL((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
-                           Q, K, V, O, dO, den, wsP, wsB, zt, Bq, S, D, E, p.nseg, p.L, nchs);
+                           Q, K, V, O, dO, den, a.wsP, a.wsB, a.zt, Bq, S, D, E, p.nseg, p.L, nchs,
+                           pre ? 1 : 0);
     }
     {
         ProfScope ps(st, "lin_bscan");
-        const long n = 2L * Bq * LIN_WS;
+        const long n = (pre ? 2L : 1L) * Bq * LIN_WS;
         hipLaunchKernelGGL(lin_bscan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                           wsP, wsB, Bq, p.nseg);
+                           a.wsP, a.wsB, Bq, p.nseg, pre ? 1 : 0);
     }
     ProfScope ps(st, "lin_bwd");
     hipLaunchKernelGGL((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
-                       dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt,
-                       S, D, E, p.nseg, p.L, nchs);
+                       dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, a.wsP, a.wsB,
+                       pre ? a.zt : a.c.zt, a.c.rec, a.c.tot, a.mf, a.nsegf, S, D, E, p.nseg, p.L,
+                       nchs);
 }
 
 template <int PHI>
 static void bwd_dispatch(const LinPlan& p, const float* Q, const float* K, const float* V,
                          const float* O, const float* dO, const float* den, float* dQ, float* dK,
-                         float* dV, float* wsP, float* wsB, float* zt, int Bq, int S, int D, int E,
-                         hipStream_t st)
+                         float* dV, const BwdArgs& a, int Bq, int S, int D, int E, hipStream_t st)
 {
     const bool vec = D % 4 == 0 && E % 4 == 0 && al16(Q) && al16(K) && al16(V) && al16(O) &&
                      al16(dO) && al16(dQ) && al16(dK) && al16(dV);
     if (vec && D == 64 && E == 64)
-        bwd_launch_t<PHI, true, true>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D,
-                                      E, st);
+        bwd_launch_t<PHI, true, true>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else if (vec)
-        bwd_launch_t<PHI, true, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S,
-                                       D, E, st);
+        bwd_launch_t<PHI, true, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
-        bwd_launch_t<PHI, false, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S,
-                                        D, E, st);
+        bwd_launch_t<PHI, false, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
+}
+
+// Backward segments: the backward's own plan, or with a context whole groups
+// of mf forward segments (so every backward segment ends on a boundary whose
+// prefix record the forward kept), about as many as the backward's own plan.
+static LinPlan bwd_plan(int Bq, int S, int D, int E, bool with_ctx, int* mf, int* nsegf)
+{
+    LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_BWD);
+    *mf = 1;
+    *nsegf = 0;
+    if (with_ctx) {
+        const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
+        *nsegf = pf.nseg;
+        *mf = max(1, pf.nseg / max(1, p.nseg));
+        p.L = pf.L * *mf;
+        p.nseg = (pf.nseg + *mf - 1) / *mf;
+    }
+    return p;
 }
 
 hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const float* V,
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
-                                hipStream_t st)
+                                hipStream_t st, const void* ctx)
 {
-    const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_BWD);
-    float* wsP = (float*)ws;
-    float* wsB = wsP + (size_t)Bq * p.nseg * LIN_WS;
-    float* zt = wsB + (size_t)Bq * p.nseg * LIN_WS;
+    BwdArgs a;
+    const LinPlan p = bwd_plan(Bq, S, D, E, ctx != nullptr, &a.mf, &a.nsegf);
+    a.wsP = (float*)ws;
+    a.wsB = a.wsP + (size_t)Bq * p.nseg * LIN_WS;
+    a.zt = a.wsB + (size_t)Bq * p.nseg * LIN_WS;
+    a.c = ctx != nullptr ? lin_ctx_split(const_cast<void*>(ctx), Bq, S, D, E)
+                         : LinCtx{nullptr, nullptr, nullptr};
     if (phi == PHI_ELU1)
-        bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D, E, st);
+        bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
-        bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, wsP, wsB, zt, Bq, S, D, E, st);
+        bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     return hipGetLastError();
+}
+
+size_t lin_bwd_fused_ws_bytes(int Bq, int S, int D, int E, bool with_ctx)
+{
+    int mf, nsegf;
+    return lin_bwd_ws_bytes(bwd_plan(Bq, S, D, E, with_ctx, &mf, &nsegf), Bq, S);
 }
 
 } // namespace cxg

@@ -38,12 +38,15 @@ SIGNATURES = {
     "cxg_kattn_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_kattn_bwd_dQ": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_kattn_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
-    "cxg_kattn_bwd": [_vp] * 9 + [_sz] * 4 + [_vp],
+    "cxg_kattn_bwd": [_vp] * 10 + [_sz] * 4 + [_vp],
+    "cxg_kattn_fwd_ctx": [_vp] * 6 + [_sz] * 5 + [_vp],
+    "cxg_lin_ctx_size": [_sz] * 4,
     "cxg_lin_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_lin_bwd_dQ": [_vp] * 7 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
-    "cxg_lin_bwd": [_vp] * 9 + [_sz] * 4 + [_vp],
+    "cxg_lin_bwd": [_vp] * 10 + [_sz] * 4 + [_vp],
+    "cxg_lin_fwd_ctx": [_vp] * 6 + [_sz] * 5 + [_vp],
     "cxg_phi_elu_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
@@ -59,6 +62,7 @@ _RESTYPES = {
     "cxg_status_str": ctypes.c_char_p,
     "cxg_version": ctypes.c_char_p,
     "cxg_mha_bwd_workspace_size": ctypes.c_size_t,
+    "cxg_lin_ctx_size": ctypes.c_size_t,
     "cxg_prof_enable": None,
     "cxg_prof_reset": None,
 }
@@ -173,10 +177,21 @@ def kattn_bwd_dKdV(Q, K, V, dnum, dden, dK, dV, B, S, D, E, stream=None):
           _ptr(dV), B, S, D, E, _stream(stream))
 
 
-def kattn_bwd(Q, K, V, O, dO, den, dQ, dK, dV, B, S, D, E, stream=None):
-    """Fused step1 + dQ + dKdV (no z_cache, no dnum/dden round trip)."""
-    _call("cxg_kattn_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(dQ),
-          _ptr(dK), _ptr(dV), B, S, D, E, _stream(stream))
+def kattn_bwd(Q, K, V, O, dO, den, dQ, dK, dV, B, S, D, E, ctx=None, stream=None):
+    """Fused step1 + dQ + dKdV (no z_cache, no dnum/dden round trip); ctx from kattn_fwd_ctx."""
+    _call("cxg_kattn_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(ctx),
+          _ptr(dQ), _ptr(dK), _ptr(dV), B, S, D, E, _stream(stream))
+
+
+def lin_ctx_size(B, S, D, E):
+    """Bytes of the forward-to-backward context of the fused pair (0: not used)."""
+    return lib().cxg_lin_ctx_size(B, S, D, E)
+
+
+def kattn_fwd_ctx(Q, K, V, O, den, ctx, B, S, D, E, stream=None):
+    nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
+    _call("cxg_kattn_fwd_ctx", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
+          B, S, D, E, _stream(stream))
 
 
 # ------------------------------------------------------------------ linear_cuda API
@@ -200,10 +215,16 @@ def lin_bwd_dKdV(Qp, Kp, V, dnum, dden, dKp, dV, B, S, D, E, stream=None):
           _ptr(dV), B, S, D, E, _stream(stream))
 
 
-def lin_bwd(Qp, Kp, V, O, dO, den, dQp, dKp, dV, B, S, D, E, stream=None):
-    """Fused step1 + dQ + dKdV of the linear_cuda API."""
-    _call("cxg_lin_bwd", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(dQp),
-          _ptr(dKp), _ptr(dV), B, S, D, E, _stream(stream))
+def lin_bwd(Qp, Kp, V, O, dO, den, dQp, dKp, dV, B, S, D, E, ctx=None, stream=None):
+    """Fused step1 + dQ + dKdV of the linear_cuda API; ctx from lin_fwd_ctx."""
+    _call("cxg_lin_bwd", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(dO), _ptr(den), _ptr(ctx),
+          _ptr(dQp), _ptr(dKp), _ptr(dV), B, S, D, E, _stream(stream))
+
+
+def lin_fwd_ctx(Qp, Kp, V, O, den, ctx, B, S, D, E, stream=None):
+    nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
+    _call("cxg_lin_fwd_ctx", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
+          B, S, D, E, _stream(stream))
 
 
 def phi_elu_fwd(x, phi, N, D, E, stream=None):

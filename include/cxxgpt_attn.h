@@ -124,12 +124,28 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
  * (two_stage_cuda_kernels.cuh:46-61).  No single counterpart in the reference.
  * Reads Q, K, V, O, dO and den_cache once and writes dQ, dK, dV; the step-1
  * intermediates (dnum = dO/den, dden = -sum_e dO*O/den) stay on chip and no
- * z_cache is needed.  D <= 64 and E <= 64 take the fused kernels; wider heads
+ * z_cache is needed.  ctx: NULL, or the context cxg_kattn_fwd_ctx wrote for the
+ * same Q, K, V and dimensions (the backward then skips re-reading K and V for
+ * the prefix state).  D <= 64 and E <= 64 take the fused kernels; wider heads
  * run the split kernels inside the call (z_cache, dnum, dden in stream-ordered
- * scratch). */
+ * scratch; ctx is not used). */
 int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O,
-                  const float *dO, const float *den_cache, float *dQ, float *dK, float *dV,
-                  size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+                  const float *dO, const float *den_cache, const void *ctx, float *dQ,
+                  float *dK, float *dV, size_t B, size_t S, size_t D, size_t E,
+                  cxg_stream_t stream);
+
+/* Forward that leaves a context for the fused backward instead of z_cache:
+ * O and den_cache as cxg_kattn_fwd writes them, plus in ctx (device memory of
+ * cxg_lin_ctx_size() bytes) the per-segment prefix states, each sequence's
+ * final state and z before every 16-row chunk.  No counterpart in the
+ * reference (its forward hands the backward z_cache, B*S*D floats; the context
+ * is about a fifth of that at B' = 96, S = 4096, D = E = 64).  For shapes the
+ * fused kernels do not take, cxg_lin_ctx_size() is 0, ctx may be NULL and
+ * nothing is written to it. */
+size_t cxg_lin_ctx_size(size_t B, size_t S, size_t D, size_t E);
+int cxg_kattn_fwd_ctx(const float *Q, const float *K, const float *V, float *O,
+                      float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
+                      size_t D, size_t E, cxg_stream_t stream);
 
 /* ============ causal linear attention, linear_cuda API (phi outside) ==========
  * Inputs are feature-mapped already: Q_phi/K_phi (B*S, D), V/O (B*S, E).
@@ -146,11 +162,17 @@ int cxg_lin_fwd(const float *Q_phi, const float *K_phi, const float *V, float *O
 /* Fused backward of the linear_cuda API: causal_linear_attention_bwd_step1 +
  * _bwd_dQ + _bwd_dKdV in one call, as linear_gpt.hpp:154-167 issues them.  No
  * single counterpart in the reference.  den_cache as written by cxg_lin_fwd
- * (eps included); widths as cxg_kattn_bwd.  z_cache of cxg_lin_fwd may be
- * NULL when this backward is used. */
+ * (eps included); widths and ctx as cxg_kattn_bwd (ctx from cxg_lin_fwd_ctx).
+ * z_cache of cxg_lin_fwd may be NULL when this backward is used. */
 int cxg_lin_bwd(const float *Q_phi, const float *K_phi, const float *V, const float *O,
-                const float *dO, const float *den_cache, float *dQ_phi, float *dK_phi,
-                float *dV, size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
+                const float *dO, const float *den_cache, const void *ctx, float *dQ_phi,
+                float *dK_phi, float *dV, size_t B, size_t S, size_t D, size_t E,
+                cxg_stream_t stream);
+/* The context-writing forward of the linear_cuda API (as cxg_kattn_fwd_ctx;
+ * den_cache includes eps). */
+int cxg_lin_fwd_ctx(const float *Q_phi, const float *K_phi, const float *V, float *O,
+                    float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
+                    size_t D, size_t E, cxg_stream_t stream);
 
 /* linear_cuda::causal_linear_attention_bwd_step1 (linear_cuda_kernels.cuh:18-22,
  * linear_cuda_kernels.cu:101-150). */

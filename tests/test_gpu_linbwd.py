@@ -33,21 +33,36 @@ def _np(t):
     return t.cpu().numpy()
 
 
-def fused_kattn(dev, Q, K, V, dO, B, S, D, E):
+def _ctx(dev, B, S, D, E):
+    """Context buffer for the fused pair (None when the shape does not use one)."""
+    import torch
+    import cxxgpt_attn as cx
+    n = cx.lin_ctx_size(B, S, D, E)
+    return torch.full((n // 4,), float("nan"), device=dev) if n else None
+
+
+def fused_kattn(dev, Q, K, V, dO, B, S, D, E, use_ctx=False):
+    """Forward (z_cache not written; with use_ctx the context-writing forward),
+    then the one-call backward."""
     import torch
     import cxxgpt_attn as cx
     N = B * S
     tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
     O, den = _nan(dev, N, E), _nan(dev, N)
-    cx.kattn_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+    ctx = _ctx(dev, B, S, D, E) if use_ctx else None
+    if use_ctx:
+        cx.kattn_fwd_ctx(tQ, tK, tV, O, den, ctx, B, S, D, E)
+    else:
+        cx.kattn_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
     dQ, dK, dV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
-    cx.kattn_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E)
+    cx.kattn_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E, ctx=ctx)
     torch.cuda.synchronize()
     return dict(O=_np(O), den=_np(den), dQ=_np(dQ), dK=_np(dK), dV=_np(dV))
 
 
-def check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=False, tag=""):
-    g = fused_kattn(dev, Q, K, V, dO, B, S, D, E)
+def check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=False, tag="", use_ctx=False):
+    g = fused_kattn(dev, Q, K, V, dO, B, S, D, E, use_ctx)
+    tag = f"{tag}{' ctx' if use_ctx else ''}"
     rO, rden, rzc = orc.kattn_fwd(Q, K, V, B, S, D, E, nthreads=8)
     assert_close(g["O"], rO, f"{tag} O")
     assert_close(g["den"], rden, f"{tag} den")
@@ -71,12 +86,13 @@ def test_kernel_test_blocks(dev, block):
                       blk["D"], blk["E"], literal=True, tag=block)
 
 
+@pytest.mark.parametrize("use_ctx", [False, True])
 @pytest.mark.parametrize("S", [256, 4096])
-def test_config3_elu(dev, S):
+def test_config3_elu(dev, S, use_ctx):
     """C3 (B' = 96, D = E = 64): several segments per sequence at S4096."""
     B, D, E = 96, 64, 64
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 300 + S)
-    check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"fused C3 S{S}")
+    check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"fused C3 S{S}", use_ctx=use_ctx)
 
 
 @pytest.mark.parametrize("B,S,D,E", [
@@ -85,9 +101,12 @@ def test_config3_elu(dev, S):
     (1, 50, 128, 64), (2, 20, 64, 96),   # wider than 64: the split kernels inside the call
 ])
 def test_ragged_shapes(dev, B, S, D, E):
-    """Partial last chunks, one and many segments, narrow and non-multiple-of-4 widths."""
+    """Partial last chunks, one and many segments, narrow and non-multiple-of-4 widths;
+    each with and without the forward's context."""
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 17 * S + D + E)
-    check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=(S <= 40), tag=f"B{B}S{S}D{D}E{E}")
+    for use_ctx in (False, True):
+        check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, literal=(S <= 40),
+                          tag=f"B{B}S{S}D{D}E{E}", use_ctx=use_ctx)
 
 
 def test_unaligned_rows(dev):
@@ -145,15 +164,19 @@ def test_matches_split_chain(dev):
     assert_close(_np(fV), _np(sV), "dV fused vs split")
 
 
-def fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag):
+def fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag, use_ctx=False):
     import torch
     import cxxgpt_attn as cx
     N = B * S
     tQ, tK, tV, tdO = _t(Qp, dev), _t(Kp, dev), _t(V, dev), _t(dO, dev)
     O, den = _nan(dev, N, E), _nan(dev, N)
-    cx.lin_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+    ctx = _ctx(dev, B, S, D, E) if use_ctx else None
+    if use_ctx:
+        cx.lin_fwd_ctx(tQ, tK, tV, O, den, ctx, B, S, D, E)
+    else:
+        cx.lin_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
     dQ, dK, dV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
-    cx.lin_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E)
+    cx.lin_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E, ctx=ctx)
     torch.cuda.synchronize()
     rO, rden, rzc, _, _ = orc.lcu_fwd(Qp, Kp, V, B, S, D, E, nthreads=8)
     assert_close(_np(O), rO, f"{tag} O")
@@ -173,6 +196,7 @@ def test_linear_cuda_elu(dev, B, S, E):
     Xq, Xk, V, dO = normal_inputs((B * S, E), (B * S, E), 7 + E)
     Qp, Kp = orc.phi_elu_forward(Xq, D, E), orc.phi_elu_forward(Xk, D, E)
     fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu fused E{E}")
+    fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu fused ctx E{E}", use_ctx=True)
 
 
 @pytest.mark.parametrize("B,S", [(96, 1024), (3, 100)])
@@ -183,7 +207,7 @@ def test_config4_hadamard_exp(dev, B, S):
     Q, K, _, _ = normal_inputs((N, D), (N, E), 400, q_std=0.5)
     _, _, V, dO = normal_inputs((N, D), (N, E), 400)
     Qp, Kp = orc.phi_hexp_forward(Q, D, D), orc.phi_hexp_forward(K, D, D)
-    fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag="C4 fused")
+    fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag="C4 fused", use_ctx=True)
 
 
 def test_error_paths(dev):
@@ -192,10 +216,18 @@ def test_error_paths(dev):
     t = torch.zeros(64, device=dev)
     P = cx._ptr
     st = cx._stream(None)
-    p9 = [P(t)] * 9
+    p = [P(t)] * 10
     for fn in ("cxg_kattn_bwd", "cxg_lin_bwd"):
-        assert cx.call_status(fn, *p9, 1, 4, 0, 8, st) == cx.CXG_ERR_DIMS
-        assert cx.call_status(fn, *p9, 1, 4, 8, 0, st) == cx.CXG_ERR_DIMS
-        assert cx.call_status(fn, *([None] + p9[1:]), 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
-        assert cx.call_status(fn, *p9[:5], None, *p9[6:], 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
-        assert cx.call_status(fn, *([None] * 9), 0, 4, 8, 8, st) == cx.CXG_OK   # empty
+        assert cx.call_status(fn, *p, 1, 4, 0, 8, st) == cx.CXG_ERR_DIMS
+        assert cx.call_status(fn, *p, 1, 4, 8, 0, st) == cx.CXG_ERR_DIMS
+        assert cx.call_status(fn, *([None] + p[1:]), 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
+        assert cx.call_status(fn, *p[:5], None, *p[6:], 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
+        assert cx.call_status(fn, *([None] * 10), 0, 4, 8, 8, st) == cx.CXG_OK   # empty
+    # the context: none for heads wider than 64; a short buffer is refused
+    assert cx.lin_ctx_size(2, 100, 128, 64) == 0
+    n = cx.lin_ctx_size(2, 100, 64, 64)
+    assert n > 0
+    for fn in ("cxg_kattn_fwd_ctx", "cxg_lin_fwd_ctx"):
+        assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 100, 64, 64, st) == \
+            cx.CXG_ERR_WORKSPACE
+        assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 100, 64, 64, st) == cx.CXG_ERR_NULL
