@@ -20,6 +20,8 @@ them can be made the reported workload with --workload NAME):
   c3fused   c3 through the fused pair: cxg_kattn_fwd_ctx (O, den and a segment-
             state context instead of z_cache) -> cxg_kattn_bwd (step1 + dQ + dKdV
             in one pass, prefix state from the context); c3fuseds256 at S=256
+  c3lgpt    c3's shape through LinearGPT's block with phi_elu fused as well
+            (cxg_lin_elu_fwd -> cxg_lin_elu_bwd on the raw q/k projections)
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
@@ -234,16 +236,25 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
 
 
-def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
-    """fused: kernel_attn_fwd without z_cache, then the one-call backward
-    (cxg_kattn_bwd); otherwise the reference's four-call chain."""
+def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False, lgpt=False):
+    """fused: the fused pair (context-writing forward, one-call backward);
+    otherwise the reference's four-call chain.  lgpt: LinearGPT's block with
+    phi_elu fused too (cxg_lin_elu_fwd / _bwd on the raw projections)."""
     g = c.gen(seed)
     E, N = D, Bq * S
     Q, K, V, dO = c.randn(g, N, D), c.randn(g, N, D), c.randn(g, N, E), c.randn(g, N, E)
     O, den = c.empty(N, E), c.empty(N)
     dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
     P = _ptr
-    if fused:
+    if lgpt:
+        nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+        ctx = c.empty(max(1, nctx // 4))
+        step = Stepper(c.cx.lib(), [
+            ("cxg_lin_elu_fwd", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, E, c.sp)),
+            ("cxg_lin_elu_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ), P(dK),
+                                 P(dV), Bq, S, E, c.sp)),
+        ])
+    elif fused:
         nctx = c.cx.lin_ctx_size(Bq, S, D, E)
         ctx = c.empty(max(1, nctx // 4))
         step = Stepper(c.cx.lib(), [
@@ -267,7 +278,7 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
     att = attribute(c.cx, step, max(10, min(steps, 50)))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
-    kb = lin_kernel_bytes(Bq, S, D, fused)
+    kb = lin_kernel_bytes(Bq, S, D, fused or lgpt)
     dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
     ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
@@ -276,6 +287,8 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False):
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, " + (
+                            "LinearGPT block, phi_elu fused (cxg_lin_elu_fwd -> cxg_lin_elu_bwd)"
+                            if lgpt else
                             "fused pair (cxg_kattn_fwd_ctx -> cxg_kattn_bwd with the context)"
                             if fused else "two_stage API chain (fwd, step1, dQ, dKdV)"),
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
@@ -404,6 +417,9 @@ def run_workload(c, name, steps, warmup):
                       fused=True)
     if name == "c3fuseds256":
         return _kattn(c, name, 96, 256, 64, 78, steps, warmup, fused=True)
+    if name == "c3lgpt":
+        return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2),
+                      lgpt=True)
     if name == "c4":
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
     raise ValueError(f"unknown workload {name}")
@@ -470,8 +486,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c4",
-                             "c5", "rope", "c2rope", "c2ropesep", "copy"])
+                    choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
+                             "c4", "c5", "rope", "c2rope", "c2ropesep", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -512,8 +528,8 @@ def main():
     }
     sec = {}
     if not args.no_secondary and args.workload == "c2":
-        for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c4", "c5", "rope",
-                     "c2rope", "c2ropesep"):
+        for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c4", "c5",
+                     "rope", "c2rope", "c2ropesep"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

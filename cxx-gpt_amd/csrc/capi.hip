@@ -499,6 +499,22 @@ int cxg_lin_bwd(const float* Q_phi, const float* K_phi, const float* V, const fl
                           B, S, D, E, stream);
 }
 
+int cxg_lin_elu_fwd(const float* Xq, const float* Xk, const float* V, float* O,
+                    float* den_cache, void* ctx, size_t ctx_bytes, size_t B, size_t S, size_t E,
+                    cxg_stream_t stream)
+{
+    return lin_fwd_common(PHI_ELU1_LG, 1, 1, Xq, Xk, V, O, den_cache, nullptr, nullptr, nullptr,
+                          B, S, E, E, stream, ctx, ctx_bytes);
+}
+
+int cxg_lin_elu_bwd(const float* Xq, const float* Xk, const float* V, const float* O,
+                    const float* dO, const float* den_cache, const void* ctx, float* dXq,
+                    float* dXk, float* dV, size_t B, size_t S, size_t E, cxg_stream_t stream)
+{
+    return lin_bwd_common(PHI_ELU1_LG, Xq, Xk, V, O, dO, den_cache, ctx, dXq, dXk, dV, B, S, E,
+                          E, stream);
+}
+
 static int phi_check(size_t N, size_t D, size_t E, bool hexp, bool* empty)
 {
     *empty = (N == 0);

@@ -1353,6 +1353,9 @@ hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* 
     if (phi == PHI_ELU1)
         return fwd_impl<PHI_ELU1>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps,
                                   Bq, S, D, E, ws, st);
+    if (phi == PHI_ELU1_LG)
+        return fwd_impl<PHI_ELU1_LG>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de,
+                                     den_eps, Bq, S, D, E, ws, st);
     return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq,
                               S, D, E, ws, st);
 }
@@ -1415,6 +1418,8 @@ hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* d
 {
     if (phi == PHI_ELU1)
         return dq_impl<PHI_ELU1>(K, V, dnum, dden, zc, Q, dQ, Bq, S, D, E, ws, st);
+    if (phi == PHI_ELU1_LG)
+        return dq_impl<PHI_ELU1_LG>(K, V, dnum, dden, zc, Q, dQ, Bq, S, D, E, ws, st);
     return dq_impl<PHI_NONE>(K, V, dnum, dden, zc, Q, dQ, Bq, S, D, E, ws, st);
 }
 
@@ -1462,6 +1467,8 @@ hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float*
 {
     if (phi == PHI_ELU1)
         return dkdv_impl<PHI_ELU1>(Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, ws, st);
+    if (phi == PHI_ELU1_LG)
+        return dkdv_impl<PHI_ELU1_LG>(Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, ws, st);
     return dkdv_impl<PHI_NONE>(Q, K, V, dnum, dden, dK, dV, Bq, S, D, E, ws, st);
 }
 
@@ -1496,6 +1503,8 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
         dim3 grid((unsigned)((D + 255) / 256), (unsigned)Bq);
         if (phi == PHI_ELU1)
             hipLaunchKernelGGL(lin_zc_kernel<PHI_ELU1>, grid, dim3(256), 0, st, K, zc, S, D);
+        else if (phi == PHI_ELU1_LG)
+            hipLaunchKernelGGL(lin_zc_kernel<PHI_ELU1_LG>, grid, dim3(256), 0, st, K, zc, S, D);
         else
             hipLaunchKernelGGL(lin_zc_kernel<PHI_NONE>, grid, dim3(256), 0, st, K, zc, S, D);
     }

@@ -6,7 +6,10 @@
 
 namespace cxg {
 
-enum { PHI_ELU1 = 0, PHI_NONE = 1 };
+// Feature map applied inside the kernels: ELU+1 as two_stage computes it, none
+// (inputs are features already: linear_cuda), or ELU+1 in linear_cuda's
+// phi_elu form (LinearGPT's feature map fused into the scans).
+enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2 };
 
 // floats per segment record in the scan workspace: 64x64 state [d][e] + z[64]
 constexpr int LIN_WS = 64 * 64 + 64;

@@ -26,6 +26,18 @@ struct Phi<PHI_ELU1> {
     static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
 };
 template <>
+struct Phi<PHI_ELU1_LG> {
+    // linear_cuda_kernels.cu:316-320 (phi_elu_fwd_kernel): ELU(x) + 1 with
+    // ELU(x) = expf(x) - 1 for x <= 0, the two roundings kept
+    static __device__ __forceinline__ float f(float x) { return x > 0.0f ? x + 1.0f : (expf(x) - 1.0f) + 1.0f; }
+    // :347-364 (phi_elu_bwd_kernel)
+    static __device__ __forceinline__ float d(float x) { return x > 0.0f ? 1.0f : expf(x); }
+    // from phi: 1 for x > 0; for x <= 0, phi is expf(x) rounded to a multiple of
+    // 2^-24 (expf(x) - 1 is rounded in [-1, -0.5)), so min(phi, 1) is within
+    // 2^-25 of expf(x)
+    static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
+};
+template <>
 struct Phi<PHI_NONE> {
     static __device__ __forceinline__ float f(float x) { return x; }
     static __device__ __forceinline__ float d(float) { return 1.0f; }

@@ -699,6 +699,8 @@ hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const f
                          : LinCtx{nullptr, nullptr, nullptr};
     if (phi == PHI_ELU1)
         bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
+    else if (phi == PHI_ELU1_LG)
+        bwd_dispatch<PHI_ELU1_LG>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
         bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     return hipGetLastError();

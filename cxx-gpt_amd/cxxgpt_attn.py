@@ -47,6 +47,8 @@ SIGNATURES = {
     "cxg_lin_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd": [_vp] * 10 + [_sz] * 4 + [_vp],
     "cxg_lin_fwd_ctx": [_vp] * 6 + [_sz] * 5 + [_vp],
+    "cxg_lin_elu_fwd": [_vp] * 6 + [_sz] * 4 + [_vp],
+    "cxg_lin_elu_bwd": [_vp] * 10 + [_sz] * 3 + [_vp],
     "cxg_phi_elu_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
@@ -225,6 +227,19 @@ def lin_fwd_ctx(Qp, Kp, V, O, den, ctx, B, S, D, E, stream=None):
     nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
     _call("cxg_lin_fwd_ctx", _ptr(Qp), _ptr(Kp), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
           B, S, D, E, _stream(stream))
+
+
+def lin_elu_fwd(Xq, Xk, V, O, den, ctx, B, S, E, stream=None):
+    """LinearGPT attention forward with phi_elu fused (raw projections in)."""
+    nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
+    _call("cxg_lin_elu_fwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
+          B, S, E, _stream(stream))
+
+
+def lin_elu_bwd(Xq, Xk, V, O, dO, den, dXq, dXk, dV, B, S, E, ctx=None, stream=None):
+    """LinearGPT attention backward: step1 + dQ + dKdV + phi_elu_backward, fused."""
+    _call("cxg_lin_elu_bwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(dO), _ptr(den),
+          _ptr(ctx), _ptr(dXq), _ptr(dXk), _ptr(dV), B, S, E, _stream(stream))
 
 
 def phi_elu_fwd(x, phi, N, D, E, stream=None):

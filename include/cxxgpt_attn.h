@@ -191,6 +191,23 @@ int cxg_lin_bwd_dKdV(const float *Q_phi, const float *K_phi, const float *V,
                      const float *dnum, const float *dden, float *dK_phi, float *dV,
                      size_t B, size_t S, size_t D, size_t E, cxg_stream_t stream);
 
+/* LinearGPT's attention block with the feature map fused into the scans
+ * (linear_gpt.hpp:100-112 forward, :154-172 backward).  No single counterpart
+ * in the reference.  cxg_lin_elu_fwd = phi_elu_forward(Xq), phi_elu_forward(Xk)
+ * then causal_linear_attention_fwd, on the raw projections Xq, Xk (B*S, E)
+ * (phi in the (expf(x)-1)+1 form of phi_elu_fwd_kernel; the reference's
+ * zero-padded phi columns E..D-1 contribute nothing and are not formed): O and
+ * den_cache (eps included) as the reference's, plus the context for the
+ * backward (cxg_lin_ctx_size(B, S, E, E) bytes; may be NULL with ctx_bytes 0).
+ * cxg_lin_elu_bwd = step1, dQ, dKdV and the two phi_elu_backward calls: dXq,
+ * dXk (B*S, E) with respect to the raw projections, and dV. */
+int cxg_lin_elu_fwd(const float *Xq, const float *Xk, const float *V, float *O,
+                    float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
+                    size_t E, cxg_stream_t stream);
+int cxg_lin_elu_bwd(const float *Xq, const float *Xk, const float *V, const float *O,
+                    const float *dO, const float *den_cache, const void *ctx, float *dXq,
+                    float *dXk, float *dV, size_t B, size_t S, size_t E, cxg_stream_t stream);
+
 /* linear_cuda::phi_elu_forward / phi_elu_backward (linear_cuda_kernels.cuh:39-46,
  * linear_cuda_kernels.cu:305-378).  x (N, E) -> phi (N, D), columns >= E zero;
  * dx (N, E) = dphi[:, :E] * phi'(x). */

@@ -199,6 +199,38 @@ def test_linear_cuda_elu(dev, B, S, E):
     fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu fused ctx E{E}", use_ctx=True)
 
 
+@pytest.mark.parametrize("B,S,E", [(96, 256, 64), (2, 64, 64), (3, 77, 48), (2, 500, 20),
+                                   (1, 3000, 64), (2, 30, 100)])
+@pytest.mark.parametrize("use_ctx", [False, True])
+def test_linear_gpt_fused(dev, B, S, E, use_ctx):
+    """cxg_lin_elu_fwd / _bwd against LinearGPT's own chain (linear_gpt.hpp:100-172):
+    phi_elu_forward x2 -> causal_linear_attention_fwd; step1 -> dQ -> dKdV ->
+    phi_elu_backward x2, with D = next_pow2(E) zero-padded feature columns."""
+    import torch
+    import cxxgpt_attn as cx
+    D = 1 << (E - 1).bit_length()
+    N = B * S
+    Xq, Xk, V, dO = normal_inputs((N, E), (N, E), 5 * S + E)
+    tq, tk, tv, tdo = _t(Xq, dev), _t(Xk, dev), _t(V, dev), _t(dO, dev)
+    O, den = _nan(dev, N, E), _nan(dev, N)
+    ctx = _ctx(dev, B, S, E, E) if use_ctx else None
+    cx.lin_elu_fwd(tq, tk, tv, O, den, ctx, B, S, E)
+    dXq, dXk, dV = _nan(dev, N, E), _nan(dev, N, E), _nan(dev, N, E)
+    cx.lin_elu_bwd(tq, tk, tv, O, tdo, den, dXq, dXk, dV, B, S, E, ctx=ctx)
+    torch.cuda.synchronize()
+    Qp, Kp = orc.phi_elu_forward(Xq, D, E), orc.phi_elu_forward(Xk, D, E)
+    rO, rden, rzc, _, _ = orc.lcu_fwd(Qp, Kp, V, B, S, D, E, nthreads=8)
+    tag = f"lin_elu B{B}S{S}E{E}{' ctx' if use_ctx else ''}"
+    assert_close(_np(O), rO, f"{tag} O")
+    assert_close(_np(den), rden, f"{tag} den_cache")
+    dnum, dden = orc.lcu_bwd_step1(_np(O), dO, _np(den), N, E)
+    rdQp = orc.lcu_bwd_dQ(Kp, V, dnum, dden, rzc, B, S, D, E, nthreads=8)
+    rdKp, rdV = orc.lcu_bwd_dKdV(Qp, Kp, V, dnum, dden, B, S, D, E, nthreads=8)
+    assert_close(_np(dXq), orc.phi_elu_backward(rdQp, Xq, D, E), f"{tag} dXq")
+    assert_close(_np(dXk), orc.phi_elu_backward(rdKp, Xk, D, E), f"{tag} dXk")
+    assert_close(_np(dV), rdV, f"{tag} dV")
+
+
 @pytest.mark.parametrize("B,S", [(96, 1024), (3, 100)])
 def test_config4_hadamard_exp(dev, B, S):
     """C4: Hadamard+Exp features (phi outside), Q, K ~ N(0, 0.25), V, dO ~ N(0, 1)."""
