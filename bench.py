@@ -29,6 +29,8 @@ them can be made the reported workload with --workload NAME):
             GB/s of compulsory I/O (each tensor read and written once)
   c2rope    C2 with RoPE fused into the MHA kernels (cxg_mha_rope_fwd/bwd)
   c2ropesep C2 with RoPE as separate passes, the reference's call sequence
+  gpt       GPT's attention at its training shape (B8 S256, one head of E=512,
+            gpt_train.cpp:139/156): cxg_gpt_attn_fwd -> cxg_gpt_attn_bwd
   copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
@@ -136,7 +138,8 @@ def attribute(cx, step, steps):
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "phi_hexp_fwd", "phi_hexp_bwd",
-              "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd"):
+              "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
+              "mha_wide_stats", "mha_wide_bwd"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)
@@ -234,6 +237,45 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
                         "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops},
                 frac=value / FP32_MFMA_PEAK_TFLOPS,
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
+
+
+def _gpt(c, name, B, S, E, seed, steps, warmup):
+    """GPT's attention (one head over the embedding) through cxg_gpt_attn_fwd
+    (with lse) -> cxg_gpt_attn_bwd: the reference GPT training shape."""
+    g = c.gen(seed)
+    N = B * S
+    Q, K, V, dO = [c.randn(g, N, E) for _ in range(4)]
+    O, dQ, dK, dV = c.empty(N, E), c.empty(N, E), c.empty(N, E), c.empty(N, E)
+    lse = c.empty(B * S)
+    ws_bytes = c.cx.lib().cxg_gpt_attn_bwd_workspace_size(B, S, E)
+    ws = c.empty(max(1, ws_bytes // 4))
+    P = _ptr
+    step = Stepper(c.cx.lib(), [
+        ("cxg_gpt_attn_fwd", (P(Q), P(K), P(V), P(O), P(lse), B, S, E, c.sp)),
+        ("cxg_gpt_attn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(lse), P(dQ), P(dK), P(dV),
+                              B, S, E, P(ws), ws_bytes, c.sp)),
+    ])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    flops = mha_flops(B, S, 1, E)
+    value = flops / (ms * 1e-3) / 1e12
+    kflops = {"mha_wide_fwd": mha_flops(B, S, 1, E, bwd=False),
+              "mha_wide_bwd": mha_flops(B, S, 1, E, fwd=False),
+              "mha_fwd": mha_flops(B, S, 1, E, bwd=False),
+              "mha_bwd": mha_flops(B, S, 1, E, fwd=False)}
+    dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
+    ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"), "flops_per_launch": kflops[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: GPT attention (one head over the embedding, "
+                                    "gpt_gpt.hpp:365-438) via cxg_gpt_attn_fwd -> "
+                                    "cxg_gpt_attn_bwd",
+                        "B": B, "S": S, "E": E, "flops_per_step": flops},
+                frac=value / FP32_MFMA_PEAK_TFLOPS, cpu_inputs=None)
 
 
 def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False, lgpt=False):
@@ -417,6 +459,8 @@ def run_workload(c, name, steps, warmup):
                       fused=True)
     if name == "c3fuseds256":
         return _kattn(c, name, 96, 256, 64, 78, steps, warmup, fused=True)
+    if name == "gpt":
+        return _gpt(c, name, 8, 256, 512, 91, steps, warmup)
     if name == "c3lgpt":
         return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2),
                       lgpt=True)
@@ -487,7 +531,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c4", "c5", "rope", "c2rope", "c2ropesep", "copy"])
+                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -529,7 +573,7 @@ def main():
     sec = {}
     if not args.no_secondary and args.workload == "c2":
         for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c4", "c5",
-                     "rope", "c2rope", "c2ropesep"):
+                     "rope", "c2rope", "c2ropesep", "gpt"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

@@ -258,6 +258,82 @@ int cxg_mha_rope_bwd(const float* Q, const float* K, const float* V, const float
 }
 
 // ---------------------------------------------------------------------------
+// GPT's attention: one head over the embedding (H = 1, Dh = E)
+// ---------------------------------------------------------------------------
+static int gpt_check(size_t B, size_t S, size_t E, bool* empty)
+{
+    *empty = (B == 0 || S == 0);
+    if (E == 0)
+        return CXG_ERR_DIMS;
+    if (E > (size_t)MHA_WIDE_MAX_DH)
+        return CXG_ERR_HEAD_DIM;
+    if (*empty)
+        return CXG_OK;
+    if (!fits_int(B) || !fits_int(S) || B * ((S + 15) / 16) > ((size_t)1 << 23))
+        return CXG_ERR_DIMS;
+    // the wide kernels address one sequence with 32-bit byte offsets
+    if (E > 256 && S * E > ((size_t)1 << 28))
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, float* lse,
+                     size_t B, size_t S, size_t E, cxg_stream_t stream)
+{
+    if (E > 0 && E <= 256)
+        return cxg_mha_fwd(Q, K, V, O, lse, B, S, 1, E, stream);
+    bool empty;
+    int st = gpt_check(B, S, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O)
+        return CXG_ERR_NULL;
+    return hip_status(mha_wide_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, 1, (int)E,
+                                          (hipStream_t)stream));
+}
+
+size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
+{
+    return cxg_mha_bwd_workspace_size(B, S, 1, E);
+}
+
+int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float* O,
+                     const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                     size_t B, size_t S, size_t E, void* workspace, size_t workspace_bytes,
+                     cxg_stream_t stream)
+{
+    if (E > 0 && E <= 256)
+        return cxg_mha_bwd(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, 1, E, workspace,
+                           workspace_bytes, stream);
+    bool empty;
+    int st = gpt_check(B, S, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t half = round_up(B * S * sizeof(float), 256);
+    Scratch ws;
+    st = ws.acquire(workspace, workspace_bytes, cxg_gpt_attn_bwd_workspace_size(B, S, E), s);
+    if (st != CXG_OK)
+        return st;
+    float* Di = (float*)ws.p;
+    float* lse_ws = (float*)((char*)ws.p + half);
+    const int iB = (int)B, iS = (int)S, iE = (int)E;
+    hipError_t e;
+    if (lse == nullptr) {
+        e = mha_wide_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, 1, iE, s);
+        if (e != hipSuccess)
+            return hip_status(e);
+        lse = lse_ws;
+    }
+    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, 1, iE, s);
+    if (e != hipSuccess)
+        return hip_status(e);
+    return hip_status(mha_wide_bwd_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, 1, iE, s));
+}
+
+// ---------------------------------------------------------------------------
 // linear attention
 // ---------------------------------------------------------------------------
 // Dimensions of a (B sequences x S rows) problem with Q/K width D and V width E.

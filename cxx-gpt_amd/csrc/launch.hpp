@@ -55,6 +55,15 @@ hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
                                float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,
                                hipStream_t st, const MhaRope* rope = nullptr);
 
+// Causal softmax attention for 256 < Dh <= 512 (same layout, lse and backward
+// contract as the launchers above; O may be null: statistics only).
+constexpr int MHA_WIDE_MAX_DH = 512;
+hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                               float* lse, int B, int S, int H, int Dh, hipStream_t st);
+hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
+                               const float* lse, const float* Di, float* dQ, float* dK,
+                               float* dV, int B, int S, int H, int Dh, hipStream_t st);
+
 // Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
 // may be null, and they may be one buffer).  Frequencies of pairs 0 ..
 // head_dim/2-1 travel in the kernel arguments.

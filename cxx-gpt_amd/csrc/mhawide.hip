@@ -1,0 +1,384 @@
+// mhawide.hip -- causal softmax attention for head dims 257..512 (gfx950, FP32 MFMA).
+//
+// GPT's attention (src/GPT/gpt_gpt.hpp:365-380 forward, :420-438 backward) is
+// one head over the whole embedding: scores = Q K^T / sqrt(E) on (B*S) x (B*S)
+// with a block-diagonal causal mask (gpt_cuda_kernels.cu:458-480, -1e10 on
+// cross-batch and future entries), softmax, times V; the backward goes through
+// softmax_backward (:131-173).  Per batch that is causal attention with H = 1
+// and Dh = E.  The fused MHA kernels (mha.hip) cover Dh <= 256; the reference
+// GPT's training configuration has E = 512 (gpt_train.cpp:139).  These kernels
+// take 256 < Dh <= 512 with the same layout ((B*S, H*Dh) rows), scale, lse
+// convention and backward contract as mha.hip.
+//
+// Design.  16 query rows (forward) or 16 keys (backward) per workgroup of four
+// waves; the head dim is split over the waves, 128 columns each, so the
+// 16x16 score tile is four partial products summed through LDS, and each wave
+// keeps its own column slice of the O (forward) or dK/dV (backward)
+// accumulators in registers.  Scores are formed transposed in the forward (a
+// lane owns a query row: its online-softmax state is per lane).  The backward
+// runs key-block jobs (dK, dV) and query-block jobs (dQ) side by side in one
+// launch, each owning its outputs, so no atomics are needed.  Tiles stream
+// through LDS with 16-byte row loads, fetched one block ahead.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace cxg {
+
+constexpr int WB = 16;                 // rows per tile (queries and keys)
+constexpr int WIDE_DHP = 512;          // padded head dim
+constexpr int WLD = WIDE_DHP + 4;      // LDS row stride of a staged tile
+constexpr int WSL = WIDE_DHP / 4;      // head-dim columns per wave
+constexpr int WNT = WSL / 16;          // 16-column tiles per wave
+
+// Rows [r0, r0+16) x [0, Dh) of one head, eight 16-byte units per thread of
+// 256 (unit u = tid + 256k: row u / 128, column 4 (u % 128)): rows past S
+// repeat row S-1 (clamped loads), columns past Dh are zeroed when stored.
+struct WideRegs {
+    f4 v[8];
+};
+
+template <bool VEC>
+__device__ __forceinline__ void wide_fetch(WideRegs& R, const float* __restrict__ head, long ld,
+                                           int r0, int S, int Dh, int tid)
+{
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int u = tid + 256 * k;
+        const int row = u / (WIDE_DHP / 4), c = 4 * (u % (WIDE_DHP / 4));
+        R.v[k] = load4c<VEC>(head + (long)min(r0 + row, S - 1) * ld, c, Dh);
+    }
+}
+
+__device__ __forceinline__ void wide_store(float* __restrict__ dst, const WideRegs& R, int Dh,
+                                           int tid)
+{
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const int u = tid + 256 * k;
+        const int row = u / (WIDE_DHP / 4), c = 4 * (u % (WIDE_DHP / 4));
+        *reinterpret_cast<f4*>(&dst[row * WLD + c]) = mask4(R.v[k], c, Dh, true);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// forward: job = (bh, 16-query block), heaviest (latest) blocks first.
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, float qscale)
+{
+    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 4 * 256];
+    float* Sp = lds + 4 * WB * WLD;   // partial scores [wave][lane * 4 + r]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int nqb = (S + WB - 1) / WB;
+    const int BH = gridDim.x / nqb;
+    const int qb = nqb - 1 - (int)(blockIdx.x / BH);
+    const int bh = (int)(blockIdx.x % BH);
+    const int b = bh / H, h = bh - b * H;
+    const long ld = (long)H * Dh;
+    const long hoff = (long)b * S * ld + (long)h * Dh;
+    const int q0 = qb * WB, c0 = w * WSL;
+
+    // this wave's column slice of Q rows q0 + l16 (pre-scaled by scale*log2e)
+    f4 q[WNT], o[WNT];
+    {
+        const float* qrow = Q + hoff + (long)min(q0 + l16, S - 1) * ld;
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int c = c0 + 16 * t + 4 * g;
+            q[t] = mask4(load4c<VEC>(qrow, c, Dh), c, Dh, true) * qscale;
+            o[t] = f4zero();
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    const int qi = q0 + l16;   // this lane's query row
+
+    // key blocks are fetched one ahead into registers and stored to the
+    // double-buffered LDS tiles at the top of their step
+    WideRegs kr, vr;
+    wide_fetch<VEC>(kr, K + hoff, ld, 0, S, Dh, tid);
+    wide_fetch<VEC>(vr, V + hoff, ld, 0, S, Dh, tid);
+    for (int kb = 0; kb <= qb; kb++) {
+        const int k0 = kb * WB;
+        float* Ks = lds + (kb & 1) * 2 * WB * WLD;
+        float* Vs = Ks + WB * WLD;
+        wide_store(Ks, kr, Dh, tid);
+        wide_store(Vs, vr, Dh, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kn = min(kb + 1, qb) * WB;   // the last step refetches its own block
+        wide_fetch<VEC>(kr, K + hoff, ld, kn, S, Dh, tid);
+        wide_fetch<VEC>(vr, V + hoff, ld, kn, S, Dh, tid);
+        __syncthreads();
+        // S^T[j][i] over this wave's columns: lane i = l16, element r <-> key 4g + r
+        // two accumulation chains (one wave per SIMD issues a single chain at
+        // two thirds of the MFMA rate)
+        f4 sp = f4zero(), sp2 = f4zero();
+#pragma unroll
+        for (int t = 0; t < WNT; t += 2) {
+            const f4 kv = *reinterpret_cast<const f4*>(&Ks[l16 * WLD + c0 + 16 * t + 4 * g]);
+            const f4 kv2 = *reinterpret_cast<const f4*>(&Ks[l16 * WLD + c0 + 16 * t + 16 + 4 * g]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sp = mfma16(kv[r], q[t][r], sp);
+                sp2 = mfma16(kv2[r], q[t + 1][r], sp2);
+            }
+        }
+        *reinterpret_cast<f4*>(&Sp[w * 256 + lane * 4]) = sp + sp2;
+        __syncthreads();
+        f4 s = f4zero();
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            s += *reinterpret_cast<const f4*>(&Sp[u * 256 + lane * 4]);
+        // causal and length masks, online softmax per query row (lane)
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int kj = k0 + 4 * g + r;
+            s[r] = (kj <= qi && kj < S) ? s[r] : -INFINITY;
+            mloc = fmaxf(mloc, s[r]);
+        }
+        const float m_new = fmaxf(m_run, xrow_max(mloc));
+        const float alpha = fast_exp2(m_run - m_new);
+        f4 p;
+        float ploc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = fast_exp2(s[r] - m_new);
+            ploc += p[r];
+        }
+        l_run = l_run * alpha + xrow_sum(ploc);
+        m_run = m_new;
+        // O^T[d][i] += sum_j V[j][d] P[i][j] over this wave's columns
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            f4 a = o[t] * alpha;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                a = mfma16(Vs[(4 * g + r) * WLD + c0 + 16 * t + l16], p[r], a);
+            o[t] = a;
+        }
+    }
+    if (qi < S) {
+        const float inv = 1.0f / l_run;
+        if (O != nullptr) {
+            float* orow = O + hoff + (long)qi * ld;
+#pragma unroll
+            for (int t = 0; t < WNT; t++)
+                store4<VEC>(orow, c0 + 16 * t + 4 * g, Dh, o[t] * inv);
+        }
+        if (lse != nullptr && w == 0 && g == 0)
+            lse[(long)bh * S + qi] = (m_run + fast_log2(l_run)) * kLn2;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward: one launch, two kinds of job and no atomics.
+//  * key jobs (bh, key block kb): for every query block from kb on, S and dP
+//    (lane = key), P = exp2(S*c - lse2), dS = P (dP - Di) * scale, and over
+//    this wave's columns dV^T += dO^T P, dK^T += Q^T dS; dK, dV stored at the end.
+//  * query jobs (bh, query block qb): for every key block up to qb, S^T and
+//    dP^T (lane = query), the same P and dS, and dQ^T += K^T dS^T; dQ stored.
+// The query jobs recompute S and dP (96 MFMA per block pair and wave against
+// the 32 dQ atomics per lane they replace: the float atomics of a dQ update per
+// 16x16 block pair at Dh = 512 bounded the atomic version).  Jobs are ordered
+// longest first within each kind; score partials over the waves' column slices
+// are summed through LDS; the streamed tile is fetched one ahead.
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void mha_wide_bwd_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
+    float qscale, float scale)
+{
+    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 2 * 4 * 256 + 2 * WB];
+    float* Ks = lds;                     // key job: its K, V; query job: the streamed K, V
+    float* Vs = Ks + WB * WLD;
+    float* Qs = Vs + WB * WLD;           // key job: the streamed Q, dO; query job: its Q, dO
+    float* dOs = Qs + WB * WLD;
+    float* Sp = dOs + WB * WLD;          // [wave][S, dP][lane * 4 + r]
+    float* st = Sp + 2 * 4 * 256;        // lse2[16], Di[16] of the current query block
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int nb = (S + WB - 1) / WB;
+    const int BH = gridDim.x / (2 * nb);
+    const bool kjob = (int)blockIdx.x < BH * nb;
+    const int jid = kjob ? (int)blockIdx.x : (int)blockIdx.x - BH * nb;
+    const int blk = kjob ? jid / BH : nb - 1 - jid / BH;   // key block / query block
+    const int bh = jid % BH;
+    const int b = bh / H, h = bh - b * H;
+    const long ld = (long)H * Dh;
+    const long hoff = (long)b * S * ld + (long)h * Dh;
+    const int c0 = w * WSL, x0 = blk * WB;
+    // the job's own tiles: K, V (key job) or Q, dO (query job)
+    {
+        WideRegs t;
+        wide_fetch<VEC>(t, (kjob ? K : Q) + hoff, ld, x0, S, Dh, tid);
+        wide_store(kjob ? Ks : Qs, t, Dh, tid);
+        wide_fetch<VEC>(t, (kjob ? V : dO) + hoff, ld, x0, S, Dh, tid);
+        wide_store(kjob ? Vs : dOs, t, Dh, tid);
+    }
+    auto load_stats = [&](int q0) {
+        if (tid < WB) {
+            const int qr = min(q0 + tid, S - 1);
+            st[tid] = lse[(long)bh * S + qr] * kLog2e;
+            st[WB + tid] = Di[(long)bh * S + qr];
+        }
+    };
+    f4 acc1[WNT], acc2[WNT];   // key job: dK^T, dV^T; query job: dQ^T (acc1)
+#pragma unroll
+    for (int t = 0; t < WNT; t++) {
+        acc1[t] = f4zero();
+        acc2[t] = f4zero();
+    }
+    // streamed blocks: key job: query blocks blk .. nb-1; query job: key blocks 0 .. blk
+    const int sbeg = kjob ? blk : 0, send = kjob ? nb : blk + 1;
+    const float* s1 = (kjob ? Q : K) + hoff;
+    const float* s2 = (kjob ? dO : V) + hoff;
+    float* d1 = kjob ? Qs : Ks;
+    float* d2 = kjob ? dOs : Vs;
+    if (!kjob)
+        load_stats(x0);
+    WideRegs r1, r2;
+    wide_fetch<VEC>(r1, s1, ld, sbeg * WB, S, Dh, tid);
+    wide_fetch<VEC>(r2, s2, ld, sbeg * WB, S, Dh, tid);
+    for (int sb = sbeg; sb < send; sb++) {
+        const int y0 = sb * WB;
+        wide_store(d1, r1, Dh, tid);
+        wide_store(d2, r2, Dh, tid);
+        if (kjob)
+            load_stats(y0);
+        __builtin_amdgcn_sched_barrier(0);
+        const int yn = min(sb + 1, send - 1) * WB;   // the last step refetches its own block
+        wide_fetch<VEC>(r1, s1, ld, yn, S, Dh, tid);
+        wide_fetch<VEC>(r2, s2, ld, yn, S, Dh, tid);
+        __syncthreads();
+        // key job: S[i][j], dP[i][j] (lane j = key, element r <-> query 4g + r);
+        // query job: S^T, dP^T (lane i = query, element r <-> key 4g + r)
+        f4 sp = f4zero(), dpp = f4zero();
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int c = c0 + 16 * t + 4 * g;
+            const f4 qa = *reinterpret_cast<const f4*>(&Qs[l16 * WLD + c]);
+            const f4 ka = *reinterpret_cast<const f4*>(&Ks[l16 * WLD + c]);
+            const f4 oa = *reinterpret_cast<const f4*>(&dOs[l16 * WLD + c]);
+            const f4 va = *reinterpret_cast<const f4*>(&Vs[l16 * WLD + c]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (kjob) {
+                    sp = mfma16(qa[r], ka[r], sp);
+                    dpp = mfma16(oa[r], va[r], dpp);
+                } else {
+                    sp = mfma16(ka[r], qa[r], sp);
+                    dpp = mfma16(va[r], oa[r], dpp);
+                }
+            }
+        }
+        *reinterpret_cast<f4*>(&Sp[(2 * w) * 256 + lane * 4]) = sp;
+        *reinterpret_cast<f4*>(&Sp[(2 * w + 1) * 256 + lane * 4]) = dpp;
+        __syncthreads();
+        f4 sv = f4zero(), dp = f4zero();
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            sv += *reinterpret_cast<const f4*>(&Sp[(2 * u) * 256 + lane * 4]);
+            dp += *reinterpret_cast<const f4*>(&Sp[(2 * u + 1) * 256 + lane * 4]);
+        }
+        const int q0 = kjob ? y0 : x0, k0 = kjob ? x0 : y0;
+        f4 p, ds;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int qo = kjob ? 4 * g + r : l16;   // query row within the block
+            const int kj = k0 + (kjob ? l16 : 4 * g + r);
+            const int qi = q0 + qo;
+            const bool ok = kj <= qi && qi < S && kj < S;
+            p[r] = ok ? fast_exp2(sv[r] * qscale - st[qo]) : 0.0f;
+            ds[r] = p[r] * (dp[r] - st[WB + qo]) * scale;
+        }
+        if (kjob) {
+            // dV^T[d][j] += sum_i dO[i][d] P[i][j];  dK^T[d][j] += sum_i Q[i][d] dS[i][j]
+#pragma unroll
+            for (int t = 0; t < WNT; t++) {
+                f4 ak = acc1[t], av = acc2[t];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int e = (4 * g + r) * WLD + c0 + 16 * t + l16;
+                    ak = mfma16(Qs[e], ds[r], ak);
+                    av = mfma16(dOs[e], p[r], av);
+                }
+                acc1[t] = ak;
+                acc2[t] = av;
+            }
+        } else {
+            // dQ^T[d][i] += sum_j K[j][d] dS[i][j]
+#pragma unroll
+            for (int t = 0; t < WNT; t++) {
+                f4 a = acc1[t];
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    a = mfma16(Ks[(4 * g + r) * WLD + c0 + 16 * t + l16], ds[r], a);
+                acc1[t] = a;
+            }
+        }
+        __syncthreads();   // the streamed tiles, stats and partials are rewritten next
+    }
+    // rows x0 + l16 of dK and dV (key job) or dQ (query job)
+    const int row = x0 + l16;
+    if (row < S) {
+        const long ro = hoff + (long)row * ld;
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int c = c0 + 16 * t + 4 * g;
+            if (kjob) {
+                store4<VEC>(dK + ro, c, Dh, acc1[t]);
+                store4<VEC>(dV + ro, c, Dh, acc2[t]);
+            } else {
+                store4<VEC>(dQ + ro, c, Dh, acc1[t]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline bool al16w(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                               float* lse, int B, int S, int H, int Dh, hipStream_t st)
+{
+    const int nqb = (S + WB - 1) / WB;
+    const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
+    dim3 grid((unsigned)((long)B * H * nqb)), block(256);
+    const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(O);
+    ProfScope ps(st, O != nullptr ? "mha_wide_fwd" : "mha_wide_stats");
+    if (vec)
+        hipLaunchKernelGGL(mha_wide_fwd_kernel<true>, grid, block, 0, st, Q, K, V, O, lse, S, H,
+                           Dh, qscale);
+    else
+        hipLaunchKernelGGL(mha_wide_fwd_kernel<false>, grid, block, 0, st, Q, K, V, O, lse, S, H,
+                           Dh, qscale);
+    return hipGetLastError();
+}
+
+hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
+                               const float* lse, const float* Di, float* dQ, float* dK,
+                               float* dV, int B, int S, int H, int Dh, hipStream_t st)
+{
+    const int nb = (S + WB - 1) / WB;
+    const float scale = 1.0f / sqrtf((float)Dh);
+    dim3 grid((unsigned)(2L * B * H * nb)), block(256);
+    const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(dO) &&
+                     al16w(dQ) && al16w(dK) && al16w(dV);
+    ProfScope ps(st, "mha_wide_bwd");
+    if (vec)
+        hipLaunchKernelGGL(mha_wide_bwd_kernel<true>, grid, block, 0, st, Q, K, V, dO, lse, Di,
+                           dQ, dK, dV, S, H, Dh, scale * kLog2e, scale);
+    else
+        hipLaunchKernelGGL(mha_wide_bwd_kernel<false>, grid, block, 0, st, Q, K, V, dO, lse, Di,
+                           dQ, dK, dV, S, H, Dh, scale * kLog2e, scale);
+    return hipGetLastError();
+}
+
+} // namespace cxg

@@ -34,6 +34,9 @@ SIGNATURES = {
     "cxg_mha_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_mha_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp,
                          _sz, _vp],
+    "cxg_gpt_attn_fwd": [_vp] * 5 + [_sz] * 3 + [_vp],
+    "cxg_gpt_attn_bwd": [_vp] * 9 + [_sz] * 3 + [_vp, _sz, _vp],
+    "cxg_gpt_attn_bwd_workspace_size": [_sz] * 3,
     "cxg_kattn_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_kattn_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
     "cxg_kattn_bwd_dQ": [_vp] * 8 + [_sz] * 4 + [_vp],
@@ -65,6 +68,7 @@ _RESTYPES = {
     "cxg_version": ctypes.c_char_p,
     "cxg_mha_bwd_workspace_size": ctypes.c_size_t,
     "cxg_lin_ctx_size": ctypes.c_size_t,
+    "cxg_gpt_attn_bwd_workspace_size": ctypes.c_size_t,
     "cxg_prof_enable": None,
     "cxg_prof_reset": None,
 }
@@ -156,6 +160,18 @@ def mha_rope_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, workspace=No
 
 def mha_bwd_workspace_size(B, S, H, Dh):
     return lib().cxg_mha_bwd_workspace_size(B, S, H, Dh)
+
+
+# ------------------------------------------------------------------ GPT's attention (H = 1)
+def gpt_attn_fwd(Q, K, V, O, B, S, E, lse=None, stream=None):
+    _call("cxg_gpt_attn_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(lse), B, S, E,
+          _stream(stream))
+
+
+def gpt_attn_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, E, lse=None, workspace=None, stream=None):
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _call("cxg_gpt_attn_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
+          _ptr(dK), _ptr(dV), B, S, E, _ptr(workspace), nbytes, _stream(stream))
 
 
 # ------------------------------------------------------------------ ELU+1, two_stage API

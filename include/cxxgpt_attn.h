@@ -85,6 +85,23 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
                      size_t B, size_t S, size_t H, size_t Dh, void *workspace,
                      size_t workspace_bytes, cxg_stream_t stream);
 
+/* GPT's attention (src/GPT/gpt_gpt.hpp:365-380 forward, :420-438 backward):
+ * one head over the embedding, scores (B*S) x (B*S) with the block-diagonal
+ * causal mask of gpt_cuda::attention_mask (gpt_cuda_kernels.cu:458-480),
+ * softmax, times V, and the backward through gpt_cuda::softmax_backward.  No
+ * single counterpart in the reference (it is matmuls, a mask, a softmax and
+ * transposes).  Q, K, V, O (B*S, E) row-major; lse [B][S] natural log; the
+ * same as cxg_mha_fwd / cxg_mha_bwd with H = 1, Dh = E, which serve E <= 256;
+ * 256 < E <= 512 (the reference GPT's training configuration has E = 512)
+ * takes wider-head kernels; CXG_ERR_HEAD_DIM above 512. */
+int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
+                     size_t B, size_t S, size_t E, cxg_stream_t stream);
+int cxg_gpt_attn_bwd(const float *Q, const float *K, const float *V, const float *O,
+                     const float *dO, const float *lse, float *dQ, float *dK, float *dV,
+                     size_t B, size_t S, size_t E, void *workspace, size_t workspace_bytes,
+                     cxg_stream_t stream);
+size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E);
+
 /* ============ ELU+1 linear "kernel" attention, two_stage_cuda API ============
  * phi(x) = x > 0 ? x + 1 : exp(x), fused.  Q/K (B*S, D), V/O (B*S, E); one
  * sequence per b (multi-head callers pass B = batch*heads, head-major rows).
