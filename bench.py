@@ -31,6 +31,8 @@ them can be made the reported workload with --workload NAME):
   c2ropesep C2 with RoPE as separate passes, the reference's call sequence
   gpt       GPT's attention at its training shape (B8 S256, one head of E=512,
             gpt_train.cpp:139/156): cxg_gpt_attn_fwd -> cxg_gpt_attn_bwd
+  gelu      exact GELU + derivative over the q/k/v expander FFN activations at
+            the C2 shape (3 x 2048 x 6144 floats; two_stage_gpt.hpp:86-99), GB/s
   copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
@@ -139,7 +141,7 @@ def attribute(cx, step, steps):
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
-              "mha_wide_stats", "mha_wide_bwd"):
+              "mha_wide_stats", "mha_wide_bwd", "gelu", "gelu_deriv"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)
@@ -237,6 +239,44 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
                         "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops},
                 frac=value / FP32_MFMA_PEAK_TFLOPS,
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
+
+
+def _gelu(c, name, rows, cols, seed, steps, warmup):
+    """Exact GELU and its derivative as the two-stage block's q/k/v expander
+    FFNs apply them (two_stage_gpt.hpp:86-99 forward, :177-195 backward):
+    per expander gelu_exact(f, act) then gelu_exact_deriv(act, g), on three
+    separate [rows, cols] tensors, so the 450 MiB footprint exceeds the
+    last-level cache.  GB/s of compulsory I/O (each call reads and writes its
+    tensor once)."""
+    g = c.gen(seed)
+    n = rows * cols
+    P = _ptr
+    calls = []
+    keep = []
+    for _ in range(3):
+        f = c.randn(g, n)
+        act, gd = c.empty(n), c.empty(n)
+        keep += [f, act, gd]
+        calls += [("cxg_gelu_exact", (P(f), P(act), n, c.sp)),
+                  ("cxg_gelu_exact_deriv", (P(act), P(gd), n, c.sp))]
+    step = Stepper(c.cx.lib(), calls)
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    total = len(calls) * 2 * n * 4
+    value = total / (ms * 1e-3) / 1e9
+    kb = {"gelu": 2 * n * 4, "gelu_deriv": 2 * n * 4}
+    dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
+    ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: exact GELU + derivative over the q/k/v expander "
+                                    f"FFN activations (two_stage_gpt.hpp:86-99, :177-195) at "
+                                    f"the C2 shape",
+                        "rows": rows, "cols": cols, "tensors": 3, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
 
 def _gpt(c, name, B, S, E, seed, steps, warmup):
@@ -459,6 +499,8 @@ def run_workload(c, name, steps, warmup):
                       fused=True)
     if name == "c3fuseds256":
         return _kattn(c, name, 96, 256, 64, 78, steps, warmup, fused=True)
+    if name == "gelu":
+        return _gelu(c, name, 8 * 256, 8 * 768, 93, steps, warmup)
     if name == "gpt":
         return _gpt(c, name, 8, 256, 512, 91, steps, warmup)
     if name == "c3lgpt":
@@ -531,7 +573,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "copy"])
+                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -573,7 +615,7 @@ def main():
     sec = {}
     if not args.no_secondary and args.workload == "c2":
         for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c4", "c5",
-                     "rope", "c2rope", "c2ropesep", "gpt"):
+                     "rope", "c2rope", "c2ropesep", "gpt", "gelu"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

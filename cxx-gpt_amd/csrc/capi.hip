@@ -656,6 +656,30 @@ int cxg_phi_hexp_bwd(const float* dphi, const float* x, float* dx, size_t N, siz
 }
 
 // ---------------------------------------------------------------------------
+// exact GELU
+// ---------------------------------------------------------------------------
+static int gelu_common(const float* A, float* C, size_t n, bool deriv, cxg_stream_t stream)
+{
+    if (n == 0)
+        return CXG_OK;
+    if (n > ((size_t)1 << 40))
+        return CXG_ERR_DIMS;
+    if (!A || !C)
+        return CXG_ERR_NULL;
+    return hip_status(gelu_launch(A, C, (long)n, deriv, (hipStream_t)stream));
+}
+
+int cxg_gelu_exact(const float* A, float* C, size_t n, cxg_stream_t stream)
+{
+    return gelu_common(A, C, n, false, stream);
+}
+
+int cxg_gelu_exact_deriv(const float* A, float* C, size_t n, cxg_stream_t stream)
+{
+    return gelu_common(A, C, n, true, stream);
+}
+
+// ---------------------------------------------------------------------------
 // rotary position embedding
 // ---------------------------------------------------------------------------
 static int rope_common(float* Q, float* K, size_t B, size_t S, size_t D, size_t head_dim,

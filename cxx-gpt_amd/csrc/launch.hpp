@@ -64,6 +64,9 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
                                const float* lse, const float* Di, float* dQ, float* dK,
                                float* dV, int B, int S, int H, int Dh, hipStream_t st);
 
+// Exact (erf) GELU or its derivative over n elements (C may alias A).
+hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t st);
+
 // Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
 // may be null, and they may be one buffer).  Frequencies of pairs 0 ..
 // head_dim/2-1 travel in the kernel arguments.

@@ -56,6 +56,8 @@ SIGNATURES = {
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
+    "cxg_gelu_exact": [_vp, _vp, _sz, _vp],
+    "cxg_gelu_exact_deriv": [_vp, _vp, _sz, _vp],
     "cxg_rope_fwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_rope_bwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_prof_enable": [ctypes.c_int],
@@ -256,6 +258,14 @@ def lin_elu_bwd(Xq, Xk, V, O, dO, den, dXq, dXk, dV, B, S, E, ctx=None, stream=N
     """LinearGPT attention backward: step1 + dQ + dKdV + phi_elu_backward, fused."""
     _call("cxg_lin_elu_bwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(dO), _ptr(den),
           _ptr(ctx), _ptr(dXq), _ptr(dXk), _ptr(dV), B, S, E, _stream(stream))
+
+
+def gelu_exact(A, C, n, stream=None):
+    _call("cxg_gelu_exact", _ptr(A), _ptr(C), n, _stream(stream))
+
+
+def gelu_exact_deriv(A, C, n, stream=None):
+    _call("cxg_gelu_exact_deriv", _ptr(A), _ptr(C), n, _stream(stream))
 
 
 def phi_elu_fwd(x, phi, N, D, E, stream=None):

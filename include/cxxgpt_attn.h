@@ -264,6 +264,12 @@ void cxg_prof_enable(int on);
 void cxg_prof_reset(void);
 int cxg_prof_query(const char *kernel_name, double *total_ms, int *count);
 
+/* two_stage_cuda::gelu_exact / gelu_exact_deriv (two_stage_cuda_kernels.cuh:84-85,
+ * two_stage_cuda_kernels.cu:1888-1924): C = gelu(A) or gelu'(A) over n floats,
+ * exact (erf) form; C may be A. */
+int cxg_gelu_exact(const float *A, float *C, size_t n, cxg_stream_t stream);
+int cxg_gelu_exact_deriv(const float *A, float *C, size_t n, cxg_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

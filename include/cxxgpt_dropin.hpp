@@ -138,6 +138,21 @@ void rope_bwd(CT& dQ, CT& dK, size_t B, size_t S, size_t D, size_t head_dim)
     check(cxg_rope_bwd(mptr(dQ), mptr(dK), B, S, D, head_dim, nullptr), "rope_bwd");
 }
 
+// two_stage_cuda_kernels.cuh:84-85 (n = A.size(), as the reference's wrappers)
+template <class CT>
+void gelu_exact(const CT& A, CT& C)
+{
+    using namespace cxg_dropin;
+    check(cxg_gelu_exact(cptr(A), mptr(C), A.size(), nullptr), "gelu_exact");
+}
+
+template <class CT>
+void gelu_exact_deriv(const CT& A, CT& C)
+{
+    using namespace cxg_dropin;
+    check(cxg_gelu_exact_deriv(cptr(A), mptr(C), A.size(), nullptr), "gelu_exact_deriv");
+}
+
 } // namespace two_stage_cuda
 
 namespace linear_cuda {

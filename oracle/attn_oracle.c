@@ -777,3 +777,22 @@ void orc_rope(float *X, size_t B, size_t S, size_t D, size_t head_dim, float sig
             }
     }
 }
+
+/* two_stage_cuda_kernels.cu:1888-1895 */
+void orc_gelu_exact(const float *A, float *C, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        const float x = A[i];
+        C[i] = 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+    }
+}
+
+/* two_stage_cuda_kernels.cu:1906-1914 */
+void orc_gelu_exact_deriv(const float *A, float *C, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        const float x = A[i];
+        const float a = x * 0.7071067811865476f;
+        C[i] = 0.5f * (1.0f + erff(a)) + x * expf(-0.5f * x * x) * 0.3989422804014327f;
+    }
+}

@@ -158,6 +158,14 @@ void orc_phi_hexp_backward(const float *dphi, const float *x, float *dx,
  * In place. */
 void orc_rope(float *X, size_t B, size_t S, size_t D, size_t head_dim, float sign);
 
+/* ---------------- exact GELU ----------------
+ * src/TwoStage/two_stage_cuda_kernels.cu:1888-1924 (gelu_exact_kernel,
+ * gelu_exact_deriv_kernel), in float with the C library's erff / expf:
+ *   gelu(x) = 0.5 x (1 + erf(x * 0.7071067811865476))
+ *   gelu'(x) = 0.5 (1 + erf(x * 0.70710678...)) + x exp(-0.5 x^2) * 0.3989422804014327 */
+void orc_gelu_exact(const float *A, float *C, size_t n);
+void orc_gelu_exact_deriv(const float *A, float *C, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

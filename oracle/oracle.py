@@ -255,3 +255,19 @@ def rope(X, B, S, D, head_dim, sign):
     Y = np.array(X, dtype=np.float32, copy=True, order="C")
     lib().orc_rope(_p(Y), _sz(B), _sz(S), _sz(D), _sz(head_dim), ctypes.c_float(sign))
     return Y
+
+
+def gelu_exact(A):
+    """two_stage_cuda_kernels.cu:1888-1895 (gelu_exact_kernel)."""
+    A = _c(A)
+    C = np.zeros_like(A)
+    lib().orc_gelu_exact(_p(A), _p(C), _sz(A.size))
+    return C
+
+
+def gelu_exact_deriv(A):
+    """two_stage_cuda_kernels.cu:1906-1914 (gelu_exact_deriv_kernel)."""
+    A = _c(A)
+    C = np.zeros_like(A)
+    lib().orc_gelu_exact_deriv(_p(A), _p(C), _sz(A.size))
+    return C

@@ -409,3 +409,38 @@ def test_rope_planted_mistakes_are_caught(kt):
     assert _rejects(got, _np_rope64(X, S, D, hd, 1.0, freq_exp=-1.0))    # wrong frequencies
     assert _rejects(got, _np_rope64(X, S, D, hd, 1.0, swap=True))        # pair order swapped
     assert _rejects(got, _np_rope64(X, S + 1, D, hd, 1.0))               # wrong positions
+
+
+# ---------------------------------------------------------------- exact GELU
+def _gelu64(x):
+    from math import erf, sqrt
+    return np.array([0.5 * v * (1.0 + erf(v / sqrt(2.0))) for v in np.asarray(x, float)])
+
+
+def test_gelu_oracle_closed_form_and_derivative():
+    """orc_gelu_exact(_deriv) (two_stage_cuda_kernels.cu:1888-1924) against the
+    float64 erf form, central differences of it, and the fixed points
+    gelu(0) = 0, gelu'(0) = 1/2, gelu(x) - gelu(-x) = x."""
+    x = np.linspace(-9.0, 9.0, 721).astype(np.float32)
+    g = orc.gelu_exact(x)
+    d = orc.gelu_exact_deriv(x)
+    assert np.allclose(g, _gelu64(x), rtol=2e-6, atol=2e-7)
+    h = 1e-4
+    fd = (_gelu64(x.astype(float) + h) - _gelu64(x.astype(float) - h)) / (2 * h)
+    assert np.allclose(d, fd, rtol=2e-5, atol=2e-6)
+    z = orc.gelu_exact(np.zeros(1, np.float32))
+    dz = orc.gelu_exact_deriv(np.zeros(1, np.float32))
+    assert z[0] == 0.0 and dz[0] == 0.5
+    assert np.allclose(g - orc.gelu_exact(-x), x, atol=2e-6)
+
+
+def test_gelu_planted_mistakes_are_caught():
+    """The tanh approximation and a wrong erf argument scale both fail the
+    float64 closed-form check above."""
+    x = np.linspace(-9.0, 9.0, 721)
+    ref = _gelu64(x)
+    tanh_form = 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)))
+    from math import erf
+    wrong_scale = np.array([0.5 * v * (1.0 + erf(v * 0.5)) for v in x])
+    for bad in (tanh_form, wrong_scale):
+        assert not np.allclose(bad, ref, rtol=2e-6, atol=2e-7)
