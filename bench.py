@@ -33,6 +33,8 @@ them can be made the reported workload with --workload NAME):
             gpt_train.cpp:139/156): cxg_gpt_attn_fwd -> cxg_gpt_attn_bwd
   gelu      exact GELU + derivative over the q/k/v expander FFN activations at
             the C2 shape (3 x 2048 x 6144 floats; two_stage_gpt.hpp:86-99), GB/s
+  ffn       one expander FFN fwd+bwd (X [2048][768], W1 [6144][768], W2
+            [768][6144]; two_stage_gpt.hpp:86-89,177-183), six FP32 GEMMs, TFLOP/s
   copy      256 MiB device copy: HBM counter calibration for the profiles
 
 Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
@@ -141,7 +143,8 @@ def attribute(cx, step, steps):
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
-              "mha_wide_stats", "mha_wide_bwd", "gelu", "gelu_deriv"):
+              "mha_wide_stats", "mha_wide_bwd", "gelu", "gelu_deriv", "ffn_gemm",
+              "ffn_reduce"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)
@@ -277,6 +280,47 @@ def _gelu(c, name, rows, cols, seed, steps, warmup):
                                     f"the C2 shape",
                         "rows": rows, "cols": cols, "tensors": 3, "bytes_per_step": total},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=None)
+
+
+def _ffn(c, name, M, E, F, seed, steps, warmup):
+    """One expander FFN forward + backward (two_stage_gpt.hpp:86-89, :177-183)
+    through cxg_ffn_fwd / cxg_ffn_bwd: six FP32 GEMMs of 2*M*E*F flops each,
+    GELU in the first's epilogue and gelu' in the first backward one's."""
+    import torch
+    g = c.gen(seed)
+    X = c.randn(g, M * E)
+    W1 = c.randn(g, F * E, std=(2.0 / E) ** 0.5)
+    W2 = c.randn(g, E * F, std=(2.0 / F) ** 0.5)
+    dY = c.randn(g, M * E, std=1.0 / M)
+    act, Y = c.empty(M * F), c.empty(M * E)
+    dX = c.empty(M * E)
+    dW1 = torch.zeros(F * E, device=X.device)
+    dW2 = torch.zeros(E * F, device=X.device)
+    nb = c.cx.lib().cxg_ffn_workspace_size(M, E, F)
+    ws = c.empty(max(nb, 4) // 4)
+    P = _ptr
+    step = Stepper(c.cx.lib(), [
+        ("cxg_ffn_fwd", (P(X), P(W1), P(W2), None, P(act), P(Y), M, E, F, P(ws), nb, c.sp)),
+        ("cxg_ffn_bwd", (P(X), P(W1), P(W2), P(act), P(act), P(dY), P(dX), P(dW1), P(dW2),
+                         M, E, F, P(ws), nb, c.sp))])
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    flops = 12.0 * M * E * F
+    value = flops / (ms * 1e-3) / 1e12
+    per_launch = 2.0 * M * E * F
+    ach = per_launch / (att["ffn_gemm"][0] * 1e-3) / 1e12
+    roof = {"bound": "mfma", "kernel": "ffn_gemm", "achieved": round(ach, 2),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": c.traffic.get(f"{name}/ffn_gemm"), "flops_per_launch": per_launch,
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()},
+            "launches_per_step": {k: round(v[1], 2) for k, v in att.items()}}
+    return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: one expander FFN (Linear -> exact GELU -> Linear, "
+                                    f"no bias) forward + backward at the C2 shape, "
+                                    f"two_stage_gpt.hpp:86-89,177-183",
+                        "rows": M, "n_embd": E, "hidden": F, "flops_per_step": flops},
+                frac=value / FP32_MFMA_PEAK_TFLOPS, cpu_inputs=None)
 
 
 def _gpt(c, name, B, S, E, seed, steps, warmup):
@@ -499,6 +543,8 @@ def run_workload(c, name, steps, warmup):
                       fused=True)
     if name == "c3fuseds256":
         return _kattn(c, name, 96, 256, 64, 78, steps, warmup, fused=True)
+    if name == "ffn":
+        return _ffn(c, name, 8 * 256, 768, 4 * 2 * 768, 97, steps, warmup)
     if name == "gelu":
         return _gelu(c, name, 8 * 256, 8 * 768, 93, steps, warmup)
     if name == "gpt":
@@ -573,7 +619,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu", "copy"])
+                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -615,7 +661,7 @@ def main():
     sec = {}
     if not args.no_secondary and args.workload == "c2":
         for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c4", "c5",
-                     "rope", "c2rope", "c2ropesep", "gpt", "gelu"):
+                     "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn"):
             s = run_workload(c, name, args.steps, args.warmup)
             sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),

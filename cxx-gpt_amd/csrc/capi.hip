@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 
 #include <limits.h>
+#include <stdint.h>
+
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -130,6 +133,7 @@ const char* cxg_status_str(int status)
     case CXG_ERR_HEAD_DIM: return "head_dim > 256 not supported";
     case CXG_ERR_HIP: return "HIP runtime error";
     case CXG_ERR_WORKSPACE: return "workspace too small or allocation failed";
+    case CXG_ERR_ALIGN: return "tensor not 16-byte aligned or width not a multiple of 4";
     default: return "unknown status";
     }
 }
@@ -677,6 +681,111 @@ int cxg_gelu_exact(const float* A, float* C, size_t n, cxg_stream_t stream)
 int cxg_gelu_exact_deriv(const float* A, float* C, size_t n, cxg_stream_t stream)
 {
     return gelu_common(A, C, n, true, stream);
+}
+
+// ---------------------------------------------------------------------------
+// expander FFN (Linear -> exact GELU -> Linear, no bias)
+// ---------------------------------------------------------------------------
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static int ffn_check(size_t M, size_t E, size_t F, bool* empty)
+{
+    *empty = M == 0;
+    if (E == 0 || F == 0)
+        return CXG_ERR_DIMS;
+    if (!fits_int(M) || !fits_int(E) || !fits_int(F) || M * F > ((size_t)1 << 40) ||
+        M * E > ((size_t)1 << 40) || E * F > ((size_t)1 << 40))
+        return CXG_ERR_DIMS;
+    if (E % 4 != 0 || F % 4 != 0)
+        return CXG_ERR_ALIGN;
+    return CXG_OK;
+}
+
+static size_t ffn_fwd_ws(int M, int E, int F)
+{
+    return std::max(ffn_gemm_ws_floats(M, F, E), ffn_gemm_ws_floats(M, E, F));
+}
+
+static size_t ffn_bwd_ws(int M, int E, int F)
+{
+    size_t part = std::max(std::max(ffn_gemm_ws_floats(M, F, E), ffn_gemm_ws_floats(E, F, M)),
+                           std::max(ffn_gemm_ws_floats(M, E, F), ffn_gemm_ws_floats(F, E, M)));
+    return round_up((size_t)M * F, 64) + part;
+}
+
+size_t cxg_ffn_workspace_size(size_t M, size_t E, size_t F)
+{
+    bool empty;
+    if (ffn_check(M, E, F, &empty) != CXG_OK || empty)
+        return 0;
+    const size_t fl = std::max(ffn_fwd_ws((int)M, (int)E, (int)F), ffn_bwd_ws((int)M, (int)E, (int)F));
+    return round_up(fl * sizeof(float), 256);
+}
+
+int cxg_ffn_fwd(const float* X, const float* W1, const float* W2, float* pre, float* act,
+                float* Y, size_t M, size_t E, size_t F, void* workspace, size_t ws_bytes,
+                cxg_stream_t stream)
+{
+    bool empty;
+    int st = ffn_check(M, E, F, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!X || !W1 || !W2 || !act || !Y)
+        return CXG_ERR_NULL;
+    for (const void* p : {(const void*)X, (const void*)W1, (const void*)W2, (const void*)pre,
+                          (const void*)act, (const void*)Y})
+        if (!aligned16(p))
+            return CXG_ERR_ALIGN;
+    const int m = (int)M, e = (int)E, f = (int)F;
+    hipStream_t hs = (hipStream_t)stream;
+    Scratch ws;
+    st = ws.acquire(workspace, ws_bytes, ffn_fwd_ws(m, e, f) * sizeof(float), hs);
+    if (st != CXG_OK)
+        return st;
+    float* part = (float*)ws.p;
+    FfnGemm fc{X, e, true, W1, e, true, m, f, e, FFN_EPI_GELU, act, f, nullptr, pre};
+    FfnGemm proj{act, f, true, W2, f, true, m, e, f, FFN_EPI_STORE, Y, e, nullptr, nullptr};
+    hipError_t he = ffn_gemm_launch(fc, part, hs);
+    if (he == hipSuccess)
+        he = ffn_gemm_launch(proj, part, hs);
+    return hip_status(he);
+}
+
+int cxg_ffn_bwd(const float* X, const float* W1, const float* W2, const float* act,
+                const float* G, const float* dY, float* dX, float* dW1, float* dW2, size_t M,
+                size_t E, size_t F, void* workspace, size_t ws_bytes, cxg_stream_t stream)
+{
+    bool empty;
+    int st = ffn_check(M, E, F, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!X || !W1 || !W2 || !act || !G || !dY || !dX || !dW1 || !dW2)
+        return CXG_ERR_NULL;
+    for (const void* p : {(const void*)X, (const void*)W1, (const void*)W2, (const void*)act,
+                          (const void*)G, (const void*)dY, (const void*)dX, (const void*)dW1,
+                          (const void*)dW2})
+        if (!aligned16(p))
+            return CXG_ERR_ALIGN;
+    const int m = (int)M, e = (int)E, f = (int)F;
+    hipStream_t hs = (hipStream_t)stream;
+    Scratch ws;
+    st = ws.acquire(workspace, ws_bytes, ffn_bwd_ws(m, e, f) * sizeof(float), hs);
+    if (st != CXG_OK)
+        return st;
+    float* dact = (float*)ws.p;
+    float* part = dact + round_up((size_t)M * F, 64);
+    FfnGemm dp{dY, e, true, W2, f, false, m, f, e, FFN_EPI_DGELU, dact, f, G, nullptr};
+    FfnGemm w2{dY, e, false, act, f, false, e, f, m, FFN_EPI_ACCUM, dW2, f, nullptr, nullptr};
+    FfnGemm dx{dact, f, true, W1, e, false, m, e, f, FFN_EPI_STORE, dX, e, nullptr, nullptr};
+    FfnGemm w1{dact, f, false, X, e, false, f, e, m, FFN_EPI_ACCUM, dW1, e, nullptr, nullptr};
+    hipError_t he = ffn_gemm_launch(dp, part, hs);
+    if (he == hipSuccess)
+        he = ffn_gemm_launch(w2, part, hs);
+    if (he == hipSuccess)
+        he = ffn_gemm_launch(dx, part, hs);
+    if (he == hipSuccess)
+        he = ffn_gemm_launch(w1, part, hs);
+    return hip_status(he);
 }
 
 // ---------------------------------------------------------------------------

@@ -9,21 +9,12 @@
 // (erf from the device math library; the reference's derivative uses the
 // fast exp, and so does this one).  HBM-bound: 8 bytes per element.
 #include "common.hpp"
+#include "gelu_dev.hpp"
 #include "launch.hpp"
-
-#include <math.h>
 
 #include <algorithm>
 
 namespace cxg {
-
-__device__ __forceinline__ float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
-
-__device__ __forceinline__ float gelu_d(float x)
-{
-    return 0.5f * (1.0f + erff(x * 0.7071067811865476f)) +
-           x * __expf(-0.5f * x * x) * 0.3989422804014327f;
-}
 
 // Aligned path: a workgroup takes tiles of GELU_TILE 4-element groups; each
 // thread issues its GELU_U 16-byte loads before any arithmetic, so a compute

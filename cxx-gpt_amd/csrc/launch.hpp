@@ -67,6 +67,33 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
 // Exact (erf) GELU or its derivative over n elements (C may alias A).
 hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t st);
 
+// FP32 GEMM for the expander FFNs: C[M][N] = epi(sum_k A(i,k) B(k,j)).
+//   ak: A(i,k) = A[i*lda + k], else A[k*lda + i]  (ak = false needs bk = false)
+//   bk: B(k,j) = B[j*ldb + k], else B[k*ldb + j]
+// Epilogues: STORE C = acc; GELU pre = acc (if pre != null), C = gelu(acc);
+// DGELU C = acc * gelu'(G) (G indexed like C); ACCUM C += acc.
+// N % 4 == 0; a k-contiguous operand needs K % 4 == 0, a row-contiguous one
+// its row count % 4 == 0; all tensors 16-byte aligned, strides % 4 == 0.
+// ws: ffn_gemm_ws_floats(M, N, K) floats when that is nonzero (split K).
+enum { FFN_EPI_STORE = 0, FFN_EPI_GELU = 1, FFN_EPI_DGELU = 2, FFN_EPI_ACCUM = 3 };
+struct FfnGemm {
+    const float* A;
+    long lda;
+    bool ak;
+    const float* B;
+    long ldb;
+    bool bk;
+    int M, N, K;
+    int epi;
+    float* C;
+    long ldc;
+    const float* G;
+    float* pre;
+};
+int ffn_gemm_splits(int M, int N, int K);
+size_t ffn_gemm_ws_floats(int M, int N, int K);
+hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st);
+
 // Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
 // may be null, and they may be one buffer).  Frequencies of pairs 0 ..
 // head_dim/2-1 travel in the kernel arguments.

@@ -18,6 +18,7 @@ CXG_ERR_DIMS = 2
 CXG_ERR_HEAD_DIM = 3
 CXG_ERR_HIP = 4
 CXG_ERR_WORKSPACE = 5
+CXG_ERR_ALIGN = 6
 
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -58,6 +59,9 @@ SIGNATURES = {
     "cxg_phi_hexp_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_gelu_exact": [_vp, _vp, _sz, _vp],
     "cxg_gelu_exact_deriv": [_vp, _vp, _sz, _vp],
+    "cxg_ffn_workspace_size": [_sz] * 3,
+    "cxg_ffn_fwd": [_vp] * 6 + [_sz] * 3 + [_vp, _sz, _vp],
+    "cxg_ffn_bwd": [_vp] * 9 + [_sz] * 3 + [_vp, _sz, _vp],
     "cxg_rope_fwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_rope_bwd": [_vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_prof_enable": [ctypes.c_int],
@@ -71,6 +75,7 @@ _RESTYPES = {
     "cxg_mha_bwd_workspace_size": ctypes.c_size_t,
     "cxg_lin_ctx_size": ctypes.c_size_t,
     "cxg_gpt_attn_bwd_workspace_size": ctypes.c_size_t,
+    "cxg_ffn_workspace_size": ctypes.c_size_t,
     "cxg_prof_enable": None,
     "cxg_prof_reset": None,
 }
@@ -266,6 +271,26 @@ def gelu_exact(A, C, n, stream=None):
 
 def gelu_exact_deriv(A, C, n, stream=None):
     _call("cxg_gelu_exact_deriv", _ptr(A), _ptr(C), n, _stream(stream))
+
+
+def ffn_workspace_size(M, E, F):
+    return lib().cxg_ffn_workspace_size(M, E, F)
+
+
+def ffn_fwd(X, W1, W2, pre, act, Y, M, E, F, workspace=None, stream=None):
+    """Expander FFN forward: pre = X W1^T (if pre is not None), act = gelu(pre),
+    Y = act W2^T."""
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _call("cxg_ffn_fwd", _ptr(X), _ptr(W1), _ptr(W2), _ptr(pre), _ptr(act), _ptr(Y), M, E, F,
+          _ptr(workspace), nbytes, _stream(stream))
+
+
+def ffn_bwd(X, W1, W2, act, G, dY, dX, dW1, dW2, M, E, F, workspace=None, stream=None):
+    """Expander FFN backward: dact = (dY W2) * gelu'(G); dW2 += dY^T act;
+    dX = dact W1; dW1 += dact^T X."""
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _call("cxg_ffn_bwd", _ptr(X), _ptr(W1), _ptr(W2), _ptr(act), _ptr(G), _ptr(dY), _ptr(dX),
+          _ptr(dW1), _ptr(dW2), M, E, F, _ptr(workspace), nbytes, _stream(stream))
 
 
 def phi_elu_fwd(x, phi, N, D, E, stream=None):

@@ -37,7 +37,8 @@ enum {
     CXG_ERR_DIMS = 2,      /* a dimension is zero where it may not be, or too large */
     CXG_ERR_HEAD_DIM = 3,  /* softmax head_dim > 256 (the reference aborts) */
     CXG_ERR_HIP = 4,       /* the HIP runtime reported an error */
-    CXG_ERR_WORKSPACE = 5  /* workspace too small, or its allocation failed */
+    CXG_ERR_WORKSPACE = 5, /* workspace too small, or its allocation failed */
+    CXG_ERR_ALIGN = 6      /* a tensor is not 16-byte aligned, or a width is not a multiple of 4 */
 };
 
 /* Human-readable name of a status code (static string). */
@@ -269,6 +270,31 @@ int cxg_prof_query(const char *kernel_name, double *total_ms, int *count);
  * exact (erf) form; C may be A. */
 int cxg_gelu_exact(const float *A, float *C, size_t n, cxg_stream_t stream);
 int cxg_gelu_exact_deriv(const float *A, float *C, size_t n, cxg_stream_t stream);
+
+/* The two-stage block's expander FFN: two bias-free Linear layers with the
+ * exact GELU between them (two_stage_gpt.hpp:37-40; the call sequence
+ * q_ffn_fc.forward -> gelu_exact -> q_ffn_proj.forward at :86-89, and the
+ * same for k, v and the final FFN at :91-99, :126-129; Linear::forward /
+ * backward at gpt_gpt.hpp:86-112).  Row-major X [M][E], W1 [F][E] (the fc
+ * weight), W2 [E][F] (the proj weight); the reference's F is 4*N*n_embd.
+ *   cxg_ffn_fwd:  pre = X W1^T (stored if pre != NULL, else not kept),
+ *                 act = gelu(pre), Y = act W2^T.
+ *   cxg_ffn_bwd:  dact = (dY W2) * gelu'(G); dW2 += dY^T act; dX = dact W1;
+ *                 dW1 += dact^T X  (weight gradients accumulate, as Linear
+ *                 does).  G is the tensor gelu' is evaluated at: the
+ *                 reference's q/k/v expanders pass act (:179,187,195), its
+ *                 final FFN the pre-activation (:141).
+ * FP32 MFMA GEMMs with GELU / gelu' in their epilogues.  E and F multiples of
+ * 4 and every tensor 16-byte aligned (else CXG_ERR_ALIGN); any M.  workspace
+ * of cxg_ffn_workspace_size(M, E, F) bytes (fwd and bwd), or NULL for
+ * stream-ordered scratch per call. */
+size_t cxg_ffn_workspace_size(size_t M, size_t E, size_t F);
+int cxg_ffn_fwd(const float *X, const float *W1, const float *W2, float *pre, float *act,
+                float *Y, size_t M, size_t E, size_t F, void *workspace, size_t ws_bytes,
+                cxg_stream_t stream);
+int cxg_ffn_bwd(const float *X, const float *W1, const float *W2, const float *act,
+                const float *G, const float *dY, float *dX, float *dW1, float *dW2, size_t M,
+                size_t E, size_t F, void *workspace, size_t ws_bytes, cxg_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -796,3 +796,75 @@ void orc_gelu_exact_deriv(const float *A, float *C, size_t n)
         C[i] = 0.5f * (1.0f + erff(a)) + x * expf(-0.5f * x * x) * 0.3989422804014327f;
     }
 }
+
+/* ------------------------------------------------------------------ */
+/* expander FFN (two_stage_gpt.hpp:86-99, :177-195)                    */
+/* ------------------------------------------------------------------ */
+/* C[i][j] (= or +=) sum_k A(i,k) B(k,j), double accumulation; ak: A(i,k) at
+ * A[i*lda + k] else A[k*lda + i]; bk: B(k,j) at B[j*ldb + k] else B[k*ldb + j]. */
+typedef struct {
+    const float *A, *B;
+    size_t lda, ldb, ldc, N, K;
+    int ak, bk, accum;
+    float *C;
+} orc_gemm_ctx;
+
+static void orc_gemm_row(void *vc, size_t i)
+{
+    const orc_gemm_ctx *c = (const orc_gemm_ctx *)vc;
+    double *acc = (double *)calloc(c->N, sizeof(double));
+    for (size_t k = 0; k < c->K; k++) {
+        const double a = c->ak ? c->A[i * c->lda + k] : c->A[k * c->lda + i];
+        if (c->bk) {
+            for (size_t j = 0; j < c->N; j++)
+                acc[j] += a * (double)c->B[j * c->ldb + k];
+        } else {
+            const float *b = c->B + k * c->ldb;
+            for (size_t j = 0; j < c->N; j++)
+                acc[j] += a * (double)b[j];
+        }
+    }
+    float *out = c->C + i * c->ldc;
+    for (size_t j = 0; j < c->N; j++)
+        out[j] = c->accum ? (float)((double)out[j] + acc[j]) : (float)acc[j];
+    free(acc);
+}
+
+static void orc_gemm(const float *A, size_t lda, int ak, const float *B, size_t ldb, int bk,
+                     size_t M, size_t N, size_t K, float *C, size_t ldc, int accum, int nthreads)
+{
+    orc_gemm_ctx c = {A, B, lda, ldb, ldc, N, K, ak, bk, accum, C};
+    orc_parallel_for(M, nthreads, orc_gemm_row, &c);
+}
+
+/* q_ffn_fc.forward (X W1^T, gpt_gpt.hpp:86-93) -> gelu_exact -> q_ffn_proj.forward */
+void orc_ffn_fwd(const float *X, const float *W1, const float *W2, float *pre, float *act,
+                 float *Y, size_t M, size_t E, size_t F, int nthreads)
+{
+    float *p = pre ? pre : (float *)malloc(sizeof(float) * M * F);
+    orc_gemm(X, E, 1, W1, E, 1, M, F, E, p, F, 0, nthreads);
+    orc_gelu_exact(p, act, M * F);
+    orc_gemm(act, F, 1, W2, F, 1, M, E, F, Y, E, 0, nthreads);
+    if (!pre)
+        free(p);
+}
+
+/* q_ffn_proj.backward (dY W2; W2.grad += dY^T act, gpt_gpt.hpp:98-105) ->
+ * gelu_exact_deriv(G) -> multiply -> q_ffn_fc.backward (dact W1; W1.grad +=
+ * dact^T X), two_stage_gpt.hpp:177-183 */
+void orc_ffn_bwd(const float *X, const float *W1, const float *W2, const float *act,
+                 const float *G, const float *dY, float *dX, float *dW1, float *dW2, size_t M,
+                 size_t E, size_t F, int nthreads)
+{
+    float *dact = (float *)malloc(sizeof(float) * M * F);
+    float *gd = (float *)malloc(sizeof(float) * M * F);
+    orc_gemm(dY, E, 1, W2, F, 0, M, F, E, dact, F, 0, nthreads);
+    orc_gemm(dY, E, 0, act, F, 0, E, F, M, dW2, F, 1, nthreads);
+    orc_gelu_exact_deriv(G, gd, M * F);
+    for (size_t i = 0; i < M * F; i++)
+        dact[i] *= gd[i];
+    orc_gemm(dact, F, 1, W1, E, 0, M, E, F, dX, E, 0, nthreads);
+    orc_gemm(dact, F, 0, X, E, 0, F, E, M, dW1, E, 1, nthreads);
+    free(gd);
+    free(dact);
+}

@@ -166,6 +166,22 @@ void orc_rope(float *X, size_t B, size_t S, size_t D, size_t head_dim, float sig
 void orc_gelu_exact(const float *A, float *C, size_t n);
 void orc_gelu_exact_deriv(const float *A, float *C, size_t n);
 
+/* The two-stage block's expander FFN (two_stage_gpt.hpp:86-99, :177-195):
+ * Linear (no bias, gpt_gpt.hpp:86-112) -> exact GELU -> Linear.
+ * X [M][E], W1 [F][E], W2 [E][F] row-major.
+ *   fwd: pre = X W1^T (if pre != NULL), act = gelu(X W1^T), Y = act W2^T
+ *   bwd: dact = (dY W2) * gelu'(G); dW2 += dY^T act; dX = dact W1;
+ *        dW1 += dact^T X
+ * Products accumulate in double and round once to float (the reference's
+ * GEMMs are TensorN's cuBLAS calls, whose summation order is not available;
+ * this is the correctly rounded fp32 result any order is measured against).
+ * Rows are spread over nthreads threads. */
+void orc_ffn_fwd(const float *X, const float *W1, const float *W2, float *pre, float *act,
+                 float *Y, size_t M, size_t E, size_t F, int nthreads);
+void orc_ffn_bwd(const float *X, const float *W1, const float *W2, const float *act,
+                 const float *G, const float *dY, float *dX, float *dW1, float *dW2, size_t M,
+                 size_t E, size_t F, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

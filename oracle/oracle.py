@@ -265,6 +265,29 @@ def gelu_exact(A):
     return C
 
 
+def ffn_fwd(X, W1, W2, M, E, F, nthreads=8):
+    """Expander FFN forward (two_stage_gpt.hpp:86-89): returns pre, act, Y."""
+    X, W1, W2 = _c(X), _c(W1), _c(W2)
+    pre = np.zeros((M, F), np.float32)
+    act = np.zeros((M, F), np.float32)
+    Y = np.zeros((M, E), np.float32)
+    lib().orc_ffn_fwd(_p(X), _p(W1), _p(W2), _p(pre), _p(act), _p(Y), _sz(M), _sz(E), _sz(F),
+                      ctypes.c_int(nthreads))
+    return pre, act, Y
+
+
+def ffn_bwd(X, W1, W2, act, G, dY, M, E, F, dW1=None, dW2=None, nthreads=8):
+    """Expander FFN backward (two_stage_gpt.hpp:177-183): returns dX, dW1, dW2
+    (the weight gradients accumulate onto dW1 / dW2 when given)."""
+    X, W1, W2, act, G, dY = (_c(a) for a in (X, W1, W2, act, G, dY))
+    dX = np.zeros((M, E), np.float32)
+    dW1 = np.zeros((F, E), np.float32) if dW1 is None else _c(dW1).copy()
+    dW2 = np.zeros((E, F), np.float32) if dW2 is None else _c(dW2).copy()
+    lib().orc_ffn_bwd(_p(X), _p(W1), _p(W2), _p(act), _p(G), _p(dY), _p(dX), _p(dW1), _p(dW2),
+                      _sz(M), _sz(E), _sz(F), ctypes.c_int(nthreads))
+    return dX, dW1, dW2
+
+
 def gelu_exact_deriv(A):
     """two_stage_cuda_kernels.cu:1906-1914 (gelu_exact_deriv_kernel)."""
     A = _c(A)

@@ -21,6 +21,8 @@ oracle is pinned by:
 """
 import os
 
+import math
+
 import numpy as np
 import pytest
 
@@ -444,3 +446,70 @@ def test_gelu_planted_mistakes_are_caught():
     wrong_scale = np.array([0.5 * v * (1.0 + erf(v * 0.5)) for v in x])
     for bad in (tanh_form, wrong_scale):
         assert not np.allclose(bad, ref, rtol=2e-6, atol=2e-7)
+
+
+# ------------------------------------------------------------ expander FFN
+def _ffn_inputs(M, E, F, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((M, E)).astype(np.float32)
+    W1 = (rng.standard_normal((F, E)) * np.sqrt(2.0 / E)).astype(np.float32)   # gpt_gpt.hpp:79
+    W2 = (rng.standard_normal((E, F)) * np.sqrt(2.0 / F)).astype(np.float32)
+    dY = rng.standard_normal((M, E)).astype(np.float32)
+    return X, W1, W2, dY
+
+
+def test_ffn_oracle_against_float64_and_autograd():
+    """orc_ffn_fwd / orc_ffn_bwd (two_stage_gpt.hpp:86-89, :177-183) against
+    float64 products and, with G = pre, float64 autograd of
+    L = sum(Y * dY), Y = gelu(X W1^T) W2^T (the true gradients); with G = act
+    (the reference's q/k/v call) the closed form dact = (dY W2) gelu'(act)."""
+    import torch
+    M, E, F = 37, 12, 40
+    X, W1, W2, dY = _ffn_inputs(M, E, F, 5)
+    pre, act, Y = orc.ffn_fwd(X, W1, W2, M, E, F)
+    pre64 = X.astype(float) @ W1.T.astype(float)
+    assert np.allclose(pre, pre64, rtol=1e-6, atol=1e-7)
+    assert np.allclose(act, _gelu64(pre64.ravel()).reshape(M, F), rtol=2e-6, atol=2e-7)
+    assert np.allclose(Y, act.astype(float) @ W2.T.astype(float), rtol=1e-6, atol=1e-7)
+
+    tX, tW1, tW2 = (torch.from_numpy(a.astype(np.float64)).requires_grad_() for a in (X, W1, W2))
+    tY = torch.nn.functional.gelu(tX @ tW1.T) @ tW2.T
+    (tY * torch.from_numpy(dY.astype(np.float64))).sum().backward()
+    dX, dW1, dW2 = orc.ffn_bwd(X, W1, W2, act, pre, dY, M, E, F)
+    for got, want in ((dX, tX.grad), (dW1, tW1.grad), (dW2, tW2.grad)):
+        assert np.allclose(got, want.numpy(), rtol=2e-5, atol=2e-6)
+
+    # reference's q/k/v form: gelu' at the GELU output; weight grads accumulate
+    W1g0 = np.full((F, E), 0.25, np.float32)
+    dX2, dW1b, dW2b = orc.ffn_bwd(X, W1, W2, act, act, dY, M, E, F, dW1=W1g0)
+    gd = np.array([0.5 * (1 + math.erf(v / math.sqrt(2))) + v * math.exp(-0.5 * v * v) /
+                   math.sqrt(2 * math.pi) for v in act.astype(float).ravel()]).reshape(M, F)
+    dact = (dY.astype(float) @ W2.astype(float)) * gd
+    assert np.allclose(dX2, dact @ W1.astype(float), rtol=2e-5, atol=2e-6)
+    assert np.allclose(dW1b, 0.25 + dact.T @ X.astype(float), rtol=2e-5, atol=2e-6)
+    assert np.allclose(dW2b, dW2, rtol=1e-6, atol=1e-7)
+    # the two G choices differ: a swapped argument would be caught above
+    assert not np.allclose(dX2, dX, rtol=1e-3, atol=1e-4)
+
+
+def test_ffn_planted_mistakes_are_caught():
+    """A transposed weight, a dropped gelu' factor and the tanh GELU each fail
+    the float64 autograd comparison used above."""
+    import torch
+    M, E, F = 24, 16, 16
+    X, W1, W2, dY = _ffn_inputs(M, E, F, 9)
+    tX, tW1, tW2 = (torch.from_numpy(a.astype(np.float64)).requires_grad_() for a in (X, W1, W2))
+    tY = torch.nn.functional.gelu(tX @ tW1.T) @ tW2.T
+    (tY * torch.from_numpy(dY.astype(np.float64))).sum().backward()
+    _, _, Y = orc.ffn_fwd(X, W1, W2, M, E, F)
+    assert np.allclose(Y, tY.detach().numpy(), rtol=1e-5, atol=1e-6)
+    Yt = orc.ffn_fwd(X, W1.T.copy(), W2, M, E, F)[2]
+    assert not np.allclose(Yt, tY.detach().numpy(), rtol=1e-3, atol=1e-4)
+    tanh_y = torch.nn.functional.gelu(tX @ tW1.T, approximate="tanh") @ tW2.T
+    assert not np.allclose(Y, tanh_y.detach().numpy(), rtol=1e-5, atol=1e-6)
+    pre = X.astype(float) @ W1.T.astype(float)
+    no_deriv = (dY.astype(float) @ W2.astype(float)) @ W1.astype(float)
+    assert not np.allclose(no_deriv, tX.grad.numpy(), rtol=1e-3, atol=1e-4)
+    dX = orc.ffn_bwd(X, W1, W2, orc.gelu_exact(pre.astype(np.float32)), pre.astype(np.float32),
+                     dY, M, E, F)[0]
+    assert np.allclose(dX, tX.grad.numpy(), rtol=2e-5, atol=2e-6)
