@@ -144,7 +144,7 @@ def attribute(cx, step, steps):
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "gelu", "gelu_deriv", "ffn_gemm",
-              "ffn_reduce"):
+              "ffn_fixup"):
         tot, cnt = cx.prof_query(n)
         if cnt:
             out[n] = (tot / cnt, cnt / steps)

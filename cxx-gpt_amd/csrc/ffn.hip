@@ -23,9 +23,14 @@
 // and a row-contiguous one its k-rows ([k][row], stride 132).  The MFMA takes
 // the B fragment as its first operand, so a lane's accumulator holds four
 // consecutive columns of one row of C and every epilogue access is 16 bytes.
-// Shapes whose tile count leaves most compute units idle (N = E = 768 at
-// M = 2048) split K over workgroups: partial tiles go to a workspace and a
-// reduction applies the epilogue.
+// Work is spread stream-K: two workgroups per compute unit, each taking an
+// equal run of (tile, k-tile) units in tile-major order, so every shape keeps
+// every unit equally busy (a tile count just above the unit count would
+// otherwise leave most units idle for a second round).  A run computes whole
+// tiles straight into C with the epilogue; a tile cut by a run boundary is
+// left as partial tiles in the workspace (at most two per run, no waiting on
+// other workgroups) and a fix-up kernel sums them in run order and applies
+// the epilogue.
 //
 // Requires E, F multiples of 4 and 16-byte aligned tensors (checked at the C
 // ABI); any M.
@@ -49,13 +54,30 @@ struct GemmArgs {
     float* C;
     const float* G;
     float* pre;
+    float* part;       // 2 * P partial tiles of GT * GT floats (slot 0, 1 per workgroup)
     long lda, ldb, ldc;
     int M, N, K;
     int tn;            // tiles along N
-    int tiles;         // tiles per split
-    int ktp;           // k-tiles per split
-    long sstride;      // floats between split partials (0: no split)
+    int T;             // tiles
+    int KT;            // k-tiles per tile
+    int P;             // workgroups
+    long U;            // T * KT units
 };
+
+// Stream-K partition: the U (tile, k-tile) units, tile-major, are cut into P
+// contiguous runs of equal length; run w is [sk_begin(w), sk_begin(w + 1)).
+__host__ __device__ inline long sk_begin(long U, int P, int w) { return U * w / P; }
+
+// The workgroup whose run holds unit u.
+__device__ inline int sk_owner(long U, int P, long u)
+{
+    int w = (int)(u * P / U);
+    while (w + 1 < P && sk_begin(U, P, w + 1) <= u)
+        w++;
+    while (w > 0 && sk_begin(U, P, w) > u)
+        w--;
+    return w;
+}
 
 // Epilogue for four consecutive columns of one row of C at element offset off.
 template <int EPI>
@@ -140,92 +162,128 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
 {
     __shared__ __attribute__((aligned(16))) float lds[2][2][OPF];   // [stage][A, B]
 
-    const int split = blockIdx.x / a.tiles;
-    const int tile = blockIdx.x - split * a.tiles;
-    const int m0 = (tile / a.tn) * GT;
-    const int n0 = (tile % a.tn) * GT;
-    const int kt0 = split * a.ktp;
-    const int nkt = min(a.ktp, (a.K + GKT - 1) / GKT - kt0);
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
 
-    f4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            acc[i][j] = f4zero();
+    const long ub = sk_begin(a.U, a.P, blockIdx.x);
+    const long ue = sk_begin(a.U, a.P, blockIdx.x + 1);
+    for (long u = ub; u < ue;) {
+        // segment: k-tiles [ka, kb) of tile t
+        const int t = (int)(u / a.KT);
+        const int ka = (int)(u - (long)t * a.KT);
+        const int kb = (int)min((long)a.KT, (long)ka + (ue - u));
+        const int m0 = (t / a.tn) * GT;
+        const int n0 = (t % a.tn) * GT;
+        const int nkt = kb - ka;
 
-    f4 ra[4], rb[4];
-    tile_fetch<AK>(a.A, a.lda, m0, a.M, kt0 * GKT, a.K, ra);
-    tile_fetch<BK>(a.B, a.ldb, n0, a.N, kt0 * GKT, a.K, rb);
-    tile_put<AK>(lds[0][0], ra);
-    tile_put<BK>(lds[0][1], rb);
-    __syncthreads();
-
-    for (int kt = 0; kt < nkt; kt++) {
-        const int st = kt & 1;
-        // Next k-tile in flight during this one's MFMAs (past the split's end
-        // it reads valid memory that is never used).
-        tile_fetch<AK>(a.A, a.lda, m0, a.M, (kt0 + kt + 1) * GKT, a.K, ra);
-        tile_fetch<BK>(a.B, a.ldb, n0, a.N, (kt0 + kt + 1) * GKT, a.K, rb);
-        const float* LA = lds[st][0];
-        const float* LB = lds[st][1];
+        f4 acc[4][4];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            f4 fa[4], fb[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                fa[i] = frag<AK>(LA, wm + 16 * i, h, l16, g);
+        for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                fb[j] = frag<BK>(LB, wn + 16 * j, h, l16, g);
+                acc[i][j] = f4zero();
+
+        // (LDS is free here: the previous segment's last reads precede its
+        // final barrier.)
+        f4 ra[4], rb[4];
+        tile_fetch<AK>(a.A, a.lda, m0, a.M, ka * GKT, a.K, ra);
+        tile_fetch<BK>(a.B, a.ldb, n0, a.N, ka * GKT, a.K, rb);
+        tile_put<AK>(lds[0][0], ra);
+        tile_put<BK>(lds[0][1], rb);
+        __syncthreads();
+
+        for (int kt = 0; kt < nkt; kt++) {
+            const int st = kt & 1;
+            // Next k-tile in flight during this one's MFMAs (past the
+            // segment's end it reads valid memory that is never used).
+            tile_fetch<AK>(a.A, a.lda, m0, a.M, (ka + kt + 1) * GKT, a.K, ra);
+            tile_fetch<BK>(a.B, a.ldb, n0, a.N, (ka + kt + 1) * GKT, a.K, rb);
+            const float* LA = lds[st][0];
+            const float* LB = lds[st][1];
 #pragma unroll
-            for (int r = 0; r < 4; r++)
+            for (int h = 0; h < 2; h++) {
+                f4 fa[4], fb[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++)
+                    fa[i] = frag<AK>(LA, wm + 16 * i, h, l16, g);
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[i][j] = mfma16(fb[j][r], fa[i][r], acc[i][j]);
+                for (int j = 0; j < 4; j++)
+                    fb[j] = frag<BK>(LB, wn + 16 * j, h, l16, g);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            acc[i][j] = mfma16(fb[j][r], fa[i][r], acc[i][j]);
+            }
+            tile_put<AK>(lds[st ^ 1][0], ra);
+            tile_put<BK>(lds[st ^ 1][1], rb);
+            __syncthreads();
         }
-        tile_put<AK>(lds[st ^ 1][0], ra);
-        tile_put<BK>(lds[st ^ 1][1], rb);
-        __syncthreads();
-    }
 
-    // lane (l16, g), accumulator (i, j): row m0 + wm + 16i + l16, columns
-    // n0 + wn + 16j + 4g .. +3.
-    float* C = a.C + (long)split * a.sstride;
+        // lane (l16, g), accumulator (i, j): tile row wm + 16i + l16, columns
+        // wn + 16j + 4g .. +3.
+        if (ka == 0 && kb == a.KT) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = m0 + wm + 16 * i + l16;
+            for (int i = 0; i < 4; i++) {
+                const int row = m0 + wm + 16 * i + l16;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int col = n0 + wn + 16 * j + 4 * g;
-            if (row < a.M && col < a.N)
-                epi_apply<EPI>(acc[i][j], (long)row * a.ldc + col, C, a.G, a.pre);
+                for (int j = 0; j < 4; j++) {
+                    const int col = n0 + wn + 16 * j + 4 * g;
+                    if (row < a.M && col < a.N)
+                        epi_apply<EPI>(acc[i][j], (long)row * a.ldc + col, a.C, a.G, a.pre);
+                }
+            }
+        } else {
+            // A piece of a tile shared with neighbouring runs: slot 0 if it
+            // opens this run, else slot 1 (then it closes the run).
+            float* P = a.part + ((long)2 * blockIdx.x + (u == ub ? 0 : 1)) * (GT * GT);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    *reinterpret_cast<f4*>(P + (wm + 16 * i + l16) * GT + wn + 16 * j + 4 * g) =
+                        acc[i][j];
         }
+        u += nkt;
     }
 }
 
-// C = epilogue(sum over splits of P[s]), rows of N floats with stride ldc.
+// Tiles whose units span more than one run: sum the pieces in run order and
+// apply the epilogue.  One workgroup per tile; whole tiles return at once.
 template <int EPI>
-__global__ __launch_bounds__(256) void ffn_reduce_kernel(const float* __restrict__ P, int splits,
-                                                         long sstride, int M, int N, float* C,
-                                                         long ldc, const float* G, float* pre)
+__global__ __launch_bounds__(256) void ffn_fixup_kernel(GemmArgs a)
 {
-    const long n4 = (long)M * (N / 4);
-    const long stride = (long)gridDim.x * 256;
-    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
-        const long row = i / (N / 4);
-        const long col = (i - row * (N / 4)) * 4;
-        const long off = row * N + col;
-        f4 v = *reinterpret_cast<const f4*>(P + off);
-        for (int s = 1; s < splits; s++)
-            v += *reinterpret_cast<const f4*>(P + s * sstride + off);
-        epi_apply<EPI>(v, row * ldc + col, C, G, pre);
+    const int t = blockIdx.x;
+    const long u0 = (long)t * a.KT;
+    const int wa = sk_owner(a.U, a.P, u0);
+    const int wb = sk_owner(a.U, a.P, u0 + a.KT - 1);
+    if (wa == wb)
+        return;
+    // thread's float4s: q = threadIdx.x + 256 e, tile row q / 32, column 4 (q % 32)
+    f4 v[GT * GT / 1024];
+#pragma unroll
+    for (int e = 0; e < GT * GT / 1024; e++)
+        v[e] = f4zero();
+    for (int w = wa; w <= wb; w++) {
+        const long b = sk_begin(a.U, a.P, w);
+        if (sk_begin(a.U, a.P, w + 1) == b)
+            continue;   // empty run
+        const float* src = a.part + ((long)2 * w + (b >= u0 ? 0 : 1)) * (GT * GT);
+#pragma unroll
+        for (int e = 0; e < GT * GT / 1024; e++)
+            v[e] += *reinterpret_cast<const f4*>(src + (threadIdx.x + 256 * e) * 4);
+    }
+    const int m0 = (t / a.tn) * GT;
+    const int n0 = (t % a.tn) * GT;
+#pragma unroll
+    for (int e = 0; e < GT * GT / 1024; e++) {
+        const int q = threadIdx.x + 256 * e;
+        const int row = m0 + (q >> 5), col = n0 + (q & 31) * 4;
+        if (row < a.M && col < a.N)
+            epi_apply<EPI>(v[e], (long)row * a.ldc + col, a.C, a.G, a.pre);
     }
 }
 
@@ -237,22 +295,14 @@ static int dev_cus()
     return cus;
 }
 
-int ffn_gemm_splits(int M, int N, int K)
-{
-    const long tiles = (long)((M + GT - 1) / GT) * ((N + GT - 1) / GT);
-    const long slots = 2L * dev_cus();   // two workgroups per compute unit
-    const int ktiles = (K + GKT - 1) / GKT;
-    if (tiles >= slots / 2)
-        return 1;
-    int s = (int)std::min<long>(8, slots / tiles);
-    s = std::min(s, std::max(1, ktiles / 4));   // at least 4 k-tiles per split
-    return std::max(1, s);
-}
+// Two workgroups per compute unit (LDS and registers allow two; one alone
+// leaves the MFMA pipe idle half the time), or one per unit of work.
+static int sk_wgs(long U) { return (int)std::min<long>(2L * dev_cus(), U); }
 
 size_t ffn_gemm_ws_floats(int M, int N, int K)
 {
-    const int s = ffn_gemm_splits(M, N, K);
-    return s > 1 ? (size_t)s * M * N : 0;
+    const long U = (long)((M + GT - 1) / GT) * ((N + GT - 1) / GT) * ((K + GKT - 1) / GKT);
+    return (size_t)2 * sk_wgs(U) * GT * GT;
 }
 
 template <bool AK, bool BK>
@@ -273,73 +323,61 @@ static void launch_main(int epi, dim3 grid, hipStream_t st, const GemmArgs& a)
     }
 }
 
+template <int EPI>
+static void launch_fixup(dim3 grid, hipStream_t st, const GemmArgs& a)
+{
+    hipLaunchKernelGGL((ffn_fixup_kernel<EPI>), grid, dim3(256), 0, st, a);
+}
+
 hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st)
 {
     if (op.M <= 0 || op.N <= 0 || op.K <= 0)
         return hipSuccess;
-    if (!op.ak && op.bk)
+    if ((!op.ak && op.bk) || ws == nullptr)
         return hipErrorInvalidValue;   // no caller needs A row-contiguous with B k-contiguous
-    const int s = ffn_gemm_splits(op.M, op.N, op.K);
-    if (s > 1 && ws == nullptr)
-        return hipErrorInvalidValue;
-    const int ktiles = (op.K + GKT - 1) / GKT;
     GemmArgs a;
     a.A = op.A;
     a.B = op.B;
+    a.C = op.C;
+    a.G = op.G;
+    a.pre = op.pre;
+    a.part = ws;
     a.lda = op.lda;
     a.ldb = op.ldb;
+    a.ldc = op.ldc;
     a.M = op.M;
     a.N = op.N;
     a.K = op.K;
     a.tn = (op.N + GT - 1) / GT;
-    a.tiles = ((op.M + GT - 1) / GT) * a.tn;
-    a.ktp = (ktiles + s - 1) / s;
-    const int used = (ktiles + a.ktp - 1) / a.ktp;   // splits that get k-tiles
-    a.G = op.G;
-    a.pre = op.pre;
-    int epi = op.epi;
-    if (used > 1) {
-        a.C = ws;
-        a.ldc = op.N;
-        a.sstride = (long)op.M * op.N;
-        epi = FFN_EPI_STORE;
-    } else {
-        a.C = op.C;
-        a.ldc = op.ldc;
-        a.sstride = 0;
-    }
-    const dim3 grid((unsigned)(a.tiles * used));
+    a.T = ((op.M + GT - 1) / GT) * a.tn;
+    a.KT = (op.K + GKT - 1) / GKT;
+    a.U = (long)a.T * a.KT;
+    a.P = sk_wgs(a.U);
     {
         ProfScope ps(st, "ffn_gemm");
+        const dim3 grid((unsigned)a.P);
         if (op.ak && op.bk)
-            launch_main<true, true>(epi, grid, st, a);
+            launch_main<true, true>(op.epi, grid, st, a);
         else if (op.ak)
-            launch_main<true, false>(epi, grid, st, a);
+            launch_main<true, false>(op.epi, grid, st, a);
         else
-            launch_main<false, false>(epi, grid, st, a);
+            launch_main<false, false>(op.epi, grid, st, a);
     }
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || used == 1)
+    if (e != hipSuccess)
         return e;
-    const long want = ((long)op.M * (op.N / 4) + 255) / 256;
-    const unsigned blocks = (unsigned)std::max(1L, std::min(want, 8L * dev_cus()));
-    ProfScope ps(st, "ffn_reduce");
+    bool split = false;   // does any run boundary fall inside a tile?
+    for (int w = 1; w < a.P && !split; w++)
+        split = sk_begin(a.U, a.P, w) % a.KT != 0;
+    if (!split)
+        return hipSuccess;
+    ProfScope ps(st, "ffn_fixup");
+    const dim3 grid((unsigned)a.T);
     switch (op.epi) {
-    case FFN_EPI_GELU:
-        hipLaunchKernelGGL((ffn_reduce_kernel<FFN_EPI_GELU>), dim3(blocks), dim3(256), 0, st, ws,
-                           used, a.sstride, op.M, op.N, op.C, op.ldc, op.G, op.pre);
-        break;
-    case FFN_EPI_DGELU:
-        hipLaunchKernelGGL((ffn_reduce_kernel<FFN_EPI_DGELU>), dim3(blocks), dim3(256), 0, st, ws,
-                           used, a.sstride, op.M, op.N, op.C, op.ldc, op.G, op.pre);
-        break;
-    case FFN_EPI_ACCUM:
-        hipLaunchKernelGGL((ffn_reduce_kernel<FFN_EPI_ACCUM>), dim3(blocks), dim3(256), 0, st, ws,
-                           used, a.sstride, op.M, op.N, op.C, op.ldc, op.G, op.pre);
-        break;
-    default:
-        hipLaunchKernelGGL((ffn_reduce_kernel<FFN_EPI_STORE>), dim3(blocks), dim3(256), 0, st, ws,
-                           used, a.sstride, op.M, op.N, op.C, op.ldc, op.G, op.pre);
+    case FFN_EPI_GELU: launch_fixup<FFN_EPI_GELU>(grid, st, a); break;
+    case FFN_EPI_DGELU: launch_fixup<FFN_EPI_DGELU>(grid, st, a); break;
+    case FFN_EPI_ACCUM: launch_fixup<FFN_EPI_ACCUM>(grid, st, a); break;
+    default: launch_fixup<FFN_EPI_STORE>(grid, st, a);
     }
     return hipGetLastError();
 }

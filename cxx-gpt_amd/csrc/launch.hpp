@@ -74,7 +74,7 @@ hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t
 // DGELU C = acc * gelu'(G) (G indexed like C); ACCUM C += acc.
 // N % 4 == 0; a k-contiguous operand needs K % 4 == 0, a row-contiguous one
 // its row count % 4 == 0; all tensors 16-byte aligned, strides % 4 == 0.
-// ws: ffn_gemm_ws_floats(M, N, K) floats when that is nonzero (split K).
+// ws: ffn_gemm_ws_floats(M, N, K) floats (partial tiles).
 enum { FFN_EPI_STORE = 0, FFN_EPI_GELU = 1, FFN_EPI_DGELU = 2, FFN_EPI_ACCUM = 3 };
 struct FfnGemm {
     const float* A;
@@ -90,7 +90,6 @@ struct FfnGemm {
     const float* G;
     float* pre;
 };
-int ffn_gemm_splits(int M, int N, int K);
 size_t ffn_gemm_ws_floats(int M, int N, int K);
 hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st);
 
