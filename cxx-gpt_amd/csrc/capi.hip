@@ -292,13 +292,25 @@ int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, f
         return st;
     if (!Q || !K || !V || !O)
         return CXG_ERR_NULL;
-    return hip_status(mha_wide_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, 1, (int)E,
-                                          (hipStream_t)stream));
+    hipStream_t s = (hipStream_t)stream;
+    Scratch ws;   // split-KV partial states (few-job shapes), stream-ordered
+    st = ws.acquire(nullptr, 0, mha_wide_fwd_ws_floats((int)B, (int)S) * sizeof(float), s);
+    if (st != CXG_OK)
+        return st;
+    return hip_status(
+        mha_wide_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, 1, (int)E, (float*)ws.p, s));
 }
 
 size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
 {
-    return cxg_mha_bwd_workspace_size(B, S, 1, E);
+    if (E <= 256)
+        return cxg_mha_bwd_workspace_size(B, S, 1, E);
+    bool empty;
+    if (gpt_check(B, S, E, &empty) != CXG_OK || empty)
+        return 0;
+    // Di, lse, and the split-KV records of the statistics pass
+    return 2 * round_up(B * S * sizeof(float), 256) +
+           round_up(mha_wide_fwd_ws_floats((int)B, (int)S) * sizeof(float), 256);
 }
 
 int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float* O,
@@ -323,15 +335,16 @@ int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float
         return st;
     float* Di = (float*)ws.p;
     float* lse_ws = (float*)((char*)ws.p + half);
+    float* part = (float*)((char*)ws.p + 2 * half);
     const int iB = (int)B, iS = (int)S, iE = (int)E;
     hipError_t e;
     if (lse == nullptr) {
-        e = mha_wide_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, 1, iE, s);
+        e = mha_wide_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, 1, iE, part, s);
         if (e != hipSuccess)
             return hip_status(e);
         lse = lse_ws;
     }
-    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, 1, iE, s);
+    e = mha_bwd_prep_launch(O, dO, Di, nullptr, iB, iS, 1, iE, s);   // dQ is stored outright
     if (e != hipSuccess)
         return hip_status(e);
     return hip_status(mha_wide_bwd_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, 1, iE, s));

@@ -58,8 +58,12 @@ hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
 // Causal softmax attention for 256 < Dh <= 512 (same layout, lse and backward
 // contract as the launchers above; O may be null: statistics only).
 constexpr int MHA_WIDE_MAX_DH = 512;
+// Split-KV partial records for few-job shapes: mha_wide_fwd_ws_floats(B*H, S)
+// floats at `part` (0: no split, part may be null).
+size_t mha_wide_fwd_ws_floats(int BH, int S);
 hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
-                               float* lse, int B, int S, int H, int Dh, hipStream_t st);
+                               float* lse, int B, int S, int H, int Dh, float* part,
+                               hipStream_t st);
 hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
                                float* dV, int B, int S, int H, int Dh, hipStream_t st);

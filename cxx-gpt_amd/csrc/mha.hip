@@ -544,25 +544,29 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
 // backward pre-pass: Di = rowsum(dO * O) (the reference's gs, kernel_test.cpp:76-78)
 // and dQ = 0.  16 lanes per (row, head) segment.
 // ----------------------------------------------------------------------------
-template <bool VEC>
+template <bool VEC, bool ZERO, int TPR>
 __global__ __launch_bounds__(256) void mha_bwd_prep_kernel(
     const float* __restrict__ O, const float* __restrict__ dO, float* __restrict__ Di,
     float* __restrict__ dQ, int S, int H, int Dh, long nseg)
 {
-    const long seg = ((long)blockIdx.x * 256 + threadIdx.x) >> 4;
-    const int sub = threadIdx.x & 15;
+    // TPR threads per (row, head) segment: 16, or a whole wave for wide heads
+    const long seg = ((long)blockIdx.x * 256 + threadIdx.x) / TPR;
+    const int sub = threadIdx.x & (TPR - 1);
     const bool ok = seg < nseg;
     float acc = 0.0f;
     if (ok) {
         const long off = seg * Dh;   // segment (b*S + s)*H + h starts at seg*Dh
-        for (int c = 4 * sub; c < Dh; c += 64) {
+        for (int c = 4 * sub; c < Dh; c += 4 * TPR) {
             const f4 o = load4<VEC>(O + off, c, Dh, true);
             const f4 d = load4<VEC>(dO + off, c, Dh, true);
             acc += o[0] * d[0] + o[1] * d[1] + o[2] * d[2] + o[3] * d[3];
-            store4<VEC>(dQ + off, c, Dh, f4zero());
+            if (ZERO)
+                store4<VEC>(dQ + off, c, Dh, f4zero());
         }
     }
     acc = row16_sum(acc);
+    if (TPR == 64)
+        acc = xrow_sum(acc);
     if (ok && sub == 0) {
         const long row = seg / H;
         const int h = (int)(seg - row * H);
@@ -1172,19 +1176,40 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
     return fwd_dispatch<256>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
 }
 
+template <bool VEC, bool ZERO>
+static void prep_go(bool wide, long nseg, const float* O, const float* dO, float* Di, float* dQ,
+                    int S, int H, int Dh, hipStream_t st)
+{
+    const int tpr = wide ? 64 : 16;
+    dim3 grid((unsigned)((nseg * tpr + 255) / 256)), block(256);
+    if (wide)
+        hipLaunchKernelGGL((mha_bwd_prep_kernel<VEC, ZERO, 64>), grid, block, 0, st, O, dO, Di,
+                           dQ, S, H, Dh, nseg);
+    else
+        hipLaunchKernelGGL((mha_bwd_prep_kernel<VEC, ZERO, 16>), grid, block, 0, st, O, dO, Di,
+                           dQ, S, H, Dh, nseg);
+}
+
+// Di = rowsum(O * dO) per (row, head); dQ zeroed for the atomic backward
+// (dQ == nullptr: not touched, for kernels that store dQ outright).
 hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ, int B,
                                int S, int H, int Dh, hipStream_t st)
 {
     const long nseg = (long)B * S * H;
-    dim3 grid((unsigned)((nseg * 16 + 255) / 256)), block(256);
+    const bool wide = Dh > 256;
     ProfScope ps(st, "mha_bwd_prep");
     const bool vec = (Dh % 4 == 0) && aligned16(O) && aligned16(dO) && aligned16(dQ);
-    if (vec)
-        hipLaunchKernelGGL((mha_bwd_prep_kernel<true>), grid, block, 0, st, O, dO, Di, dQ, S, H,
-                           Dh, nseg);
-    else
-        hipLaunchKernelGGL((mha_bwd_prep_kernel<false>), grid, block, 0, st, O, dO, Di, dQ, S,
-                           H, Dh, nseg);
+    if (vec) {
+        if (dQ)
+            prep_go<true, true>(wide, nseg, O, dO, Di, dQ, S, H, Dh, st);
+        else
+            prep_go<true, false>(wide, nseg, O, dO, Di, dQ, S, H, Dh, st);
+    } else {
+        if (dQ)
+            prep_go<false, true>(wide, nseg, O, dO, Di, dQ, S, H, Dh, st);
+        else
+            prep_go<false, false>(wide, nseg, O, dO, Di, dQ, S, H, Dh, st);
+    }
     return hipGetLastError();
 }
 

@@ -22,6 +22,12 @@
 #include "common.hpp"
 #include "launch.hpp"
 
+#include <algorithm>
+#include <functional>
+#include <queue>
+#include <unordered_map>
+#include <vector>
+
 namespace cxg {
 
 constexpr int WB = 16;                 // rows per tile (queries and keys)
@@ -61,21 +67,43 @@ __device__ __forceinline__ void wide_store(float* __restrict__ dst, const WideRe
 }
 
 // ---------------------------------------------------------------------------
-// forward: job = (bh, 16-query block), heaviest (latest) blocks first.
+// forward: job = (bh, 16-query block, chunk of key blocks), latest query
+// blocks first.  With few jobs (B*H*nqb well under two per compute unit) a
+// query block's key blocks are cut into chunks of C (split-KV), so that the
+// last blocks of a sequence, which see every key, do not set the kernel's
+// length alone; a chunked block's jobs leave unnormalised partial states
+// (o, m, l) in a workspace and mha_wide_merge_kernel combines them.
+// C >= nqb: one chunk per query block, written directly.
 // ---------------------------------------------------------------------------
+constexpr int WREC = WB * WIDE_DHP + 2 * WB;   // partial record: o[16][512], m[16], l[16]
+
+__host__ __device__ inline int wide_nch(int qb, int C) { return (qb + C) / C; }
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, float qscale)
+    float* __restrict__ O, float* __restrict__ lse, float* __restrict__ part, int S, int H,
+    int Dh, int BH, int C, float qscale)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 4 * 256];
     float* Sp = lds + 4 * WB * WLD;   // partial scores [wave][lane * 4 + r]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int nqb = (S + WB - 1) / WB;
-    const int BH = gridDim.x / nqb;
-    const int qb = nqb - 1 - (int)(blockIdx.x / BH);
+    const int ent = (int)(blockIdx.x / BH);
     const int bh = (int)(blockIdx.x % BH);
+    int qb = nqb - 1 - ent, ch = 0;
+    if (C < nqb) {   // entries: query blocks from the last, each as its chunks
+        qb = nqb - 1;
+        ch = ent;
+        while (ch >= wide_nch(qb, C)) {
+            ch -= wide_nch(qb, C);
+            qb--;
+        }
+    }
+    const bool chunked = C < nqb && wide_nch(qb, C) > 1;
+    const int kb0 = C < nqb ? ch * C : 0;
+    const int kb1 = C < nqb ? min(qb + 1, kb0 + C) : qb + 1;
     const int b = bh / H, h = bh - b * H;
     const long ld = (long)H * Dh;
     const long hoff = (long)b * S * ld + (long)h * Dh;
@@ -98,16 +126,16 @@ __global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
     // key blocks are fetched one ahead into registers and stored to the
     // double-buffered LDS tiles at the top of their step
     WideRegs kr, vr;
-    wide_fetch<VEC>(kr, K + hoff, ld, 0, S, Dh, tid);
-    wide_fetch<VEC>(vr, V + hoff, ld, 0, S, Dh, tid);
-    for (int kb = 0; kb <= qb; kb++) {
+    wide_fetch<VEC>(kr, K + hoff, ld, kb0 * WB, S, Dh, tid);
+    wide_fetch<VEC>(vr, V + hoff, ld, kb0 * WB, S, Dh, tid);
+    for (int kb = kb0; kb < kb1; kb++) {
         const int k0 = kb * WB;
-        float* Ks = lds + (kb & 1) * 2 * WB * WLD;
+        float* Ks = lds + ((kb - kb0) & 1) * 2 * WB * WLD;
         float* Vs = Ks + WB * WLD;
         wide_store(Ks, kr, Dh, tid);
         wide_store(Vs, vr, Dh, tid);
         __builtin_amdgcn_sched_barrier(0);
-        const int kn = min(kb + 1, qb) * WB;   // the last step refetches its own block
+        const int kn = min(kb + 1, kb1 - 1) * WB;   // the last step refetches its own block
         wide_fetch<VEC>(kr, K + hoff, ld, kn, S, Dh, tid);
         wide_fetch<VEC>(vr, V + hoff, ld, kn, S, Dh, tid);
         __syncthreads();
@@ -160,7 +188,16 @@ __global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
             o[t] = a;
         }
     }
-    if (qi < S) {
+    if (chunked) {
+        float* rec = part + (long)blockIdx.x * WREC;
+#pragma unroll
+        for (int t = 0; t < WNT; t++)
+            *reinterpret_cast<f4*>(&rec[l16 * WIDE_DHP + c0 + 16 * t + 4 * g]) = o[t];
+        if (w == 0 && g == 0) {
+            rec[WB * WIDE_DHP + l16] = m_run;
+            rec[WB * WIDE_DHP + WB + l16] = l_run;
+        }
+    } else if (qi < S) {
         const float inv = 1.0f / l_run;
         if (O != nullptr) {
             float* orow = O + hoff + (long)qi * ld;
@@ -342,23 +379,191 @@ __global__ __launch_bounds__(256) void mha_wide_bwd_kernel(
 
 // ---------------------------------------------------------------------------
 // launchers
+// Combine the chunks of every chunked query block: M = max m_c,
+// L = sum 2^(m_c - M) l_c, O = sum 2^(m_c - M) o_c / L, lse = (M + log2 L) ln 2.
+// Workgroup (query block, bh, column quarter); 16 threads form the per-row
+// chunk weights 2^(m_c - M) / L in LDS, then each thread sums two float4
+// columns of one row over the chunks.  Unchunked blocks return at once.
+constexpr int WIDE_MAXCH = 256;   // chunks per query block: nqb < 512 and C >= 2 when split
+
+__global__ __launch_bounds__(256) void mha_wide_merge_kernel(const float* __restrict__ part,
+                                                            float* __restrict__ O,
+                                                            float* __restrict__ lse, int S,
+                                                            int H, int Dh, int BH, int C)
+{
+    __shared__ float wsh[WB][WIDE_MAXCH];
+    const int nqb = (S + WB - 1) / WB;
+    const int quarter = (int)(blockIdx.x & 3);
+    const int job = (int)(blockIdx.x >> 2);
+    const int qb = job / BH, bh = job - (job / BH) * BH;
+    const int nch = wide_nch(qb, C);
+    if (nch == 1)
+        return;
+    int e0 = 0;   // entry of the block's first chunk
+    for (int q = nqb - 1; q > qb; q--)
+        e0 += wide_nch(q, C);
+    const float* rec0 = part + ((long)e0 * BH + bh) * WREC;
+    const long cstride = (long)BH * WREC;   // between a block's consecutive chunks
+    const int tid = threadIdx.x;
+    if (tid < WB) {
+        float M = -INFINITY;
+        for (int j = 0; j < nch; j++)
+            M = fmaxf(M, rec0[j * cstride + WB * WIDE_DHP + tid]);
+        float L = 0.0f;
+        for (int j = 0; j < nch; j++) {
+            const float wgt = fast_exp2(rec0[j * cstride + WB * WIDE_DHP + tid] - M);
+            wsh[tid][j] = wgt;
+            L += wgt * rec0[j * cstride + WB * WIDE_DHP + WB + tid];
+        }
+        const float inv = 1.0f / L;
+        for (int j = 0; j < nch; j++)
+            wsh[tid][j] *= inv;
+        const int qi = qb * WB + tid;
+        if (lse != nullptr && quarter == 0 && qi < S)
+            lse[(long)bh * S + qi] = (M + fast_log2(L)) * kLn2;
+    }
+    __syncthreads();
+    if (O == nullptr)
+        return;
+    const int row = tid >> 4;
+    const int c0 = quarter * (WIDE_DHP / 4) + 4 * (tid & 15), c1 = c0 + 64;
+    f4 a0 = f4zero(), a1 = f4zero();
+    for (int j = 0; j < nch; j++) {
+        const float* rec = rec0 + j * cstride + row * WIDE_DHP;
+        const float wgt = wsh[row][j];
+        a0 += *reinterpret_cast<const f4*>(rec + c0) * wgt;
+        a1 += *reinterpret_cast<const f4*>(rec + c1) * wgt;
+    }
+    const int qi = qb * WB + row;
+    if (qi >= S)
+        return;
+    const int b = bh / H, h = bh - b * H;
+    const long ld = (long)H * Dh;
+    float* orow = O + (long)b * S * ld + (long)h * Dh + (long)qi * ld;
+    const bool vec = Dh % 4 == 0 && (((uintptr_t)orow & 15u) == 0);
+    for (int k = 0; k < 2; k++) {
+        const int c = k ? c1 : c0;
+        const f4 v = k ? a1 : a0;
+        if (c >= Dh)
+            continue;
+        if (vec) {
+            *reinterpret_cast<f4*>(orow + c) = v;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (c + i < Dh)
+                    orow[c + i] = v[i];
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 static inline bool al16w(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
-hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
-                               float* lse, int B, int S, int H, int Dh, hipStream_t st)
+// Key-block chunk for the forward: list-schedule the jobs (heaviest query
+// blocks first, one workgroup per compute unit, a job costing its key blocks
+// plus ~0.6 of a block of set-up) for a few chunk sizes, charging a split
+// for its merge, and keep the shortest.  Only when jobs are few: with two or
+// more whole query blocks per compute unit the plain grid balances itself.
+static int wide_fwd_chunk(int BH, int S)
 {
     const int nqb = (S + WB - 1) / WB;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if ((long)BH * nqb >= 2L * cus || nqb < 4)
+        return nqb;
+    // decisions cached per thread (the simulation is a few thousand heap steps)
+    static thread_local std::unordered_map<long long, int> cache;
+    const long long key = ((long long)BH << 40) ^ ((long long)S << 12) ^ cus;
+    auto hit = cache.find(key);
+    if (hit != cache.end())
+        return hit->second;
+    int best_c = nqb;
+    double best = 0.0;
+    bool first = true;
+    for (int C : {nqb, 2, 3, 4, 5, 6, 8, 12, 16}) {
+        if (!first && (C >= nqb || wide_nch(nqb - 1, C) > WIDE_MAXCH))
+            continue;
+        std::priority_queue<double, std::vector<double>, std::greater<double>> freeq;
+        for (int i = 0; i < cus; i++)
+            freeq.push(0.0);
+        long parts = 0;
+        for (int qb = nqb - 1; qb >= 0; qb--) {
+            const int nch = C < nqb ? wide_nch(qb, C) : 1;
+            for (int c = 0; c < nch; c++) {
+                const int len = nch > 1 ? std::min(C, qb + 1 - c * C) : qb + 1;
+                for (int b = 0; b < BH; b++) {
+                    const double t = freeq.top();
+                    freeq.pop();
+                    freeq.push(t + len + 0.6);
+                }
+                if (nch > 1)
+                    parts += BH;
+            }
+        }
+        double t = 0.0;
+        while (!freeq.empty()) {
+            t = std::max(t, freeq.top());
+            freeq.pop();
+        }
+        if (C < nqb)
+            t += 1.0 + 0.1 * (double)parts / cus;   // merge launch and traffic
+        if (first || t < best) {
+            best = t;
+            best_c = C;
+        }
+        first = false;
+    }
+    cache[key] = best_c;
+    return best_c;
+}
+
+size_t mha_wide_fwd_ws_floats(int BH, int S)
+{
+    const int nqb = (S + WB - 1) / WB;
+    const int C = wide_fwd_chunk(BH, S);
+    if (C >= nqb)
+        return 0;
+    long nent = 0;
+    for (int qb = 0; qb < nqb; qb++)
+        nent += wide_nch(qb, C);
+    return (size_t)nent * BH * WREC;
+}
+
+hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                               float* lse, int B, int S, int H, int Dh, float* part,
+                               hipStream_t st)
+{
+    const int nqb = (S + WB - 1) / WB;
+    const int BH = B * H;
+    const int C = wide_fwd_chunk(BH, S);
+    if (C < nqb && part == nullptr)
+        return hipErrorInvalidValue;
+    long nent = nqb;
+    if (C < nqb) {
+        nent = 0;
+        for (int qb = 0; qb < nqb; qb++)
+            nent += wide_nch(qb, C);
+    }
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid((unsigned)((long)B * H * nqb)), block(256);
+    dim3 grid((unsigned)(nent * BH)), block(256);
     const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(O);
-    ProfScope ps(st, O != nullptr ? "mha_wide_fwd" : "mha_wide_stats");
-    if (vec)
-        hipLaunchKernelGGL(mha_wide_fwd_kernel<true>, grid, block, 0, st, Q, K, V, O, lse, S, H,
-                           Dh, qscale);
-    else
-        hipLaunchKernelGGL(mha_wide_fwd_kernel<false>, grid, block, 0, st, Q, K, V, O, lse, S, H,
-                           Dh, qscale);
+    {
+        ProfScope ps(st, O != nullptr ? "mha_wide_fwd" : "mha_wide_stats");
+        if (vec)
+            hipLaunchKernelGGL(mha_wide_fwd_kernel<true>, grid, block, 0, st, Q, K, V, O, lse,
+                               part, S, H, Dh, BH, C, qscale);
+        else
+            hipLaunchKernelGGL(mha_wide_fwd_kernel<false>, grid, block, 0, st, Q, K, V, O, lse,
+                               part, S, H, Dh, BH, C, qscale);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || C >= nqb)
+        return e;
+    ProfScope ps(st, "mha_wide_merge");
+    hipLaunchKernelGGL(mha_wide_merge_kernel, dim3((unsigned)((long)nqb * BH * 4)), block, 0, st,
+                       part, O, lse, S, H, Dh, BH, C);
     return hipGetLastError();
 }
 
