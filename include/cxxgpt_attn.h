@@ -94,7 +94,11 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * transposes).  Q, K, V, O (B*S, E) row-major; lse [B][S] natural log; the
  * same as cxg_mha_fwd / cxg_mha_bwd with H = 1, Dh = E, which serve E <= 256;
  * 256 < E <= 512 (the reference GPT's training configuration has E = 512)
- * takes wider-head kernels; CXG_ERR_HEAD_DIM above 512. */
+ * takes wider-head kernels; CXG_ERR_HEAD_DIM above 512.  There, shapes with
+ * few 16-row query blocks split the forward's key range over more
+ * workgroups and merge the partial softmax states: the forward then takes
+ * stream-ordered scratch for them, and cxg_gpt_attn_bwd_workspace_size
+ * counts them for the backward's statistics pass (lse == NULL). */
 int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
                      size_t B, size_t S, size_t E, cxg_stream_t stream);
 int cxg_gpt_attn_bwd(const float *Q, const float *K, const float *V, const float *O,
