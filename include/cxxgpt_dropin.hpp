@@ -155,6 +155,36 @@ void gelu_exact_deriv(const CT& A, CT& C)
 
 } // namespace two_stage_cuda
 
+// The two-stage block's expander FFN as one call each way: StageBlock's
+// q_ffn_fc.forward -> gelu_exact -> q_ffn_proj.forward (two_stage_gpt.hpp:86-89;
+// likewise k, v and the final FFN) and its backward (:177-183).  Not a
+// reference function: it replaces that call sequence.  X [M][E], W1 [F][E]
+// (the fc weight), W2 [E][F] (the proj weight); pre may be null; dW1/dW2
+// accumulate (Linear's W.grad +=); G is the tensor gelu' is evaluated at.
+namespace cxg_blocks {
+
+template <class CT>
+void expander_ffn_fwd(const CT& X, const CT& W1, const CT& W2, CT* pre, CT& act, CT& Y, size_t M,
+                      size_t E, size_t F)
+{
+    using namespace cxg_dropin;
+    check(cxg_ffn_fwd(cptr(X), cptr(W1), cptr(W2), pre ? mptr(*pre) : nullptr, mptr(act),
+                      mptr(Y), M, E, F, nullptr, 0, nullptr),
+          "expander_ffn_fwd");
+}
+
+template <class CT>
+void expander_ffn_bwd(const CT& X, const CT& W1, const CT& W2, const CT& act, const CT& G,
+                      const CT& dY, CT& dX, CT& dW1, CT& dW2, size_t M, size_t E, size_t F)
+{
+    using namespace cxg_dropin;
+    check(cxg_ffn_bwd(cptr(X), cptr(W1), cptr(W2), cptr(act), cptr(G), cptr(dY), mptr(dX),
+                      mptr(dW1), mptr(dW2), M, E, F, nullptr, 0, nullptr),
+          "expander_ffn_bwd");
+}
+
+} // namespace cxg_blocks
+
 namespace linear_cuda {
 
 // linear_cuda_kernels.cuh:11-16

@@ -199,6 +199,51 @@ static void rope_block()
     expect("rope roundtrip", t2v(cQ2.toTensor()), Q0);
 }
 
+// The two-stage block's q expander (two_stage_gpt.hpp:86-89, :177-183) through
+// cxg_blocks::expander_ffn_*, with gelu_exact / gelu_exact_deriv on its
+// pre-activation through two_stage_cuda::, against the C oracle.
+static void expander_block(size_t M, size_t E, size_t F)
+{
+    auto X = draw(M * E), W1 = draw(F * E), W2 = draw(E * F), dY = draw(M * E);
+    for (auto& w : W1)
+        w *= std::sqrt(3.0f / E);   // uniform[-1,1] scaled to Linear's kaiming variance 2/in
+    for (auto& w : W2)
+        w *= std::sqrt(3.0f / F);
+    auto cX = up(X, {M, E}), cW1 = up(W1, {F, E}), cW2 = up(W2, {E, F}), cdY = up(dY, {M, E});
+    CudaTensor<float> pre({M, F}), act({M, F}), Y({M, E});
+    cxg_blocks::expander_ffn_fwd(cX, cW1, cW2, &pre, act, Y, M, E, F);
+    std::vector<float> rpre(M * F), ract(M * F), rY(M * E);
+    orc_ffn_fwd(X.data(), W1.data(), W2.data(), rpre.data(), ract.data(), rY.data(), M, E, F, 8);
+    expect("ffn pre", t2v(pre.toTensor()), rpre);
+    expect("ffn act", t2v(act.toTensor()), ract);
+    expect("ffn Y", t2v(Y.toTensor()), rY);
+    // gelu_exact on the kept pre-activation is the epilogue's GELU, bit for bit
+    CudaTensor<float> act2({M, F}), gd({M, F});
+    two_stage_cuda::gelu_exact(pre, act2);
+    auto a1 = t2v(act.toTensor()), a2 = t2v(act2.toTensor());
+    size_t diff = 0;
+    for (size_t i = 0; i < a1.size(); i++)
+        diff += a1[i] != a2[i];
+    std::printf("%-22s %zu differing %s\n", "gelu_exact == epilogue", diff, diff ? "FAIL" : "ok");
+    g_fail += diff != 0;
+    auto gpre = t2v(pre.toTensor());
+    two_stage_cuda::gelu_exact_deriv(pre, gd);
+    std::vector<float> rgd(M * F);
+    orc_gelu_exact_deriv(gpre.data(), rgd.data(), M * F);
+    expect("gelu_exact_deriv", t2v(gd.toTensor()), rgd);
+    // backward with gelu' at the GELU output, as the q/k/v expanders call it
+    CudaTensor<float> dX({M, E}), dW1({F, E}), dW2({E, F});
+    dW1.memset_zero();
+    dW2.memset_zero();
+    cxg_blocks::expander_ffn_bwd(cX, cW1, cW2, act, act, cdY, dX, dW1, dW2, M, E, F);
+    std::vector<float> rdX(M * E), rdW1(F * E, 0.0f), rdW2(E * F, 0.0f);
+    orc_ffn_bwd(X.data(), W1.data(), W2.data(), a1.data(), a1.data(), dY.data(), rdX.data(),
+                rdW1.data(), rdW2.data(), M, E, F, 8);
+    expect("ffn dX", t2v(dX.toTensor()), rdX);
+    expect("ffn dW1", t2v(dW1.toTensor()), rdW1);
+    expect("ffn dW2", t2v(dW2.toTensor()), rdW2);
+}
+
 int main()
 {
     orc_mt_seed(&g_rng, 1234);   // kernel_test.cpp:12
@@ -212,6 +257,8 @@ int main()
     rope_block();
     // LinearGPT's path, which the reference's kernel test does not cover
     linear_gpt_block(2, 40, 48);
+    // the expander FFN with its GELU (n_embd 128, N = 2: F = 1024)
+    expander_block(40, 128, 1024);
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         std::printf("hip error %s\n", hipGetErrorString(e));
