@@ -252,35 +252,44 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
 }
 
 // Tiles whose units span more than one run: sum the pieces in run order and
-// apply the epilogue.  One workgroup per tile; whole tiles return at once.
+// apply the epilogue.  Four workgroups per tile (32 rows each, four float4
+// per thread, so the pieces' loads of many tiles are in flight at once);
+// whole tiles return at once.
 template <int EPI>
 __global__ __launch_bounds__(256) void ffn_fixup_kernel(GemmArgs a)
 {
-    const int t = blockIdx.x;
+    const int t = (int)(blockIdx.x >> 2), quarter = (int)(blockIdx.x & 3);
     const long u0 = (long)t * a.KT;
     const int wa = sk_owner(a.U, a.P, u0);
     const int wb = sk_owner(a.U, a.P, u0 + a.KT - 1);
     if (wa == wb)
         return;
-    // thread's float4s: q = threadIdx.x + 256 e, tile row q / 32, column 4 (q % 32)
-    f4 v[GT * GT / 1024];
+    // thread's float4s: q = quarter * 1024 + threadIdx.x + 256 e: tile row q / 32,
+    // column 4 (q % 32)
+    constexpr int NE = GT * GT / 4 / 4 / 256;
+    f4 v[NE];
 #pragma unroll
-    for (int e = 0; e < GT * GT / 1024; e++)
+    for (int e = 0; e < NE; e++)
         v[e] = f4zero();
     for (int w = wa; w <= wb; w++) {
         const long b = sk_begin(a.U, a.P, w);
         if (sk_begin(a.U, a.P, w + 1) == b)
             continue;   // empty run
-        const float* src = a.part + ((long)2 * w + (b >= u0 ? 0 : 1)) * (GT * GT);
+        const float* src = a.part + ((long)2 * w + (b >= u0 ? 0 : 1)) * (GT * GT) +
+                           (long)quarter * (GT * GT / 4);
+        f4 x[NE];
 #pragma unroll
-        for (int e = 0; e < GT * GT / 1024; e++)
-            v[e] += *reinterpret_cast<const f4*>(src + (threadIdx.x + 256 * e) * 4);
+        for (int e = 0; e < NE; e++)
+            x[e] = *reinterpret_cast<const f4*>(src + (threadIdx.x + 256 * e) * 4);
+#pragma unroll
+        for (int e = 0; e < NE; e++)
+            v[e] += x[e];
     }
     const int m0 = (t / a.tn) * GT;
     const int n0 = (t % a.tn) * GT;
 #pragma unroll
-    for (int e = 0; e < GT * GT / 1024; e++) {
-        const int q = threadIdx.x + 256 * e;
+    for (int e = 0; e < NE; e++) {
+        const int q = quarter * (GT * GT / 16) + threadIdx.x + 256 * e;
         const int row = m0 + (q >> 5), col = n0 + (q & 31) * 4;
         if (row < a.M && col < a.N)
             epi_apply<EPI>(v[e], (long)row * a.ldc + col, a.C, a.G, a.pre);
@@ -372,7 +381,7 @@ hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st)
     if (!split)
         return hipSuccess;
     ProfScope ps(st, "ffn_fixup");
-    const dim3 grid((unsigned)a.T);
+    const dim3 grid((unsigned)a.T * 4);
     switch (op.epi) {
     case FFN_EPI_GELU: launch_fixup<FFN_EPI_GELU>(grid, st, a); break;
     case FFN_EPI_DGELU: launch_fixup<FFN_EPI_DGELU>(grid, st, a); break;
