@@ -18,7 +18,10 @@
 // lane owns a query row: its online-softmax state is per lane).  The backward
 // runs key-block jobs (dK, dV) and query-block jobs (dQ) side by side in one
 // launch, each owning its outputs, so no atomics are needed.  Tiles stream
-// through LDS with 16-byte row loads, fetched one block ahead.
+// through LDS with 16-byte row loads, fetched one block ahead.  When a shape
+// has few query blocks for the device (under two per compute unit), the
+// forward splits each block's keys into chunks over more workgroups and a
+// merge kernel combines their partial softmax states.
 #include "common.hpp"
 #include "launch.hpp"
 
