@@ -437,7 +437,9 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx,
                             TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) {
                 const float* cur = smem + (kb & 1) * SM::TILES;
+                __builtin_amdgcn_s_setprio(1);
                 tile(cur, cur + MHA_BN * KS, kb);
+                __builtin_amdgcn_s_setprio(0);
                 store_kv(kx, vx, smem + ((kb + 1) & 1) * SM::TILES, kb + 1);
                 // Keep the refill below the LDS writes: issued earlier, the
                 // wait for the old data would include the new loads.
@@ -456,7 +458,9 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             // The last key tile; then the next job's first loads (all register
             // stages are free by then).
             const float* cur = smem + (kb & 1) * SM::TILES;
+            __builtin_amdgcn_s_setprio(1);
             tile(cur, cur + MHA_BN * KS, kb);
+            __builtin_amdgcn_s_setprio(0);
             __builtin_amdgcn_sched_barrier(0);   // not above the math: it reads qreg
             if (more)
                 load_first(jnext);
