@@ -10,9 +10,10 @@
 // take 256 < Dh <= 512 with the same layout ((B*S, H*Dh) rows), scale, lse
 // convention and backward contract as mha.hip.
 //
-// Design.  16 query rows (forward) or 16 keys (backward) per workgroup of four
-// waves; the head dim is split over the waves, 128 columns each, so the
-// 16x16 score tile is four partial products summed through LDS, and each wave
+// Design.  16 query rows (forward) or 16 keys (backward) per workgroup of
+// eight waves (two per SIMD, one workgroup per compute unit by LDS); the head
+// dim is split over the waves, 64 columns each, so the 16x16 score tile is
+// eight partial products summed through LDS, and each wave
 // keeps its own column slice of the O (forward) or dK/dV (backward)
 // accumulators in registers.  Scores are formed transposed in the forward (a
 // lane owns a query row: its online-softmax state is per lane).  The backward
@@ -36,14 +37,17 @@ namespace cxg {
 constexpr int WB = 16;                 // rows per tile (queries and keys)
 constexpr int WIDE_DHP = 512;          // padded head dim
 constexpr int WLD = WIDE_DHP + 4;      // LDS row stride of a staged tile
-constexpr int WSL = WIDE_DHP / 4;      // head-dim columns per wave
+constexpr int WW = 8;                  // waves per workgroup (two per SIMD)
+constexpr int WT = 64 * WW;            // threads per workgroup
+constexpr int WSL = WIDE_DHP / WW;     // head-dim columns per wave
 constexpr int WNT = WSL / 16;          // 16-column tiles per wave
+constexpr int WU = WB * WIDE_DHP / 4 / WT;   // 16-byte units of a tile per thread
 
-// Rows [r0, r0+16) x [0, Dh) of one head, eight 16-byte units per thread of
-// 256 (unit u = tid + 256k: row u / 128, column 4 (u % 128)): rows past S
-// repeat row S-1 (clamped loads), columns past Dh are zeroed when stored.
+// Rows [r0, r0+16) x [0, Dh) of one head, WU 16-byte units per thread of WT
+// (unit u = tid + WT k: row u / 128, column 4 (u % 128)): rows past S repeat
+// row S-1 (clamped loads), columns past Dh are zeroed when stored.
 struct WideRegs {
-    f4 v[8];
+    f4 v[WU];
 };
 
 template <bool VEC>
@@ -51,8 +55,8 @@ __device__ __forceinline__ void wide_fetch(WideRegs& R, const float* __restrict_
                                            int r0, int S, int Dh, int tid)
 {
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int u = tid + 256 * k;
+    for (int k = 0; k < WU; k++) {
+        const int u = tid + WT * k;
         const int row = u / (WIDE_DHP / 4), c = 4 * (u % (WIDE_DHP / 4));
         R.v[k] = load4c<VEC>(head + (long)min(r0 + row, S - 1) * ld, c, Dh);
     }
@@ -62,8 +66,8 @@ __device__ __forceinline__ void wide_store(float* __restrict__ dst, const WideRe
                                            int tid)
 {
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const int u = tid + 256 * k;
+    for (int k = 0; k < WU; k++) {
+        const int u = tid + WT * k;
         const int row = u / (WIDE_DHP / 4), c = 4 * (u % (WIDE_DHP / 4));
         *reinterpret_cast<f4*>(&dst[row * WLD + c]) = mask4(R.v[k], c, Dh, true);
     }
@@ -83,12 +87,12 @@ constexpr int WREC = WB * WIDE_DHP + 2 * WB;   // partial record: o[16][512], m[
 __host__ __device__ inline int wide_nch(int qb, int C) { return (qb + C) / C; }
 
 template <bool VEC>
-__global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
+__global__ __launch_bounds__(WT) void mha_wide_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, float* __restrict__ part, int S, int H,
     int Dh, int BH, int C, float qscale)
 {
-    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 4 * 256];
+    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + WW * 256];
     float* Sp = lds + 4 * WB * WLD;   // partial scores [wave][lane * 4 + r]
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
         __syncthreads();
         f4 s = f4zero();
 #pragma unroll
-        for (int u = 0; u < 4; u++)
+        for (int u = 0; u < WW; u++)
             s += *reinterpret_cast<const f4*>(&Sp[u * 256 + lane * 4]);
         // causal and length masks, online softmax per query row (lane)
         float mloc = -INFINITY;
@@ -227,19 +231,19 @@ __global__ __launch_bounds__(256) void mha_wide_fwd_kernel(
 // are summed through LDS; the streamed tile is fetched one ahead.
 // ---------------------------------------------------------------------------
 template <bool VEC>
-__global__ __launch_bounds__(256) void mha_wide_bwd_kernel(
+__global__ __launch_bounds__(WT) void mha_wide_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
     float qscale, float scale)
 {
-    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 2 * 4 * 256 + 2 * WB];
+    __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 2 * WW * 256 + 2 * WB];
     float* Ks = lds;                     // key job: its K, V; query job: the streamed K, V
     float* Vs = Ks + WB * WLD;
     float* Qs = Vs + WB * WLD;           // key job: the streamed Q, dO; query job: its Q, dO
     float* dOs = Qs + WB * WLD;
     float* Sp = dOs + WB * WLD;          // [wave][S, dP][lane * 4 + r]
-    float* st = Sp + 2 * 4 * 256;        // lse2[16], Di[16] of the current query block
+    float* st = Sp + 2 * WW * 256;       // lse2[16], Di[16] of the current query block
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int nb = (S + WB - 1) / WB;
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(256) void mha_wide_bwd_kernel(
         __syncthreads();
         f4 sv = f4zero(), dp = f4zero();
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < WW; u++) {
             sv += *reinterpret_cast<const f4*>(&Sp[(2 * u) * 256 + lane * 4]);
             dp += *reinterpret_cast<const f4*>(&Sp[(2 * u + 1) * 256 + lane * 4]);
         }
@@ -550,7 +554,7 @@ hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, f
             nent += wide_nch(qb, C);
     }
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
-    dim3 grid((unsigned)(nent * BH)), block(256);
+    dim3 grid((unsigned)(nent * BH)), block(WT);
     const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(O);
     {
         ProfScope ps(st, O != nullptr ? "mha_wide_fwd" : "mha_wide_stats");
@@ -565,7 +569,7 @@ hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, f
     if (e != hipSuccess || C >= nqb)
         return e;
     ProfScope ps(st, "mha_wide_merge");
-    hipLaunchKernelGGL(mha_wide_merge_kernel, dim3((unsigned)((long)nqb * BH * 4)), block, 0, st,
+    hipLaunchKernelGGL(mha_wide_merge_kernel, dim3((unsigned)((long)nqb * BH * 4)), dim3(256), 0, st,
                        part, O, lse, S, H, Dh, BH, C);
     return hipGetLastError();
 }
@@ -576,7 +580,7 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
 {
     const int nb = (S + WB - 1) / WB;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid((unsigned)(2L * B * H * nb)), block(256);
+    dim3 grid((unsigned)(2L * B * H * nb)), block(WT);
     const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(dO) &&
                      al16w(dQ) && al16w(dK) && al16w(dV);
     ProfScope ps(st, "mha_wide_bwd");
