@@ -143,7 +143,7 @@ def attribute(cx, step, steps):
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
-              "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "gelu", "gelu_deriv", "ffn_gemm",
+              "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",
               "ffn_fixup"):
         tot, cnt = cx.prof_query(n)
         if cnt:

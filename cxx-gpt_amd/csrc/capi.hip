@@ -308,9 +308,11 @@ size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
     bool empty;
     if (gpt_check(B, S, E, &empty) != CXG_OK || empty)
         return 0;
-    // Di, lse, and the split-KV records of the statistics pass
-    return 2 * round_up(B * S * sizeof(float), 256) +
-           round_up(mha_wide_fwd_ws_floats((int)B, (int)S) * sizeof(float), 256);
+    // Di, lse, and the partial records of the statistics pass and of the
+    // backward (used one after the other)
+    const size_t part = std::max(mha_wide_fwd_ws_floats((int)B, (int)S),
+                                 mha_wide_bwd_ws_floats((int)B, (int)S));
+    return 2 * round_up(B * S * sizeof(float), 256) + round_up(part * sizeof(float), 256);
 }
 
 int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float* O,
@@ -347,7 +349,8 @@ int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float
     e = mha_bwd_prep_launch(O, dO, Di, nullptr, iB, iS, 1, iE, s);   // dQ is stored outright
     if (e != hipSuccess)
         return hip_status(e);
-    return hip_status(mha_wide_bwd_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, 1, iE, s));
+    return hip_status(
+        mha_wide_bwd_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, 1, iE, part, s));
 }
 
 // ---------------------------------------------------------------------------

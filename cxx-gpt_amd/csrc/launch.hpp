@@ -64,9 +64,13 @@ size_t mha_wide_fwd_ws_floats(int BH, int S);
 hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                                float* lse, int B, int S, int H, int Dh, float* part,
                                hipStream_t st);
+// Chunked backward jobs' partial records: mha_wide_bwd_ws_floats(B*H, S)
+// floats at `part` (0: not chunked, part may be null).
+size_t mha_wide_bwd_ws_floats(int BH, int S);
 hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
-                               float* dV, int B, int S, int H, int Dh, hipStream_t st);
+                               float* dV, int B, int S, int H, int Dh, float* part,
+                               hipStream_t st);
 
 // Exact (erf) GELU or its derivative over n elements (C may alias A).
 hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t st);

@@ -83,6 +83,7 @@ __device__ __forceinline__ void wide_store(float* __restrict__ dst, const WideRe
 // C >= nqb: one chunk per query block, written directly.
 // ---------------------------------------------------------------------------
 constexpr int WREC = WB * WIDE_DHP + 2 * WB;   // partial record: o[16][512], m[16], l[16]
+constexpr int WBREC = 2 * WB * WIDE_DHP;       // backward: dK (or dQ) rows, then dV rows
 
 __host__ __device__ inline int wide_nch(int qb, int C) { return (qb + C) / C; }
 
@@ -234,8 +235,8 @@ template <bool VEC>
 __global__ __launch_bounds__(WT) void mha_wide_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
-    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
-    float qscale, float scale)
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
+    float* __restrict__ part, int S, int H, int Dh, int BH, int Cb, float qscale, float scale)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * WB * WLD + 2 * WW * 256 + 2 * WB];
     float* Ks = lds;                     // key job: its K, V; query job: the streamed K, V
@@ -247,11 +248,21 @@ __global__ __launch_bounds__(WT) void mha_wide_bwd_kernel(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int nb = (S + WB - 1) / WB;
-    const int BH = gridDim.x / (2 * nb);
-    const bool kjob = (int)blockIdx.x < BH * nb;
-    const int jid = kjob ? (int)blockIdx.x : (int)blockIdx.x - BH * nb;
-    const int blk = kjob ? jid / BH : nb - 1 - jid / BH;   // key block / query block
-    const int bh = jid % BH;
+    const int ent = (int)(blockIdx.x / BH);
+    const int bh = (int)(blockIdx.x % BH);
+    int L = nb - ent / 2, e = ent & 1;
+    if (Cb < nb) {
+        L = nb;
+        e = ent;
+        while (e >= 2 * wide_nch(L - 1, Cb)) {
+            e -= 2 * wide_nch(L - 1, Cb);
+            L--;
+        }
+    }
+    const int nchL = Cb < nb ? wide_nch(L - 1, Cb) : 1;
+    const bool kjob = e < nchL;
+    const int chk = kjob ? e : e - nchL;
+    const int blk = kjob ? nb - L : L - 1;
     const int b = bh / H, h = bh - b * H;
     const long ld = (long)H * Dh;
     const long hoff = (long)b * S * ld + (long)h * Dh;
@@ -277,8 +288,9 @@ __global__ __launch_bounds__(WT) void mha_wide_bwd_kernel(
         acc1[t] = f4zero();
         acc2[t] = f4zero();
     }
-    // streamed blocks: key job: query blocks blk .. nb-1; query job: key blocks 0 .. blk
-    const int sbeg = kjob ? blk : 0, send = kjob ? nb : blk + 1;
+    const int sfirst = kjob ? blk : 0;
+    const int sbeg = sfirst + chk * (Cb < nb ? Cb : nb);
+    const int send = Cb < nb ? min(sfirst + L, sbeg + Cb) : sfirst + L;
     const float* s1 = (kjob ? Q : K) + hoff;
     const float* s2 = (kjob ? dO : V) + hoff;
     float* d1 = kjob ? Qs : Ks;
@@ -367,7 +379,17 @@ __global__ __launch_bounds__(WT) void mha_wide_bwd_kernel(
         }
         __syncthreads();   // the streamed tiles, stats and partials are rewritten next
     }
-    // rows x0 + l16 of dK and dV (key job) or dQ (query job)
+    if (nchL > 1) {
+        float* rec = part + (long)blockIdx.x * WBREC;
+#pragma unroll
+        for (int t = 0; t < WNT; t++) {
+            const int c = c0 + 16 * t + 4 * g;
+            *reinterpret_cast<f4*>(&rec[l16 * WIDE_DHP + c]) = acc1[t];
+            if (kjob)
+                *reinterpret_cast<f4*>(&rec[WB * WIDE_DHP + l16 * WIDE_DHP + c]) = acc2[t];
+        }
+        return;
+    }
     const int row = x0 + l16;
     if (row < S) {
         const long ro = hoff + (long)row * ld;
@@ -460,6 +482,66 @@ __global__ __launch_bounds__(256) void mha_wide_merge_kernel(const float* __rest
             for (int i = 0; i < 4; i++)
                 if (c + i < Dh)
                     orow[c + i] = v[i];
+        }
+    }
+}
+
+// Sum the chunks of every chunked backward job (jobs numbered like the
+// backward's entries) into dK and dV, or dQ.  Workgroup (job, column quarter).
+__global__ __launch_bounds__(256) void mha_wide_bsum_kernel(const float* __restrict__ part,
+    float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
+    int BH, int Cb)
+{
+    const int nb = (S + WB - 1) / WB;
+    const int quarter = (int)(blockIdx.x & 3);
+    const int job = (int)(blockIdx.x >> 2);
+    const int bh = job % BH;
+    const int kind = (job / BH) & 1;
+    const int L = job / (2 * BH) + 1;
+    const int nch = wide_nch(L - 1, Cb);
+    if (nch == 1)
+        return;
+    int e0 = 0;
+    for (int l = nb; l > L; l--)
+        e0 += 2 * wide_nch(l - 1, Cb);
+    e0 += kind ? nch : 0;
+    const float* rec0 = part + ((long)e0 * BH + bh) * WBREC;
+    const long cstride = (long)BH * WBREC;
+    const int tid = threadIdx.x, row = tid >> 4;
+    const int c0 = quarter * (WIDE_DHP / 4) + 4 * (tid & 15), c1 = c0 + 64;
+    f4 a0 = f4zero(), a1 = f4zero(), b0 = f4zero(), b1 = f4zero();
+    for (int j = 0; j < nch; j++) {
+        const float* rec = rec0 + j * cstride + row * WIDE_DHP;
+        a0 += *reinterpret_cast<const f4*>(rec + c0);
+        a1 += *reinterpret_cast<const f4*>(rec + c1);
+        if (kind == 0) {
+            b0 += *reinterpret_cast<const f4*>(rec + WB * WIDE_DHP + c0);
+            b1 += *reinterpret_cast<const f4*>(rec + WB * WIDE_DHP + c1);
+        }
+    }
+    const int blk = kind ? L - 1 : nb - L;
+    const int x = blk * WB + row;
+    if (x >= S)
+        return;
+    const int b = bh / H, h = bh - b * H;
+    const long ld = (long)H * Dh;
+    const long ro = (long)b * S * ld + (long)h * Dh + (long)x * ld;
+    for (int k = 0; k < 2; k++) {
+        const int c = k ? c1 : c0;
+        if (c >= Dh)
+            continue;
+        const f4 va = k ? a1 : a0, vb = k ? b1 : b0;
+        for (int o = 0; o < (kind ? 1 : 2); o++) {
+            float* dst = (kind ? dQ : (o ? dV : dK)) + ro;
+            const f4 v = o ? vb : va;
+            if (Dh % 4 == 0 && (((uintptr_t)dst & 15u) == 0)) {
+                *reinterpret_cast<f4*>(dst + c) = v;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (c + i < Dh)
+                        dst[c + i] = v[i];
+            }
         }
     }
 }
@@ -574,22 +656,66 @@ hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, f
     return hipGetLastError();
 }
 
-hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
-                               const float* lse, const float* Di, float* dQ, float* dK,
-                               float* dV, int B, int S, int H, int Dh, hipStream_t st)
+// Backward stream chunk: with few jobs (2*B*H*nb under three per compute
+// unit) the long key and query jobs are cut into chunks of nb/3 blocks (at
+// least 2) whose partial dK/dV/dQ mha_wide_bsum_kernel adds up.  Tuned on
+// B8 S256 E512 (nb = 16): chunks of 2..8 blocks gave 99.9, 95.0, 93.5,
+// 86.7, 91.7, -, 101.9 us per fwd+bwd step against 95.1 unchunked; nb/3 = 5.
+static int wide_bwd_chunk(int BH, int S)
 {
     const int nb = (S + WB - 1) / WB;
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (2L * BH * nb >= 3L * cus || nb < 6)
+        return nb;
+    return std::max(2, nb / 3);
+}
+
+static long wide_bwd_entries(int nb, int Cb)
+{
+    long n = 0;
+    for (int L = 1; L <= nb; L++)
+        n += 2 * (Cb < nb ? wide_nch(L - 1, Cb) : 1);
+    return n;
+}
+
+size_t mha_wide_bwd_ws_floats(int BH, int S)
+{
+    const int nb = (S + WB - 1) / WB;
+    const int Cb = wide_bwd_chunk(BH, S);
+    return Cb < nb ? (size_t)wide_bwd_entries(nb, Cb) * BH * WBREC : 0;
+}
+
+hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
+                               const float* lse, const float* Di, float* dQ, float* dK,
+                               float* dV, int B, int S, int H, int Dh, float* part,
+                               hipStream_t st)
+{
+    const int nb = (S + WB - 1) / WB;
+    const int BH = B * H;
+    const int Cb = wide_bwd_chunk(BH, S);
+    if (Cb < nb && part == nullptr)
+        return hipErrorInvalidValue;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid((unsigned)(2L * B * H * nb)), block(WT);
+    dim3 grid((unsigned)(wide_bwd_entries(nb, Cb) * BH)), block(WT);
     const bool vec = Dh % 4 == 0 && al16w(Q) && al16w(K) && al16w(V) && al16w(dO) &&
                      al16w(dQ) && al16w(dK) && al16w(dV);
-    ProfScope ps(st, "mha_wide_bwd");
-    if (vec)
-        hipLaunchKernelGGL(mha_wide_bwd_kernel<true>, grid, block, 0, st, Q, K, V, dO, lse, Di,
-                           dQ, dK, dV, S, H, Dh, scale * kLog2e, scale);
-    else
-        hipLaunchKernelGGL(mha_wide_bwd_kernel<false>, grid, block, 0, st, Q, K, V, dO, lse, Di,
-                           dQ, dK, dV, S, H, Dh, scale * kLog2e, scale);
+    {
+        ProfScope ps(st, "mha_wide_bwd");
+        if (vec)
+            hipLaunchKernelGGL(mha_wide_bwd_kernel<true>, grid, block, 0, st, Q, K, V, dO, lse,
+                               Di, dQ, dK, dV, part, S, H, Dh, BH, Cb, scale * kLog2e, scale);
+        else
+            hipLaunchKernelGGL(mha_wide_bwd_kernel<false>, grid, block, 0, st, Q, K, V, dO, lse,
+                               Di, dQ, dK, dV, part, S, H, Dh, BH, Cb, scale * kLog2e, scale);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || Cb >= nb)
+        return e;
+    ProfScope ps(st, "mha_wide_bsum");
+    hipLaunchKernelGGL(mha_wide_bsum_kernel, dim3((unsigned)(2L * nb * BH * 4)), dim3(256), 0, st,
+                       part, dQ, dK, dV, S, H, Dh, BH, Cb);
     return hipGetLastError();
 }
 

@@ -57,6 +57,7 @@ def gpt_whole_matrix(Q, K, V, dO, B, S, E):
     (3, 33, 260),     # just past 256
     (1, 16, 512),     # one tile
     (2, 50, 258),     # width not a multiple of 4 (scalar loads)
+    (1, 130, 258),    # chunked backward and split-KV forward with scalar stores
     (4, 128, 512),
 ])
 def test_gpt_attention(dev, B, S, E):
