@@ -98,7 +98,8 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * few 16-row query blocks split the forward's key range over more
  * workgroups and merge the partial softmax states: the forward then takes
  * stream-ordered scratch for them, and cxg_gpt_attn_bwd_workspace_size
- * counts them for the backward's statistics pass (lse == NULL). */
+ * counts them for the backward's statistics pass (lse == NULL), as well as
+ * the partial sums of the backward's own chunked jobs. */
 int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
                      size_t B, size_t S, size_t E, cxg_stream_t stream);
 int cxg_gpt_attn_bwd(const float *Q, const float *K, const float *V, const float *O,
