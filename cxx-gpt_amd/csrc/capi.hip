@@ -397,7 +397,7 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
         const LinCtx c = lin_ctx_split(ctx, (int)B, (int)S, (int)D, (int)E);
         return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de,
                                          den_eps, (int)B, (int)S, (int)D, (int)E, c.rec, s, c.tot,
-                                         c.zt));
+                                         c.zt, c.anch));
     }
     Scratch ws;
     st = ws.acquire(nullptr, 0, lin_ws_bytes(p, (int)B, (int)D, (int)E), s);

@@ -275,8 +275,8 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zcache,
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
-    float* __restrict__ ctot, float* __restrict__ ztab, int sfin_de, int den_incl_eps, int Bq,
-    int S, int D, int E, int nseg, int L)
+    float* __restrict__ ctot, float* __restrict__ ztab, float* __restrict__ anch, int sfin_de,
+    int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * FWD_STAGE + CHUNK];
     const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
@@ -341,6 +341,20 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         float* bK = st + CHUNK;
         float* bV = st + 2 * CHUNK;
         const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        // context: the state before chunk 2^k of the sequence is anchor k (a
+        // wave-uniform branch taken log2(S / 16) times per sequence)
+        const int cabs = tbeg / 16 + c;
+        if (anch != nullptr && cabs > 0 && (cabs & (cabs - 1)) == 0) {
+            float* R = anch + ((long)seq * lin_nanch((S + 15) / 16) + __builtin_ctz(cabs)) *
+                                  LIN_ANCH;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        R[(16 * dt + 4 * g + r) * 64 + 16 * (2 * h + j) + l16] = St[dt][j][r];
+        }
         // context: z before the chunk (lanes l16 = 0 of wave 0 store, others dropped)
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
@@ -1298,8 +1312,8 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
 template <int PHI>
 static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float* O, float* den,
                            float* zc, float* Sfin, float* zfin, float* ctot, float* ztab,
-                           int sfin_de, int den_eps, int Bq, int S, int D, int E, void* ws,
-                           hipStream_t st)
+                           float* anch, int sfin_de, int den_eps, int Bq, int S, int D, int E,
+                           void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
     if (!p.fast) {
@@ -1332,15 +1346,15 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
     ProfScope ps(st, "lin_fwd");
     if (mode == 2)
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     else if (mode == 1)
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     else
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
-                           wsf, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq, S, D, E, p.nseg,
+                           wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     return hipGetLastError();
 }
@@ -1348,16 +1362,16 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
 hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                           float* den, float* zc, float* Sfin, float* zfin, int sfin_de,
                           int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st,
-                          float* ctot, float* ztab)
+                          float* ctot, float* ztab, float* anch)
 {
     if (phi == PHI_ELU1)
-        return fwd_impl<PHI_ELU1>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps,
-                                  Bq, S, D, E, ws, st);
+        return fwd_impl<PHI_ELU1>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
+                                  den_eps, Bq, S, D, E, ws, st);
     if (phi == PHI_ELU1_LG)
-        return fwd_impl<PHI_ELU1_LG>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de,
+        return fwd_impl<PHI_ELU1_LG>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
                                      den_eps, Bq, S, D, E, ws, st);
-    return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, sfin_de, den_eps, Bq,
-                              S, D, E, ws, st);
+    return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
+                              den_eps, Bq, S, D, E, ws, st);
 }
 
 hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, float* dnum,

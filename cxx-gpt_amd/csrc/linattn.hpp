@@ -14,6 +14,25 @@ enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2 };
 // floats per segment record in the scan workspace: 64x64 state [d][e] + z[64]
 constexpr int LIN_WS = 64 * 64 + 64;
 
+// State anchors of the fused backward.  The fused backward walks each segment
+// from its last chunk to its first and obtains the prefix state S before a
+// chunk by subtracting chunk products from a later exact prefix.  The
+// rounding error of that subtraction is relative to the later prefix, so the
+// prefix before chunk 2^k (k = 0, 1, ...) of every sequence, as a forward sum
+// forms it, is kept as an anchor (a 64x64 [d][e] record, LIN_ANCH floats) and
+// chunk 0 starts from zero: the state of a chunk c >= 1 is then recovered
+// from a forward-summed prefix at most c chunks later (of at most about twice
+// its size), and chunks of later segments (which start at least one segment
+// length into the sequence) from their own segment's end prefix.  lin_nanch(n): anchors below chunk n, i.e. #{k : 2^k < n}.
+constexpr int LIN_ANCH = 64 * 64;
+__host__ __device__ inline int lin_nanch(long nchunks)
+{
+    int k = 0;
+    while ((1L << k) < nchunks)
+        k++;
+    return k;
+}
+
 struct LinPlan {
     bool fast;   // D <= 64 and E <= 64: chunked MFMA scan
     int nseg;    // segments per sequence (fast path)
@@ -31,13 +50,15 @@ size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E);
 // den_eps: 1 stores den + 1e-8 (linear_cuda), 0 stores den (two_stage).  O is
 // num / (den + 1e-8) either way.  Sfin/zfin (nullable) receive the final state,
 // sfin_de selecting [d][e] (1) or [e][d] (0) layout.
-// ctot / ztab (nullable, fast path only): the context for the fused backward:
-// each sequence's final state as a segment record, and z before every 16-row
-// chunk ([S / 16][64] per sequence).  ws then holds the segment prefix records.
+// ctot / ztab / anch (nullable, fast path only): the context for the fused
+// backward: each sequence's final state as a segment record, z before every
+// 16-row chunk ([S / 16][64] per sequence) and the state anchors
+// ([lin_nanch(S / 16)][LIN_ANCH] per sequence).  ws then holds the segment
+// prefix records.
 hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                           float* den, float* zc, float* Sfin, float* zfin, int sfin_de,
                           int den_eps, int Bq, int S, int D, int E, void* ws, hipStream_t st,
-                          float* ctot = nullptr, float* ztab = nullptr);
+                          float* ctot = nullptr, float* ztab = nullptr, float* anch = nullptr);
 hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, float* dnum,
                             float* dden, long N, int E, hipStream_t st);
 hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* dnum,
@@ -55,9 +76,10 @@ size_t lin_bwd_fused_ws_bytes(int Bq, int S, int D, int E, bool with_ctx);
 // Forward-to-backward context of the fused pair: the forward's segment prefix
 // records, each sequence's final-state record and the z table.
 struct LinCtx {
-    float* rec;   // Bq * nseg_fwd records (the forward's scan workspace)
-    float* tot;   // Bq records
-    float* zt;    // Bq * ceil(S / 16) * 64
+    float* rec;    // Bq * nseg_fwd records (the forward's scan workspace)
+    float* tot;    // Bq records
+    float* zt;     // Bq * ceil(S / 16) * 64
+    float* anch;   // Bq * lin_nanch(ceil(S / 16)) anchors of LIN_ANCH floats
 };
 size_t lin_ctx_bytes(int Bq, int S, int D, int E);   // 0: shapes the fused kernels do not take
 LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E);

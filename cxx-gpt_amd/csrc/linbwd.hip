@@ -31,13 +31,19 @@
 //    is read once.  z is not recovered by subtraction (cancellation near a
 //    segment start would reach ~1e-4 relative): a chunk's starting z is the
 //    segment's exclusive prefix plus its z table entry, both forward sums.
-//    The S subtraction keeps dQ within a tenth of the parity tolerance at
-//    S = 4096 (its error is relative to |S| at the segment end, which stays
-//    within a small factor of |S_t| away from the sequence start).
+//    The S subtraction is re-anchored: a chunk whose index within the sequence
+//    is a power of two takes a forward-summed state (an anchor, written by the
+//    forward's context or by lin_bagg) instead, and chunk 0 takes zero.  The
+//    rounding error of S then stays relative to a state at most about twice
+//    the size of S_t; subtracting from the segment end alone put it relative
+//    to the whole segment's sum, and once V has a non-zero mean (|S| growing
+//    like t) that exceeded the parity tolerance near the sequence start.
 #include "common.hpp"
 #include "launch.hpp"
 #include "linattn.hpp"
 #include "linattn_dev.hpp"
+
+#include <algorithm>
 
 namespace cxg {
 
@@ -72,8 +78,8 @@ template <int PHI, bool VEC, bool FW, bool SUF>
 __device__ __attribute__((always_inline)) inline void bagg_body(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
-    float* __restrict__ rec, float* __restrict__ ztab_seg, float* __restrict__ lds, int seq,
-    int seg, int S, int D, int E, int L)
+    float* __restrict__ rec, float* __restrict__ ztab_seg, float* __restrict__ anch_seq,
+    float* __restrict__ lds, int seq, int seg, int S, int D, int E, int L)
 {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -160,6 +166,17 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
                 a = mfma16(xC[dt][r], yC[r], a);
             acc[dt] = a;
         }
+        // Segment 0's prefix (anch_seq != null): the state before chunk c + 1 is
+        // anchor k when c + 1 = 2^k lies inside the segment (a wave-uniform
+        // branch taken log2(L / 16) times).
+        if (anch_seq != nullptr && c + 1 < nch && ((c + 1) & c) == 0) {
+            float* R = anch_seq + __builtin_ctz(c + 1) * LIN_ANCH;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    R[(16 * dt + 4 * g + r) * 64 + 16 * w + l16] = acc[dt][r];
+        }
         // z table: the exclusive prefix before this chunk (lanes l16 = 0 store)
         buffer_store_f4(rz, l16 == 0 ? (unsigned)(c * 64 + 16 * w + 4 * g) * 4u : kDropOffset,
                         zrun);
@@ -191,22 +208,25 @@ template <int PHI, bool VEC, bool FW>
 __global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
-    float* __restrict__ wsP, float* __restrict__ wsB, float* __restrict__ ztab, int Bq, int S,
-    int D, int E, int nseg, int L, int nchs, int with_prefix)
+    float* __restrict__ wsP, float* __restrict__ wsB, float* __restrict__ ztab,
+    float* __restrict__ anch, int nanch, int Bq, int S, int D, int E, int nseg, int L, int nchs,
+    int with_prefix)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * BAGG_STAGE];
     const int nP = with_prefix ? Bq * nseg : 0;
     if ((int)blockIdx.x < nP) {
         const int seq = blockIdx.x / nseg, seg = blockIdx.x - seq * nseg;
         bagg_body<PHI, VEC, FW, false>(Q, K, V, O, dO, den, wsP + (long)blockIdx.x * LIN_WS,
-                                       ztab + ((long)seq * nchs + seg * (L / 16)) * 64, lds, seq,
-                                       seg, S, D, E, L);
+                                       ztab + ((long)seq * nchs + seg * (L / 16)) * 64,
+                                       seg == 0 && nanch > 0 ? anch + (long)seq * nanch * LIN_ANCH
+                                                             : nullptr,
+                                       lds, seq, seg, S, D, E, L);
     } else {
         const int b = blockIdx.x - nP;
         const int seq = b / (nseg - 1), seg = 1 + (b - seq * (nseg - 1));
         bagg_body<PHI, VEC, FW, true>(Q, K, V, O, dO, den,
-                                      wsB + ((long)seq * nseg + seg) * LIN_WS, nullptr, lds, seq,
-                                      seg, S, D, E, L);
+                                      wsB + ((long)seq * nseg + seg) * LIN_WS, nullptr, nullptr,
+                                      lds, seq, seg, S, D, E, L);
     }
 }
 
@@ -277,8 +297,8 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ wsP, const float* __restrict__ wsB, const float* __restrict__ ztab,
-    const float* __restrict__ crec, const float* __restrict__ ctot, int mf, int nsegf, int S, int D,
-    int E, int nseg, int L, int nchs)
+    const float* __restrict__ crec, const float* __restrict__ ctot, const float* __restrict__ anch,
+    int nanch, int mf, int nsegf, int S, int D, int E, int nseg, int L, int nchs)
 {
     __shared__ __attribute__((aligned(16))) float lds[BWD_LDS];
     float* sS = lds + 2 * BWD_STAGE;   // S* [d][e]
@@ -356,6 +376,22 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     Set sa, sb;
     fetch(sa, nch - 1);
     fetch(sb, max(nch - 2, 0));
+    // State anchors (forward-summed S before chunk 2^k of the sequence, [d][e],
+    // k < nanch): the one for chunk c is loaded while chunk c + 1 is worked, into
+    // `an` in StT's layout.  Every chunk issues the loads; for a chunk that is no
+    // anchor the descriptor has no records and they return zeros without a
+    // memory access, so the waits on the other loads stay exact.
+    const int cb = tbeg / 16;
+    auto is_anchor = [&](int ca) { return ca > 0 && (ca & (ca - 1)) == 0 && __builtin_ctz(ca) < nanch; };
+    f4 an[4];
+    auto fetch_anchor = [&](int ca) {
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(
+            is_anchor(ca) ? anch + ((long)seq * nanch + __builtin_ctz(ca)) * LIN_ANCH : nullptr);
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+            an[a] = buffer_load_f4(ra, (unsigned)((16 * w + l16) * 64 + 16 * a + 4 * g) * 4u);
+    };
+    fetch_anchor(cb + nch - 1);
     auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * BWD_STAGE;
@@ -509,6 +545,14 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                     a = mfma16(vC[et][r], nk[r], a);
                 StT[et] = a;
             }
+            // re-anchor: chunk 0 of the sequence starts from zero, an anchor chunk
+            // from its forward-summed state; then request the next chunk's anchor
+            const int ca = cb + c;
+            const bool anc = is_anchor(ca);
+#pragma unroll
+            for (int et = 0; et < 4; et++)
+                StT[et] = ca == 0 ? f4zero() : (anc ? an[et] : StT[et]);
+            fetch_anchor(ca - 1);
         }
         // dQ^T[d][t] = (z_t[d] dden_t + sum_e S[d][e] dnum_t[e]) phi'(Q_t[d]), with
         // z_t = zb + sum_{s<=t} phi(K_s) and S_t = S + sum_{s<=t} phi(K_s) V_s^T:
@@ -591,10 +635,20 @@ int lin_bwd_slots()
     return per_cu;
 }
 
+// Anchors kept without a context: those inside the first backward segment
+// (later segments start from their own end prefix), formed by lin_bagg.
+static int bwd_nanch_noctx(const LinPlan& p, int S)
+{
+    const long nchs = (S + 15) / 16;
+    return lin_nanch(std::min<long>(p.L / 16, nchs));
+}
+
 size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S)
 {
     const long nchs = (S + 15) / 16;
-    return ((size_t)2 * Bq * p.nseg * LIN_WS + (size_t)Bq * nchs * 64) * sizeof(float);
+    return ((size_t)2 * Bq * p.nseg * LIN_WS + (size_t)Bq * nchs * 64 +
+            (size_t)Bq * bwd_nanch_noctx(p, S) * LIN_ANCH) *
+           sizeof(float);
 }
 
 size_t lin_ctx_bytes(int Bq, int S, int D, int E)
@@ -603,16 +657,20 @@ size_t lin_ctx_bytes(int Bq, int S, int D, int E)
         return 0;
     const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
     const long nchs = (S + 15) / 16;
-    return ((size_t)Bq * (pf.nseg + 1) * LIN_WS + (size_t)Bq * nchs * 64) * sizeof(float);
+    return ((size_t)Bq * (pf.nseg + 1) * LIN_WS + (size_t)Bq * nchs * 64 +
+            (size_t)Bq * lin_nanch(nchs) * LIN_ANCH) *
+           sizeof(float);
 }
 
 LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E)
 {
     const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
+    const long nchs = (S + 15) / 16;
     LinCtx c;
     c.rec = (float*)ctx;
     c.tot = c.rec + (size_t)Bq * pf.nseg * LIN_WS;
     c.zt = c.tot + (size_t)Bq * LIN_WS;
+    c.anch = c.zt + (size_t)Bq * nchs * 64;
     return c;
 }
 
@@ -620,7 +678,7 @@ LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E)
 // records and the z table come from it and only the suffix aggregates are
 // formed; mf forward segments make one backward segment.
 struct BwdArgs {
-    float *wsP, *wsB, *zt;
+    float *wsP, *wsB, *zt, *anch;   // anch: the anchors lin_bagg forms (no context)
     LinCtx c;
     int mf, nsegf;
 };
@@ -632,12 +690,15 @@ static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const
 {
     const int nchs = (S + 15) / 16;
     const bool pre = a.c.tot == nullptr;
+    // anchors: the context's (every 2^k below the sequence's chunk count), or
+    // those lin_bagg forms inside the first segment
+    const int nanch = pre ? bwd_nanch_noctx(p, S) : lin_nanch(nchs);
     const unsigned nb = (unsigned)((pre ? Bq * p.nseg : 0) + Bq * (p.nseg - 1));
     if (nb > 0) {
         ProfScope ps(st, "lin_bagg");
         hipLaunchKernelGGL((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
-                           Q, K, V, O, dO, den, a.wsP, a.wsB, a.zt, Bq, S, D, E, p.nseg, p.L, nchs,
-                           pre ? 1 : 0);
+                           Q, K, V, O, dO, den, a.wsP, a.wsB, a.zt, a.anch, pre ? nanch : 0, Bq,
+                           S, D, E, p.nseg, p.L, nchs, pre ? 1 : 0);
     }
     {
         ProfScope ps(st, "lin_bscan");
@@ -648,8 +709,8 @@ static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const
     ProfScope ps(st, "lin_bwd");
     hipLaunchKernelGGL((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
                        dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, a.wsP, a.wsB,
-                       pre ? a.zt : a.c.zt, a.c.rec, a.c.tot, a.mf, a.nsegf, S, D, E, p.nseg, p.L,
-                       nchs);
+                       pre ? a.zt : a.c.zt, a.c.rec, a.c.tot, pre ? a.anch : a.c.anch, nanch,
+                       a.mf, a.nsegf, S, D, E, p.nseg, p.L, nchs);
 }
 
 template <int PHI>
@@ -695,8 +756,9 @@ hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const f
     a.wsP = (float*)ws;
     a.wsB = a.wsP + (size_t)Bq * p.nseg * LIN_WS;
     a.zt = a.wsB + (size_t)Bq * p.nseg * LIN_WS;
+    a.anch = a.zt + (size_t)Bq * ((S + 15) / 16) * 64;
     a.c = ctx != nullptr ? lin_ctx_split(const_cast<void*>(ctx), Bq, S, D, E)
-                         : LinCtx{nullptr, nullptr, nullptr};
+                         : LinCtx{nullptr, nullptr, nullptr, nullptr};
     if (phi == PHI_ELU1)
         bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else if (phi == PHI_ELU1_LG)

@@ -72,13 +72,14 @@ def kernel_test_inputs():
     return out
 
 
-def normal_inputs(shape_q, shape_v, seed, q_std=1.0, v_std=1.0, d_shape=None):
+def normal_inputs(shape_q, shape_v, seed, q_std=1.0, v_std=1.0, d_shape=None, k_mean=0.0,
+                  v_mean=0.0):
     """Benchmark-style inputs: one splitmix64/Box-Muller stream per tensor,
-    seeds base+{Q:0, K:1, V:2, dO:3}."""
+    seeds base+{Q:0, K:1, V:2, dO:3}; K and V may carry a mean."""
     nq = int(np.prod(shape_q))
     nv = int(np.prod(shape_v))
     Q = orc.normal(seed + 0, nq, 0.0, q_std).reshape(shape_q)
-    K = orc.normal(seed + 1, nq, 0.0, q_std).reshape(shape_q)
-    V = orc.normal(seed + 2, nv, 0.0, v_std).reshape(shape_v)
+    K = orc.normal(seed + 1, nq, k_mean, q_std).reshape(shape_q)
+    V = orc.normal(seed + 2, nv, v_mean, v_std).reshape(shape_v)
     dO = orc.normal(seed + 3, nv, 0.0, v_std).reshape(d_shape or shape_v)
     return Q, K, V, dO

@@ -263,3 +263,83 @@ def test_error_paths(dev):
         assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 100, 64, 64, st) == \
             cx.CXG_ERR_WORKSPACE
         assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 100, 64, 64, st) == cx.CXG_ERR_NULL
+
+
+# ---------------------------------------------------------------------------
+# Inputs with a mean: |S| then grows like t, which is where recovering the
+# prefix state by subtraction loses precision (test_lin_bwd_numerics.py models
+# it on the CPU).  The GPU runs the whole batch; the oracle checks a sample of
+# sequences (each sequence is independent).
+# ---------------------------------------------------------------------------
+def _seq_rows(a, seqs, S):
+    return np.concatenate([a[s * S:(s + 1) * S] for s in seqs])
+
+
+def _check_sampled(g, ref_fn, seqs, S, tag):
+    ref = ref_fn(seqs)
+    for name, r in ref.items():
+        assert_close(_seq_rows(g[name], seqs, S), r, f"{tag} {name}")
+
+
+@pytest.mark.parametrize("api", ["kattn", "lin", "lin_elu"])
+@pytest.mark.parametrize("use_ctx", [False, True])
+@pytest.mark.parametrize("B,v_mean,k_mean", [(96, 1.0, 0.0), (96, 3.0, 0.0), (96, 3.0, 1.0),
+                                             (300, 3.0, 0.0)])
+def test_mean_shifted_inputs(dev, api, use_ctx, B, v_mean, k_mean):
+    """C3 S4096 shapes with V ~ N(mu, 1) (and K shifted): B' = 96 has several
+    backward segments per sequence; B' = 300 fills every resident slot, so each
+    sequence is one 4096-row segment."""
+    import torch
+    import cxxgpt_attn as cx
+    S, D, E = 4096, 64, 64
+    N = B * S
+    Q, K, V, dO = normal_inputs((N, D), (N, E), 900 + int(10 * v_mean + k_mean),
+                                k_mean=k_mean, v_mean=v_mean)
+    if api == "lin":
+        Q, K = orc.phi_elu_forward(Q, D, D), orc.phi_elu_forward(K, D, D)
+    tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
+    O, den = _nan(dev, N, E), _nan(dev, N)
+    ctx = _ctx(dev, B, S, D, E) if use_ctx else None
+    dQ, dK, dV = _nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)
+    if api == "kattn":
+        if use_ctx:
+            cx.kattn_fwd_ctx(tQ, tK, tV, O, den, ctx, B, S, D, E)
+        else:
+            cx.kattn_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+        cx.kattn_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E, ctx=ctx)
+    elif api == "lin":
+        if use_ctx:
+            cx.lin_fwd_ctx(tQ, tK, tV, O, den, ctx, B, S, D, E)
+        else:
+            cx.lin_fwd(tQ, tK, tV, O, den, None, None, None, B, S, D, E)
+        cx.lin_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, D, E, ctx=ctx)
+    else:
+        cx.lin_elu_fwd(tQ, tK, tV, O, den, ctx, B, S, E)
+        cx.lin_elu_bwd(tQ, tK, tV, O, tdO, den, dQ, dK, dV, B, S, E, ctx=ctx)
+    torch.cuda.synchronize()
+    g = dict(O=_np(O), den=_np(den), dQ=_np(dQ), dK=_np(dK), dV=_np(dV))
+    del tQ, tK, tV, tdO, O, den, dQ, dK, dV, ctx
+    seqs = [0, 1, B // 2, B - 1]
+    n = len(seqs)
+
+    def ref(sq):
+        q, k, v, do = (_seq_rows(a, sq, S) for a in (Q, K, V, dO))
+        gO, gden = _seq_rows(g["O"], sq, S), _seq_rows(g["den"], sq, S)
+        if api == "kattn":
+            rO, rden, rzc = orc.kattn_fwd(q, k, v, n, S, D, E, nthreads=8)
+            dnum, dden = orc.kattn_bwd_step1(gO, do, gden, n * S, E)
+            rdQ = orc.kattn_bwd_dQ(k, v, dnum, dden, rzc, q, n, S, D, E, nthreads=8)
+            rdK, rdV = orc.kattn_bwd_dKdV(q, k, v, dnum, dden, n, S, D, E, nthreads=8)
+        else:
+            qp, kp = (q, k) if api == "lin" else (orc.phi_elu_forward(q, D, E),
+                                                  orc.phi_elu_forward(k, D, E))
+            rO, rden, rzc, _, _ = orc.lcu_fwd(qp, kp, v, n, S, D, E, nthreads=8)
+            dnum, dden = orc.lcu_bwd_step1(gO, do, gden, n * S, E)
+            rdQ = orc.lcu_bwd_dQ(kp, v, dnum, dden, rzc, n, S, D, E, nthreads=8)
+            rdK, rdV = orc.lcu_bwd_dKdV(qp, kp, v, dnum, dden, n, S, D, E, nthreads=8)
+            if api == "lin_elu":
+                rdQ, rdK = orc.phi_elu_backward(rdQ, q, D, E), orc.phi_elu_backward(rdK, k, D, E)
+        return dict(O=rO, den=rden, dQ=rdQ, dK=rdK, dV=rdV)
+
+    _check_sampled(g, ref, seqs, S,
+                   f"{api} B{B} muV{v_mean} muK{k_mean}{' ctx' if use_ctx else ''}")
