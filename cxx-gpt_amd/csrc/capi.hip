@@ -252,6 +252,88 @@ int cxg_mha_bwd(const float* Q, const float* K, const float* V, const float* O,
                           workspace_bytes, stream, false);
 }
 
+// ---------------------------------------------------------------------------
+// allocation-free backward: the scratch (Di and the statistics pass's lse) lives
+// in a file-scope device array instead of a workspace
+// ---------------------------------------------------------------------------
+} // extern "C"
+
+namespace cxg {
+// One copy per GPU the library runs on, held until the process ends.  In host
+// code `scratch` is only a handle: its device address (per device) comes from
+// hipGetSymbolAddress, and only that address reaches kernels.
+constexpr size_t kNoAllocScratchFloats = 2 * (size_t)CXG_MHA_BWD_NOALLOC_MAX_ROWS;
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices];
+
+// Device address of this device's scratch array (resolved once per device, with
+// that device current); nullptr and *err set on failure.
+float* scratch_ptr(hipError_t* err)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices))
+        e = hipErrorInvalidDevice;
+    if (e != hipSuccess) {
+        *err = e;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = (float*)p;
+    }
+    return g_scratch_ptr[dev];
+}
+} // namespace
+} // namespace cxg
+
+extern "C" {
+
+int cxg_mha_bwd_noalloc(const float* Q, const float* K, const float* V, const float* O,
+                        const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                        size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream)
+{
+    bool empty;
+    int st = mha_check(B, S, H, Dh, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
+    const size_t rows = B * H * S;
+    if (rows > (size_t)CXG_MHA_BWD_NOALLOC_MAX_ROWS)
+        return CXG_ERR_WORKSPACE;
+    hipError_t e = hipSuccess;
+    float* sp = scratch_ptr(&e);
+    if (sp == nullptr)
+        return hip_status(e);
+    // Di in the first half, the statistics pass's lse in the second; both are
+    // written in full before they are read, so nothing needs clearing
+    float* Di = sp;
+    float* lse_ws = sp + CXG_MHA_BWD_NOALLOC_MAX_ROWS;
+    hipStream_t s = (hipStream_t)stream;
+    const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
+    if (lse == nullptr) {
+        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s);
+        if (e != hipSuccess)
+            return hip_status(e);
+        lse = lse_ws;
+    }
+    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
+    if (e != hipSuccess)
+        return hip_status(e);
+    return hip_status(mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s));
+}
+
 int cxg_mha_rope_bwd(const float* Q, const float* K, const float* V, const float* O,
                      const float* dO, const float* lse, float* dQ, float* dK, float* dV,
                      size_t B, size_t S, size_t H, size_t Dh, void* workspace,

@@ -32,6 +32,7 @@ SIGNATURES = {
     "cxg_mha_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz,
                     _vp],
     "cxg_mha_bwd_workspace_size": [_sz, _sz, _sz, _sz],
+    "cxg_mha_bwd_noalloc": [_vp] * 9 + [_sz] * 4 + [_vp],
     "cxg_mha_rope_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_mha_rope_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp,
                          _sz, _vp],
@@ -150,6 +151,15 @@ def mha_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, workspace=None, s
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _call("cxg_mha_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse), _ptr(dQ),
           _ptr(dK), _ptr(dV), B, S, H, Dh, _ptr(workspace), ws_bytes, _stream(stream))
+
+
+def mha_bwd_noalloc(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh, lse=None, stream=None):
+    """cxg_mha_bwd without a workspace or any allocation (static device scratch)."""
+    _call("cxg_mha_bwd_noalloc", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(lse),
+          _ptr(dQ), _ptr(dK), _ptr(dV), B, S, H, Dh, _stream(stream))
+
+
+MHA_BWD_NOALLOC_MAX_ROWS = 1 << 19
 
 
 def mha_rope_fwd(Q, K, V, O, B, S, H, Dh, lse=None, stream=None):

@@ -71,6 +71,22 @@ int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
                 size_t workspace_bytes, cxg_stream_t stream);
 size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh);
 
+/* Allocation-free cxg_mha_bwd.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
+ * and errors as cxg_mha_bwd without a workspace; the scratch (the row sums
+ * Di and, with lse == NULL, the statistics pass's lse) is a static device
+ * array of 2 * CXG_MHA_BWD_NOALLOC_MAX_ROWS floats (4 MiB) per GPU, held
+ * until the process ends.  B*H*S above CXG_MHA_BWD_NOALLOC_MAX_ROWS returns
+ * CXG_ERR_WORKSPACE and launches nothing.  The call allocates nothing
+ * (no hipMalloc, hipFree or allocating library routine).  Every call on one
+ * GPU uses that GPU's array: calls that overlap on one GPU (other streams,
+ * other host threads) race. */
+#define CXG_MHA_BWD_NOALLOC_MAX_ROWS (1u << 19)
+int cxg_mha_bwd_noalloc(const float *Q, const float *K, const float *V, const float *O,
+                        const float *dO, const float *lse, float *dQ, float *dK, float *dV,
+                        size_t B, size_t S, size_t H, size_t Dh, cxg_stream_t stream);
+
 /* RoPE fused into the MHA kernels.  No single counterpart in the reference:
  * cxg_mha_rope_fwd(Q, K, ...) computes what two_stage_gpt.hpp:102-106 does
  * with rope_fwd(Q, K, B, S, H*Dh, Dh) followed by fused_mha_fwd, reading Q
