@@ -127,10 +127,26 @@ def timed(step, steps, warmup, stream):
     return e0.elapsed_time(e1) / steps
 
 
+# Seconds of GPU work per secondary workload's timed region and per kernel
+# attribution pass: long enough for a sampler polling the GPU every few seconds
+# to see it busy, short enough for the whole run to stay within minutes.
+SUSTAIN_S = 0.4
+
+
+def steps_for(ms_per_step, floor, seconds=SUSTAIN_S, cap=20000):
+    """Steps that fill about `seconds` of GPU time at ms_per_step (at least floor)."""
+    return int(max(floor, min(cap, seconds * 1e3 / max(ms_per_step, 1e-4))))
+
+
 def attribute(cx, step, steps):
     """Mean device duration (ms) and launch count per kernel tag, from the
-    library's per-launch HIP events on the launch stream."""
+    library's per-launch HIP events on the launch stream (the event pair adds
+    a microsecond or two to each launch; rocprofv3's kernel trace is the
+    cross-check).  `steps`: a count, or ("seconds", ms_per_step) for a
+    time-based pass."""
     import torch
+    if isinstance(steps, tuple):
+        steps = steps_for(steps[1], 10)
     torch.cuda.synchronize()
     cx.prof_reset()
     cx.prof_enable(True)
@@ -141,6 +157,7 @@ def attribute(cx, step, steps):
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
               "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
+              "lin_wide_fwd", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd", "lin_wide_state",
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",
@@ -215,7 +232,7 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
                 [("cxg_rope_bwd", (P(dQ), P(dK), B, S, H * Dh, Dh, c.sp))]
     step = Stepper(c.cx.lib(), calls)
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    att = attribute(c.cx, step, ("seconds", ms))
     flops = mha_flops(B, S, H, Dh)
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
@@ -264,7 +281,7 @@ def _gelu(c, name, rows, cols, seed, steps, warmup):
                   ("cxg_gelu_exact_deriv", (P(act), P(gd), n, c.sp))]
     step = Stepper(c.cx.lib(), calls)
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    att = attribute(c.cx, step, ("seconds", ms))
     total = len(calls) * 2 * n * 4
     value = total / (ms * 1e-3) / 1e9
     kb = {"gelu": 2 * n * 4, "gelu_deriv": 2 * n * 4}
@@ -304,7 +321,7 @@ def _ffn(c, name, M, E, F, seed, steps, warmup):
         ("cxg_ffn_bwd", (P(X), P(W1), P(W2), P(act), P(act), P(dY), P(dX), P(dW1), P(dW2),
                          M, E, F, P(ws), nb, c.sp))])
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    att = attribute(c.cx, step, ("seconds", ms))
     flops = 12.0 * M * E * F
     value = flops / (ms * 1e-3) / 1e12
     per_launch = 2.0 * M * E * F
@@ -340,7 +357,7 @@ def _gpt(c, name, B, S, E, seed, steps, warmup):
                               B, S, E, P(ws), ws_bytes, c.sp)),
     ])
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    att = attribute(c.cx, step, ("seconds", ms))
     flops = mha_flops(B, S, 1, E)
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_wide_fwd": mha_flops(B, S, 1, E, bwd=False),
@@ -401,7 +418,7 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False, lgpt=False):
                                     Bq, S, D, E, c.sp)),
         ])
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    att = attribute(c.cx, step, ("seconds", ms))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
     kb = lin_kernel_bytes(Bq, S, D, fused or lgpt)
@@ -418,6 +435,76 @@ def _kattn(c, name, Bq, S, D, seed, steps, warmup, fused=False, lgpt=False):
                             "fused pair (cxg_kattn_fwd_ctx -> cxg_kattn_bwd with the context)"
                             if fused else "two_stage API chain (fwd, step1, dQ, dKdV)"),
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
+
+
+def lin_wide_flops(Bq, S, D, E):
+    """Algorithmic FLOPs of the quadratic form per kernel, P = S(S+1)/2 causal
+    pairs per sequence: forward A = phi(Q)phi(K)^T and A V; dQ needs
+    X = dnum V^T and G phi(K); dK, dV need G^T phi(Q) and A^T dnum (A and X
+    recomputed there, not credited)."""
+    P = S * (S + 1) // 2
+    f = 2 * P * (D + E) * Bq
+    return {"lin_wide_fwd": f, "lin_wide_dq": f, "lin_wide_dkdv": f, "lin_wide_bwd": 2 * f}
+
+
+def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
+    """Linear attention with wide heads at the reference's training shapes.
+    mode "chain": the two_stage API's four calls (TwoStageGPT stage 2,
+    two_stage_gpt.hpp:115-157); "fused": kernel_attn_fwd then the one-call
+    backward; "lgpt": LinearGPT's block with phi_elu fused (cxg_lin_elu_*)."""
+    g = c.gen(seed)
+    E, N = D, Bq * S
+    Q, K, V, dO = c.randn(g, N, D), c.randn(g, N, D), c.randn(g, N, E), c.randn(g, N, E)
+    O, den = c.empty(N, E), c.empty(N)
+    dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
+    P = _ptr
+    if mode == "lgpt":
+        step = Stepper(c.cx.lib(), [
+            ("cxg_lin_elu_fwd", (P(Q), P(K), P(V), P(O), P(den), None, 0, Bq, S, E, c.sp)),
+            ("cxg_lin_elu_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), None, P(dQ), P(dK),
+                                 P(dV), Bq, S, E, c.sp)),
+        ])
+        desc = "LinearGPT block, phi_elu fused (cxg_lin_elu_fwd -> cxg_lin_elu_bwd)"
+    elif mode == "fused":
+        step = Stepper(c.cx.lib(), [
+            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), None, None, None, Bq, S, D, E,
+                               c.sp)),
+            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), None, P(dQ), P(dK),
+                               P(dV), Bq, S, D, E, c.sp)),
+        ])
+        desc = "two_stage API forward then the one-call backward (cxg_kattn_bwd)"
+    else:
+        zc, dnum, dden = c.empty(N, D), c.empty(N, E), c.empty(N)
+        step = Stepper(c.cx.lib(), [
+            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E,
+                               c.sp)),
+            ("cxg_kattn_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, c.sp)),
+            ("cxg_kattn_bwd_dQ", (P(K), P(V), P(dnum), P(dden), P(zc), P(Q), P(dQ), None,
+                                  Bq, S, D, E, c.sp)),
+            ("cxg_kattn_bwd_dKdV", (P(Q), P(K), P(V), P(dnum), P(dden), P(dK), P(dV),
+                                    Bq, S, D, E, c.sp)),
+        ])
+        desc = "two_stage API chain (fwd with z_cache, step1, dQ, dKdV)"
+    ms = timed(step, steps, warmup, c.stream)
+    att = attribute(c.cx, step, ("seconds", ms))
+    total = lin_bytes(Bq, S, D)
+    value = total / (ms * 1e-3) / 1e9
+    kf = lin_wide_flops(Bq, S, D, E)
+    dom = max((k for k in att if k in kf), key=lambda k: att[k][0])
+    ach = kf[dom] / (att[dom][0] * 1e-3) / 1e12
+    step_flops = 3 * kf["lin_wide_fwd"]
+    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": c.traffic.get(f"{name}/{dom}"),
+            "flops_per_launch": kf[dom],
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, wide heads "
+                                    f"(quadratic form), {desc}",
+                        "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total,
+                        "algorithmic_flops_per_step": step_flops,
+                        "step_tflops": round(step_flops / (ms * 1e-3) / 1e12, 3)},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
 
@@ -445,7 +532,7 @@ def _hexp(c, name, Bq, S, seed, steps, warmup):
         ("cxg_phi_hexp_bwd", (P(dpk), P(Xk), P(dxk), N, D, E, sp)),
     ])
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 50)))
+    att = attribute(c.cx, step, ("seconds", ms))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
     kb = lin_kernel_bytes(Bq, S, D)
@@ -501,7 +588,7 @@ def _rope(c, name, B, S, H, Dh, seed, steps, warmup):
         ("cxg_rope_bwd", (P(dQ), P(dK), B, S, D, Dh, c.sp)),
     ])
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, max(10, min(steps, 100)))
+    att = attribute(c.cx, step, ("seconds", ms))
     per_call = 2 * 2 * B * S * D * 4        # two tensors, read + write
     total = 2 * per_call
     value = total / (ms * 1e-3) / 1e9
@@ -554,6 +641,12 @@ def run_workload(c, name, steps, warmup):
                       lgpt=True)
     if name == "c4":
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
+    if name == "c3wide":     # TwoStageGPT stage 2 (two_stage_train.cpp:168-170, 193)
+        return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "chain")
+    if name == "c3widefused":
+        return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "fused")
+    if name == "lgptwide":   # LinearGPT (linear_train.cpp:168-172, 191)
+        return _linwide(c, name, 8, 256, 512, 84, steps, warmup, "lgpt")
     raise ValueError(f"unknown workload {name}")
 
 
@@ -612,6 +705,11 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 
 
 # ---------------------------------------------------------------------------- main
+SECONDARY = ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c3wide",
+             "c3widefused", "lgptwide", "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu",
+             "ffn")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -619,7 +717,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn", "copy"])
+                             "c3wide", "c3widefused", "lgptwide", "c4", "c5", "rope", "c2rope",
+                             "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline")
@@ -658,12 +757,20 @@ def main():
         "roofline": r["roofline"],
         "step_frac_of_peak": round(r["frac"], 4),
     }
+    out["roofline"]["duration_source"] = (
+        "mean of HIP-event pairs recorded around each launch on its stream (library hook), "
+        f"over about {SUSTAIN_S} s of steps; rocprofv3 kernel-trace averages are in profiles/")
+    out["roofline"]["traffic_source"] = (
+        "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the same counters "
+        "on a 256 MiB copy (profiles/hbm_traffic.md, run of the date given there)")
     sec = {}
     if not args.no_secondary and args.workload == "c2":
-        for name in ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c4", "c5",
-                     "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn"):
-            s = run_workload(c, name, args.steps, args.warmup)
-            sec[name] = {"value": round(s["value"], 3), "unit": s["unit"],
+        for name in SECONDARY:
+            # a short probe fixes the step count that fills SUSTAIN_S of GPU time
+            probe = run_workload(c, name, 3, 1)
+            n = steps_for(probe["ms"], args.steps)
+            s = run_workload(c, name, n, args.warmup)
+            sec[name] = {"value": round(s["value"], 3), "unit": s["unit"], "steps": n,
                          "ms_per_step": round(s["ms"], 5), "frac_of_peak": round(s["frac"], 4),
                          "roofline": s["roofline"], "config": s["config"]}
             if name == "c3":

@@ -1272,7 +1272,7 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
 {
     if (!p.fast)
-        return (size_t)Bq * D * E * sizeof(float);
+        return lin_wide_ok(D, E) ? 0 : (size_t)Bq * D * E * sizeof(float);
     if (p.nseg <= 1)
         return 0;
     return (size_t)Bq * p.nseg * LIN_WS * sizeof(float);
@@ -1316,6 +1316,12 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
                            void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
+    if (!p.fast && lin_wide_ok(D, E)) {
+        hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, st);
+        if (e == hipSuccess && Sfin != nullptr)
+            e = lin_wide_state_launch(PHI, K, V, Sfin, zfin, sfin_de, Bq, S, D, E, st);
+        return e;
+    }
     if (!p.fast) {
         float* state = (float*)ws;
         const size_t sm = (size_t)(3 * D + 256) * sizeof(float);
@@ -1395,6 +1401,9 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
                           void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DQ);
+    if (!p.fast && lin_wide_ok(D, E))   // the quadratic form needs no z_cache
+        return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, dQ, nullptr, nullptr, Bq, S, D, E, 2,
+                                   st);
     if (!p.fast) {
         ProfScope ps(st, "lin_dq_generic");
         hipLaunchKernelGGL((lin_dq_generic_kernel<PHI>), dim3(Bq), dim3(256), 0, st, K, V, dnum,
@@ -1443,6 +1452,8 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
                             void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DKDV);
+    if (!p.fast && lin_wide_ok(D, E))
+        return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, nullptr, dK, dV, Bq, S, D, E, 1, st);
     if (!p.fast) {
         ProfScope ps(st, "lin_dkdv_generic");
         hipLaunchKernelGGL((lin_dkdv_generic_kernel<PHI>), dim3(Bq), dim3(256),
@@ -1494,6 +1505,8 @@ static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E)
 {
     const size_t N = (size_t)Bq * S;
+    if (lin_wide_ok(D, E))   // dnum and dden only
+        return al256(N * E * 4) + al256(N * 4);
     const size_t a = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DQ), Bq, D, E);
     const size_t b = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DKDV), Bq, D, E);
     return al256(N * D * 4) + al256(N * E * 4) + al256(N * 4) + (a > b ? a : b);
@@ -1506,6 +1519,16 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
 {
     const size_t N = (size_t)Bq * S;
     char* p = (char*)ws;
+    if (lin_wide_ok(D, E)) {
+        // wide heads: step 1, then every gradient from one launch of the
+        // quadratic-form backward
+        float* dnum = (float*)p;
+        float* dden = (float*)(p + al256(N * E * 4));
+        hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);
+        if (e == hipSuccess)
+            e = lin_wide_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, st);
+        return e;
+    }
     float* zc = (float*)p;
     p += al256(N * D * 4);
     float* dnum = (float*)p;

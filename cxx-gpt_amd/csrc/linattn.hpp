@@ -96,6 +96,23 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
                                 hipStream_t st);
+// Wide heads (64 < max(D, E) <= LIN_WIDE_MAX, linwide.hip): the quadratic
+// form on FP32 MFMA.  Forward: O, den (den_eps as lin_fwd_launch) and
+// z_cache (nullable).
+// Backward from step 1's dnum, dden: kinds 1 = dK, dV; 2 = dQ; 3 = all three
+// (Q may be null for kinds 2 with PHI_NONE).  State: the final S (layout as
+// lin_fwd_launch's sfin_de) and z (nullable) of every sequence.
+constexpr int LIN_WIDE_MAX = 512;
+bool lin_wide_ok(int D, int E);
+hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
+                               float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
+                               hipStream_t st);
+hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
+                               const float* dnum, const float* dden, float* dQ, float* dK,
+                               float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st);
+hipError_t lin_wide_state_launch(int phi, const float* K, const float* V, float* Sfin,
+                                 float* zfin, int sfin_de, int Bq, int S, int D, int E,
+                                 hipStream_t st);
 hipError_t phi_elu_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st);
 hipError_t phi_elu_bwd_launch(const float* dphi, const float* x, float* dx, long N, int D, int E,
                               hipStream_t st);
