@@ -208,10 +208,12 @@ class Ctx:
         return self.torch.empty(*shape, device=self.dev)
 
 
-def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
+def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only=False,
+         null_ws=False):
     """rope: None (plain MHA), "fused" (cxg_mha_rope_fwd/bwd) or "separate"
     (cxg_rope_fwd, cxg_mha_fwd, cxg_mha_bwd, cxg_rope_bwd: the reference's call
-    sequence at two_stage_gpt.hpp:102-106, :171-174)."""
+    sequence at two_stage_gpt.hpp:102-106, :171-174).  fwd_only: the forward
+    alone (inference: generate() re-runs it per token, two_stage_gpt.hpp:453-470)."""
     g = c.gen(seed)
     shp = (B * S, H * Dh)
     Q, K, V, dO = [c.randn(g, *shp) for _ in range(4)]
@@ -219,6 +221,8 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
     lse = c.empty(B * H * S) if use_lse else None
     ws_bytes = c.cx.mha_bwd_workspace_size(B, S, H, Dh)
     ws = c.empty(max(1, ws_bytes // 4))
+    if null_ws:   # as the drop-in wrappers call it: stream-ordered scratch per call
+        ws, ws_bytes = None, 0
     P = _ptr
     fwd, bwd = ("cxg_mha_rope_fwd", "cxg_mha_rope_bwd") if rope == "fused" else \
         ("cxg_mha_fwd", "cxg_mha_bwd")
@@ -230,10 +234,12 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
     if rope == "separate":
         calls = [("cxg_rope_fwd", (P(Q), P(K), B, S, H * Dh, Dh, c.sp))] + calls + \
                 [("cxg_rope_bwd", (P(dQ), P(dK), B, S, H * Dh, Dh, c.sp))]
+    if fwd_only:
+        calls = calls[:1]
     step = Stepper(c.cx.lib(), calls)
     ms = timed(step, steps, warmup, c.stream)
     att = attribute(c.cx, step, ("seconds", ms))
-    flops = mha_flops(B, S, H, Dh)
+    flops = mha_flops(B, S, H, Dh, bwd=not fwd_only)
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
               "mha_bwd": mha_flops(B, S, H, Dh, fwd=False),
@@ -248,15 +254,19 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None):
             "flops_per_launch": kflops[dom],
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
-                config={"workload": f"{name}: causal softmax MHA fwd+bwd ("
+                config={"workload": f"{name}: causal softmax MHA "
+                                    + ("forward only (" if fwd_only else "fwd+bwd (")
                                     + {None: ("cxg_mha_fwd with lse -> cxg_mha_bwd" if use_lse
-                                              else "legacy signatures, no lse"),
+                                              else "legacy signatures, no lse" +
+                                              (", no workspace (the drop-in wrappers' call)"
+                                               if null_ws else ", caller workspace")),
                                        "fused": "RoPE fused: cxg_mha_rope_fwd -> "
                                                 "cxg_mha_rope_bwd",
                                        "separate": "RoPE as separate passes: cxg_rope_fwd, "
                                                    "cxg_mha_fwd, cxg_mha_bwd, cxg_rope_bwd"}[rope]
                                     + ")",
-                        "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops},
+                        "B": B, "H": H, "S": S, "Dh": Dh, "flops_per_step": flops,
+                        "us_per_step": round(ms * 1e3, 2)},
                 frac=value / FP32_MFMA_PEAK_TFLOPS,
                 cpu_inputs=(Q, K, V, dO, B, S, H, Dh))
 
@@ -508,7 +518,9 @@ def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
 
-def _hexp(c, name, Bq, S, seed, steps, warmup):
+def _hexp(c, name, Bq, S, seed, steps, warmup, fused=False):
+    """fused: the feature maps around the fused pair (cxg_lin_fwd_ctx ->
+    cxg_lin_bwd with the context) instead of the four-call linear_cuda chain."""
     g = c.gen(seed)
     D = E = 64
     N = Bq * S
@@ -519,15 +531,29 @@ def _hexp(c, name, Bq, S, seed, steps, warmup):
     dnum, dden, dpq, dpk, dV, dxq, dxk = e(N, E), e(N), e(N, D), e(N, D), e(N, E), e(N, D), \
         e(N, D)
     P, sp = _ptr, c.sp
+    if fused:
+        nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+        ctx = c.empty(max(1, nctx // 4))
+        mid = [
+            ("cxg_lin_fwd_ctx", (P(pq), P(pk), P(V), P(O), P(den), P(ctx), nctx, Bq, S, D, E,
+                                 sp)),
+            ("cxg_lin_bwd", (P(pq), P(pk), P(V), P(O), P(dO), P(den), P(ctx), P(dpq), P(dpk),
+                             P(dV), Bq, S, D, E, sp)),
+        ]
+    else:
+        mid = [
+            ("cxg_lin_fwd", (P(pq), P(pk), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E,
+                             sp)),
+            ("cxg_lin_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, sp)),
+            ("cxg_lin_bwd_dQ", (P(pk), P(V), P(dnum), P(dden), P(zc), P(dpq), None, Bq, S, D, E,
+                                sp)),
+            ("cxg_lin_bwd_dKdV", (P(pq), P(pk), P(V), P(dnum), P(dden), P(dpk), P(dV), Bq, S, D,
+                                  E, sp)),
+        ]
     step = Stepper(c.cx.lib(), [
         ("cxg_phi_hexp_fwd", (P(Xq), P(pq), N, D, E, sp)),
         ("cxg_phi_hexp_fwd", (P(Xk), P(pk), N, D, E, sp)),
-        ("cxg_lin_fwd", (P(pq), P(pk), P(V), P(O), P(den), P(zc), None, None, Bq, S, D, E, sp)),
-        ("cxg_lin_bwd_step1", (P(O), P(dO), P(den), P(dnum), P(dden), N, E, sp)),
-        ("cxg_lin_bwd_dQ", (P(pk), P(V), P(dnum), P(dden), P(zc), P(dpq), None, Bq, S, D, E,
-                            sp)),
-        ("cxg_lin_bwd_dKdV", (P(pq), P(pk), P(V), P(dnum), P(dden), P(dpk), P(dV), Bq, S, D, E,
-                              sp)),
+    ] + mid + [
         ("cxg_phi_hexp_bwd", (P(dpq), P(Xq), P(dxq), N, D, E, sp)),
         ("cxg_phi_hexp_bwd", (P(dpk), P(Xk), P(dxk), N, D, E, sp)),
     ])
@@ -535,7 +561,7 @@ def _hexp(c, name, Bq, S, seed, steps, warmup):
     att = attribute(c.cx, step, ("seconds", ms))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
-    kb = lin_kernel_bytes(Bq, S, D)
+    kb = lin_kernel_bytes(Bq, S, D, fused)
     dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
     ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
@@ -543,8 +569,9 @@ def _hexp(c, name, Bq, S, seed, steps, warmup):
             "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
-                config={"workload": f"{name}: Hadamard+Exp linear attention fwd+bwd, "
-                                    "linear_cuda API chain incl. feature map",
+                config={"workload": f"{name}: Hadamard+Exp linear attention fwd+bwd, " + (
+                            "feature maps around the fused pair (cxg_lin_fwd_ctx -> cxg_lin_bwd)"
+                            if fused else "linear_cuda API chain incl. feature map"),
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
@@ -618,9 +645,15 @@ def run_workload(c, name, steps, warmup):
         return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
     if name == "c2legacy":
         return _mha(c, name, 8, 256, 12, 64, False, 1234, steps, warmup)
+    if name == "c2dropin":
+        return _mha(c, name, 8, 256, 12, 64, False, 1234, steps, warmup, null_ws=True)
     if name == "c5":
         return _mha(c, name, 2, 4096, 12, 64, True, 555, max(10, steps // 10),
                     max(3, warmup // 4))
+    if name == "mhats":      # TwoStageGPT stage 1 (two_stage_train.cpp:168-170, 193): legacy calls
+        return _mha(c, name, 32, 256, 64, 8, False, 1301, steps, warmup)
+    if name in ("gen1", "gen64", "gen256"):   # generate() forward at B = 1 (probe shape H8 Dh32)
+        return _mha(c, name, 1, int(name[3:]), 8, 32, True, 1302, steps, warmup, fwd_only=True)
     if name == "c3":
         return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2))
     if name == "c3s256":
@@ -641,6 +674,8 @@ def run_workload(c, name, steps, warmup):
                       lgpt=True)
     if name == "c4":
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
+    if name == "c4fused":
+        return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup, fused=True)
     if name == "c3wide":     # TwoStageGPT stage 2 (two_stage_train.cpp:168-170, 193)
         return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "chain")
     if name == "c3widefused":
@@ -705,9 +740,9 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 
 
 # ---------------------------------------------------------------------------- main
-SECONDARY = ("c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c3wide",
-             "c3widefused", "lgptwide", "c4", "c5", "rope", "c2rope", "c2ropesep", "gpt", "gelu",
-             "ffn")
+SECONDARY = ("c2legacy", "c2dropin", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c3wide",
+             "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1", "gen64", "gen256",
+             "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn")
 
 
 def main():
@@ -716,8 +751,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c3wide", "c3widefused", "lgptwide", "c4", "c5", "rope", "c2rope",
+                    choices=["c2", "c2legacy", "c2dropin", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
+                             "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1",
+                             "gen64", "gen256", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

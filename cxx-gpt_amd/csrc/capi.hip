@@ -10,6 +10,8 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -83,12 +85,31 @@ static int hip_status(hipError_t e)
 
 static bool fits_int(size_t v) { return v <= (size_t)INT_MAX; }
 
-// Stream-ordered scratch: caller memory if provided, else hipMallocAsync for
-// the duration of the call.
+// Scratch for calls without a caller workspace, cached per (device, stream):
+// a buffer that grows to the largest request seen on that stream and is kept
+// until the process ends.  Calls on one stream are ordered on the device, so
+// reuse needs no synchronisation; the entry's mutex is held for the whole
+// call, so host threads sharing a stream do not swap the buffer under one
+// another.  Growth frees the old buffer with hipFree (which waits for the
+// device), so it happens only while a caller's sizes are still rising.
+namespace {
+struct StreamScratch {
+    std::mutex mu;
+    void* p = nullptr;
+    size_t n = 0;
+};
+std::mutex g_scratch_map_mu;
+std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch_map;
+} // namespace
+
+// Scratch for one call: caller memory if provided; else the stream's cached
+// buffer; under stream capture, stream-ordered memory for the duration of the
+// call (hipMallocAsync, which capture records as graph memory nodes).
 struct Scratch {
     void* p = nullptr;
     bool owned = false;
     hipStream_t st = nullptr;
+    std::unique_lock<std::mutex> held;
     int acquire(void* ws, size_t ws_bytes, size_t need, hipStream_t s)
     {
         st = s;
@@ -98,6 +119,36 @@ struct Scratch {
             if (ws_bytes < need)
                 return CXG_ERR_WORKSPACE;
             p = ws;
+            return CXG_OK;
+        }
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        int dev = -1;
+        if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+            hipGetDevice(&dev) == hipSuccess) {
+            StreamScratch* e;
+            {
+                std::lock_guard<std::mutex> lk(g_scratch_map_mu);
+                auto& slot = g_scratch_map[std::make_pair(dev, s)];
+                if (!slot)
+                    slot.reset(new StreamScratch);
+                e = slot.get();
+            }
+            held = std::unique_lock<std::mutex>(e->mu);
+            if (e->n < need) {
+                if (e->p != nullptr)
+                    (void)hipFree(e->p);
+                e->p = nullptr;
+                e->n = 0;
+                const size_t want = need + need / 4;   // room for slightly larger calls
+                hipError_t err = hipMalloc(&e->p, want);
+                if (err != hipSuccess) {
+                    t_last_hip = (int)err;
+                    e->p = nullptr;
+                    return CXG_ERR_WORKSPACE;
+                }
+                e->n = want;
+            }
+            p = e->p;
             return CXG_OK;
         }
         hipError_t e = hipMallocAsync(&p, need, s);

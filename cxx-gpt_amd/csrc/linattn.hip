@@ -1196,6 +1196,107 @@ __global__ __launch_bounds__(256) void phi_hexp_bwd_kernel(const float* __restri
     dx[n * E + c] = t * 0.125f;
 }
 
+// Vector forms: a lane holds columns 4q .. 4q+3 (q = lane % 16) of a 64-column
+// block, so the transform's bits 0-1 are in-lane butterflies and bits 2-5
+// exchanges within the 16-lane group, in the same order as fwht64 (bit 0
+// first): the results are fwht64's.  Each thread keeps HX rows' 16-byte
+// loads in flight before any arithmetic.
+constexpr int HX = 4;
+
+__device__ __forceinline__ f4 fwht64_f4(f4 v, int lane)
+{
+    f4 t;
+    t[0] = v[0] + v[1];
+    t[1] = v[0] - v[1];
+    t[2] = v[2] + v[3];
+    t[3] = v[2] - v[3];
+    v[0] = t[0] + t[2];
+    v[1] = t[1] + t[3];
+    v[2] = t[0] - t[2];
+    v[3] = t[1] - t[3];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float u = __shfl_xor(v[i], m, 64);
+            v[i] = (lane & m) ? (u - v[i]) : (v[i] + u);
+        }
+    }
+    return v;
+}
+
+// phi (N x D, D % 64 == 0): f4 unit u of a row is columns 4u .. 4u+3; blocks
+// that lie within E transform x, the others are zero.  Units past the end
+// repeat the last one (clamped) and are not stored.
+__global__ __launch_bounds__(256) void phi_hexp_fwd_vec_kernel(const float* __restrict__ x,
+                                                              float* __restrict__ phi, long N,
+                                                              int D, int E)
+{
+    const int lane = threadIdx.x & 63;
+    const long upr = D / 4, total = N * upr;
+    const long u0 = (long)blockIdx.x * 256 * HX + threadIdx.x;
+    f4 v[HX];
+#pragma unroll
+    for (int k = 0; k < HX; k++) {
+        const long u = min(u0 + 256L * k, total - 1);
+        const long n = u / upr;
+        const int c = 4 * (int)(u - n * upr);
+        v[k] = (c / 64) * 64 + 64 <= E ? *reinterpret_cast<const f4*>(x + n * E + c) : f4zero();
+    }
+#pragma unroll
+    for (int k = 0; k < HX; k++) {
+        const long u = u0 + 256L * k;
+        const long uc = min(u, total - 1);
+        const long n = uc / upr;
+        const int c = 4 * (int)(uc - n * upr);
+        const bool tr = (c / 64) * 64 + 64 <= E;   // uniform over the 16-lane group
+        f4 y = fwht64_f4(v[k], lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            y[i] = tr ? __expf(y[i] * 0.125f) : 0.0f;
+        if (u < total)
+            *reinterpret_cast<f4*>(phi + n * D + c) = y;
+    }
+}
+
+// dx (N x E, E % 64 == 0) = H (dphi * phi) / 8, phi recomputed from x.
+__global__ __launch_bounds__(256) void phi_hexp_bwd_vec_kernel(const float* __restrict__ dphi,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ dx, long N,
+                                                              int D, int E)
+{
+    // No multiply-add contraction: the product dphi * phi is rounded before the
+    // transform's first (in-lane) additions, as in the one-element-per-lane
+    // kernel, where a lane exchange separates them.
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const long upr = E / 4, total = N * upr;
+    const long u0 = (long)blockIdx.x * 256 * HX + threadIdx.x;
+    f4 xv[HX], gv[HX];
+#pragma unroll
+    for (int k = 0; k < HX; k++) {
+        const long u = min(u0 + 256L * k, total - 1);
+        const long n = u / upr;
+        const int c = 4 * (int)(u - n * upr);
+        xv[k] = *reinterpret_cast<const f4*>(x + n * E + c);
+        gv[k] = *reinterpret_cast<const f4*>(dphi + n * D + c);
+    }
+#pragma unroll
+    for (int k = 0; k < HX; k++) {
+        const long u = u0 + 256L * k;
+        const long uc = min(u, total - 1);
+        const long n = uc / upr;
+        const int c = 4 * (int)(uc - n * upr);
+        f4 y = fwht64_f4(xv[k], lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            y[i] = gv[k][i] * __expf(y[i] * 0.125f);
+        const f4 t = fwht64_f4(y, lane) * 0.125f;
+        if (u < total)
+            *reinterpret_cast<f4*>(dx + n * E + c) = t;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -1574,8 +1675,15 @@ hipError_t phi_elu_bwd_launch(const float* dphi, const float* x, float* dx, long
 
 hipError_t phi_hexp_fwd_launch(const float* x, float* phi, long N, int D, int E, hipStream_t st)
 {
-    const long waves = N * ((D + 63) / 64);
     ProfScope ps(st, "phi_hexp_fwd");
+    if (D % 64 == 0 && E % 4 == 0 && al16(x) && al16(phi)) {
+        const long units = N * (D / 4);
+        hipLaunchKernelGGL(phi_hexp_fwd_vec_kernel,
+                           dim3((unsigned)((units + 256L * HX - 1) / (256L * HX))), dim3(256), 0,
+                           st, x, phi, N, D, E);
+        return hipGetLastError();
+    }
+    const long waves = N * ((D + 63) / 64);
     hipLaunchKernelGGL(phi_hexp_fwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
                        0, st, x, phi, N, D, E);
     return hipGetLastError();
@@ -1584,8 +1692,15 @@ hipError_t phi_hexp_fwd_launch(const float* x, float* phi, long N, int D, int E,
 hipError_t phi_hexp_bwd_launch(const float* dphi, const float* x, float* dx, long N, int D,
                                int E, hipStream_t st)
 {
-    const long waves = N * (E / 64);
     ProfScope ps(st, "phi_hexp_bwd");
+    if (E % 64 == 0 && D % 4 == 0 && al16(dphi) && al16(x) && al16(dx)) {
+        const long units = N * (E / 4);
+        hipLaunchKernelGGL(phi_hexp_bwd_vec_kernel,
+                           dim3((unsigned)((units + 256L * HX - 1) / (256L * HX))), dim3(256), 0,
+                           st, dphi, x, dx, N, D, E);
+        return hipGetLastError();
+    }
+    const long waves = N * (E / 64);
     hipLaunchKernelGGL(phi_hexp_bwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
                        0, st, dphi, x, dx, N, D, E);
     return hipGetLastError();

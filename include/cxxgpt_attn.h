@@ -17,6 +17,14 @@
  *     HIP runtime at launch).
  *   - Empty problems (B, S, H or N equal to 0) return CXG_OK and launch
  *     nothing.
+ *   - Scratch.  Where an entry point needs device scratch and the caller
+ *     passes no workspace, the library uses a buffer it keeps per (device,
+ *     stream), grown to the largest request seen on that stream (growth
+ *     calls hipFree/hipMalloc, which wait for the device) and held until the
+ *     process ends; under stream capture it takes stream-ordered memory for
+ *     the call instead (hipMallocAsync, recorded as graph memory nodes).  A
+ *     stream handle that is destroyed and reused inherits its buffer: destroy
+ *     a stream only once its work is done.
  *
  * Citations are relative to the reference tree (yauntyour/CXX-GPT).
  */
@@ -63,8 +71,8 @@ int cxg_mha_fwd(const float *Q, const float *K, const float *V, float *O, float 
 /* two_stage_cuda::fused_mha_bwd (two_stage_cuda_kernels.cuh:22-27,
  * two_stage_cuda_kernels.cu:830-882).  lse: as written by cxg_mha_fwd, or NULL
  * to recompute it (the reference's signature has no lse).  workspace: at least
- * cxg_mha_bwd_workspace_size() bytes of device memory, or NULL to let the
- * library allocate stream-ordered scratch for the call. */
+ * cxg_mha_bwd_workspace_size() bytes of device memory, or NULL for the
+ * library's scratch (see the conventions above). */
 int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
                 const float *dO, const float *lse, float *dQ, float *dK, float *dV,
                 size_t B, size_t S, size_t H, size_t Dh, void *workspace,
@@ -113,7 +121,7 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * takes wider-head kernels; CXG_ERR_HEAD_DIM above 512.  There, shapes with
  * few 16-row query blocks split the forward's key range over more
  * workgroups and merge the partial softmax states: the forward then takes
- * stream-ordered scratch for them, and cxg_gpt_attn_bwd_workspace_size
+ * the library's scratch for them, and cxg_gpt_attn_bwd_workspace_size
  * counts them for the backward's statistics pass (lse == NULL), as well as
  * the partial sums of the backward's own chunked jobs. */
 int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
@@ -165,9 +173,9 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
  * intermediates (dnum = dO/den, dden = -sum_e dO*O/den) stay on chip and no
  * z_cache is needed.  ctx: NULL, or the context cxg_kattn_fwd_ctx wrote for the
  * same Q, K, V and dimensions (the backward then skips re-reading K and V for
- * the prefix state).  D <= 64 and E <= 64 take the fused kernels; wider heads
- * run the split kernels inside the call (z_cache, dnum, dden in stream-ordered
- * scratch; ctx is not used). */
+ * the prefix state).  D <= 64 and E <= 64 take the fused kernels; widths up
+ * to 512 run step 1 and one quadratic-form backward launch (dnum, dden in the
+ * library's scratch; ctx is not used), wider ones the split kernels. */
 int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O,
                   const float *dO, const float *den_cache, const void *ctx, float *dQ,
                   float *dK, float *dV, size_t B, size_t S, size_t D, size_t E,
@@ -307,8 +315,8 @@ int cxg_gelu_exact_deriv(const float *A, float *C, size_t n, cxg_stream_t stream
  *                 final FFN the pre-activation (:141).
  * FP32 MFMA GEMMs with GELU / gelu' in their epilogues.  E and F multiples of
  * 4 and every tensor 16-byte aligned (else CXG_ERR_ALIGN); any M.  workspace
- * of cxg_ffn_workspace_size(M, E, F) bytes (fwd and bwd), or NULL for
- * stream-ordered scratch per call. */
+ * of cxg_ffn_workspace_size(M, E, F) bytes (fwd and bwd), or NULL for the
+ * library's scratch. */
 size_t cxg_ffn_workspace_size(size_t M, size_t E, size_t F);
 int cxg_ffn_fwd(const float *X, const float *W1, const float *W2, float *pre, float *act,
                 float *Y, size_t M, size_t E, size_t F, void *workspace, size_t ws_bytes,

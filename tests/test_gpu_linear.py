@@ -220,3 +220,34 @@ def test_error_paths(dev):
     assert cx.call_status("cxg_phi_hexp_fwd", p, p, 1, 64, 32, st) == cx.CXG_ERR_DIMS
     assert cx.call_status("cxg_phi_elu_fwd", p, p, 1, 4, 8, st) == cx.CXG_ERR_DIMS
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("N,D,E", [(1001, 64, 64), (77, 128, 128), (130, 128, 64), (5, 192, 128)])
+def test_hexp_vector_and_scalar_paths(dev, N, D, E):
+    """The 16-byte-load feature-map kernels (aligned rows, D % 64 == 0) against
+    the one-element-per-lane kernels (taken by an unaligned view), bit for
+    bit, and both against the oracle; columns E..D of phi are zero."""
+    import torch
+    import cxxgpt_attn as cx
+    x, _, _, _ = normal_inputs((N, E), (N, E), 31 + N, q_std=0.5)
+    g = orc.normal(7 + N, N * D).reshape(N, D)
+
+    def view(a, off):
+        buf = torch.zeros(a.size + off, device=dev)
+        buf[off:] = _t(a, dev).reshape(-1)
+        return buf[off:]
+
+    out = {}
+    for off in (0, 1):
+        tx, tg = view(x, off), view(g, off)
+        phi = torch.full((N * D + off,), float("nan"), device=dev)[off:]
+        dx = torch.full((N * E + off,), float("nan"), device=dev)[off:]
+        cx.phi_hexp_fwd(tx, phi, N, D, E)
+        cx.phi_hexp_bwd(tg, tx, dx, N, D, E)
+        torch.cuda.synchronize()
+        out[off] = (_np(phi).reshape(N, D), _np(dx).reshape(N, E))
+    assert np.array_equal(out[0][0], out[1][0]), "phi: vector and scalar kernels differ"
+    assert np.array_equal(out[0][1], out[1][1]), "dx: vector and scalar kernels differ"
+    assert_close(out[0][0], orc.phi_hexp_forward(x, D, E), f"phi_hexp N{N}D{D}E{E}")
+    assert np.all(out[0][0][:, (E // 64) * 64:] == 0.0)
+    assert_close(out[0][1], orc.phi_hexp_backward(g, x, D, E), f"phi_hexp_bwd N{N}D{D}E{E}")
