@@ -86,13 +86,21 @@ def lin_kernel_bytes(Bq, S, D, fused=False):
     own signature: inputs read once, outputs written once.  fused: the forward
     without z_cache and the one-call backward."""
     T, r = Bq * S * D * 4, Bq * S * 4   # one (rows x 64) tensor, one per-row vector
+    # quadratic-form kernels (short sequences): the one-call backward is step 1
+    # then lin_wide_bwd
+    quad = {"lin_step1": 2 * T + r + T + r,      # O, dO, den -> dnum, dden
+            "lin_wide_dq": 4 * T + r + T,        # K, V, dnum, dden, Q (phi') -> dQ
+            "lin_wide_dkdv": 4 * T + r + 2 * T,  # Q, K, V, dnum, dden -> dK, dV
+            "lin_wide_bwd": 4 * T + r + 3 * T}   # Q, K, V, dnum, dden -> dQ, dK, dV
     if fused:
         return {"lin_fwd": 3 * T + T + r,        # Q,K,V -> O, den
-                "lin_bwd": 5 * T + r + 3 * T}    # Q,K,V,O,dO, den -> dQ, dK, dV
+                "lin_bwd": 5 * T + r + 3 * T,    # Q,K,V,O,dO, den -> dQ, dK, dV
+                "lin_wide_fwd": 3 * T + T + r, **quad}
     return {"lin_fwd": 3 * T + 2 * T + r,        # Q,K,V -> O, z_cache, den
             "lin_step1": 2 * T + r + T + r,      # O, dO, den -> dnum, dden
             "lin_dq": 5 * T + r + T,             # K, V, dnum, z_cache, Q, dden -> dQ
-            "lin_dkdv": 4 * T + r + 2 * T}       # Q, K, V, dnum, dden -> dK, dV
+            "lin_dkdv": 4 * T + r + 2 * T,       # Q, K, V, dnum, dden -> dK, dV
+            "lin_wide_fwd": 3 * T + 2 * T + r, **quad}
 
 
 def _ptr(t):

@@ -1346,7 +1346,8 @@ static int lin_slots(int pass)
 LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 {
     LinPlan p;
-    p.fast = (D <= 64 && E <= 64);
+    p.quad = lin_quad_ok(D, E, S);
+    p.fast = !p.quad && (D <= 64 && E <= 64);
     p.nseg = 1;
     p.L = S;
     if (p.fast) {
@@ -1373,7 +1374,7 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
 {
     if (!p.fast)
-        return lin_wide_ok(D, E) ? 0 : (size_t)Bq * D * E * sizeof(float);
+        return p.quad ? 0 : (size_t)Bq * D * E * sizeof(float);
     if (p.nseg <= 1)
         return 0;
     return (size_t)Bq * p.nseg * LIN_WS * sizeof(float);
@@ -1417,7 +1418,7 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
                            void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
-    if (!p.fast && lin_wide_ok(D, E)) {
+    if (p.quad) {
         hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, st);
         if (e == hipSuccess && Sfin != nullptr)
             e = lin_wide_state_launch(PHI, K, V, Sfin, zfin, sfin_de, Bq, S, D, E, st);
@@ -1502,7 +1503,7 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
                           void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DQ);
-    if (!p.fast && lin_wide_ok(D, E))   // the quadratic form needs no z_cache
+    if (p.quad)   // the quadratic form needs no z_cache
         return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, dQ, nullptr, nullptr, Bq, S, D, E, 2,
                                    st);
     if (!p.fast) {
@@ -1553,7 +1554,7 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
                             void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DKDV);
-    if (!p.fast && lin_wide_ok(D, E))
+    if (p.quad)
         return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, nullptr, dK, dV, Bq, S, D, E, 1, st);
     if (!p.fast) {
         ProfScope ps(st, "lin_dkdv_generic");
@@ -1606,7 +1607,7 @@ static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E)
 {
     const size_t N = (size_t)Bq * S;
-    if (lin_wide_ok(D, E))   // dnum and dden only
+    if (lin_quad_ok(D, E, S))   // dnum and dden only
         return al256(N * E * 4) + al256(N * 4);
     const size_t a = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DQ), Bq, D, E);
     const size_t b = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DKDV), Bq, D, E);
@@ -1620,9 +1621,9 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
 {
     const size_t N = (size_t)Bq * S;
     char* p = (char*)ws;
-    if (lin_wide_ok(D, E)) {
-        // wide heads: step 1, then every gradient from one launch of the
-        // quadratic-form backward
+    if (lin_quad_ok(D, E, S)) {
+        // step 1, then every gradient from one launch of the quadratic-form
+        // backward
         float* dnum = (float*)p;
         float* dden = (float*)(p + al256(N * E * 4));
         hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);

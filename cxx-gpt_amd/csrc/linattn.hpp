@@ -34,7 +34,8 @@ __host__ __device__ inline int lin_nanch(long nchunks)
 }
 
 struct LinPlan {
-    bool fast;   // D <= 64 and E <= 64: chunked MFMA scan
+    bool quad;   // the quadratic-form kernels (lin_quad_ok)
+    bool fast;   // D <= 64 and E <= 64 and not quad: chunked MFMA scan
     int nseg;    // segments per sequence (fast path)
     int L;       // rows per segment (multiple of 16)
 };
@@ -67,7 +68,8 @@ hipError_t lin_dq_launch(int phi, const float* K, const float* V, const float* d
 hipError_t lin_dkdv_launch(int phi, const float* Q, const float* K, const float* V,
                            const float* dnum, const float* dden, float* dK, float* dV, int Bq,
                            int S, int D, int E, void* ws, hipStream_t st);
-// Fused backward (step 1 + dQ + dK/dV, linbwd.hip) for D, E <= 64.  den is the
+// Fused backward (step 1 + dQ + dK/dV, linbwd.hip) for D, E <= 64 and sequences
+// the quadratic form does not take (lin_bwd_fused_ok).  den is the
 // forward's den_cache; dnum = dO / den and dden = -(dO . O) / den as in step 1.
 bool lin_bwd_fused_ok(int D, int E, long S);
 int lin_bwd_slots();   // resident fused-backward workgroups per compute unit
@@ -104,6 +106,13 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
 // lin_fwd_launch's sfin_de) and z (nullable) of every sequence.
 constexpr int LIN_WIDE_MAX = 512;
 bool lin_wide_ok(int D, int E);
+// The quadratic form serves every width in (64, 512] and, for D, E <= 64,
+// sequences of at most LIN_QUAD_MAX_S rows, where the chunked scan is bound by
+// its launches and its serial chunk chain rather than by work.  Measured at
+// B' = 96, D = E = 64 (fwd + one-call bwd): S = 128, 42.0 against 48.7 us;
+// S = 256, 84.6 against 66.5 us.
+constexpr int LIN_QUAD_MAX_S = 128;
+bool lin_quad_ok(int D, int E, long S);
 hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                                float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
                                hipStream_t st);

@@ -614,10 +614,11 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // The fused kernels take D, E <= 64 and address a sequence's rows with 32-bit
-// byte offsets.
+// byte offsets; short sequences take the quadratic form instead.
 bool lin_bwd_fused_ok(int D, int E, long S)
 {
-    return D >= 1 && E >= 1 && D <= 64 && E <= 64 && S >= 1 && S < (1L << 22);
+    return D >= 1 && E >= 1 && D <= 64 && E <= 64 && S >= 1 && S < (1L << 22) &&
+           !lin_quad_ok(D, E, S);
 }
 
 int lin_bwd_slots()

@@ -496,6 +496,11 @@ bool lin_wide_ok(int D, int E)
     return D >= 1 && E >= 1 && m > 64 && m <= LIN_WIDE_MAX;
 }
 
+bool lin_quad_ok(int D, int E, long S)
+{
+    return lin_wide_ok(D, E) || (D >= 1 && E >= 1 && D <= 64 && E <= 64 && S <= LIN_QUAD_MAX_S);
+}
+
 static inline bool al16x(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
 template <int PHI, int NW>
@@ -538,6 +543,8 @@ static hipError_t wide_fwd_p(const float* Q, const float* K, const float* V, flo
                              bool vec, hipStream_t st)
 {
     const int m = std::max(D, E);
+    if (m <= 64)
+        return wide_fwd_t<PHI, 1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
     if (m <= 128)
         return wide_fwd_t<PHI, 2>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
     if (m <= 256)
@@ -551,6 +558,8 @@ static hipError_t wide_bwd_p(const float* Q, const float* K, const float* V, con
                              int D, int E, int kinds, bool vec, hipStream_t st)
 {
     const int m = std::max(D, E);
+    if (m <= 64)
+        return wide_bwd_t<PHI, 1>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
     if (m <= 128)
         return wide_bwd_t<PHI, 2>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
     if (m <= 256)

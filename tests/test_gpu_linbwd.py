@@ -255,14 +255,16 @@ def test_error_paths(dev):
         assert cx.call_status(fn, *([None] + p[1:]), 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
         assert cx.call_status(fn, *p[:5], None, *p[6:], 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
         assert cx.call_status(fn, *([None] * 10), 0, 4, 8, 8, st) == cx.CXG_OK   # empty
-    # the context: none for heads wider than 64; a short buffer is refused
-    assert cx.lin_ctx_size(2, 100, 128, 64) == 0
-    n = cx.lin_ctx_size(2, 100, 64, 64)
+    # the context: none for heads wider than 64 or for sequences short enough
+    # for the quadratic form; a short buffer is refused
+    assert cx.lin_ctx_size(2, 300, 128, 64) == 0
+    assert cx.lin_ctx_size(2, 100, 64, 64) == 0
+    n = cx.lin_ctx_size(2, 300, 64, 64)
     assert n > 0
     for fn in ("cxg_kattn_fwd_ctx", "cxg_lin_fwd_ctx"):
-        assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 100, 64, 64, st) == \
+        assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 300, 64, 64, st) == \
             cx.CXG_ERR_WORKSPACE
-        assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 100, 64, 64, st) == cx.CXG_ERR_NULL
+        assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 300, 64, 64, st) == cx.CXG_ERR_NULL
 
 
 # ---------------------------------------------------------------------------
