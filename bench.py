@@ -216,8 +216,31 @@ class Ctx:
         return self.torch.empty(*shape, device=self.dev)
 
 
+class GraphStep:
+    """A step captured once into a HIP graph (torch.cuda.CUDAGraph on a side
+    stream) and replayed: the same kernels with their launch overheads and
+    inter-kernel gaps reduced, as a caller that captures its training step
+    runs them.  `make(stream_handle)` builds the step's C-ABI calls on the
+    capture stream."""
+
+    def __init__(self, torch, make):
+        self.g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            warm = make(ctypes.c_void_p(s.cuda_stream))
+            warm()   # scratch allocations and first-call set-up happen outside capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(self.g, stream=s):
+            make(ctypes.c_void_p(s.cuda_stream))()
+        torch.cuda.synchronize()
+
+    def __call__(self):
+        self.g.replay()
+
+
 def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only=False,
-         null_ws=False):
+         null_ws=False, graph=False):
     """rope: None (plain MHA), "fused" (cxg_mha_rope_fwd/bwd) or "separate"
     (cxg_rope_fwd, cxg_mha_fwd, cxg_mha_bwd, cxg_rope_bwd: the reference's call
     sequence at two_stage_gpt.hpp:102-106, :171-174).  fwd_only: the forward
@@ -245,8 +268,16 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only
     if fwd_only:
         calls = calls[:1]
     step = Stepper(c.cx.lib(), calls)
+    eager = step
+    if graph:
+        def make(sp):
+            return Stepper(c.cx.lib(), [(n, tuple(sp if a is c.sp else a for a in args))
+                                        for n, args in calls])
+        step = GraphStep(c.torch, make)
     ms = timed(step, steps, warmup, c.stream)
-    att = attribute(c.cx, step, ("seconds", ms))
+    # per-kernel durations from the eager calls (the hook's events are not
+    # recorded inside a graph)
+    att = attribute(c.cx, eager, ("seconds", ms))
     flops = mha_flops(B, S, H, Dh, bwd=not fwd_only)
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
@@ -264,6 +295,7 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only
     return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: causal softmax MHA "
                                     + ("forward only (" if fwd_only else "fwd+bwd (")
+                                    + ("replayed as a captured HIP graph: " if graph else "")
                                     + {None: ("cxg_mha_fwd with lse -> cxg_mha_bwd" if use_lse
                                               else "legacy signatures, no lse" +
                                               (", no workspace (the drop-in wrappers' call)"
@@ -653,6 +685,8 @@ def run_workload(c, name, steps, warmup):
         return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup)
     if name == "c2legacy":
         return _mha(c, name, 8, 256, 12, 64, False, 1234, steps, warmup)
+    if name == "c2graph":
+        return _mha(c, name, 8, 256, 12, 64, True, 1234, steps, warmup, graph=True)
     if name == "c2dropin":
         return _mha(c, name, 8, 256, 12, 64, False, 1234, steps, warmup, null_ws=True)
     if name == "c5":
@@ -759,7 +793,7 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
-                    choices=["c2", "c2legacy", "c2dropin", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
+                    choices=["c2", "c2legacy", "c2dropin", "c2graph", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
                              "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1",
                              "gen64", "gen256", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])

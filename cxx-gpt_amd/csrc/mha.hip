@@ -1103,7 +1103,8 @@ struct MhaSplits {
     static constexpr int FWD = DHP <= 128 ? 2 : 1;
     static constexpr int BWD = DHP <= 64 ? 2 : 1;
     static constexpr int BWD_BM = DHP <= 128 ? 64 : 32;
-    // Resident workgroups per CU assumed for the persistent grids.
+    // Resident workgroups per CU assumed for the persistent grids (the
+    // backward's is read from the kernel's occupancy; this is its fallback).
     static constexpr int FWD_PER_CU = 1;
     static constexpr int BWD_PER_CU = 1;
     // Two forward workgroups fit one compute unit (at most 128 VGPRs under
@@ -1180,10 +1181,74 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
     return fwd_dispatch<256>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
 }
 
+// The same for Dh = 4U (U = 1, 2, 4, 8, 16 lanes per (row, head) segment) with
+// aligned rows: O and dO are read as one flat array of 16-byte units, thread
+// t taking units t + j*T (T threads in the grid, j < PREP_UNITS) with every
+// load issued before any arithmetic (one unit per thread ran at 3.8 TB/s at
+// Dh = 64 and 2 lanes of 16 busy at Dh = 8).  A segment's U units sit in U
+// consecutive lanes; their partial dot products are summed by lane exchange.
+constexpr int PREP_UNITS = 4;
+
+template <int U, bool ZERO>
+__global__ __launch_bounds__(256) void mha_bwd_prep_vec_kernel(
+    const float* __restrict__ O, const float* __restrict__ dO, float* __restrict__ Di,
+    float* __restrict__ dQ, int S, int H, long nunits)
+{
+    const long t0 = (long)blockIdx.x * 256 + threadIdx.x;
+    const long T = (long)gridDim.x * 256;
+    const int sub = threadIdx.x & (U - 1);
+    f4 o[PREP_UNITS], d[PREP_UNITS];
+#pragma unroll
+    for (int j = 0; j < PREP_UNITS; j++) {
+        const long u = min(t0 + j * T, nunits - 1);   // past the end: a repeated unit
+        o[j] = *reinterpret_cast<const f4*>(O + 4 * u);
+        d[j] = *reinterpret_cast<const f4*>(dO + 4 * u);
+    }
+#pragma unroll
+    for (int j = 0; j < PREP_UNITS; j++) {
+        const long u = t0 + j * T;
+        float acc = o[j][0] * d[j][0] + o[j][1] * d[j][1] + o[j][2] * d[j][2] + o[j][3] * d[j][3];
+#pragma unroll
+        for (int m = 1; m < U; m <<= 1)
+            acc += __shfl_xor(acc, m, 64);
+        if (u < nunits) {
+            if (ZERO)
+                *reinterpret_cast<f4*>(dQ + 4 * u) = f4zero();
+            if (sub == 0) {
+                const long seg = u / U;
+                const long row = seg / H;
+                const int h = (int)(seg - row * H);
+                const long b = row / S;
+                Di[(b * H + h) * (long)S + (row - b * S)] = acc;
+            }
+        }
+    }
+}
+
+template <int U, bool ZERO>
+static void prep_vec_go(long nseg, const float* O, const float* dO, float* Di, float* dQ, int S,
+                        int H, hipStream_t st)
+{
+    const long nunits = nseg * U;
+    const long threads = (nunits + PREP_UNITS - 1) / PREP_UNITS;
+    hipLaunchKernelGGL((mha_bwd_prep_vec_kernel<U, ZERO>), dim3((unsigned)((threads + 255) / 256)),
+                       dim3(256), 0, st, O, dO, Di, dQ, S, H, nunits);
+}
+
 template <bool VEC, bool ZERO>
 static void prep_go(bool wide, long nseg, const float* O, const float* dO, float* Di, float* dQ,
                     int S, int H, int Dh, hipStream_t st)
 {
+    if (VEC) {
+        switch (Dh) {
+        case 4: prep_vec_go<1, ZERO>(nseg, O, dO, Di, dQ, S, H, st); return;
+        case 8: prep_vec_go<2, ZERO>(nseg, O, dO, Di, dQ, S, H, st); return;
+        case 16: prep_vec_go<4, ZERO>(nseg, O, dO, Di, dQ, S, H, st); return;
+        case 32: prep_vec_go<8, ZERO>(nseg, O, dO, Di, dQ, S, H, st); return;
+        case 64: prep_vec_go<16, ZERO>(nseg, O, dO, Di, dQ, S, H, st); return;
+        default: break;
+        }
+    }
     const int tpr = wide ? 64 : 16;
     dim3 grid((unsigned)((nseg * tpr + 255) / 256)), block(256);
     if (wide)
@@ -1227,7 +1292,20 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
     const int BH = B * H;
     const int nkb = (S + MHA_BN - 1) / MHA_BN;
     const float scale = 1.0f / sqrtf((float)Dh);
-    dim3 grid(job_grid((long)nkb * BH, MhaSplits<DHP>::BWD_PER_CU, true)), block(256 * NS);
+    // Resident workgroups per compute unit for the persistent grid: what the
+    // kernel's registers and LDS allow (two for Dh <= 16, one above), found
+    // once; jobs are claimed by index, so any grid size is correct.
+    static int per_cu = 0;
+    if (per_cu <= 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)mha_bwd_kernel<DHP, BM, NS, true, ROPE>, 256 * NS, 0) !=
+                hipSuccess ||
+            n <= 0)
+            n = MhaSplits<DHP>::BWD_PER_CU;
+        per_cu = n;
+    }
+    dim3 grid(job_grid((long)nkb * BH, per_cu, true)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, ROPE ? "mha_rope_bwd" : "mha_bwd");

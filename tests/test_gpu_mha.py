@@ -82,6 +82,29 @@ def test_config2_fwd_bwd(dev):
         assert_close(dV, rV, f"C2 dV lse={use_lse}")
 
 
+def test_two_stage_stage1_shape(dev):
+    """TwoStageGPT's stage-1 attention at its training shape: B = 32, S = 256,
+    64 heads of Dh = 8 (two_stage_train.cpp:168-170, 193), through the legacy
+    signatures (no lse), on a sample of heads in full."""
+    B, S, H, Dh = 32, 256, 64, 8
+    Q, K, V, dO = normal_inputs((B * S, H * Dh), (B * S, H * Dh), 601)
+    O, _ = _run_fwd(dev, Q, K, V, B, S, H, Dh)
+    dQ, dK, dV = _run_bwd(dev, Q, K, V, O, dO, B, S, H, Dh)
+    heads = [0, 63, 64 * 17 + 5, B * H - 1]
+    rO = orc.mha_fwd_heads(Q, K, V, B, S, H, Dh, heads, nthreads=8)
+    rQ, rK, rV = orc.mha_bwd_heads(Q, K, V, O, dO, B, S, H, Dh, heads, nthreads=8)
+    for bh in heads:
+        b, h = divmod(bh, H)
+        rows = slice(b * S, (b + 1) * S)
+        cols = slice(h * Dh, (h + 1) * Dh)
+        assert_close(O[rows, cols], rO[rows, cols], f"stage1 fwd head {bh}")
+        assert_close(dQ[rows, cols], rQ[rows, cols], f"stage1 dQ head {bh}")
+        assert_close(dK[rows, cols], rK[rows, cols], f"stage1 dK head {bh}")
+        assert_close(dV[rows, cols], rV[rows, cols], f"stage1 dV head {bh}")
+    for a in (O, dQ, dK, dV):
+        assert np.all(np.isfinite(a))
+
+
 def test_config5_long_sequence(dev):
     """C5: B2 H12 S4096 Dh64 (the reference's long-sequence fallback regime).
 
@@ -111,7 +134,7 @@ def test_config5_long_sequence(dev):
 
 
 @pytest.mark.parametrize("B,S,H,Dh", [
-    (1, 1, 1, 64), (1, 5, 3, 8), (2, 65, 2, 16), (1, 130, 1, 24), (3, 100, 2, 7),
+    (1, 1, 1, 64), (1, 5, 3, 8), (2, 65, 2, 16), (1, 130, 1, 24), (3, 100, 2, 7), (2, 33, 3, 4),
     (1, 200, 2, 100), (1, 96, 1, 128), (1, 70, 1, 200), (1, 129, 2, 256), (2, 64, 1, 1),
 ])
 def test_ragged_shapes(dev, B, S, H, Dh):
