@@ -413,7 +413,10 @@ def _gpt(c, name, B, S, E, seed, steps, warmup):
     kflops = {"mha_wide_fwd": mha_flops(B, S, 1, E, bwd=False),
               "mha_wide_bwd": mha_flops(B, S, 1, E, fwd=False),
               "mha_fwd": mha_flops(B, S, 1, E, bwd=False),
-              "mha_bwd": mha_flops(B, S, 1, E, fwd=False)}
+              "mha_bwd": mha_flops(B, S, 1, E, fwd=False),
+              # E > 512: one sequence's S x S x E product per GEMM launch,
+              # credited with its causal half (S^2 E of the 2 S^2 E executed)
+              "ffn_gemm": 1.0 * S * S * E}
     dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
     ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
     roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
@@ -711,6 +714,8 @@ def run_workload(c, name, steps, warmup):
         return _gelu(c, name, 8 * 256, 8 * 768, 93, steps, warmup)
     if name == "gpt":
         return _gpt(c, name, 8, 256, 512, 91, steps, warmup)
+    if name == "gpt768":     # a GPT-2-small width: the scores-in-memory path
+        return _gpt(c, name, 8, 256, 768, 92, steps, warmup)
     if name == "c3lgpt":
         return _kattn(c, name, 96, 4096, 64, 77, max(20, steps // 4), max(5, warmup // 2),
                       lgpt=True)
@@ -784,7 +789,7 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 # ---------------------------------------------------------------------------- main
 SECONDARY = ("c2legacy", "c2dropin", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c3wide",
              "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1", "gen64", "gen256",
-             "rope", "c2rope", "c2ropesep", "gpt", "gelu", "ffn")
+             "rope", "c2rope", "c2ropesep", "gpt", "gpt768", "gelu", "ffn")
 
 
 def main():
@@ -795,7 +800,7 @@ def main():
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c2dropin", "c2graph", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
                              "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1",
-                             "gen64", "gen256", "rope", "c2rope",
+                             "gen64", "gen256", "gpt768", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

@@ -169,6 +169,8 @@ struct Scratch {
 
 static size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+static bool al16c(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 } // namespace cxg
 
 using namespace cxg;
@@ -402,10 +404,15 @@ static int gpt_check(size_t B, size_t S, size_t E, bool* empty)
     *empty = (B == 0 || S == 0);
     if (E == 0)
         return CXG_ERR_DIMS;
-    if (E > (size_t)MHA_WIDE_MAX_DH)
-        return CXG_ERR_HEAD_DIM;
     if (*empty)
         return CXG_OK;
+    if (E > (size_t)MHA_WIDE_MAX_DH) {
+        // scores in memory: S x S floats per sequence (S <= 16384: 1 GiB), GEMM
+        // shapes in int
+        if (!fits_int(B) || !fits_int(E) || S > 16384 || B * S * E > ((size_t)1 << 40))
+            return CXG_ERR_DIMS;
+        return gpt_mat_ok((int)S, (int)E) ? CXG_OK : CXG_ERR_ALIGN;
+    }
     if (!fits_int(B) || !fits_int(S) || B * ((S + 15) / 16) > ((size_t)1 << 23))
         return CXG_ERR_DIMS;
     // the wide kernels address one sequence with 32-bit byte offsets
@@ -426,7 +433,17 @@ int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, f
     if (!Q || !K || !V || !O)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
-    Scratch ws;   // split-KV partial states (few-job shapes), stream-ordered
+    if (E > (size_t)MHA_WIDE_MAX_DH) {
+        if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(O))
+            return CXG_ERR_ALIGN;
+        Scratch ws;
+        st = ws.acquire(nullptr, 0, gpt_mat_ws_floats((int)S, (int)E) * sizeof(float), s);
+        if (st != CXG_OK)
+            return st;
+        return hip_status(gpt_mat_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)E,
+                                             (float*)ws.p, s));
+    }
+    Scratch ws;   // split-KV partial states (few-job shapes)
     st = ws.acquire(nullptr, 0, mha_wide_fwd_ws_floats((int)B, (int)S) * sizeof(float), s);
     if (st != CXG_OK)
         return st;
@@ -441,6 +458,8 @@ size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
     bool empty;
     if (gpt_check(B, S, E, &empty) != CXG_OK || empty)
         return 0;
+    if (E > (size_t)MHA_WIDE_MAX_DH)   // the scores of one sequence, and GEMM partial tiles
+        return gpt_mat_ws_floats((int)S, (int)E) * sizeof(float);
     // Di, lse, and the partial records of the statistics pass and of the
     // backward (used one after the other)
     const size_t part = std::max(mha_wide_fwd_ws_floats((int)B, (int)S),
@@ -468,6 +487,13 @@ int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float
     st = ws.acquire(workspace, workspace_bytes, cxg_gpt_attn_bwd_workspace_size(B, S, E), s);
     if (st != CXG_OK)
         return st;
+    if (E > (size_t)MHA_WIDE_MAX_DH) {
+        if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(dO) || !al16c(dQ) || !al16c(dK) ||
+            !al16c(dV) || !al16c(ws.p))
+            return CXG_ERR_ALIGN;
+        return hip_status(gpt_mat_bwd_launch(Q, K, V, dO, lse, dQ, dK, dV, (int)B, (int)S,
+                                             (int)E, (float*)ws.p, s));
+    }
     float* Di = (float*)ws.p;
     float* lse_ws = (float*)((char*)ws.p + half);
     float* part = (float*)((char*)ws.p + 2 * half);

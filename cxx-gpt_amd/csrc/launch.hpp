@@ -72,6 +72,19 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
                                float* dV, int B, int S, int H, int Dh, float* part,
                                hipStream_t st);
 
+// GPT's attention for E > 512 (gptmat.hip): each sequence's S x S scores in
+// memory, products on the FP32 GEMM below.  S and E multiples of 4 and
+// 16-byte aligned rows; scratch gpt_mat_ws_floats(S, E) floats (used one
+// sequence at a time).  O may be null (statistics only); lse [B][S] natural
+// log, nullable in both.
+bool gpt_mat_ok(int S, int E);
+size_t gpt_mat_ws_floats(int S, int E);
+hipError_t gpt_mat_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                              float* lse, int B, int S, int E, float* ws, hipStream_t st);
+hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
+                              const float* lse, float* dQ, float* dK, float* dV, int B, int S,
+                              int E, float* ws, hipStream_t st);
+
 // Exact (erf) GELU or its derivative over n elements (C may alias A).
 hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t st);
 

@@ -118,12 +118,17 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * transposes).  Q, K, V, O (B*S, E) row-major; lse [B][S] natural log; the
  * same as cxg_mha_fwd / cxg_mha_bwd with H = 1, Dh = E, which serve E <= 256;
  * 256 < E <= 512 (the reference GPT's training configuration has E = 512)
- * takes wider-head kernels; CXG_ERR_HEAD_DIM above 512.  There, shapes with
- * few 16-row query blocks split the forward's key range over more
- * workgroups and merge the partial softmax states: the forward then takes
- * the library's scratch for them, and cxg_gpt_attn_bwd_workspace_size
- * counts them for the backward's statistics pass (lse == NULL), as well as
- * the partial sums of the backward's own chunked jobs. */
+ * takes wider-head kernels.  There, shapes with few 16-row query blocks
+ * split the forward's key range over more workgroups and merge the partial
+ * softmax states: the forward then takes the library's scratch for them, and
+ * cxg_gpt_attn_bwd_workspace_size counts them for the backward's statistics
+ * pass (lse == NULL), as well as the partial sums of the backward's own
+ * chunked jobs.  Above E = 512 (the reference has no limit) each sequence's
+ * S x S scores are kept in scratch and the products run as FP32 MFMA GEMMs;
+ * S and E must be multiples of 4 and the tensors 16-byte aligned
+ * (CXG_ERR_ALIGN otherwise), S <= 16384 (CXG_ERR_DIMS); the forward takes the
+ * library's scratch and the backward's workspace holds two S x S matrices
+ * and the GEMMs' partial tiles. */
 int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
                      size_t B, size_t S, size_t E, cxg_stream_t stream);
 int cxg_gpt_attn_bwd(const float *Q, const float *K, const float *V, const float *O,

@@ -5,7 +5,8 @@ attention with whole-matrix TensorN calls: scores = Q K^T / sqrt(E) over all
 B*S rows, gpt_cuda::attention_mask (gpt_cuda_kernels.cu:458-480: -1e10 on
 cross-batch and future entries), softmax, times V; the backward goes through
 gpt_cuda::softmax_backward (:131-173) and three products.  The entry points
-compute it as causal attention with H = 1, Dh = E.  Each case is checked
+compute it as causal attention with H = 1, Dh = E (above E = 512 with each
+sequence's scores in memory and FP32 MFMA GEMMs).  Each case is checked
 against the C oracle's MHA (ref_mha_fwd / ref_mha_bwd restated, H = 1) and,
 for small B*S, against a float64 restatement of the reference's whole-matrix
 formulation itself (mask value -1e10, row softmax, softmax_backward's
@@ -59,6 +60,10 @@ def gpt_whole_matrix(Q, K, V, dO, B, S, E):
     (2, 50, 258),     # width not a multiple of 4 (scalar loads)
     (1, 130, 258),    # chunked backward and split-KV forward with scalar stores
     (4, 128, 512),
+    (2, 64, 768),     # wider than 512: scores in memory, FP32 MFMA GEMMs
+    (3, 100, 516),
+    (1, 256, 1024),
+    (2, 12, 2048),
 ])
 def test_gpt_attention(dev, B, S, E):
     import torch
@@ -97,13 +102,18 @@ def test_gpt_attention_errors(dev):
     t = torch.zeros(64, device=dev)
     P = cx._ptr
     st = cx._stream(None)
+    # above 512 the scores-in-memory path needs S and E multiples of 4
     assert cx.call_status("cxg_gpt_attn_fwd", P(t), P(t), P(t), P(t), None, 1, 4, 513, st) == \
-        cx.CXG_ERR_HEAD_DIM
+        cx.CXG_ERR_ALIGN
+    assert cx.call_status("cxg_gpt_attn_fwd", P(t), P(t), P(t), P(t), None, 1, 6, 516, st) == \
+        cx.CXG_ERR_ALIGN
+    assert cx.call_status("cxg_gpt_attn_fwd", P(t), P(t), P(t), P(t), None, 1, 20000, 516, st) \
+        == cx.CXG_ERR_DIMS
     assert cx.call_status("cxg_gpt_attn_fwd", P(t), P(t), P(t), P(t), None, 1, 4, 0, st) == \
         cx.CXG_ERR_DIMS
     assert cx.call_status("cxg_gpt_attn_fwd", None, P(t), P(t), P(t), None, 1, 4, 300, st) == \
         cx.CXG_ERR_NULL
     assert cx.call_status("cxg_gpt_attn_fwd", None, None, None, None, None, 0, 4, 300, st) == \
         cx.CXG_OK
-    assert cx.call_status("cxg_gpt_attn_bwd", *[P(t)] * 5, None, *[P(t)] * 3, 1, 4, 600, None, 0,
-                          st) == cx.CXG_ERR_HEAD_DIM
+    assert cx.call_status("cxg_gpt_attn_bwd", *[P(t)] * 5, None, *[P(t)] * 3, 1, 4, 601, None, 0,
+                          st) == cx.CXG_ERR_ALIGN
