@@ -531,6 +531,39 @@ static int lin_check(size_t B, size_t S, size_t D, size_t E, bool* empty)
     return CXG_OK;
 }
 
+// Contexts the forwards have written: device, shape and feature map per
+// context pointer, so that the fused backward refuses a context written for
+// another problem (whose records it would read at the wrong offsets) or by
+// another API's forward (whose sums use another feature map).
+namespace {
+struct CtxTag {
+    int dev, phi;
+    size_t B, S, D, E;
+};
+std::mutex g_ctx_mu;
+std::unordered_map<const void*, CtxTag> g_ctx_tags;
+
+void ctx_record(const void* ctx, int phi, size_t B, size_t S, size_t D, size_t E)
+{
+    int dev = -1;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    g_ctx_tags[ctx] = CtxTag{dev, phi, B, S, D, E};
+}
+
+bool ctx_matches(const void* ctx, int phi, size_t B, size_t S, size_t D, size_t E)
+{
+    int dev = -1;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    auto it = g_ctx_tags.find(ctx);
+    if (it == g_ctx_tags.end())
+        return false;
+    const CtxTag& t = it->second;
+    return t.dev == dev && t.phi == phi && t.B == B && t.S == S && t.D == D && t.E == E;
+}
+} // namespace
+
 static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, const float* K,
                           const float* V, float* O, float* den, float* zc, float* S_buf,
                           float* z_buf, size_t B, size_t S, size_t D, size_t E,
@@ -553,6 +586,7 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
             return CXG_ERR_NULL;
         if (ctx_bytes < need)
             return CXG_ERR_WORKSPACE;
+        ctx_record(ctx, phi, B, S, D, E);
         const LinCtx c = lin_ctx_split(ctx, (int)B, (int)S, (int)D, (int)E);
         return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de,
                                          den_eps, (int)B, (int)S, (int)D, (int)E, c.rec, s, c.tot,
@@ -645,6 +679,8 @@ static int lin_bwd_common(int phi, const float* Q, const float* K, const float* 
         return hip_status(lin_bwd_split_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B,
                                                (int)S, (int)D, (int)E, ws.p, s));
     }
+    if (ctx != nullptr && !ctx_matches(ctx, phi, B, S, D, E))
+        return CXG_ERR_WORKSPACE;
     st = ws.acquire(nullptr, 0,
                     lin_bwd_fused_ws_bytes((int)B, (int)S, (int)D, (int)E, ctx != nullptr), s);
     if (st != CXG_OK)

@@ -178,9 +178,15 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
  * intermediates (dnum = dO/den, dden = -sum_e dO*O/den) stay on chip and no
  * z_cache is needed.  ctx: NULL, or the context cxg_kattn_fwd_ctx wrote for the
  * same Q, K, V and dimensions (the backward then skips re-reading K and V for
- * the prefix state).  D <= 64 and E <= 64 take the fused kernels; widths up
- * to 512 run step 1 and one quadratic-form backward launch (dnum, dden in the
- * library's scratch; ctx is not used), wider ones the split kernels. */
+ * the prefix state).  The library remembers, per context pointer, the device,
+ * dimensions and feature map of the forward that last wrote it: a context
+ * with no such record, or written for other dimensions, another device or
+ * another API's forward (cxg_lin_fwd_ctx, cxg_lin_elu_fwd), is refused with
+ * CXG_ERR_WORKSPACE before any launch.  D <= 64 and E <= 64 take the fused
+ * kernels (sequences of up to 128 rows the quadratic form); widths up to 512
+ * run step 1 and one quadratic-form backward launch (dnum, dden in the
+ * library's scratch); wider ones the split kernels; ctx is not read on these
+ * paths (the forward wrote none: cxg_lin_ctx_size is 0 for them). */
 int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O,
                   const float *dO, const float *den_cache, const void *ctx, float *dQ,
                   float *dK, float *dV, size_t B, size_t S, size_t D, size_t E,

@@ -345,3 +345,34 @@ def test_mean_shifted_inputs(dev, api, use_ctx, B, v_mean, k_mean):
 
     _check_sampled(g, ref, seqs, S,
                    f"{api} B{B} muV{v_mean} muK{k_mean}{' ctx' if use_ctx else ''}")
+
+
+def test_context_pairing_is_checked(dev):
+    """The fused backward refuses a context the matching forward did not write:
+    another shape, another API's forward (another feature map), or a pointer
+    no forward wrote.  Nothing is launched for a refused call."""
+    import torch
+    import cxxgpt_attn as cx
+    B, S, D, E = 2, 300, 64, 64
+    N = B * S
+    Q, K, V, dO = (_t(a, dev) for a in normal_inputs((N, D), (N, E), 41))
+    O, den = _nan(dev, N, E), _nan(dev, N)
+    n = cx.lin_ctx_size(B, S, D, E)
+    ctx = torch.empty(n // 4, device=dev)
+    cx.kattn_fwd_ctx(Q, K, V, O, den, ctx, B, S, D, E)
+    P, st = cx._ptr, cx._stream(None)
+    outs = [_nan(dev, N, D), _nan(dev, N, D), _nan(dev, N, E)]
+    args = [P(Q), P(K), P(V), P(O), P(dO), P(den)]
+    # the matching call is accepted
+    assert cx.call_status("cxg_kattn_bwd", *args, P(ctx), *map(P, outs), B, S, D, E, st) == cx.CXG_OK
+    # another sequence length over the same rows
+    assert cx.call_status("cxg_kattn_bwd", *args, P(ctx), *map(P, outs), 4, S // 2, D, E, st) \
+        == cx.CXG_ERR_WORKSPACE
+    # the phi-outside API's backward with the ELU+1 forward's context
+    assert cx.call_status("cxg_lin_bwd", *args, P(ctx), *map(P, outs), B, S, D, E, st) \
+        == cx.CXG_ERR_WORKSPACE
+    # a buffer no forward wrote
+    other = torch.empty(n // 4, device=dev)
+    assert cx.call_status("cxg_kattn_bwd", *args, P(other), *map(P, outs), B, S, D, E, st) \
+        == cx.CXG_ERR_WORKSPACE
+    torch.cuda.synchronize()
