@@ -13,6 +13,14 @@ credited.
 Other workloads (run after the headline unless --no-secondary; any one of
 them can be made the reported workload with --workload NAME):
   c2legacy  C2 through the legacy signatures (no lse: the backward recomputes it)
+  c2dropin  c2legacy with a null workspace (the C++ drop-in wrappers' calls:
+            the library's cached per-stream scratch)
+  c2graph   c2 captured once in a HIP graph and replayed (not in the default run)
+  mhats     TwoStageGPT's stage-1 shape, B32 H64 S256 Dh8, legacy signatures
+            (two_stage_train.cpp:168-170)
+  gen1, gen64, gen256
+            generate()'s forward at B = 1, S = 1 / 64 / 256, probe heads H8 Dh32
+            (two_stage_gpt.hpp:453-470), latency per call
   c3        ELU+1 linear attention fwd+bwd, B' = 96 sequences, S=4096, D=E=64,
             two_stage API chain kernel_attn_fwd -> bwd_step1 -> bwd_dQ ->
             bwd_dKdV; GB/s of compulsory I/O, (12*S*D + 2*S)*4 bytes/sequence
@@ -24,6 +32,12 @@ them can be made the reported workload with --workload NAME):
             (cxg_lin_elu_fwd -> cxg_lin_elu_bwd on the raw q/k projections)
   c4        Hadamard+Exp linear attention (S=1024) through the linear_cuda API
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
+  c4fused   c4 with the linear part through the fused pair (cxg_lin_fwd_ctx ->
+            cxg_lin_bwd) between the feature-map passes
+  c3wide    TwoStageGPT's stage-2 shape, 32 sequences of S256 with D=E=512
+            (two_stage_train.cpp:168-170), two_stage API chain; c3widefused
+            through the fused pair; lgptwide LinearGPT's shape (8 sequences,
+            S256, D=E=512, linear_train.cpp:168-172) through cxg_lin_elu_*
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
   rope      RoPE fwd + bwd on the stage-1 q/k heads at the C2 shape (in place),
             GB/s of compulsory I/O (each tensor read and written once)
@@ -31,6 +45,7 @@ them can be made the reported workload with --workload NAME):
   c2ropesep C2 with RoPE as separate passes, the reference's call sequence
   gpt       GPT's attention at its training shape (B8 S256, one head of E=512,
             gpt_train.cpp:139/156): cxg_gpt_attn_fwd -> cxg_gpt_attn_bwd
+  gpt768    the same at E=768 (scores kept in memory, FP32 MFMA GEMMs)
   gelu      exact GELU + derivative over the q/k/v expander FFN activations at
             the C2 shape (3 x 2048 x 6144 floats; two_stage_gpt.hpp:86-99), GB/s
   ffn       one expander FFN fwd+bwd (X [2048][768], W1 [6144][768], W2
@@ -164,7 +179,7 @@ def attribute(cx, step, steps):
     cx.prof_enable(False)
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
-              "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
+              "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd", "lin_wide_state",
               "phi_hexp_fwd", "phi_hexp_bwd",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",

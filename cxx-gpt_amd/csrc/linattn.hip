@@ -1389,6 +1389,9 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
                                float* ws, int Bq, int S, int D, int E, int reverse, int mode,
                                hipStream_t st)
 {
+    // short sequences: one launch forms the scanned records
+    if (lin_seq_cpw((S + 15) / 16, p.L / 16) > 0)
+        return lin_seqrec_launch<PHI>(X, Y, w, ws, Bq, S, D, E, p.L, p.nseg, reverse, st);
     dim3 grid((unsigned)(Bq * p.nseg)), block(AGG_THREADS);
     {
         ProfScope ps(st, "lin_agg");

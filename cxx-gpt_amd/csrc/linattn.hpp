@@ -98,6 +98,15 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
                                 hipStream_t st);
+// Segment records of short sequences in one launch (linseq.hip): one pass
+// with two workgroups per sequence forms the records the aggregate + scan
+// pair writes (reverse = 0: exclusive prefix over segments of
+// sum phi(X)^T Y and sum w phi(X); 1: exclusive suffix), for plans where
+// lin_seq_cpw(chunks, chunks per segment) > 0.
+int lin_seq_cpw(int nch, int cps);
+template <int PHI>
+hipError_t lin_seqrec_launch(const float* X, const float* Y, const float* w, float* ws, int Bq,
+                             int S, int D, int E, int L, int nseg, int reverse, hipStream_t st);
 // Wide heads (64 < max(D, E) <= LIN_WIDE_MAX, linwide.hip): the quadratic
 // form on FP32 MFMA.  Forward: O, den (den_eps as lin_fwd_launch) and
 // z_cache (nullable).
