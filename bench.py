@@ -34,6 +34,8 @@ them can be made the reported workload with --workload NAME):
             (phi_hexp fwd x2, linear fwd/step1/dQ/dKdV, phi_hexp bwd x2)
   c4fused   c4 with the linear part through the fused pair (cxg_lin_fwd_ctx ->
             cxg_lin_bwd) between the feature-map passes
+  c4hexp    c4 with the feature map inside the fused pair's kernels
+            (cxg_lin_hexp_fwd -> cxg_lin_hexp_bwd on the raw projections)
   c3wide    TwoStageGPT's stage-2 shape, 32 sequences of S256 with D=E=512
             (two_stage_train.cpp:168-170), two_stage API chain; c3widefused
             through the fused pair; lgptwide LinearGPT's shape (8 sequences,
@@ -576,9 +578,11 @@ def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
 
-def _hexp(c, name, Bq, S, seed, steps, warmup, fused=False):
+def _hexp(c, name, Bq, S, seed, steps, warmup, fused=False, inside=False):
     """fused: the feature maps around the fused pair (cxg_lin_fwd_ctx ->
-    cxg_lin_bwd with the context) instead of the four-call linear_cuda chain."""
+    cxg_lin_bwd with the context) instead of the four-call linear_cuda chain;
+    inside: the feature map inside the fused pair's kernels (cxg_lin_hexp_fwd
+    -> cxg_lin_hexp_bwd on the raw projections)."""
     g = c.gen(seed)
     D = E = 64
     N = Bq * S
@@ -608,28 +612,39 @@ def _hexp(c, name, Bq, S, seed, steps, warmup, fused=False):
             ("cxg_lin_bwd_dKdV", (P(pq), P(pk), P(V), P(dnum), P(dden), P(dpk), P(dV), Bq, S, D,
                                   E, sp)),
         ]
-    step = Stepper(c.cx.lib(), [
-        ("cxg_phi_hexp_fwd", (P(Xq), P(pq), N, D, E, sp)),
-        ("cxg_phi_hexp_fwd", (P(Xk), P(pk), N, D, E, sp)),
-    ] + mid + [
-        ("cxg_phi_hexp_bwd", (P(dpq), P(Xq), P(dxq), N, D, E, sp)),
-        ("cxg_phi_hexp_bwd", (P(dpk), P(Xk), P(dxk), N, D, E, sp)),
-    ])
+    if inside:
+        nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+        ctx = c.empty(max(1, nctx // 4))
+        step = Stepper(c.cx.lib(), [
+            ("cxg_lin_hexp_fwd", (P(Xq), P(Xk), P(V), P(O), P(den), P(ctx), nctx, Bq, S, E, sp)),
+            ("cxg_lin_hexp_bwd", (P(Xq), P(Xk), P(V), P(O), P(dO), P(den), P(ctx), P(dxq),
+                                  P(dxk), P(dV), Bq, S, E, sp)),
+        ])
+    else:
+        step = Stepper(c.cx.lib(), [
+            ("cxg_phi_hexp_fwd", (P(Xq), P(pq), N, D, E, sp)),
+            ("cxg_phi_hexp_fwd", (P(Xk), P(pk), N, D, E, sp)),
+        ] + mid + [
+            ("cxg_phi_hexp_bwd", (P(dpq), P(Xq), P(dxq), N, D, E, sp)),
+            ("cxg_phi_hexp_bwd", (P(dpk), P(Xk), P(dxk), N, D, E, sp)),
+        ])
     ms = timed(step, steps, warmup, c.stream)
     att = attribute(c.cx, step, ("seconds", ms))
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
-    kb = lin_kernel_bytes(Bq, S, D, fused)
+    kb = lin_kernel_bytes(Bq, S, D, fused or inside)
     dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
     ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
             "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
             "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    how = ("feature map inside the fused pair's kernels (cxg_lin_hexp_fwd -> cxg_lin_hexp_bwd)"
+           if inside else
+           "feature maps around the fused pair (cxg_lin_fwd_ctx -> cxg_lin_bwd)" if fused else
+           "linear_cuda API chain incl. feature map")
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
-                config={"workload": f"{name}: Hadamard+Exp linear attention fwd+bwd, " + (
-                            "feature maps around the fused pair (cxg_lin_fwd_ctx -> cxg_lin_bwd)"
-                            if fused else "linear_cuda API chain incl. feature map"),
+                config={"workload": f"{name}: Hadamard+Exp linear attention fwd+bwd, " + how,
                         "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
                 frac=value / HBM_PEAK_GBS, cpu_inputs=None)
 
@@ -738,6 +753,8 @@ def run_workload(c, name, steps, warmup):
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup)
     if name == "c4fused":
         return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup, fused=True)
+    if name == "c4hexp":
+        return _hexp(c, name, 96, 1024, 79, max(20, steps // 2), warmup, inside=True)
     if name == "c3wide":     # TwoStageGPT stage 2 (two_stage_train.cpp:168-170, 193)
         return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "chain")
     if name == "c3widefused":
@@ -803,7 +820,8 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 
 # ---------------------------------------------------------------------------- main
 SECONDARY = ("c2legacy", "c2dropin", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt", "c3wide",
-             "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1", "gen64", "gen256",
+             "c3widefused", "lgptwide", "c4", "c4fused", "c4hexp", "c5", "mhats", "gen1", "gen64",
+             "gen256",
              "rope", "c2rope", "c2ropesep", "gpt", "gpt768", "gelu", "ffn")
 
 
@@ -814,7 +832,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c2dropin", "c2graph", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c5", "mhats", "gen1",
+                             "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c4hexp", "c5",
+                             "mhats", "gen1",
                              "gen64", "gen256", "gpt768", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")

@@ -806,6 +806,93 @@ int cxg_lin_elu_bwd(const float* Xq, const float* Xk, const float* V, const floa
                           E, stream);
 }
 
+// Hadamard+Exp attention block: the feature map fused into the fused pair's
+// kernels (E = D = 64, one Hadamard block, 16-byte aligned rows).  Sequences
+// the quadratic form takes (S <= LIN_QUAD_MAX_S) run the feature-map kernels
+// into scratch around the PHI_NONE kernels instead; they use no context.
+static size_t al256b(size_t b) { return (b + 255) / 256 * 256; }
+
+static int hexp_check(size_t B, size_t S, size_t E, bool* empty)
+{
+    int st = lin_check(B, S, E, E, empty);
+    if (st != CXG_OK || *empty)
+        return st;
+    if (E != 64 || S >= ((size_t)1 << 22))
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+int cxg_lin_hexp_fwd(const float* Xq, const float* Xk, const float* V, float* O,
+                     float* den_cache, void* ctx, size_t ctx_bytes, size_t B, size_t S, size_t E,
+                     cxg_stream_t stream)
+{
+    bool empty;
+    int st = hexp_check(B, S, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Xq || !Xk || !V || !O || !den_cache)
+        return CXG_ERR_NULL;
+    if (!al16c(Xq) || !al16c(Xk) || !al16c(V) || !al16c(O))
+        return CXG_ERR_ALIGN;
+    if (!lin_quad_ok(64, 64, (long)S))
+        return lin_fwd_common(PHI_HEXP, 1, 1, Xq, Xk, V, O, den_cache, nullptr, nullptr, nullptr,
+                              B, S, 64, 64, stream, ctx, ctx_bytes);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t N = B * S, t = al256b(N * 64 * sizeof(float));
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, 2 * t, s);
+    if (st != CXG_OK)
+        return st;
+    float* pq = (float*)ws.p;
+    float* pk = (float*)((char*)ws.p + t);
+    hipError_t e = phi_hexp_fwd_launch(Xq, pq, (long)N, 64, 64, s);
+    if (e == hipSuccess)
+        e = phi_hexp_fwd_launch(Xk, pk, (long)N, 64, 64, s);
+    if (e == hipSuccess)
+        e = lin_wide_fwd_launch(PHI_NONE, pq, pk, V, O, den_cache, nullptr, 1, (int)B, (int)S, 64,
+                                64, s);
+    return hip_status(e);
+}
+
+int cxg_lin_hexp_bwd(const float* Xq, const float* Xk, const float* V, const float* O,
+                     const float* dO, const float* den_cache, const void* ctx, float* dXq,
+                     float* dXk, float* dV, size_t B, size_t S, size_t E, cxg_stream_t stream)
+{
+    bool empty;
+    int st = hexp_check(B, S, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (!Xq || !Xk || !V || !O || !dO || !den_cache || !dXq || !dXk || !dV)
+        return CXG_ERR_NULL;
+    if (!al16c(Xq) || !al16c(Xk) || !al16c(V) || !al16c(O) || !al16c(dO) || !al16c(dXq) ||
+        !al16c(dXk) || !al16c(dV))
+        return CXG_ERR_ALIGN;
+    if (!lin_quad_ok(64, 64, (long)S))
+        return lin_bwd_common(PHI_HEXP, Xq, Xk, V, O, dO, den_cache, ctx, dXq, dXk, dV, B, S, 64,
+                              64, stream);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t N = B * S, t = al256b(N * 64 * sizeof(float));
+    const size_t wsb = lin_bwd_split_ws_bytes((int)B, (int)S, 64, 64);
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, 4 * t + wsb, s);
+    if (st != CXG_OK)
+        return st;
+    char* p = (char*)ws.p;
+    float *pq = (float*)p, *pk = (float*)(p + t), *dpq = (float*)(p + 2 * t),
+          *dpk = (float*)(p + 3 * t);
+    hipError_t e = phi_hexp_fwd_launch(Xq, pq, (long)N, 64, 64, s);
+    if (e == hipSuccess)
+        e = phi_hexp_fwd_launch(Xk, pk, (long)N, 64, 64, s);
+    if (e == hipSuccess)
+        e = lin_bwd_split_launch(PHI_NONE, pq, pk, V, O, dO, den_cache, dpq, dpk, dV, (int)B,
+                                 (int)S, 64, 64, p + 4 * t, s);
+    if (e == hipSuccess)
+        e = phi_hexp_bwd_launch(dpq, Xq, dXq, (long)N, 64, 64, s);
+    if (e == hipSuccess)
+        e = phi_hexp_bwd_launch(dpk, Xk, dXk, (long)N, 64, 64, s);
+    return hip_status(e);
+}
+
 static int phi_check(size_t N, size_t D, size_t E, bool hexp, bool* empty)
 {
     *empty = (N == 0);

@@ -130,11 +130,21 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const bool ok = t0 + crow + 4 * i < tend;
+            if constexpr (PHI == PHI_HEXP) {
+                // the row's 64 columns lie in this lane's 16-lane group
+                const f4 hx = hexp_row4(ax[i], lane);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float xv = Phi<PHI>::f(ax[i][e]);
-                ax[i][e] = (ok && (FW || ccol + e < D)) ? xv : 0.0f;
-                ay[i][e] = (ok && (FW || ccol + e < E)) ? ay[i][e] : 0.0f;
+                for (int e = 0; e < 4; e++) {
+                    ax[i][e] = ok ? hx[e] : 0.0f;
+                    ay[i][e] = ok ? ay[i][e] : 0.0f;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float xv = Phi<PHI>::f(ax[i][e]);
+                    ax[i][e] = (ok && (FW || ccol + e < D)) ? xv : 0.0f;
+                    ay[i][e] = (ok && (FW || ccol + e < E)) ? ay[i][e] : 0.0f;
+                }
             }
             *reinterpret_cast<f4*>(&bX[(crow + 4 * i) * CLD + ccol]) = ax[i];
             *reinterpret_cast<f4*>(&bY[(crow + 4 * i) * CLD + ccol]) = ay[i];
@@ -328,8 +338,20 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     f4 qa[2], ka[2], va[2], qb[2], kb[2], vb[2];
     auto fetch = [&](f4 (&fq)[2], f4 (&fk)[2], f4 (&fv)[2], int t0) {
         const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 2>(fq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(fk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+        if constexpr (PHI == PHI_HEXP) {
+            // Hadamard+Exp transforms whole rows (D = 64): wave h takes chunk
+            // rows 8h + 4i + g, columns 4 l16 .. +3, so that a row's 64 columns
+            // lie in one 16-lane group
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const long r = rb + t0 + min(8 * h + 4 * i + g, tlast - t0);
+                fq[i] = *reinterpret_cast<const f4*>(Q + r * 64 + 4 * l16);
+                fk[i] = *reinterpret_cast<const f4*>(K + r * 64 + 4 * l16);
+            }
+        } else {
+            ldRp<VEC, 2>(fq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+            ldRp<VEC, 2>(fk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+        }
         ldRp<VEC, 2>(fv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
     };
     fetch(qa, ka, va, tbeg);
@@ -361,11 +383,22 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             buffer_store_f4(rzt, (h == 0 && l16 == 0) ? (unsigned)(c * 64 + 16 * dt + 4 * g) * 4u
                                                       : kDropOffset,
                             zR[dt]);
-        finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
-        finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
+        if constexpr (PHI == PHI_HEXP) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int row = 8 * h + 4 * i + g;
+                const bool ok = t0 + row < tend;
+                const f4 hq = hexp_row4(aq[i], lane), hk = hexp_row4(ak[i], lane);
+                *reinterpret_cast<f4*>(&bQ[row * CLD + 4 * l16]) = ok ? hq : f4zero();
+                *reinterpret_cast<f4*>(&bK[row * CLD + 4 * l16]) = ok ? hk : f4zero();
+            }
+        } else {
+            finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
+            finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
+            putRp(bQ, aq, l16, g, 2 * h);
+            putRp(bK, ak, l16, g, 2 * h);
+        }
         finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
-        putRp(bQ, aq, l16, g, 2 * h);
-        putRp(bK, ak, l16, g, 2 * h);
         putRp(bV, av, l16, g, 2 * h);
         // Below the LDS writes, which read the set: refill it with chunk c+2.
         __builtin_amdgcn_sched_barrier(0);
@@ -1196,34 +1229,9 @@ __global__ __launch_bounds__(256) void phi_hexp_bwd_kernel(const float* __restri
     dx[n * E + c] = t * 0.125f;
 }
 
-// Vector forms: a lane holds columns 4q .. 4q+3 (q = lane % 16) of a 64-column
-// block, so the transform's bits 0-1 are in-lane butterflies and bits 2-5
-// exchanges within the 16-lane group, in the same order as fwht64 (bit 0
-// first): the results are fwht64's.  Each thread keeps HX rows' 16-byte
-// loads in flight before any arithmetic.
+// Vector forms (fwht64_f4, linattn_dev.hpp): each thread keeps HX rows'
+// 16-byte loads in flight before any arithmetic.
 constexpr int HX = 4;
-
-__device__ __forceinline__ f4 fwht64_f4(f4 v, int lane)
-{
-    f4 t;
-    t[0] = v[0] + v[1];
-    t[1] = v[0] - v[1];
-    t[2] = v[2] + v[3];
-    t[3] = v[2] - v[3];
-    v[0] = t[0] + t[2];
-    v[1] = t[1] + t[3];
-    v[2] = t[0] - t[2];
-    v[3] = t[1] - t[3];
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float u = __shfl_xor(v[i], m, 64);
-            v[i] = (lane & m) ? (u - v[i]) : (v[i] + u);
-        }
-    }
-    return v;
-}
 
 // phi (N x D, D % 64 == 0): f4 unit u of a row is columns 4u .. 4u+3; blocks
 // that lie within E transform x, the others are zero.  Units past the end
@@ -1398,6 +1406,8 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
         if (mode == 2)
             hipLaunchKernelGGL((lin_agg_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w, ws,
                                Bq, S, D, E, p.nseg, p.L);
+        else if constexpr (PHI == PHI_HEXP)
+            return hipErrorInvalidValue;   // D = E = 64 only
         else if (mode == 1)
             hipLaunchKernelGGL((lin_agg_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w, ws,
                                Bq, S, D, E, p.nseg, p.L);
@@ -1421,13 +1431,21 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
                            void* ws, hipStream_t st)
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_FWD);
-    if (p.quad) {
+    const bool vec = (D % 4 == 0) && (E % 4 == 0) && al16(Q) && al16(K) && al16(V) && al16(O) &&
+                     al16(zc);
+    const int mode = lin_mode(vec, D, E);
+    if constexpr (PHI == PHI_HEXP) {
+        // the fused Hadamard+Exp kernels: D = E = 64, 16-byte rows, the
+        // chunked scan (the callers route other shapes through the
+        // feature-map kernels)
+        if (p.quad || !p.fast || mode != 2)
+            return hipErrorInvalidValue;
+    } else if (p.quad) {
         hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, st);
         if (e == hipSuccess && Sfin != nullptr)
             e = lin_wide_state_launch(PHI, K, V, Sfin, zfin, sfin_de, Bq, S, D, E, st);
         return e;
-    }
-    if (!p.fast) {
+    } else if (!p.fast) {
         float* state = (float*)ws;
         const size_t sm = (size_t)(3 * D + 256) * sizeof(float);
         {
@@ -1442,9 +1460,6 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         }
         return hipGetLastError();
     }
-    const bool vec = (D % 4 == 0) && (E % 4 == 0) && al16(Q) && al16(K) && al16(V) && al16(O) &&
-                     al16(zc);
-    const int mode = lin_mode(vec, D, E);
     float* wsf = (float*)ws;
     if (p.nseg > 1) {
         hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, mode, st);
@@ -1459,6 +1474,8 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
+    else if constexpr (PHI == PHI_HEXP)
+        return hipErrorInvalidValue;
     else if (mode == 1)
         hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
@@ -1481,6 +1498,9 @@ hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* 
     if (phi == PHI_ELU1_LG)
         return fwd_impl<PHI_ELU1_LG>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
                                      den_eps, Bq, S, D, E, ws, st);
+    if (phi == PHI_HEXP)
+        return fwd_impl<PHI_HEXP>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
+                                  den_eps, Bq, S, D, E, ws, st);
     return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
                               den_eps, Bq, S, D, E, ws, st);
 }

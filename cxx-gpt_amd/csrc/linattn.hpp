@@ -7,9 +7,11 @@
 namespace cxg {
 
 // Feature map applied inside the kernels: ELU+1 as two_stage computes it, none
-// (inputs are features already: linear_cuda), or ELU+1 in linear_cuda's
-// phi_elu form (LinearGPT's feature map fused into the scans).
-enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2 };
+// (inputs are features already: linear_cuda), ELU+1 in linear_cuda's
+// phi_elu form (LinearGPT's feature map fused into the scans), or
+// Hadamard+Exp (exp(H x / 8) per 64-column row, phi_hexp fused into the
+// fused pair's kernels; D = E = 64 only).
+enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2, PHI_HEXP = 3 };
 
 // floats per segment record in the scan workspace: 64x64 state [d][e] + z[64]
 constexpr int LIN_WS = 64 * 64 + 64;

@@ -37,12 +37,115 @@ struct Phi<PHI_ELU1_LG> {
     // 2^-25 of expf(x)
     static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
 };
+// PHI_HEXP has no elementwise form: the kernels apply it to whole rows
+// (hexp_row4, hexp_colC below) and leave Phi<PHI_HEXP> undefined, so that no
+// elementwise site can take it by mistake.
 template <>
 struct Phi<PHI_NONE> {
     static __device__ __forceinline__ float f(float x) { return x; }
     static __device__ __forceinline__ float d(float) { return 1.0f; }
     static __device__ __forceinline__ float d_from_f(float) { return 1.0f; }
 };
+
+// ---------------------------------------------------------------------------
+// Hadamard+Exp feature map of a 64-column row: phi(x) = exp((H x) / 8), H the
+// 64x64 Sylvester Hadamard matrix (y_i = sum_j (-1)^popcount(i & j) x_j,
+// phi_hexp_* in linattn.hip).  The transform's butterflies run over the
+// column bits from bit 0 up, as the one-element-per-lane transform does, so
+// every layout gives the same roundings.
+// ---------------------------------------------------------------------------
+
+// The value of lane l ^ M (M = 1, 2, 4, 8: within the lane's 16-lane row)
+// through DPP lane moves, which stay in the VALU (a shuffle through
+// ds_bpermute takes a round trip through the LDS unit).  Rotations are
+// row_ror: lane i receives lane (i - n) mod 16.
+template <int M>
+__device__ __forceinline__ float lane_xor16(float v, int lane)
+{
+    if constexpr (M == 1)
+        return dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    else if constexpr (M == 2)
+        return dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    else if constexpr (M == 8)
+        return dpp_f<0x128>(v);   // row_ror:8
+    else {
+        static_assert(M == 4, "lane_xor16: M in {1, 2, 4, 8}");
+        const float up = dpp_f<0x12C>(v);   // row_ror:12: lane i + 4
+        const float dn = dpp_f<0x124>(v);   // row_ror:4: lane i - 4
+        return (lane & 4) ? dn : up;
+    }
+}
+
+// One butterfly stage over lane bit M: lower lane a + b, upper lane a - b
+// (a the lower lane's value, b the upper's).
+template <int M>
+__device__ __forceinline__ float bfly16(float v, int lane)
+{
+    const float u = lane_xor16<M>(v, lane);
+    return (lane & M) ? (u - v) : (v + u);
+}
+
+// Row-coalesced layout: a lane holds columns 4q .. 4q+3 (q = lane % 16) of a
+// row that the 16 lanes of its group share: bits 0-1 are in-lane, bits 2-5
+// exchanges within the 16-lane group.
+__device__ __forceinline__ f4 fwht64_f4(f4 v, int lane)
+{
+    f4 t;
+    t[0] = v[0] + v[1];
+    t[1] = v[0] - v[1];
+    t[2] = v[2] + v[3];
+    t[3] = v[2] - v[3];
+    v[0] = t[0] + t[2];
+    v[1] = t[1] + t[3];
+    v[2] = t[0] - t[2];
+    v[3] = t[1] - t[3];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        v[i] = bfly16<1>(v[i], lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        v[i] = bfly16<2>(v[i], lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        v[i] = bfly16<4>(v[i], lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        v[i] = bfly16<8>(v[i], lane);
+    return v;
+}
+
+__device__ __forceinline__ f4 hexp_row4(f4 v, int lane)
+{
+    f4 y = fwht64_f4(v, lane);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        y[i] = __expf(y[i] * 0.125f);
+    return y;
+}
+
+// MFMA column layout: x[k] is column 16k + l16 of the lane's row (the row is
+// shared by the 16 lanes of the group): bits 0-3 are exchanges within the
+// group, bits 4-5 in-lane.
+__device__ __forceinline__ void hexp_colC(float (&x)[4], int lane)
+{
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        x[k] = bfly16<1>(x[k], lane);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        x[k] = bfly16<2>(x[k], lane);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        x[k] = bfly16<4>(x[k], lane);
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        x[k] = bfly16<8>(x[k], lane);
+    const float a0 = x[0] + x[1], a1 = x[0] - x[1], a2 = x[2] + x[3], a3 = x[2] - x[3];
+    x[0] = __expf((a0 + a2) * 0.125f);
+    x[1] = __expf((a1 + a3) * 0.125f);
+    x[2] = __expf((a0 - a2) * 0.125f);
+    x[3] = __expf((a1 - a3) * 0.125f);
+}
 
 // ---------------------------------------------------------------------------
 // chunk staging helpers
@@ -69,7 +172,7 @@ __device__ __forceinline__ void ldR(f4 (&v)[4], const float* __restrict__ base, 
 template <int PHI, bool APPLY, bool FW>
 __device__ __forceinline__ void finR(f4 (&v)[4], bool full, bool rok, int ncol, int g)
 {
-    if (APPLY && PHI != PHI_NONE)
+    if constexpr (APPLY && PHI != PHI_NONE)
 #pragma unroll
         for (int ct = 0; ct < 4; ct++)
 #pragma unroll
@@ -120,7 +223,7 @@ __device__ __forceinline__ void ldRp(f4 (&v)[NCT], const float* __restrict__ bas
 template <int PHI, bool APPLY, bool FW, int NCT>
 __device__ __forceinline__ void finRp(f4 (&v)[NCT], bool full, bool rok, int ncol, int g, int ct0)
 {
-    if (APPLY && PHI != PHI_NONE)
+    if constexpr (APPLY && PHI != PHI_NONE)
 #pragma unroll
         for (int i = 0; i < NCT; i++)
 #pragma unroll

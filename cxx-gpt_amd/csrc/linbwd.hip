@@ -59,6 +59,21 @@ __device__ __forceinline__ f4 ld_row4(const float* __restrict__ base, long row, 
     return FW ? v : mask4(v, col, ncol, true);
 }
 
+// The feature map of a row-coalesced f4 (lane: columns 4(lane%16) .. +3 of
+// the row its 16-lane group shares): elementwise, or Hadamard+Exp over the row.
+template <int PHI>
+__device__ __forceinline__ f4 phi_row(f4 v, int lane)
+{
+    if constexpr (PHI == PHI_HEXP) {
+        return hexp_row4(v, lane);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = Phi<PHI>::f(v[i]);
+        return v;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // lin_bagg: per-segment aggregates.  Workgroups [0, Bq*nseg) form the prefix
 // records (X = phi(K), Y = V, w = 1, z table; skipped when the forward's
@@ -128,10 +143,11 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
         const bool ok = t0 + lrow < tend;
         f4 x, y;
         float wv;
+        const f4 px = phi_row<PHI>(s.a, lane);
         if constexpr (!SUF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                x[i] = ok ? Phi<PHI>::f(s.a[i]) : 0.0f;
+                x[i] = ok ? px[i] : 0.0f;
                 y[i] = ok ? s.b[i] : 0.0f;
             }
             wv = 1.0f;
@@ -141,7 +157,7 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
                                         s.c[3] * s.b[3]);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                x[i] = ok ? Phi<PHI>::f(s.a[i]) : 0.0f;
+                x[i] = ok ? px[i] : 0.0f;
                 y[i] = s.c[i] * inv;
             }
             wv = -dot * inv;
@@ -300,9 +316,13 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const float* __restrict__ crec, const float* __restrict__ ctot, const float* __restrict__ anch,
     int nanch, int mf, int nsegf, int S, int D, int E, int nseg, int L, int nchs)
 {
-    __shared__ __attribute__((aligned(16))) float lds[BWD_LDS];
+    // Hadamard+Exp: the chunk's dphi(Q) * phi(Q) and dphi(K) * phi(K), [t][d],
+    // for the row transform that turns them into dQ and dK (see flush below)
+    constexpr int HEXP_LDS = PHI == PHI_HEXP ? 2 * CHUNK : 0;
+    __shared__ __attribute__((aligned(16))) float lds[BWD_LDS + HEXP_LDS];
     float* sS = lds + 2 * BWD_STAGE;   // S* [d][e]
     float* sP = sS + 64 * SLD;         // partial products [wave][M1, X, X^T][lane * 4 + r]
+    float* sH = lds + BWD_LDS;         // Hadamard+Exp only
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x;
@@ -392,6 +412,25 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             an[a] = buffer_load_f4(ra, (unsigned)((16 * w + l16) * 64 + 16 * a + 4 * g) * 4u);
     };
     fetch_anchor(cb + nch - 1);
+    // Hadamard+Exp (D = E = 64): dQ_t = H (dphi(Q_t) * phi(Q_t)) / 8 transforms
+    // whole rows, which the waves hold a 16-column tile of each.  A chunk's
+    // products go to sH at its end and are transformed and stored, as whole
+    // rows (lane: row 4w + g, columns 4 l16 .. +3), by the next chunk between
+    // its two barriers (the first orders them after every wave's write, the
+    // second before the next write); the last chunk's after the walk.  ht0:
+    // first row of the chunk pending in sH, -1 for none.
+    int ht0 = -1;
+    auto flush = [&]() __attribute__((always_inline)) {
+        const f4 hq = *reinterpret_cast<const f4*>(&sH[lrow * CLD + lcol]);
+        const f4 hk = *reinterpret_cast<const f4*>(&sH[CHUNK + lrow * CLD + lcol]);
+        const f4 tq = fwht64_f4(hq, lane) * 0.125f;
+        const f4 tk = fwht64_f4(hk, lane) * 0.125f;
+        const unsigned off = (ht0 >= 0 && ht0 + lrow < tend)
+                                 ? (unsigned)((ht0 + lrow) * 64 + lcol) * 4u
+                                 : kDropOffset;
+        buffer_store_f4(buf_rsrc(dQ + rb * 64), off, tq);
+        buffer_store_f4(buf_rsrc(dK + rb * 64), off, tk);
+    };
     auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * BWD_STAGE;
@@ -407,10 +446,11 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             const float dot = row16_sum(s.d[0] * s.o[0] + s.d[1] * s.o[1] + s.d[2] * s.o[2] +
                                         s.d[3] * s.o[3]);
             f4 q, k, v;
+            const f4 pq = phi_row<PHI>(s.q, lane), pk = phi_row<PHI>(s.k, lane);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                q[i] = ok ? Phi<PHI>::f(s.q[i]) : 0.0f;
-                k[i] = ok ? Phi<PHI>::f(s.k[i]) : 0.0f;
+                q[i] = ok ? pq[i] : 0.0f;
+                k[i] = ok ? pk[i] : 0.0f;
                 v[i] = ok ? s.v[i] : 0.0f;
             }
             if (!FW) {
@@ -428,6 +468,8 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         __builtin_amdgcn_sched_barrier(0);
         fetch(s, max(c - 2, 0));
         __syncthreads();
+        if constexpr (PHI == PHI_HEXP)
+            flush();   // the previous chunk's dQ, dK rows
 
         // partial products over the contraction slice of tile w:
         //   M1[s][t] = phi(Q_s).phi(K_t),  X[s][t] = dnum_s.V_t
@@ -522,10 +564,15 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             for (int r = 0; r < 4; r++)
                 dk = mfma16(qCw[r], M2[r], dk);
             const f4 kRw = *reinterpret_cast<const f4*>(&bK[l16 * CLD + 16 * w + 4 * g]);
+            if constexpr (PHI == PHI_HEXP) {
+                *reinterpret_cast<f4*>(&sH[CHUNK + l16 * CLD + 16 * w + 4 * g]) = dk * kRw;
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                dk[i] *= Phi<PHI>::d_from_f(kRw[i]);
-            if constexpr (FW) {
+                for (int i = 0; i < 4; i++)
+                    dk[i] *= Phi<PHI>::d_from_f(kRw[i]);
+            }
+            if constexpr (PHI == PHI_HEXP) {
+            } else if constexpr (FW) {
                 buffer_store_f4(buf_rsrc(dK + (rb + t0) * D), okt ? soff * 4u : kDropOffset, dk);
             } else if (okt) {
                 store4<VEC>(dK + (rb + t0 + l16) * D, 16 * w + 4 * g, D, dk);
@@ -570,10 +617,16 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             for (int r = 0; r < 4; r++)
                 dq = mfma16(kCw[r], G[r], dq);
             const f4 qRw = *reinterpret_cast<const f4*>(&bQ[l16 * CLD + 16 * w + 4 * g]);
+            if constexpr (PHI == PHI_HEXP) {
+                *reinterpret_cast<f4*>(&sH[l16 * CLD + 16 * w + 4 * g]) = dq * qRw;
+                ht0 = t0;
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                dq[i] *= Phi<PHI>::d_from_f(qRw[i]);
-            if constexpr (FW) {
+                for (int i = 0; i < 4; i++)
+                    dq[i] *= Phi<PHI>::d_from_f(qRw[i]);
+            }
+            if constexpr (PHI == PHI_HEXP) {
+            } else if constexpr (FW) {
                 buffer_store_f4(buf_rsrc(dQ + (rb + t0) * D), okt ? soff * 4u : kDropOffset, dq);
             } else if (okt) {
                 store4<VEC>(dQ + (rb + t0 + l16) * D, 16 * w + 4 * g, D, dq);
@@ -606,6 +659,10 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     }
     if (c == 0)
         chunk(sa, 0);
+    if constexpr (PHI == PHI_HEXP) {
+        __syncthreads();
+        flush();
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -723,6 +780,8 @@ static void bwd_dispatch(const LinPlan& p, const float* Q, const float* K, const
                      al16(dO) && al16(dQ) && al16(dK) && al16(dV);
     if (vec && D == 64 && E == 64)
         bwd_launch_t<PHI, true, true>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
+    else if constexpr (PHI == PHI_HEXP)
+        return;   // D = E = 64 with 16-byte rows only (checked by the launcher)
     else if (vec)
         bwd_launch_t<PHI, true, false>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
@@ -760,10 +819,15 @@ hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const f
     a.anch = a.zt + (size_t)Bq * ((S + 15) / 16) * 64;
     a.c = ctx != nullptr ? lin_ctx_split(const_cast<void*>(ctx), Bq, S, D, E)
                          : LinCtx{nullptr, nullptr, nullptr, nullptr};
+    if (phi == PHI_HEXP && !(D == 64 && E == 64 && al16(Q) && al16(K) && al16(V) && al16(O) &&
+                             al16(dO) && al16(dQ) && al16(dK) && al16(dV)))
+        return hipErrorInvalidValue;
     if (phi == PHI_ELU1)
         bwd_dispatch<PHI_ELU1>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else if (phi == PHI_ELU1_LG)
         bwd_dispatch<PHI_ELU1_LG>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
+    else if (phi == PHI_HEXP)
+        bwd_dispatch<PHI_HEXP>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
         bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     return hipGetLastError();

@@ -123,9 +123,18 @@ __global__ __launch_bounds__(SEQ_THREADS) void lin_seqrec_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const bool rok = 16 * c + 4 * g + r < S;
+            if constexpr (PHI == PHI_HEXP) {
+                // row 16c + 4g + r: columns 16k + l16 over the 16-lane group
+                float xr[4] = {x[0][r], x[1][r], x[2][r], x[3][r]};
+                hexp_colC(xr, lane);
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                x[k][r] = (rok && (FW || 16 * k + l16 < D)) ? Phi<PHI>::f(x[k][r]) : 0.0f;
+                for (int k = 0; k < 4; k++)
+                    x[k][r] = rok ? xr[k] : 0.0f;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    x[k][r] = (rok && (FW || 16 * k + l16 < D)) ? Phi<PHI>::f(x[k][r]) : 0.0f;
+            }
 #pragma unroll
             for (int jj = 0; jj < 2; jj++)
                 y[jj][r] = (rok && (FW || 16 * (2 * h + jj) + l16 < E)) ? y[jj][r] : 0.0f;
@@ -237,20 +246,22 @@ hipError_t lin_seqrec_launch(const float* X, const float* Y, const float* w, flo
         return hipErrorInvalidValue;
     const int wps = cps / cpw;
     const bool fw = D == 64 && E == 64;
+    if (PHI == PHI_HEXP && !fw)
+        return hipErrorInvalidValue;
     const dim3 grid(seq_grid(Bq)), block(SEQ_THREADS);
     ProfScope ps(st, "lin_seqrec");
     if (reverse) {
         if (fw)
             hipLaunchKernelGGL((lin_seqrec_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
-        else
+        else if constexpr (PHI != PHI_HEXP)
             hipLaunchKernelGGL((lin_seqrec_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
     } else {
         if (fw)
             hipLaunchKernelGGL((lin_seqrec_kernel<PHI, false, true>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
-        else
+        else if constexpr (PHI != PHI_HEXP)
             hipLaunchKernelGGL((lin_seqrec_kernel<PHI, false, false>), grid, block, 0, st, X, Y,
                                w, ws, Bq, S, D, E, cpw, wps, nseg);
     }
@@ -264,5 +275,7 @@ template hipError_t lin_seqrec_launch<PHI_NONE>(const float*, const float*, cons
 template hipError_t lin_seqrec_launch<PHI_ELU1_LG>(const float*, const float*, const float*,
                                                    float*, int, int, int, int, int, int, int,
                                                    hipStream_t);
+template hipError_t lin_seqrec_launch<PHI_HEXP>(const float*, const float*, const float*, float*,
+                                                int, int, int, int, int, int, int, hipStream_t);
 
 } // namespace cxg

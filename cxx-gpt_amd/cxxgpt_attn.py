@@ -54,6 +54,8 @@ SIGNATURES = {
     "cxg_lin_fwd_ctx": [_vp] * 6 + [_sz] * 5 + [_vp],
     "cxg_lin_elu_fwd": [_vp] * 6 + [_sz] * 4 + [_vp],
     "cxg_lin_elu_bwd": [_vp] * 10 + [_sz] * 3 + [_vp],
+    "cxg_lin_hexp_fwd": [_vp] * 6 + [_sz] * 4 + [_vp],
+    "cxg_lin_hexp_bwd": [_vp] * 10 + [_sz] * 3 + [_vp],
     "cxg_phi_elu_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_elu_bwd": [_vp, _vp, _vp, _sz, _sz, _sz, _vp],
     "cxg_phi_hexp_fwd": [_vp, _vp, _sz, _sz, _sz, _vp],
@@ -272,6 +274,19 @@ def lin_elu_fwd(Xq, Xk, V, O, den, ctx, B, S, E, stream=None):
 def lin_elu_bwd(Xq, Xk, V, O, dO, den, dXq, dXk, dV, B, S, E, ctx=None, stream=None):
     """LinearGPT attention backward: step1 + dQ + dKdV + phi_elu_backward, fused."""
     _call("cxg_lin_elu_bwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(dO), _ptr(den),
+          _ptr(ctx), _ptr(dXq), _ptr(dXk), _ptr(dV), B, S, E, _stream(stream))
+
+
+def lin_hexp_fwd(Xq, Xk, V, O, den, ctx, B, S, E, stream=None):
+    """Hadamard+Exp attention forward with the feature map fused (raw projections in)."""
+    nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
+    _call("cxg_lin_hexp_fwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
+          B, S, E, _stream(stream))
+
+
+def lin_hexp_bwd(Xq, Xk, V, O, dO, den, dXq, dXk, dV, B, S, E, ctx=None, stream=None):
+    """Hadamard+Exp attention backward: step1 + dQ + dKdV + the feature map's backward, fused."""
+    _call("cxg_lin_hexp_bwd", _ptr(Xq), _ptr(Xk), _ptr(V), _ptr(O), _ptr(dO), _ptr(den),
           _ptr(ctx), _ptr(dXq), _ptr(dXk), _ptr(dV), B, S, E, _stream(stream))
 
 

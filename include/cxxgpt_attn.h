@@ -266,6 +266,27 @@ int cxg_lin_elu_bwd(const float *Xq, const float *Xk, const float *V, const floa
                     const float *dO, const float *den_cache, const void *ctx, float *dXq,
                     float *dXk, float *dV, size_t B, size_t S, size_t E, cxg_stream_t stream);
 
+/* Hadamard+Exp attention block with the feature map fused into the scans: no
+ * single counterpart in the reference, whose callers (BASELINE C4) apply
+ * phi(x) = exp(H x / 8) (cxg_phi_hexp_fwd below) to the raw projections
+ * before causal_linear_attention_fwd and map the feature gradients back with
+ * phi's backward after the three backward calls (linear_cuda_kernels.cu:
+ * 10-298).  cxg_lin_hexp_fwd: O and den_cache (eps included) from the raw
+ * Xq, Xk (B*S, E) and V, plus the context for the backward
+ * (cxg_lin_ctx_size(B, S, E, E) bytes; may be NULL with ctx_bytes 0).
+ * cxg_lin_hexp_bwd: dXq, dXk (B*S, E) with respect to the raw projections,
+ * and dV.  E must be 64 (one Hadamard block; other widths: cxg_phi_hexp_*
+ * around cxg_lin_fwd / cxg_lin_bwd) and S < 2^22; every row pointer 16-byte
+ * aligned (CXG_ERR_ALIGN otherwise).  Sequences of at most 128 rows, which
+ * the quadratic-form kernels take, run the feature-map kernels through the
+ * library's scratch instead and use no context. */
+int cxg_lin_hexp_fwd(const float *Xq, const float *Xk, const float *V, float *O,
+                     float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
+                     size_t E, cxg_stream_t stream);
+int cxg_lin_hexp_bwd(const float *Xq, const float *Xk, const float *V, const float *O,
+                     const float *dO, const float *den_cache, const void *ctx, float *dXq,
+                     float *dXk, float *dV, size_t B, size_t S, size_t E, cxg_stream_t stream);
+
 /* linear_cuda::phi_elu_forward / phi_elu_backward (linear_cuda_kernels.cuh:39-46,
  * linear_cuda_kernels.cu:305-378).  x (N, E) -> phi (N, D), columns >= E zero;
  * dx (N, E) = dphi[:, :E] * phi'(x). */
