@@ -58,8 +58,9 @@ Inputs are synthetic N(0,1) tensors generated on the GPU from fixed seeds and
 resident in HBM before timing starts.  Timing: W warmup steps, then K steps
 between two HIP events on the launch stream.  The roofline object is
 measured live: after the timed region the same steps run again with the
-library's per-launch HIP-event hook on (events recorded on the launch
-stream), giving each kernel's mean duration; the dominant kernel's
+library's timing hook on (each launch records the start and end of its own
+dispatch into HIP events on the launch stream), giving each kernel's mean
+duration; the dominant kernel's
 algorithmic FLOPs (or bytes) per launch divided by that duration is
 `achieved`.  The CPU baseline times the C oracle (the restated CPU reference,
 test infrastructure) on the host cores over a bounded sample of the same
@@ -165,10 +166,10 @@ def steps_for(ms_per_step, floor, seconds=SUSTAIN_S, cap=20000):
 
 def attribute(cx, step, steps):
     """Mean device duration (ms) and launch count per kernel tag, from the
-    library's per-launch HIP events on the launch stream (the event pair adds
-    a microsecond or two to each launch; rocprofv3's kernel trace is the
-    cross-check).  `steps`: a count, or ("seconds", ms_per_step) for a
-    time-based pass."""
+    library's timing hook: the launches record their dispatches' start and end
+    into HIP events on the launch stream (rocprofv3's kernel trace is the
+    cross-check; they agree within about 1%).  `steps`: a count, or
+    ("seconds", ms_per_step) for a time-based pass."""
     import torch
     if isinstance(steps, tuple):
         steps = steps_for(steps[1], 10)
@@ -875,7 +876,8 @@ def main():
         "step_frac_of_peak": round(r["frac"], 4),
     }
     out["roofline"]["duration_source"] = (
-        "mean of HIP-event pairs recorded around each launch on its stream (library hook), "
+        "mean dispatch duration from the start/stop HIP events each launch records itself "
+        "(hipExtLaunchKernelGGL through the library's timing hook, on the launch stream), "
         f"over about {SUSTAIN_S} s of steps; rocprofv3 kernel-trace averages are in profiles/")
     out["roofline"]["traffic_source"] = (
         "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch, scaled by the same counters "

@@ -48,7 +48,7 @@ hipEvent_t prof_event()
 
 bool prof_enabled() { return g_prof_on; }
 
-int prof_begin(hipStream_t s)
+int prof_begin(hipEvent_t* a, hipEvent_t* b)
 {
     std::lock_guard<std::mutex> lk(g_prof_mu);
     ProfRec r;
@@ -56,19 +56,45 @@ int prof_begin(hipStream_t s)
     r.b = prof_event();
     if (!r.a || !r.b)
         return -1;
-    (void)hipEventRecord(r.a, s);
+    *a = r.a;
+    *b = r.b;
     g_prof_recs.push_back(r);
     return (int)g_prof_recs.size() - 1;
 }
 
-void prof_end(int token, hipStream_t s, const char* name)
+void prof_end(int token, const char* name)
 {
     std::lock_guard<std::mutex> lk(g_prof_mu);
     if (token < 0 || token >= (int)g_prof_recs.size())
         return;
     g_prof_recs[token].name = name;
-    (void)hipEventRecord(g_prof_recs[token].b, s);
 }
+
+namespace {
+thread_local ProfScope* t_prof_scope = nullptr;
+}
+
+ProfScope::ProfScope(hipStream_t, const char* n)
+    : tok(-1), name(n), a(nullptr), b(nullptr), started(false), outer(t_prof_scope)
+{
+    if (prof_enabled())
+        tok = prof_begin(&a, &b);
+    if (tok >= 0)
+        t_prof_scope = this;
+}
+
+ProfScope::~ProfScope()
+{
+    if (tok >= 0) {
+        t_prof_scope = outer;
+        // a scope that launched nothing has unrecorded events: its record is
+        // left unnamed and never matches a query
+        if (started)
+            prof_end(tok, name);
+    }
+}
+
+ProfScope* prof_scope() { return t_prof_scope; }
 
 // ---------------------------------------------------------------------------
 // status helpers

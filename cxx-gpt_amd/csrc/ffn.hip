@@ -319,23 +319,23 @@ static void launch_main(int epi, dim3 grid, hipStream_t st, const GemmArgs& a)
 {
     switch (epi) {
     case FFN_EPI_GELU:
-        hipLaunchKernelGGL((ffn_gemm_kernel<AK, BK, FFN_EPI_GELU>), grid, dim3(256), 0, st, a);
+        CXG_LAUNCH((ffn_gemm_kernel<AK, BK, FFN_EPI_GELU>), grid, dim3(256), 0, st, a);
         break;
     case FFN_EPI_DGELU:
-        hipLaunchKernelGGL((ffn_gemm_kernel<AK, BK, FFN_EPI_DGELU>), grid, dim3(256), 0, st, a);
+        CXG_LAUNCH((ffn_gemm_kernel<AK, BK, FFN_EPI_DGELU>), grid, dim3(256), 0, st, a);
         break;
     case FFN_EPI_ACCUM:
-        hipLaunchKernelGGL((ffn_gemm_kernel<AK, BK, FFN_EPI_ACCUM>), grid, dim3(256), 0, st, a);
+        CXG_LAUNCH((ffn_gemm_kernel<AK, BK, FFN_EPI_ACCUM>), grid, dim3(256), 0, st, a);
         break;
     default:
-        hipLaunchKernelGGL((ffn_gemm_kernel<AK, BK, FFN_EPI_STORE>), grid, dim3(256), 0, st, a);
+        CXG_LAUNCH((ffn_gemm_kernel<AK, BK, FFN_EPI_STORE>), grid, dim3(256), 0, st, a);
     }
 }
 
 template <int EPI>
 static void launch_fixup(dim3 grid, hipStream_t st, const GemmArgs& a)
 {
-    hipLaunchKernelGGL((ffn_fixup_kernel<EPI>), grid, dim3(256), 0, st, a);
+    CXG_LAUNCH((ffn_fixup_kernel<EPI>), grid, dim3(256), 0, st, a);
 }
 
 hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st)

@@ -77,18 +77,18 @@ hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t
         const long ntiles = (n / 4 + GELU_TILE - 1) / GELU_TILE;
         const unsigned blocks = (unsigned)std::max(1L, std::min(ntiles, 1L << 20));
         if (deriv)
-            hipLaunchKernelGGL((gelu_vec_kernel<true>), dim3(blocks), dim3(256), 0, st, A, C, n,
+            CXG_LAUNCH((gelu_vec_kernel<true>), dim3(blocks), dim3(256), 0, st, A, C, n,
                                ntiles);
         else
-            hipLaunchKernelGGL((gelu_vec_kernel<false>), dim3(blocks), dim3(256), 0, st, A, C, n,
+            CXG_LAUNCH((gelu_vec_kernel<false>), dim3(blocks), dim3(256), 0, st, A, C, n,
                                ntiles);
     } else {
         const long want = (n + 255) / 256;
         const unsigned blocks = (unsigned)std::max(1L, std::min(want, 8L * cus));
         if (deriv)
-            hipLaunchKernelGGL((gelu_kernel<true>), dim3(blocks), dim3(256), 0, st, A, C, n);
+            CXG_LAUNCH((gelu_kernel<true>), dim3(blocks), dim3(256), 0, st, A, C, n);
         else
-            hipLaunchKernelGGL((gelu_kernel<false>), dim3(blocks), dim3(256), 0, st, A, C, n);
+            CXG_LAUNCH((gelu_kernel<false>), dim3(blocks), dim3(256), 0, st, A, C, n);
     }
     return hipGetLastError();
 }

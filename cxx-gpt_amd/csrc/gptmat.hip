@@ -118,7 +118,7 @@ static hipError_t softmax(float* P, const float* lse_in, float* lse_out, int S, 
 {
     ProfScope ps(st, "gpt_softmax");
     const float c = kLog2e / sqrtf((float)E);
-    hipLaunchKernelGGL(gpt_softmax_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256), 0, st, P,
+    CXG_LAUNCH(gpt_softmax_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256), 0, st, P,
                        lse_in, lse_out, S, c);
     return hipGetLastError();
 }
@@ -158,7 +158,7 @@ hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, co
             e = gemm(dO + r0, E, true, V + r0, E, true, dS, S, S, S, E, gws, st);
         if (e == hipSuccess) {
             ProfScope ps(st, "gpt_softmax_bwd");
-            hipLaunchKernelGGL(gpt_softmax_bwd_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256),
+            CXG_LAUNCH(gpt_softmax_bwd_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256),
                                0, st, P, dS, S, scale);
             e = hipGetLastError();
         }

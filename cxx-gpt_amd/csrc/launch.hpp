@@ -3,6 +3,7 @@
 // internal launcher declarations.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -10,29 +11,45 @@
 namespace cxg {
 
 // ---- per-kernel timing hook (off by default) --------------------------------
-// When enabled, every kernel launch is bracketed by two hipEvents recorded on
-// the launch stream; prof_query() synchronises them and reports the summed
-// device time per kernel name.  Used by the benchmark to attribute time to
-// the dominant kernel; costs nothing when disabled.
+// When enabled, a ProfScope names the kernel launches made inside it and
+// times them with two hipEvents that the launches themselves record: every
+// kernel goes out through CXG_LAUNCH, which passes the innermost open scope's
+// events to hipExtLaunchKernelGGL (the first launch of the scope sets the
+// start event, each launch the stop event), so the events carry the
+// dispatches' own start and end times, as a profiler's kernel trace does,
+// rather than those of markers placed around the launches.  prof_query()
+// synchronises them and reports the summed device time per name.  Used by the
+// benchmark to attribute time to the dominant kernel; with the hook off a
+// launch is a plain hipLaunchKernelGGL.
 bool prof_enabled();
-int prof_begin(hipStream_t s);
-void prof_end(int token, hipStream_t s, const char* name);
+int prof_begin(hipEvent_t* a, hipEvent_t* b);
+void prof_end(int token, const char* name);
 
 struct ProfScope {
     int tok;
-    hipStream_t s;
     const char* name;
-    ProfScope(hipStream_t st, const char* n) : tok(-1), s(st), name(n)
-    {
-        if (prof_enabled())
-            tok = prof_begin(s);
-    }
-    ~ProfScope()
-    {
-        if (tok >= 0)
-            prof_end(tok, s, name);
-    }
+    hipEvent_t a, b;
+    bool started;
+    ProfScope* outer;
+    ProfScope(hipStream_t, const char* n);
+    ~ProfScope();
 };
+// The innermost open scope of this thread whose events the next launch
+// records (null with the hook off or no scope open).
+ProfScope* prof_scope();
+
+#define CXG_LAUNCH(kernel, grid, block, shmem, stream, ...)                                    \
+    do {                                                                                      \
+        ::cxg::ProfScope* cxg_ps_ = ::cxg::prof_scope();                                     \
+        if (cxg_ps_ != nullptr) {                                                             \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream,                         \
+                                  cxg_ps_->started ? nullptr : cxg_ps_->a, cxg_ps_->b, 0,     \
+                                  __VA_ARGS__);                                               \
+            cxg_ps_->started = true;                                                          \
+        } else {                                                                              \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);              \
+        }                                                                                     \
+    } while (0)
 
 // ---- launchers (defined next to their kernels) -----------------------------
 // Softmax MHA.  Layout (B*S, H*Dh) row-major.  lse is [B*H][S] (natural log of

@@ -1404,21 +1404,21 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
     {
         ProfScope ps(st, "lin_agg");
         if (mode == 2)
-            hipLaunchKernelGGL((lin_agg_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w, ws,
+            CXG_LAUNCH((lin_agg_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w, ws,
                                Bq, S, D, E, p.nseg, p.L);
         else if constexpr (PHI == PHI_HEXP)
             return hipErrorInvalidValue;   // D = E = 64 only
         else if (mode == 1)
-            hipLaunchKernelGGL((lin_agg_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w, ws,
+            CXG_LAUNCH((lin_agg_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w, ws,
                                Bq, S, D, E, p.nseg, p.L);
         else
-            hipLaunchKernelGGL((lin_agg_kernel<PHI, false, false>), grid, block, 0, st, X, Y, w,
+            CXG_LAUNCH((lin_agg_kernel<PHI, false, false>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, p.nseg, p.L);
     }
     {
         ProfScope ps(st, "lin_scan");
         const long n = (long)Bq * LIN_WS;
-        hipLaunchKernelGGL(lin_scan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+        CXG_LAUNCH(lin_scan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                            ws, Bq, p.nseg, reverse);
     }
     return hipGetLastError();
@@ -1450,12 +1450,12 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         const size_t sm = (size_t)(3 * D + 256) * sizeof(float);
         {
             ProfScope ps(st, "lin_fwd_generic");
-            hipLaunchKernelGGL((lin_fwd_generic_kernel<PHI>), dim3(Bq), dim3(256), sm, st, Q, K,
+            CXG_LAUNCH((lin_fwd_generic_kernel<PHI>), dim3(Bq), dim3(256), sm, st, Q, K,
                                V, O, den, zc, state, zfin, den_eps, S, D, E);
         }
         if (Sfin != nullptr) {
             const long n = (long)Bq * D * E;
-            hipLaunchKernelGGL(lin_state_copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
+            CXG_LAUNCH(lin_state_copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256),
                                0, st, state, Sfin, (long)Bq, D, E, sfin_de);
         }
         return hipGetLastError();
@@ -1471,17 +1471,17 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
     dim3 grid((unsigned)(Bq * p.nseg)), block(FWD_THREADS);
     ProfScope ps(st, "lin_fwd");
     if (mode == 2)
-        hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
+        CXG_LAUNCH((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     else if constexpr (PHI == PHI_HEXP)
         return hipErrorInvalidValue;
     else if (mode == 1)
-        hipLaunchKernelGGL((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
+        CXG_LAUNCH((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     else
-        hipLaunchKernelGGL((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
+        CXG_LAUNCH((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
                            p.L);
     return hipGetLastError();
@@ -1512,10 +1512,10 @@ hipError_t lin_step1_launch(const float* O, const float* dO, const float* den, f
     dim3 grid((unsigned)((N * 16 + 255) / 256)), block(256);
     ProfScope ps(st, "lin_step1");
     if (vec)
-        hipLaunchKernelGGL((lin_step1_kernel<true>), grid, block, 0, st, O, dO, den, dnum, dden,
+        CXG_LAUNCH((lin_step1_kernel<true>), grid, block, 0, st, O, dO, den, dnum, dden,
                            N, E);
     else
-        hipLaunchKernelGGL((lin_step1_kernel<false>), grid, block, 0, st, O, dO, den, dnum, dden,
+        CXG_LAUNCH((lin_step1_kernel<false>), grid, block, 0, st, O, dO, den, dnum, dden,
                            N, E);
     return hipGetLastError();
 }
@@ -1531,7 +1531,7 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
                                    st);
     if (!p.fast) {
         ProfScope ps(st, "lin_dq_generic");
-        hipLaunchKernelGGL((lin_dq_generic_kernel<PHI>), dim3(Bq), dim3(256), 0, st, K, V, dnum,
+        CXG_LAUNCH((lin_dq_generic_kernel<PHI>), dim3(Bq), dim3(256), 0, st, K, V, dnum,
                            dden, zc, Q, dQ, (float*)ws, S, D, E);
         return hipGetLastError();
     }
@@ -1549,13 +1549,13 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
     dim3 grid((unsigned)(Bq * p.nseg)), block(DQ_THREADS);
     ProfScope ps(st, "lin_dq");
     if (mode == 2)
-        hipLaunchKernelGGL((lin_dq_kernel<PHI, true, true>), grid, block, 0, st, K, V, dnum, dden, zc,
+        CXG_LAUNCH((lin_dq_kernel<PHI, true, true>), grid, block, 0, st, K, V, dnum, dden, zc,
                            Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
     else if (mode == 1)
-        hipLaunchKernelGGL((lin_dq_kernel<PHI, true, false>), grid, block, 0, st, K, V, dnum, dden, zc,
+        CXG_LAUNCH((lin_dq_kernel<PHI, true, false>), grid, block, 0, st, K, V, dnum, dden, zc,
                            Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
     else
-        hipLaunchKernelGGL((lin_dq_kernel<PHI, false, false>), grid, block, 0, st, K, V, dnum, dden, zc,
+        CXG_LAUNCH((lin_dq_kernel<PHI, false, false>), grid, block, 0, st, K, V, dnum, dden, zc,
                            Q, dQ, wsf, Bq, S, D, E, p.nseg, p.L);
     return hipGetLastError();
 }
@@ -1581,7 +1581,7 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
         return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, nullptr, dK, dV, Bq, S, D, E, 1, st);
     if (!p.fast) {
         ProfScope ps(st, "lin_dkdv_generic");
-        hipLaunchKernelGGL((lin_dkdv_generic_kernel<PHI>), dim3(Bq), dim3(256),
+        CXG_LAUNCH((lin_dkdv_generic_kernel<PHI>), dim3(Bq), dim3(256),
                            (size_t)D * sizeof(float), st, Q, K, V, dnum, dden, dK, dV, (float*)ws,
                            S, D, E);
         return hipGetLastError();
@@ -1600,13 +1600,13 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
     dim3 grid((unsigned)(Bq * p.nseg)), block(DKDV_THREADS);
     ProfScope ps(st, "lin_dkdv");
     if (mode == 2)
-        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, dnum, dden,
+        CXG_LAUNCH((lin_dkdv_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, dnum, dden,
                            dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
     else if (mode == 1)
-        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, dnum, dden,
+        CXG_LAUNCH((lin_dkdv_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, dnum, dden,
                            dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
     else
-        hipLaunchKernelGGL((lin_dkdv_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, dnum, dden,
+        CXG_LAUNCH((lin_dkdv_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, dnum, dden,
                            dK, dV, wsf, Bq, S, D, E, p.nseg, p.L);
     return hipGetLastError();
 }
@@ -1664,11 +1664,11 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
         ProfScope ps(st, "lin_zc");
         dim3 grid((unsigned)((D + 255) / 256), (unsigned)Bq);
         if (phi == PHI_ELU1)
-            hipLaunchKernelGGL(lin_zc_kernel<PHI_ELU1>, grid, dim3(256), 0, st, K, zc, S, D);
+            CXG_LAUNCH(lin_zc_kernel<PHI_ELU1>, grid, dim3(256), 0, st, K, zc, S, D);
         else if (phi == PHI_ELU1_LG)
-            hipLaunchKernelGGL(lin_zc_kernel<PHI_ELU1_LG>, grid, dim3(256), 0, st, K, zc, S, D);
+            CXG_LAUNCH(lin_zc_kernel<PHI_ELU1_LG>, grid, dim3(256), 0, st, K, zc, S, D);
         else
-            hipLaunchKernelGGL(lin_zc_kernel<PHI_NONE>, grid, dim3(256), 0, st, K, zc, S, D);
+            CXG_LAUNCH(lin_zc_kernel<PHI_NONE>, grid, dim3(256), 0, st, K, zc, S, D);
     }
     hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);
     if (e == hipSuccess)
@@ -1682,7 +1682,7 @@ hipError_t phi_elu_fwd_launch(const float* x, float* phi, long N, int D, int E, 
 {
     const long n = N * D;
     ProfScope ps(st, "phi_elu_fwd");
-    hipLaunchKernelGGL(phi_elu_fwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
+    CXG_LAUNCH(phi_elu_fwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x,
                        phi, N, D, E);
     return hipGetLastError();
 }
@@ -1692,7 +1692,7 @@ hipError_t phi_elu_bwd_launch(const float* dphi, const float* x, float* dx, long
 {
     const long n = N * E;
     ProfScope ps(st, "phi_elu_bwd");
-    hipLaunchKernelGGL(phi_elu_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+    CXG_LAUNCH(phi_elu_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        dphi, x, dx, N, D, E);
     return hipGetLastError();
 }
@@ -1702,13 +1702,13 @@ hipError_t phi_hexp_fwd_launch(const float* x, float* phi, long N, int D, int E,
     ProfScope ps(st, "phi_hexp_fwd");
     if (D % 64 == 0 && E % 4 == 0 && al16(x) && al16(phi)) {
         const long units = N * (D / 4);
-        hipLaunchKernelGGL(phi_hexp_fwd_vec_kernel,
+        CXG_LAUNCH(phi_hexp_fwd_vec_kernel,
                            dim3((unsigned)((units + 256L * HX - 1) / (256L * HX))), dim3(256), 0,
                            st, x, phi, N, D, E);
         return hipGetLastError();
     }
     const long waves = N * ((D + 63) / 64);
-    hipLaunchKernelGGL(phi_hexp_fwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
+    CXG_LAUNCH(phi_hexp_fwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
                        0, st, x, phi, N, D, E);
     return hipGetLastError();
 }
@@ -1719,13 +1719,13 @@ hipError_t phi_hexp_bwd_launch(const float* dphi, const float* x, float* dx, lon
     ProfScope ps(st, "phi_hexp_bwd");
     if (E % 64 == 0 && D % 4 == 0 && al16(dphi) && al16(x) && al16(dx)) {
         const long units = N * (E / 4);
-        hipLaunchKernelGGL(phi_hexp_bwd_vec_kernel,
+        CXG_LAUNCH(phi_hexp_bwd_vec_kernel,
                            dim3((unsigned)((units + 256L * HX - 1) / (256L * HX))), dim3(256), 0,
                            st, dphi, x, dx, N, D, E);
         return hipGetLastError();
     }
     const long waves = N * (E / 64);
-    hipLaunchKernelGGL(phi_hexp_bwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
+    CXG_LAUNCH(phi_hexp_bwd_kernel, dim3((unsigned)((waves * 64 + 255) / 256)), dim3(256),
                        0, st, dphi, x, dx, N, D, E);
     return hipGetLastError();
 }

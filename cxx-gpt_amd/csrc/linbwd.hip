@@ -754,18 +754,18 @@ static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const
     const unsigned nb = (unsigned)((pre ? Bq * p.nseg : 0) + Bq * (p.nseg - 1));
     if (nb > 0) {
         ProfScope ps(st, "lin_bagg");
-        hipLaunchKernelGGL((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
+        CXG_LAUNCH((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
                            Q, K, V, O, dO, den, a.wsP, a.wsB, a.zt, a.anch, pre ? nanch : 0, Bq,
                            S, D, E, p.nseg, p.L, nchs, pre ? 1 : 0);
     }
     {
         ProfScope ps(st, "lin_bscan");
         const long n = (pre ? 2L : 1L) * Bq * LIN_WS;
-        hipLaunchKernelGGL(lin_bscan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+        CXG_LAUNCH(lin_bscan_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                            a.wsP, a.wsB, Bq, p.nseg, pre ? 1 : 0);
     }
     ProfScope ps(st, "lin_bwd");
-    hipLaunchKernelGGL((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
+    CXG_LAUNCH((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
                        dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, a.wsP, a.wsB,
                        pre ? a.zt : a.c.zt, a.c.rec, a.c.tot, pre ? a.anch : a.c.anch, nanch,
                        a.mf, a.nsegf, S, D, E, p.nseg, p.L, nchs);

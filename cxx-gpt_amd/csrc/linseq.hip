@@ -252,17 +252,17 @@ hipError_t lin_seqrec_launch(const float* X, const float* Y, const float* w, flo
     ProfScope ps(st, "lin_seqrec");
     if (reverse) {
         if (fw)
-            hipLaunchKernelGGL((lin_seqrec_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w,
+            CXG_LAUNCH((lin_seqrec_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
         else if constexpr (PHI != PHI_HEXP)
-            hipLaunchKernelGGL((lin_seqrec_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w,
+            CXG_LAUNCH((lin_seqrec_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
     } else {
         if (fw)
-            hipLaunchKernelGGL((lin_seqrec_kernel<PHI, false, true>), grid, block, 0, st, X, Y, w,
+            CXG_LAUNCH((lin_seqrec_kernel<PHI, false, true>), grid, block, 0, st, X, Y, w,
                                ws, Bq, S, D, E, cpw, wps, nseg);
         else if constexpr (PHI != PHI_HEXP)
-            hipLaunchKernelGGL((lin_seqrec_kernel<PHI, false, false>), grid, block, 0, st, X, Y,
+            CXG_LAUNCH((lin_seqrec_kernel<PHI, false, false>), grid, block, 0, st, X, Y,
                                w, ws, Bq, S, D, E, cpw, wps, nseg);
     }
     return hipGetLastError();

@@ -512,10 +512,10 @@ static hipError_t wide_fwd_t(const float* Q, const float* K, const float* V, flo
     dim3 grid((unsigned)((long)nqb * Bq)), block(64 * NW);
     ProfScope ps(st, "lin_wide_fwd");
     if (vec)
-        hipLaunchKernelGGL((lin_wide_fwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V, O,
+        CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V, O,
                            den, zc, S, D, E, Bq, den_eps);
     else
-        hipLaunchKernelGGL((lin_wide_fwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V, O,
+        CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V, O,
                            den, zc, S, D, E, Bq, den_eps);
     return hipGetLastError();
 }
@@ -529,10 +529,10 @@ static hipError_t wide_bwd_t(const float* Q, const float* K, const float* V, con
     dim3 grid((unsigned)((long)(kinds == 3 ? 2 : 1) * nb * Bq)), block(64 * NW);
     ProfScope ps(st, kinds == 3 ? "lin_wide_bwd" : kinds == 1 ? "lin_wide_dkdv" : "lin_wide_dq");
     if (vec)
-        hipLaunchKernelGGL((lin_wide_bwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V,
+        CXG_LAUNCH((lin_wide_bwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V,
                            dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds);
     else
-        hipLaunchKernelGGL((lin_wide_bwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V,
+        CXG_LAUNCH((lin_wide_bwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V,
                            dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds);
     return hipGetLastError();
 }
@@ -601,13 +601,13 @@ hipError_t lin_wide_state_launch(int phi, const float* K, const float* V, float*
     dim3 grid((unsigned)(tiles * Bq)), block(256);
     ProfScope ps(st, "lin_wide_state");
     if (phi == PHI_ELU1)
-        hipLaunchKernelGGL(lin_wide_state_kernel<PHI_ELU1>, grid, block, 0, st, K, V, Sfin, zfin,
+        CXG_LAUNCH(lin_wide_state_kernel<PHI_ELU1>, grid, block, 0, st, K, V, Sfin, zfin,
                            S, D, E, sfin_de);
     else if (phi == PHI_ELU1_LG)
-        hipLaunchKernelGGL(lin_wide_state_kernel<PHI_ELU1_LG>, grid, block, 0, st, K, V, Sfin,
+        CXG_LAUNCH(lin_wide_state_kernel<PHI_ELU1_LG>, grid, block, 0, st, K, V, Sfin,
                            zfin, S, D, E, sfin_de);
     else
-        hipLaunchKernelGGL(lin_wide_state_kernel<PHI_NONE>, grid, block, 0, st, K, V, Sfin, zfin,
+        CXG_LAUNCH(lin_wide_state_kernel<PHI_NONE>, grid, block, 0, st, K, V, Sfin, zfin,
                            S, D, E, sfin_de);
     return hipGetLastError();
 }

@@ -1132,11 +1132,11 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     }
     if (O != nullptr) {
         ProfScope ps(st, ROPE ? "mha_rope_fwd" : "mha_fwd");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, true, ROPE>), grid, block, 0, st, Q, K,
+        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, true, ROPE>), grid, block, 0, st, Q, K,
                            V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
     } else {
         ProfScope ps(st, "mha_stats");
-        hipLaunchKernelGGL((mha_fwd_kernel<DHP, NS, VEC, false, ROPE>), grid, block, 0, st, Q, K,
+        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE>), grid, block, 0, st, Q, K,
                            V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
     }
     return hipGetLastError();
@@ -1231,7 +1231,7 @@ static void prep_vec_go(long nseg, const float* O, const float* dO, float* Di, f
 {
     const long nunits = nseg * U;
     const long threads = (nunits + PREP_UNITS - 1) / PREP_UNITS;
-    hipLaunchKernelGGL((mha_bwd_prep_vec_kernel<U, ZERO>), dim3((unsigned)((threads + 255) / 256)),
+    CXG_LAUNCH((mha_bwd_prep_vec_kernel<U, ZERO>), dim3((unsigned)((threads + 255) / 256)),
                        dim3(256), 0, st, O, dO, Di, dQ, S, H, nunits);
 }
 
@@ -1252,10 +1252,10 @@ static void prep_go(bool wide, long nseg, const float* O, const float* dO, float
     const int tpr = wide ? 64 : 16;
     dim3 grid((unsigned)((nseg * tpr + 255) / 256)), block(256);
     if (wide)
-        hipLaunchKernelGGL((mha_bwd_prep_kernel<VEC, ZERO, 64>), grid, block, 0, st, O, dO, Di,
+        CXG_LAUNCH((mha_bwd_prep_kernel<VEC, ZERO, 64>), grid, block, 0, st, O, dO, Di,
                            dQ, S, H, Dh, nseg);
     else
-        hipLaunchKernelGGL((mha_bwd_prep_kernel<VEC, ZERO, 16>), grid, block, 0, st, O, dO, Di,
+        CXG_LAUNCH((mha_bwd_prep_kernel<VEC, ZERO, 16>), grid, block, 0, st, O, dO, Di,
                            dQ, S, H, Dh, nseg);
 }
 
@@ -1310,10 +1310,10 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, ROPE ? "mha_rope_bwd" : "mha_bwd");
     if (vec)
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, true, ROPE>), grid, block, 0, st, Q, K, V, dO,
+        CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE>), grid, block, 0, st, Q, K, V, dO,
                            lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
     else
-        hipLaunchKernelGGL((mha_bwd_kernel<DHP, BM, NS, false, ROPE>), grid, block, 0, st, Q, K, V, dO,
+        CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, false, ROPE>), grid, block, 0, st, Q, K, V, dO,
                            lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
     return hipGetLastError();
 }

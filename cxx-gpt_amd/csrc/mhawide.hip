@@ -641,17 +641,17 @@ hipError_t mha_wide_fwd_launch(const float* Q, const float* K, const float* V, f
     {
         ProfScope ps(st, O != nullptr ? "mha_wide_fwd" : "mha_wide_stats");
         if (vec)
-            hipLaunchKernelGGL(mha_wide_fwd_kernel<true>, grid, block, 0, st, Q, K, V, O, lse,
+            CXG_LAUNCH(mha_wide_fwd_kernel<true>, grid, block, 0, st, Q, K, V, O, lse,
                                part, S, H, Dh, BH, C, qscale);
         else
-            hipLaunchKernelGGL(mha_wide_fwd_kernel<false>, grid, block, 0, st, Q, K, V, O, lse,
+            CXG_LAUNCH(mha_wide_fwd_kernel<false>, grid, block, 0, st, Q, K, V, O, lse,
                                part, S, H, Dh, BH, C, qscale);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || C >= nqb)
         return e;
     ProfScope ps(st, "mha_wide_merge");
-    hipLaunchKernelGGL(mha_wide_merge_kernel, dim3((unsigned)((long)nqb * BH * 4)), dim3(256), 0, st,
+    CXG_LAUNCH(mha_wide_merge_kernel, dim3((unsigned)((long)nqb * BH * 4)), dim3(256), 0, st,
                        part, O, lse, S, H, Dh, BH, C);
     return hipGetLastError();
 }
@@ -704,17 +704,17 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
     {
         ProfScope ps(st, "mha_wide_bwd");
         if (vec)
-            hipLaunchKernelGGL(mha_wide_bwd_kernel<true>, grid, block, 0, st, Q, K, V, dO, lse,
+            CXG_LAUNCH(mha_wide_bwd_kernel<true>, grid, block, 0, st, Q, K, V, dO, lse,
                                Di, dQ, dK, dV, part, S, H, Dh, BH, Cb, scale * kLog2e, scale);
         else
-            hipLaunchKernelGGL(mha_wide_bwd_kernel<false>, grid, block, 0, st, Q, K, V, dO, lse,
+            CXG_LAUNCH(mha_wide_bwd_kernel<false>, grid, block, 0, st, Q, K, V, dO, lse,
                                Di, dQ, dK, dV, part, S, H, Dh, BH, Cb, scale * kLog2e, scale);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || Cb >= nb)
         return e;
     ProfScope ps(st, "mha_wide_bsum");
-    hipLaunchKernelGGL(mha_wide_bsum_kernel, dim3((unsigned)(2L * nb * BH * 4)), dim3(256), 0, st,
+    CXG_LAUNCH(mha_wide_bsum_kernel, dim3((unsigned)(2L * nb * BH * 4)), dim3(256), 0, st,
                        part, dQ, dK, dV, S, H, Dh, BH, Cb);
     return hipGetLastError();
 }

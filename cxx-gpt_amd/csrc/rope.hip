@@ -103,16 +103,16 @@ hipError_t rope_launch(float* Q, float* K, long B, int S, int D, int head_dim, f
     const bool vec = ((uintptr_t)Q & 7u) == 0 && ((uintptr_t)K & 7u) == 0;
     const bool alias = Q != nullptr && Q == K;
     if (alias && vec)
-        hipLaunchKernelGGL((rope_kernel<true, true>), grid, block, 0, st, Q, K, rows, S, D,
+        CXG_LAUNCH((rope_kernel<true, true>), grid, block, 0, st, Q, K, rows, S, D,
                            head_dim, sign, fr);
     else if (alias)
-        hipLaunchKernelGGL((rope_kernel<true, false>), grid, block, 0, st, Q, K, rows, S, D,
+        CXG_LAUNCH((rope_kernel<true, false>), grid, block, 0, st, Q, K, rows, S, D,
                            head_dim, sign, fr);
     else if (vec)
-        hipLaunchKernelGGL((rope_kernel<false, true>), grid, block, 0, st, Q, K, rows, S, D,
+        CXG_LAUNCH((rope_kernel<false, true>), grid, block, 0, st, Q, K, rows, S, D,
                            head_dim, sign, fr);
     else
-        hipLaunchKernelGGL((rope_kernel<false, false>), grid, block, 0, st, Q, K, rows, S, D,
+        CXG_LAUNCH((rope_kernel<false, false>), grid, block, 0, st, Q, K, rows, S, D,
                            head_dim, sign, fr);
     return hipGetLastError();
 }
