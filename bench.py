@@ -432,9 +432,11 @@ def _gpt(c, name, B, S, E, seed, steps, warmup):
               "mha_wide_bwd": mha_flops(B, S, 1, E, fwd=False),
               "mha_fwd": mha_flops(B, S, 1, E, bwd=False),
               "mha_bwd": mha_flops(B, S, 1, E, fwd=False),
-              # E > 512: one sequence's S x S x E product per GEMM launch,
-              # credited with its causal half (S^2 E of the 2 S^2 E executed)
-              "ffn_gemm": 1.0 * S * S * E}
+              # E > 512: each GEMM launch is one S x S x E product for every
+              # sequence of a group (as many as keep two S x S score
+              # matrices per sequence within 2^25 floats), credited with its
+              # causal half (S^2 E of the 2 S^2 E executed)
+              "ffn_gemm": 1.0 * min(B, max(1, (1 << 25) // (2 * S * S))) * S * S * E}
     dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
     ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
     roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),

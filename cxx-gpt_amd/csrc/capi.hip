@@ -463,7 +463,7 @@ int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, f
         if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(O))
             return CXG_ERR_ALIGN;
         Scratch ws;
-        st = ws.acquire(nullptr, 0, gpt_mat_ws_floats((int)S, (int)E) * sizeof(float), s);
+        st = ws.acquire(nullptr, 0, gpt_mat_ws_floats((int)B, (int)S, (int)E) * sizeof(float), s);
         if (st != CXG_OK)
             return st;
         return hip_status(gpt_mat_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)E,
@@ -485,7 +485,7 @@ size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
     if (gpt_check(B, S, E, &empty) != CXG_OK || empty)
         return 0;
     if (E > (size_t)MHA_WIDE_MAX_DH)   // the scores of one sequence, and GEMM partial tiles
-        return gpt_mat_ws_floats((int)S, (int)E) * sizeof(float);
+        return gpt_mat_ws_floats((int)B, (int)S, (int)E) * sizeof(float);
     // Di, lse, and the partial records of the statistics pass and of the
     // backward (used one after the other)
     const size_t part = std::max(mha_wide_fwd_ws_floats((int)B, (int)S),

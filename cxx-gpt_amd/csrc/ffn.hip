@@ -32,6 +32,10 @@
 // other workgroups) and a fix-up kernel sums them in run order and applies
 // the epilogue.
 //
+// A batch of same-shape products with element strides between them shares
+// one launch: its tiles are numbered product-major and the runs cut across
+// products like any other tiles.
+//
 // Requires E, F multiples of 4 and 16-byte aligned tensors (checked at the C
 // ABI); any M.
 #include "common.hpp"
@@ -58,7 +62,9 @@ struct GemmArgs {
     long lda, ldb, ldc;
     int M, N, K;
     int tn;            // tiles along N
-    int T;             // tiles
+    int Tb;            // tiles per product of the batch
+    long sA, sB, sC;   // batch strides (elements)
+    int T;             // tiles (all products)
     int KT;            // k-tiles per tile
     int P;             // workgroups
     long U;            // T * KT units
@@ -173,9 +179,13 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
         const int t = (int)(u / a.KT);
         const int ka = (int)(u - (long)t * a.KT);
         const int kb = (int)min((long)a.KT, (long)ka + (ue - u));
-        const int m0 = (t / a.tn) * GT;
-        const int n0 = (t % a.tn) * GT;
+        const int bt = t / a.Tb, tl = t - bt * a.Tb;   // product of the batch, its tile
+        const int m0 = (tl / a.tn) * GT;
+        const int n0 = (tl % a.tn) * GT;
         const int nkt = kb - ka;
+        const float* Ab = a.A + bt * a.sA;
+        const float* Bb = a.B + bt * a.sB;
+        const long cb = bt * a.sC;
 
         f4 acc[4][4];
 #pragma unroll
@@ -187,8 +197,8 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
         // (LDS is free here: the previous segment's last reads precede its
         // final barrier.)
         f4 ra[4], rb[4];
-        tile_fetch<AK>(a.A, a.lda, m0, a.M, ka * GKT, a.K, ra);
-        tile_fetch<BK>(a.B, a.ldb, n0, a.N, ka * GKT, a.K, rb);
+        tile_fetch<AK>(Ab, a.lda, m0, a.M, ka * GKT, a.K, ra);
+        tile_fetch<BK>(Bb, a.ldb, n0, a.N, ka * GKT, a.K, rb);
         tile_put<AK>(lds[0][0], ra);
         tile_put<BK>(lds[0][1], rb);
         __syncthreads();
@@ -197,8 +207,8 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
             const int st = kt & 1;
             // Next k-tile in flight during this one's MFMAs (past the
             // segment's end it reads valid memory that is never used).
-            tile_fetch<AK>(a.A, a.lda, m0, a.M, (ka + kt + 1) * GKT, a.K, ra);
-            tile_fetch<BK>(a.B, a.ldb, n0, a.N, (ka + kt + 1) * GKT, a.K, rb);
+            tile_fetch<AK>(Ab, a.lda, m0, a.M, (ka + kt + 1) * GKT, a.K, ra);
+            tile_fetch<BK>(Bb, a.ldb, n0, a.N, (ka + kt + 1) * GKT, a.K, rb);
             const float* LA = lds[st][0];
             const float* LB = lds[st][1];
 #pragma unroll
@@ -233,7 +243,8 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
                 for (int j = 0; j < 4; j++) {
                     const int col = n0 + wn + 16 * j + 4 * g;
                     if (row < a.M && col < a.N)
-                        epi_apply<EPI>(acc[i][j], (long)row * a.ldc + col, a.C, a.G, a.pre);
+                        epi_apply<EPI>(acc[i][j], cb + (long)row * a.ldc + col, a.C, a.G,
+                                       a.pre);
                 }
             }
         } else {
@@ -285,14 +296,16 @@ __global__ __launch_bounds__(256) void ffn_fixup_kernel(GemmArgs a)
         for (int e = 0; e < NE; e++)
             v[e] += x[e];
     }
-    const int m0 = (t / a.tn) * GT;
-    const int n0 = (t % a.tn) * GT;
+    const int bt = t / a.Tb, tl = t - bt * a.Tb;
+    const int m0 = (tl / a.tn) * GT;
+    const int n0 = (tl % a.tn) * GT;
+    const long cb = bt * a.sC;
 #pragma unroll
     for (int e = 0; e < NE; e++) {
         const int q = quarter * (GT * GT / 16) + threadIdx.x + 256 * e;
         const int row = m0 + (q >> 5), col = n0 + (q & 31) * 4;
         if (row < a.M && col < a.N)
-            epi_apply<EPI>(v[e], (long)row * a.ldc + col, a.C, a.G, a.pre);
+            epi_apply<EPI>(v[e], cb + (long)row * a.ldc + col, a.C, a.G, a.pre);
     }
 }
 
@@ -308,9 +321,10 @@ static int dev_cus()
 // leaves the MFMA pipe idle half the time), or one per unit of work.
 static int sk_wgs(long U) { return (int)std::min<long>(2L * dev_cus(), U); }
 
-size_t ffn_gemm_ws_floats(int M, int N, int K)
+size_t ffn_gemm_ws_floats(int M, int N, int K, int batch)
 {
-    const long U = (long)((M + GT - 1) / GT) * ((N + GT - 1) / GT) * ((K + GKT - 1) / GKT);
+    const long U = (long)std::max(batch, 1) * ((M + GT - 1) / GT) * ((N + GT - 1) / GT) *
+                   ((K + GKT - 1) / GKT);
     return (size_t)2 * sk_wgs(U) * GT * GT;
 }
 
@@ -358,7 +372,11 @@ hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st)
     a.N = op.N;
     a.K = op.K;
     a.tn = (op.N + GT - 1) / GT;
-    a.T = ((op.M + GT - 1) / GT) * a.tn;
+    a.Tb = ((op.M + GT - 1) / GT) * a.tn;
+    a.sA = op.sA;
+    a.sB = op.sB;
+    a.sC = op.sC;
+    a.T = std::max(op.batch, 1) * a.Tb;
     a.KT = (op.K + GKT - 1) / GKT;
     a.U = (long)a.T * a.KT;
     a.P = sk_wgs(a.U);

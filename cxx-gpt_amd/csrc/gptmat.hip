@@ -6,9 +6,9 @@
 // gpt_cuda::softmax_backward (:131-173) (gpt_gpt.hpp:365-380, :420-438).  The
 // reference sets no limit on E.  The fused wide-head kernels (mhawide.hip)
 // hold a 16-row block of Q, K, V at full width in LDS and stop at E = 512;
-// wider embeddings take this path, which keeps each sequence's S x S scores
-// in memory (S^2 floats per sequence, one sequence at a time) and runs the
-// products on the FP32 MFMA GEMM of ffn.hip:
+// wider embeddings take this path, which keeps the S x S scores of a group of
+// sequences in memory and runs the products on the FP32 MFMA GEMM of ffn.hip,
+// one batched launch per product for the whole group:
 //   forward   Sc = Q K^T;  P = softmax(Sc / sqrt(E)) causal (lse kept);  O = P V
 //   backward  Sc again, P from lse;  dP = dO V^T;
 //             dS = P (dP - rowsum(P dP)) / sqrt(E);
@@ -23,11 +23,12 @@
 
 namespace cxg {
 
-// Row softmax of one sequence's scores in place (one wave per row of the
-// S x S matrix, row stride S): P[i][j] = 2^(Sc[i][j] c - L_i) for j <= i, else
-// 0, with L_i the base-2 log-sum-exp of the row's unmasked scaled scores
-// (c = log2(e) / sqrt(E)).  lse_in (natural log, nullable): use it instead of
-// forming L_i; lse_out (nullable): store L_i ln 2.
+// Row softmax of a group's scores in place (one wave per row of a sequence's
+// S x S matrix, row stride S, sequence blockIdx.y of the group): P[i][j] =
+// 2^(Sc[i][j] c - L_i) for j <= i, else 0, with L_i the base-2 log-sum-exp of
+// the row's unmasked scaled scores (c = log2(e) / sqrt(E)).  lse_in (natural
+// log, nullable): use it instead of forming L_i; lse_out (nullable): store
+// L_i ln 2.
 __global__ __launch_bounds__(256) void gpt_softmax_kernel(float* __restrict__ P,
                                                          const float* __restrict__ lse_in,
                                                          float* __restrict__ lse_out, int S,
@@ -37,10 +38,11 @@ __global__ __launch_bounds__(256) void gpt_softmax_kernel(float* __restrict__ P,
     const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= S)
         return;
-    float* r = P + (long)i * S;
+    const long sq = blockIdx.y;
+    float* r = P + (sq * S + i) * S;
     float L;
     if (lse_in != nullptr) {
-        L = lse_in[i] * kLog2e;
+        L = lse_in[sq * S + i] * kLog2e;
     } else {
         float m = -INFINITY;
         for (int j = lane; j <= i; j += 64)
@@ -56,14 +58,14 @@ __global__ __launch_bounds__(256) void gpt_softmax_kernel(float* __restrict__ P,
             l += __shfl_xor(l, o, 64);
         L = m + fast_log2(l);
         if (lse_out != nullptr && lane == 0)
-            lse_out[i] = L * kLn2;
+            lse_out[sq * S + i] = L * kLn2;
     }
     for (int j = lane; j < S; j += 64)
         r[j] = j <= i ? fast_exp2(r[j] * c - L) : 0.0f;
 }
 
 // dS[i][j] = P[i][j] (dP[i][j] - sum_j P[i][j] dP[i][j]) * scale, in place
-// over dP (one wave per row).
+// over dP (one wave per row; sequence blockIdx.y of the group).
 __global__ __launch_bounds__(256) void gpt_softmax_bwd_kernel(const float* __restrict__ P,
                                                              float* __restrict__ dP, int S,
                                                              float scale)
@@ -72,8 +74,9 @@ __global__ __launch_bounds__(256) void gpt_softmax_bwd_kernel(const float* __res
     const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= S)
         return;
-    const float* p = P + (long)i * S;
-    float* d = dP + (long)i * S;
+    const long row = (long)blockIdx.y * S + i;
+    const float* p = P + row * S;
+    float* d = dP + row * S;
     float di = 0.0f;
     for (int j = lane; j <= i; j += 64)
         di += p[j] * d[j];
@@ -86,16 +89,28 @@ __global__ __launch_bounds__(256) void gpt_softmax_bwd_kernel(const float* __res
 
 bool gpt_mat_ok(int S, int E) { return S % 4 == 0 && E % 4 == 0; }
 
-// Scratch: two S x S matrices and the GEMM's partial tiles (the largest of
-// the products' needs).
-size_t gpt_mat_ws_floats(int S, int E)
+// Sequences per group: as many as keep the group's two score matrices within
+// 2^25 floats (128 MiB), at least one.
+static int gpt_group(int B, int S)
 {
-    const size_t g = std::max({ffn_gemm_ws_floats(S, S, E), ffn_gemm_ws_floats(S, E, S)});
-    return 2 * (size_t)S * S + g;
+    const long per = 2L * S * S;
+    return (int)std::max<long>(1, std::min<long>(B, (1L << 25) / per));
 }
 
-static hipError_t gemm(const float* A, long lda, bool ak, const float* B, long ldb, bool bk,
-                       float* C, long ldc, int M, int N, int K, float* ws, hipStream_t st)
+// Scratch: the group's two score matrices and the GEMM's partial tiles (the
+// largest of the products' needs).
+size_t gpt_mat_ws_floats(int B, int S, int E)
+{
+    const int nb = gpt_group(B, S);
+    const size_t g = std::max({ffn_gemm_ws_floats(S, S, E, nb), ffn_gemm_ws_floats(S, E, S, nb)});
+    return 2 * (size_t)nb * S * S + g;
+}
+
+// C_b = A_b B_b for the nb sequences of a group (A, B, C at sequence strides
+// sA, sB, sC).
+static hipError_t gemm(const float* A, long lda, bool ak, long sA, const float* B, long ldb,
+                       bool bk, long sB, float* C, long ldc, long sC, int M, int N, int K, int nb,
+                       float* ws, hipStream_t st)
 {
     FfnGemm op{};
     op.A = A;
@@ -110,31 +125,39 @@ static hipError_t gemm(const float* A, long lda, bool ak, const float* B, long l
     op.epi = FFN_EPI_STORE;
     op.C = C;
     op.ldc = ldc;
+    op.batch = nb;
+    op.sA = sA;
+    op.sB = sB;
+    op.sC = sC;
     return ffn_gemm_launch(op, ws, st);
 }
 
-static hipError_t softmax(float* P, const float* lse_in, float* lse_out, int S, int E,
+static hipError_t softmax(float* P, const float* lse_in, float* lse_out, int S, int E, int nb,
                           hipStream_t st)
 {
     ProfScope ps(st, "gpt_softmax");
     const float c = kLog2e / sqrtf((float)E);
-    CXG_LAUNCH(gpt_softmax_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256), 0, st, P,
-                       lse_in, lse_out, S, c);
+    CXG_LAUNCH(gpt_softmax_kernel, dim3((unsigned)((S + 3) / 4), (unsigned)nb), dim3(256), 0, st,
+               P, lse_in, lse_out, S, c);
     return hipGetLastError();
 }
 
 hipError_t gpt_mat_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                               float* lse, int B, int S, int E, float* ws, hipStream_t st)
 {
+    const int G = gpt_group(B, S);
+    const long SE = (long)S * E, SS = (long)S * S;
     float* Sc = ws;
-    float* gws = ws + 2 * (size_t)S * S;
-    for (int b = 0; b < B; b++) {
-        const long r0 = (long)b * S * E;
-        hipError_t e = gemm(Q + r0, E, true, K + r0, E, true, Sc, S, S, S, E, gws, st);
+    float* gws = ws + 2 * (size_t)G * SS;
+    for (int b0 = 0; b0 < B; b0 += G) {
+        const int nb = std::min(G, B - b0);
+        const long r0 = (long)b0 * SE;
+        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, Sc, S, SS, S, S, E, nb,
+                            gws, st);
         if (e == hipSuccess)
-            e = softmax(Sc, nullptr, lse != nullptr ? lse + (long)b * S : nullptr, S, E, st);
+            e = softmax(Sc, nullptr, lse != nullptr ? lse + (long)b0 * S : nullptr, S, E, nb, st);
         if (e == hipSuccess && O != nullptr)
-            e = gemm(Sc, S, true, V + r0, E, false, O + r0, E, S, E, S, gws, st);
+            e = gemm(Sc, S, true, SS, V + r0, E, false, SE, O + r0, E, SE, S, E, S, nb, gws, st);
         if (e != hipSuccess)
             return e;
     }
@@ -145,29 +168,35 @@ hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, co
                               const float* lse, float* dQ, float* dK, float* dV, int B, int S,
                               int E, float* ws, hipStream_t st)
 {
+    const int G = gpt_group(B, S);
+    const long SE = (long)S * E, SS = (long)S * S;
     float* P = ws;
-    float* dS = ws + (size_t)S * S;
-    float* gws = ws + 2 * (size_t)S * S;
+    float* dS = ws + (size_t)G * SS;
+    float* gws = ws + 2 * (size_t)G * SS;
     const float scale = 1.0f / sqrtf((float)E);
-    for (int b = 0; b < B; b++) {
-        const long r0 = (long)b * S * E;
-        hipError_t e = gemm(Q + r0, E, true, K + r0, E, true, P, S, S, S, E, gws, st);
+    for (int b0 = 0; b0 < B; b0 += G) {
+        const int nb = std::min(G, B - b0);
+        const long r0 = (long)b0 * SE;
+        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, P, S, SS, S, S, E, nb, gws,
+                            st);
         if (e == hipSuccess)
-            e = softmax(P, lse != nullptr ? lse + (long)b * S : nullptr, nullptr, S, E, st);
+            e = softmax(P, lse != nullptr ? lse + (long)b0 * S : nullptr, nullptr, S, E, nb, st);
         if (e == hipSuccess)   // dP = dO V^T
-            e = gemm(dO + r0, E, true, V + r0, E, true, dS, S, S, S, E, gws, st);
+            e = gemm(dO + r0, E, true, SE, V + r0, E, true, SE, dS, S, SS, S, S, E, nb, gws, st);
         if (e == hipSuccess) {
             ProfScope ps(st, "gpt_softmax_bwd");
-            CXG_LAUNCH(gpt_softmax_bwd_kernel, dim3((unsigned)((S + 3) / 4)), dim3(256),
-                               0, st, P, dS, S, scale);
+            CXG_LAUNCH(gpt_softmax_bwd_kernel, dim3((unsigned)((S + 3) / 4), (unsigned)nb),
+                       dim3(256), 0, st, P, dS, S, scale);
             e = hipGetLastError();
         }
         if (e == hipSuccess)   // dV = P^T dO
-            e = gemm(P, S, false, dO + r0, E, false, dV + r0, E, S, E, S, gws, st);
+            e = gemm(P, S, false, SS, dO + r0, E, false, SE, dV + r0, E, SE, S, E, S, nb, gws,
+                     st);
         if (e == hipSuccess)   // dQ = dS K
-            e = gemm(dS, S, true, K + r0, E, false, dQ + r0, E, S, E, S, gws, st);
+            e = gemm(dS, S, true, SS, K + r0, E, false, SE, dQ + r0, E, SE, S, E, S, nb, gws, st);
         if (e == hipSuccess)   // dK = dS^T Q
-            e = gemm(dS, S, false, Q + r0, E, false, dK + r0, E, S, E, S, gws, st);
+            e = gemm(dS, S, false, SS, Q + r0, E, false, SE, dK + r0, E, SE, S, E, S, nb, gws,
+                     st);
         if (e != hipSuccess)
             return e;
     }

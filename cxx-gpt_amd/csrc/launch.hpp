@@ -89,13 +89,13 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
                                float* dV, int B, int S, int H, int Dh, float* part,
                                hipStream_t st);
 
-// GPT's attention for E > 512 (gptmat.hip): each sequence's S x S scores in
-// memory, products on the FP32 GEMM below.  S and E multiples of 4 and
-// 16-byte aligned rows; scratch gpt_mat_ws_floats(S, E) floats (used one
-// sequence at a time).  O may be null (statistics only); lse [B][S] natural
-// log, nullable in both.
+// GPT's attention for E > 512 (gptmat.hip): a group of sequences' S x S
+// scores in memory, products on the FP32 GEMM below, batched over the group.
+// S and E multiples of 4 and 16-byte aligned rows; scratch
+// gpt_mat_ws_floats(B, S, E) floats.  O may be null (statistics only); lse
+// [B][S] natural log, nullable in both.
 bool gpt_mat_ok(int S, int E);
-size_t gpt_mat_ws_floats(int S, int E);
+size_t gpt_mat_ws_floats(int B, int S, int E);
 hipError_t gpt_mat_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                               float* lse, int B, int S, int E, float* ws, hipStream_t st);
 hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, const float* dO,
@@ -127,8 +127,12 @@ struct FfnGemm {
     long ldc;
     const float* G;
     float* pre;
+    // a batch of independent products: product b uses A + b sA, B + b sB and
+    // C (G, pre) + b sC (element strides)
+    int batch = 1;
+    long sA = 0, sB = 0, sC = 0;
 };
-size_t ffn_gemm_ws_floats(int M, int N, int K);
+size_t ffn_gemm_ws_floats(int M, int N, int K, int batch = 1);
 hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st);
 
 // Rotary position embedding, in place on (B*S, D) rows (Q and/or K; either
