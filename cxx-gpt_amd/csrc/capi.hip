@@ -876,7 +876,7 @@ int cxg_lin_hexp_fwd(const float* Xq, const float* Xk, const float* V, float* O,
         e = phi_hexp_fwd_launch(Xk, pk, (long)N, 64, 64, s);
     if (e == hipSuccess)
         e = lin_wide_fwd_launch(PHI_NONE, pq, pk, V, O, den_cache, nullptr, 1, (int)B, (int)S, 64,
-                                64, s);
+                                64, nullptr, s);
     return hip_status(e);
 }
 

@@ -1381,8 +1381,8 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
 {
-    if (!p.fast)
-        return p.quad ? 0 : (size_t)Bq * D * E * sizeof(float);
+    if (!p.fast)   // the quadratic form: p.L = S
+        return p.quad ? lin_wide_ws_bytes(Bq, p.L, D, E) : (size_t)Bq * D * E * sizeof(float);
     if (p.nseg <= 1)
         return 0;
     return (size_t)Bq * p.nseg * LIN_WS * sizeof(float);
@@ -1441,7 +1441,8 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         if (p.quad || !p.fast || mode != 2)
             return hipErrorInvalidValue;
     } else if (p.quad) {
-        hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, st);
+        hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, ws,
+                                           st);
         if (e == hipSuccess && Sfin != nullptr)
             e = lin_wide_state_launch(PHI, K, V, Sfin, zfin, sfin_de, Bq, S, D, E, st);
         return e;

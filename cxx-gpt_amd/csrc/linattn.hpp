@@ -124,9 +124,12 @@ bool lin_wide_ok(int D, int E);
 // S = 256, 84.6 against 66.5 us.
 constexpr int LIN_QUAD_MAX_S = 128;
 bool lin_quad_ok(int D, int E, long S);
+// ws: lin_wide_ws_bytes of scratch (query blocks may then be split over
+// their keys when B' x S / 16 leaves workgroup slots free), or null.
+size_t lin_wide_ws_bytes(int Bq, int S, int D, int E);
 hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                                float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                               hipStream_t st);
+                               void* ws, hipStream_t st);
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                                const float* dnum, const float* dden, float* dQ, float* dK,
                                float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st);

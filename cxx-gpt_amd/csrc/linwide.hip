@@ -95,16 +95,20 @@ __device__ __forceinline__ void lw_store(float* __restrict__ dst, const LwRegs<N
 }
 
 // ---------------------------------------------------------------------------
-// forward: job = (sequence, 16-query block), latest blocks first (they see the
-// most keys).  Per key block: A^T[j][i] (lane i = query, element r <-> key
-// 4g + r) from the waves' column partials, den_i += sum_j A[i][j], and over
-// the wave's V columns O^T[e][i] += sum_j V[j][e] A^T[j][i].
+// forward: job = (sequence, 16-query block, part), latest blocks first (they
+// see the most keys).  A part is a run of at most PL key blocks; with PL >= the
+// block count every job is one whole query block (the sums over keys are
+// plain, so a query block split into parts is finished by adding the parts'
+// numerators and denominators: lin_wide_fin_kernel).  Per key block: A^T[j][i]
+// (lane i = query, element r <-> key 4g + r) from the waves' column partials,
+// den_i += sum_j A[i][j], and over the wave's V columns
+// O^T[e][i] += sum_j V[j][e] A^T[j][i].
 // ---------------------------------------------------------------------------
 template <int PHI, int NW, bool VEC>
 __global__ __launch_bounds__(64 * NW) void lin_wide_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zc, int S, int D, int E,
-    int Bq, int den_eps)
+    int Bq, int den_eps, int PL, int PMAX, float* __restrict__ wsO, float* __restrict__ wsD)
 {
     using P = LW<NW>;
     __shared__ __attribute__((aligned(16))) float lds[4 * P::TILE + NW * 256];
@@ -112,7 +116,12 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_fwd_kernel(
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int nqb = (S + LWB - 1) / LWB;
-    const int qb = nqb - 1 - (int)(blockIdx.x / Bq);
+    const int unit = (int)(blockIdx.x / Bq);
+    const int qb = nqb - 1 - unit / PMAX, part = unit % PMAX;
+    const int nparts = (qb + PL) / PL;   // parts of this query block
+    if (part >= nparts)
+        return;   // the whole workgroup: no barrier is skipped
+    const int kb0 = part * PL, kb1 = min(kb0 + PL, qb + 1);
     const int seq = (int)(blockIdx.x % Bq);
     const long rb = (long)seq * S;
     const int q0 = qb * LWB, c0 = 64 * w;
@@ -134,25 +143,14 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_fwd_kernel(
         }
     }
     float dsum = 0.0f;
-    // z_cache (zc != null): column sums of phi(K) over the key blocks before
-    // this query block, columns c0 + 16t + l16 (each lane's own column)
+    // z_cache (zc != null, whole query blocks only): column sums of phi(K)
+    // over the key blocks before this query block, columns c0 + 16t + l16
+    // (each lane's own column)
     float zrun[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    LwRegs<NW> kr, vr;
-    lw_fetch<NW, VEC>(kr, K + rb * D, D, 0, S, D, tid);
-    lw_fetch<NW, VEC>(vr, V + rb * E, E, 0, S, E, tid);
-    for (int kb = 0; kb <= qb; kb++) {
-        const int k0 = kb * LWB;
-        float* Ks = lds + (kb & 1) * 2 * P::TILE;
-        float* Vs = Ks + P::TILE;
-        lw_store<NW, PHI, true>(Ks, kr, D, tid);
-        lw_store<NW, PHI, false>(Vs, vr, E, tid);
-        __builtin_amdgcn_sched_barrier(0);
-        const int kn = min(kb + 1, qb) * LWB;   // the last step refetches its own block
-        lw_fetch<NW, VEC>(kr, K + rb * D, D, kn, S, D, tid);
-        lw_fetch<NW, VEC>(vr, V + rb * E, E, kn, S, E, tid);
-        __syncthreads();
-        // A^T partial over this wave's columns, two accumulation chains
+    // A^T partial of key block kb over this wave's columns (two accumulation
+    // chains) to Sp, and z_cache from the block's phi(K) columns
+    auto scores = [&](const float* __restrict__ Ks, int kb) __attribute__((always_inline)) {
         f4 sp = f4zero(), sp2 = f4zero();
 #pragma unroll
         for (int t = 0; t < 4; t += 2) {
@@ -165,28 +163,6 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_fwd_kernel(
             }
         }
         *reinterpret_cast<f4*>(&Sp[w * 256 + lane * 4]) = sp + sp2;
-        __syncthreads();
-        f4 a = f4zero();
-#pragma unroll
-        for (int u = 0; u < NW; u++)
-            a += *reinterpret_cast<const f4*>(&Sp[u * 256 + lane * 4]);
-        float aloc = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int kj = k0 + 4 * g + r;
-            a[r] = (kj <= qi && kj < S) ? a[r] : 0.0f;
-            aloc += a[r];
-        }
-        dsum += xrow_sum(aloc);
-        // O^T[e][i] += sum_j V[j][e] A^T[j][i] over this wave's columns
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            f4 acc = o[t];
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                acc = mfma16(Vs[(4 * g + r) * P::LD + c0 + 16 * t + l16], a[r], acc);
-            o[t] = acc;
-        }
         if (zc != nullptr) {
             // z_t = zrun + inclusive prefix within the query block (the last key
             // block); rows 4g + r of this lane's columns
@@ -207,18 +183,101 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_fwd_kernel(
                             zc[(rb + q0 + 4 * g + r) * D + c] = zp[r];
             }
         }
-        // Sp and this buffer pair are rewritten two steps on, after the next
-        // step's first barrier; the partial sums were read above
+    };
+    // the waves' partials summed and masked, den, and O^T[e][i] += sum_j
+    // V[j][e] A^T[j][i] over this wave's columns
+    auto accumulate = [&](const float* __restrict__ Vs, int kb) __attribute__((always_inline)) {
+        const int k0 = kb * LWB;
+        f4 a = f4zero();
+#pragma unroll
+        for (int u = 0; u < NW; u++)
+            a += *reinterpret_cast<const f4*>(&Sp[u * 256 + lane * 4]);
+        float aloc = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int kj = k0 + 4 * g + r;
+            a[r] = (kj <= qi && kj < S) ? a[r] : 0.0f;
+            aloc += a[r];
+        }
+        dsum += xrow_sum(aloc);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            f4 acc = o[t];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                acc = mfma16(Vs[(4 * g + r) * P::LD + c0 + 16 * t + l16], a[r], acc);
+            o[t] = acc;
+        }
+    };
+    LwRegs<NW> kr, vr;
+    lw_fetch<NW, VEC>(kr, K + rb * D, D, kb0 * LWB, S, D, tid);
+    lw_fetch<NW, VEC>(vr, V + rb * E, E, kb0 * LWB, S, E, tid);
+    // two LDS copies: block kb goes to copy (kb - kb0) & 1 at the top of its
+    // step, and the register stage is refilled with block kb+1 (the last step
+    // refetches its own block)
+    for (int kb = kb0; kb < kb1; kb++) {
+        float* Ks = lds + ((kb - kb0) & 1) * 2 * P::TILE;
+        float* Vs = Ks + P::TILE;
+        lw_store<NW, PHI, true>(Ks, kr, D, tid);
+        lw_store<NW, PHI, false>(Vs, vr, E, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kn = min(kb + 1, kb1 - 1) * LWB;
+        lw_fetch<NW, VEC>(kr, K + rb * D, D, kn, S, D, tid);
+        lw_fetch<NW, VEC>(vr, V + rb * E, E, kn, S, E, tid);
+        __syncthreads();
+        scores(Ks, kb);
+        __syncthreads();
+        accumulate(Vs, kb);
+        // Sp and this copy are rewritten after a later step's first barrier;
+        // the reads above come before it
     }
     if (qi < S) {
-        const float inv = 1.0f / (dsum + 1e-8f);
-        float* orow = O + (rb + qi) * E;
+        if (nparts == 1) {
+            const float inv = 1.0f / (dsum + 1e-8f);
+            float* orow = O + (rb + qi) * E;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            store4<VEC>(orow, c0 + 16 * t + 4 * g, E, o[t] * inv);
-        if (w == 0 && g == 0)
-            den[rb + qi] = den_eps ? dsum + 1e-8f : dsum;
+            for (int t = 0; t < 4; t++)
+                store4<VEC>(orow, c0 + 16 * t + 4 * g, E, o[t] * inv);
+            if (w == 0 && g == 0)
+                den[rb + qi] = den_eps ? dsum + 1e-8f : dsum;
+        } else {
+            // this part's numerator and denominator
+            const long N = (long)Bq * S;
+            float* orow = wsO + ((long)part * N + rb + qi) * E;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                store4<VEC>(orow, c0 + 16 * t + 4 * g, E, o[t]);
+            if (w == 0 && g == 0)
+                wsD[(long)part * N + rb + qi] = dsum;
+        }
     }
+}
+
+// Rows of the query blocks split into parts: O = (sum of the parts'
+// numerators) / (sum of their denominators + 1e-8), den as the forward.  One
+// thread per element; parts are added in order.
+__global__ __launch_bounds__(256) void lin_wide_fin_kernel(
+    const float* __restrict__ wsO, const float* __restrict__ wsD, float* __restrict__ O,
+    float* __restrict__ den, int S, int E, int Bq, int PL, int den_eps)
+{
+    const long N = (long)Bq * S;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= N * E)
+        return;
+    const long row = i / E;
+    const int c = (int)(i - row * E);
+    const int qb = (int)(row % S) / LWB;
+    const int nparts = (qb + PL) / PL;
+    if (nparts == 1)
+        return;
+    float num = 0.0f, ds = 0.0f;
+    for (int p = 0; p < nparts; p++) {
+        num += wsO[((long)p * N + row) * E + c];
+        ds += wsD[(long)p * N + row];
+    }
+    O[row * E + c] = num / (ds + 1e-8f);
+    if (c == 0)
+        den[row] = den_eps ? ds + 1e-8f : ds;
 }
 
 // ---------------------------------------------------------------------------
@@ -503,20 +562,105 @@ bool lin_quad_ok(int D, int E, long S)
 
 static inline bool al16x(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
+// Compute units of the current device (cached per device).
+static int wide_cus()
+{
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Key blocks per part of the forward: whole query blocks (PL = the block
+// count) unless those jobs leave resident workgroup slots free (B' x blocks
+// below one round); then the smallest power of two whose jobs fit one round,
+// so the longest job is PL key blocks instead of S / 16.  Narrow widths
+// (NW < 4) keep whole blocks: their blocks are cheap and plentiful.
+template <int NW>
+static int wide_fwd_pl(int Bq, int nqb)
+{
+    if (NW < 4 || nqb <= 1)
+        return nqb;
+    static int per_cu = 0;
+    if (per_cu <= 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &n, (const void*)lin_wide_fwd_kernel<PHI_NONE, NW, true>, 64 * NW, 0) !=
+                hipSuccess || n <= 0)
+            n = 1;
+        per_cu = n;
+    }
+    const long slots = (long)per_cu * wide_cus();
+    if ((long)Bq * nqb >= slots)
+        return nqb;
+    for (int pl = 1; pl < nqb; pl *= 2) {
+        long units = 0;
+        for (int qb = 0; qb < nqb; qb++)
+            units += (qb + pl) / pl;
+        if ((long)Bq * units <= slots)
+            return pl;
+    }
+    return nqb;
+}
+
+template <int NW>
+static size_t wide_fwd_ws(int Bq, int S, int E)
+{
+    const int nqb = (S + LWB - 1) / LWB;
+    const int pl = wide_fwd_pl<NW>(Bq, nqb);
+    const long pmax = (nqb + pl - 1) / pl;
+    if (pmax <= 1)
+        return 0;
+    const size_t N = (size_t)Bq * S;
+    return (size_t)pmax * N * ((size_t)E + 1) * sizeof(float);
+}
+
+size_t lin_wide_ws_bytes(int Bq, int S, int D, int E)
+{
+    if (!lin_wide_ok(D, E))
+        return 0;
+    const int m = std::max(D, E);
+    if (m <= 128)
+        return 0;
+    return m <= 256 ? wide_fwd_ws<4>(Bq, S, E) : wide_fwd_ws<8>(Bq, S, E);
+}
+
+// ws: lin_wide_ws_bytes of scratch, or null (whole query blocks); z_cache
+// needs whole blocks.
 template <int PHI, int NW>
 static hipError_t wide_fwd_t(const float* Q, const float* K, const float* V, float* O,
                              float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                             bool vec, hipStream_t st)
+                             bool vec, void* ws, hipStream_t st)
 {
     const int nqb = (S + LWB - 1) / LWB;
-    dim3 grid((unsigned)((long)nqb * Bq)), block(64 * NW);
-    ProfScope ps(st, "lin_wide_fwd");
-    if (vec)
-        CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V, O,
-                           den, zc, S, D, E, Bq, den_eps);
-    else
-        CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V, O,
-                           den, zc, S, D, E, Bq, den_eps);
+    const int PL = (zc == nullptr && ws != nullptr) ? wide_fwd_pl<NW>(Bq, nqb) : nqb;
+    const int PMAX = (nqb + PL - 1) / PL;
+    const long N = (long)Bq * S;
+    float* wsO = PMAX > 1 ? (float*)ws : nullptr;
+    float* wsD = PMAX > 1 ? wsO + (size_t)PMAX * N * E : nullptr;
+    dim3 grid((unsigned)((long)nqb * PMAX * Bq)), block(64 * NW);
+    {
+        ProfScope ps(st, "lin_wide_fwd");
+        if (vec)
+            CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V, O,
+                       den, zc, S, D, E, Bq, den_eps, PL, PMAX, wsO, wsD);
+        else
+            CXG_LAUNCH((lin_wide_fwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V, O,
+                       den, zc, S, D, E, Bq, den_eps, PL, PMAX, wsO, wsD);
+    }
+    if (PMAX > 1) {
+        ProfScope ps(st, "lin_wide_fin");
+        CXG_LAUNCH(lin_wide_fin_kernel, dim3((unsigned)((N * E + 255) / 256)), dim3(256), 0, st,
+                   wsO, wsD, O, den, S, E, Bq, PL, den_eps);
+    }
     return hipGetLastError();
 }
 
@@ -540,16 +684,16 @@ static hipError_t wide_bwd_t(const float* Q, const float* K, const float* V, con
 template <int PHI>
 static hipError_t wide_fwd_p(const float* Q, const float* K, const float* V, float* O,
                              float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                             bool vec, hipStream_t st)
+                             bool vec, void* ws, hipStream_t st)
 {
     const int m = std::max(D, E);
     if (m <= 64)
-        return wide_fwd_t<PHI, 1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
+        return wide_fwd_t<PHI, 1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
     if (m <= 128)
-        return wide_fwd_t<PHI, 2>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
+        return wide_fwd_t<PHI, 2>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
     if (m <= 256)
-        return wide_fwd_t<PHI, 4>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
-    return wide_fwd_t<PHI, 8>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
+        return wide_fwd_t<PHI, 4>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
+    return wide_fwd_t<PHI, 8>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
 }
 
 template <int PHI>
@@ -569,14 +713,14 @@ static hipError_t wide_bwd_p(const float* Q, const float* K, const float* V, con
 
 hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                                float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                               hipStream_t st)
+                               void* ws, hipStream_t st)
 {
     const bool vec = D % 4 == 0 && E % 4 == 0 && al16x(Q) && al16x(K) && al16x(V) && al16x(O);
     if (phi == PHI_ELU1)
-        return wide_fwd_p<PHI_ELU1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
+        return wide_fwd_p<PHI_ELU1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
     if (phi == PHI_ELU1_LG)
-        return wide_fwd_p<PHI_ELU1_LG>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
-    return wide_fwd_p<PHI_NONE>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, st);
+        return wide_fwd_p<PHI_ELU1_LG>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
+    return wide_fwd_p<PHI_NONE>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
 }
 
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,

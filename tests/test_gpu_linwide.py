@@ -188,3 +188,57 @@ def test_wide_fused_backward_mean_shift(dev, v_mean):
     rdK, rdV = orc.kattn_bwd_dKdV(Q, K, V, dnum, dden, B, S, D, E, nthreads=8)
     assert_close(_np(dK), rdK, "dK")
     assert_close(_np(dV), rdV, "dV")
+
+
+def _launches(name):
+    import cxxgpt_attn as cx
+    return cx.prof_query(name)[1]
+
+
+# at most a few hundred jobs when split (one or two resident workgroups per CU)
+@pytest.mark.parametrize("B,S,D,E", [(1, 256, 512, 512), (8, 256, 512, 512), (6, 200, 512, 512),
+                                     (4, 333, 256, 192), (2, 17, 512, 512)])
+def test_forward_key_split(dev, B, S, D, E):
+    """Forwards that return no z_cache split the keys of each query block into
+    parts when B' x S/16 jobs would leave resident workgroups idle (widths above
+    128), and add the parts' numerators and denominators in a second launch.
+    Both forwards (two_stage with phi inside, linear_cuda with phi outside)
+    against the oracle, and against the same call with z_cache requested (whole
+    query blocks), which differs only in the order of the key sums."""
+    import torch
+    import cxxgpt_attn as cx
+    N = B * S
+    Q, K, V, _ = normal_inputs((N, D), (N, E), 11 * S + B + D)
+    Qp, Kp = orc.phi_elu_forward(Q, D, D), orc.phi_elu_forward(K, D, D)
+    tQ, tK, tV, tQp, tKp = _t(Q, dev), _t(K, dev), _t(V, dev), _t(Qp, dev), _t(Kp, dev)
+    out = {}
+    for api in ("kattn", "lcu"):
+        fn = cx.kattn_fwd if api == "kattn" else cx.lin_fwd
+        q, k = (tQ, tK) if api == "kattn" else (tQp, tKp)
+        for split in (True, False):
+            O, den = _nan(dev, N, E), _nan(dev, N)
+            zc = None if split else _nan(dev, N, D)
+            torch.cuda.synchronize()
+            cx.prof_reset()
+            cx.prof_enable(True)
+            fn(q, k, tV, O, den, zc, None, None, B, S, D, E)
+            torch.cuda.synchronize()
+            fin = _launches("lin_wide_fin")
+            cx.prof_enable(False)
+            cx.prof_reset()
+            if not split:
+                assert fin == 0
+            elif S > 16:
+                assert fin == 1, f"{api}: the keys of B{B} S{S} were not split"
+            out[api, split] = (_np(O), _np(den))
+    rO, rden, _ = orc.kattn_fwd(Q, K, V, B, S, D, E, nthreads=8)
+    lO, lden, _, _, _ = orc.lcu_fwd(Qp, Kp, V, B, S, D, E, nthreads=8)
+    for api, (ro, rd) in (("kattn", (rO, rden)), ("lcu", (lO, lden))):
+        for split in (True, False):
+            o, d = out[api, split]
+            assert_close(o, ro, f"{api} split={split} O")
+            assert_close(d, rd, f"{api} split={split} den")
+        assert_close(out[api, True][0], out[api, False][0], f"{api} O split vs whole",
+                     atol=1e-6, rtol=1e-5)
+        assert_close(out[api, True][1], out[api, False][1], f"{api} den split vs whole",
+                     atol=1e-6, rtol=1e-5)
