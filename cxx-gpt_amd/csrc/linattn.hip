@@ -1354,6 +1354,7 @@ static int lin_slots(int pass)
 LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 {
     LinPlan p;
+    p.pass = pass;
     p.quad = lin_quad_ok(D, E, S);
     p.fast = !p.quad && (D <= 64 && E <= 64);
     p.nseg = 1;
@@ -1381,8 +1382,10 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
 {
-    if (!p.fast)   // the quadratic form: p.L = S
-        return p.quad ? lin_wide_ws_bytes(Bq, p.L, D, E) : (size_t)Bq * D * E * sizeof(float);
+    if (p.quad)   // the forward's key parts (p.L = S)
+        return p.pass == LIN_PASS_FWD ? lin_wide_ws_bytes(Bq, p.L, D, E) : 0;
+    if (!p.fast)
+        return (size_t)Bq * D * E * sizeof(float);
     if (p.nseg <= 1)
         return 0;
     return (size_t)Bq * p.nseg * LIN_WS * sizeof(float);

@@ -40,6 +40,7 @@ struct LinPlan {
     bool fast;   // D <= 64 and E <= 64 and not quad: chunked MFMA scan
     int nseg;    // segments per sequence (fast path)
     int L;       // rows per segment (multiple of 16)
+    int pass;    // LinPass the plan was made for
 };
 
 // The scan pass a plan is for: each sizes its segments to its own main
