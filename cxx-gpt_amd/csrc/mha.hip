@@ -140,22 +140,6 @@ struct TileRegs {
             }
         }
     }
-    // transposed [c][row] with row stride LD floats
-    template <int LD>
-    __device__ __forceinline__ void store_t(float* __restrict__ T, int tid) const
-    {
-#pragma unroll
-        for (int i = 0; i < UPT; i++) {
-            const int u = tid + i * NT;
-            if (NU % NT == 0 || u < NU) {
-                const int row = u / CPR, c = 4 * (u - row * CPR);
-                T[(c + 0) * LD + row] = r[i][0];
-                T[(c + 1) * LD + row] = r[i][1];
-                T[(c + 2) * LD + row] = r[i][2];
-                T[(c + 3) * LD + row] = r[i][3];
-            }
-        }
-    }
 };
 
 // ----------------------------------------------------------------------------
