@@ -408,6 +408,10 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         getR(bQ, q, l16, g);
         getR(bK, k, l16, g);
 
+        // From here to the outputs the chunk is MFMA-dense: raised issue
+        // priority lets this wave run ahead of the other workgroup's wave on its
+        // SIMD while that one stages or waits (lin_fwd 116.3 -> 115.1 us at C3).
+        __builtin_amdgcn_s_setprio(1);
         // A^T[s][t] = phi(K_s).phi(Q_t), lane t = l16, element r <-> s = 4g + r; keep s <= t
         f4 At = f4zero();
 #pragma unroll
@@ -483,6 +487,7 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                     acc = mfma16(kC[dt][r], vC[j][r], acc);
                 St[dt][j] = acc;
             }
+        __builtin_amdgcn_s_setprio(0);
         // outputs of row t0 + l16: O and z_cache columns of this wave's two
         // tiles; den from wave 0
         const bool ok = full || rok;
