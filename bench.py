@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Headline step ("c2"): causal softmax MHA forward +
+Headline step ("c2", the headline metric's configuration): causal softmax MHA forward +
 backward, FP32, B=8 H=12 S=256 Dh=64, through the C ABI of
 libcxxgpt_attn.so -- cxg_mha_fwd (writes O and the row log-sum-exp) then
 cxg_mha_bwd (consumes it); these replace the reference's two_stage_cuda::

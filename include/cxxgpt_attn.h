@@ -267,10 +267,11 @@ int cxg_lin_elu_bwd(const float *Xq, const float *Xk, const float *V, const floa
                     float *dXk, float *dV, size_t B, size_t S, size_t E, cxg_stream_t stream);
 
 /* Hadamard+Exp attention block with the feature map fused into the scans: no
- * single counterpart in the reference, whose callers (BASELINE C4) apply
- * phi(x) = exp(H x / 8) (cxg_phi_hexp_fwd below) to the raw projections
- * before causal_linear_attention_fwd and map the feature gradients back with
- * phi's backward after the three backward calls (linear_cuda_kernels.cu:
+ * single counterpart in the reference; its benchmark configuration (96
+ * sequences, S = 1024, D = E = 64) applies phi(x) = exp(H x / 8)
+ * (cxg_phi_hexp_fwd below) to the raw projections before
+ * causal_linear_attention_fwd and maps the feature gradients back with phi's
+ * backward after the three backward calls (linear_cuda_kernels.cu:
  * 10-298).  cxg_lin_hexp_fwd: O and den_cache (eps included) from the raw
  * Xq, Xk (B*S, E) and V, plus the context for the backward
  * (cxg_lin_ctx_size(B, S, E, E) bytes; may be NULL with ctx_bytes 0).

@@ -98,8 +98,8 @@ def test_ffn_accumulates_and_scratch(dev):
 
 
 def test_ffn_c2_shape(dev):
-    """B*S = 2048 rows, n_embd 768, F = 6144 (BASELINE C2 with the reference's
-    N = 2): against float64 products on the GPU."""
+    """B*S = 2048 rows, n_embd 768, F = 6144 (the MHA benchmark shape B8 S256
+    with the reference's expansion N = 2): against float64 products on the GPU."""
     import torch
     M, E, F = 2048, 768, 6144
     X, W1, W2, dY = _inputs(M, E, F, 2048)

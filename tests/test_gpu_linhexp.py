@@ -2,8 +2,9 @@
 
 The entry points take the raw projections Xq, Xk and apply the feature map
 phi(x) = exp(H x / 8) (H the 64x64 Sylvester Hadamard matrix) inside the
-fused pair's kernels.  The reference's callers (BASELINE C4) run the map as
-separate passes around the linear_cuda calls (linear_cuda_kernels.cu:10-298);
+fused pair's kernels.  The benchmark configuration (96 sequences, S = 1024,
+D = E = 64) runs the map as separate passes around the linear_cuda calls
+(linear_cuda_kernels.cu:10-298);
 the oracle here is that chain: phi_hexp_forward x2 -> lcu_fwd; lcu_bwd_step1
 -> lcu_bwd_dQ -> lcu_bwd_dKdV -> phi_hexp_backward x2.  Each case also runs
 the library's own unfused path (cxg_phi_hexp_fwd, cxg_lin_fwd(_ctx),
