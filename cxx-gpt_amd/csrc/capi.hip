@@ -308,16 +308,24 @@ static int mha_bwd_common(const float* Q, const float* K, const float* V, const 
     float* lse_ws = (float*)((char*)ws.p + half);
     const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
     hipError_t e;
-    if (lse == nullptr) {
-        // statistics-only forward pass (the reference recomputes them too)
-        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s, rope);
+    if (lse == nullptr && mha_stats_prep_ok(iB, iS, iH, iD)) {
+        // statistics-only forward pass (the reference recomputes them too),
+        // with the pre-pass in the same launch
+        e = mha_stats_prep_launch(Q, K, V, O, dO, lse_ws, Di, dQ, iB, iS, iH, iD, s, rope);
         if (e != hipSuccess)
             return hip_status(e);
         lse = lse_ws;
+    } else {
+        if (lse == nullptr) {
+            e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s, rope);
+            if (e != hipSuccess)
+                return hip_status(e);
+            lse = lse_ws;
+        }
+        e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
+        if (e != hipSuccess)
+            return hip_status(e);
     }
-    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
-    if (e != hipSuccess)
-        return hip_status(e);
     e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s, rope);
     return hip_status(e);
 }
@@ -401,15 +409,22 @@ int cxg_mha_bwd_noalloc(const float* Q, const float* K, const float* V, const fl
     float* lse_ws = sp + CXG_MHA_BWD_NOALLOC_MAX_ROWS;
     hipStream_t s = (hipStream_t)stream;
     const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
-    if (lse == nullptr) {
-        e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s);
+    if (lse == nullptr && mha_stats_prep_ok(iB, iS, iH, iD)) {
+        e = mha_stats_prep_launch(Q, K, V, O, dO, lse_ws, Di, dQ, iB, iS, iH, iD, s);
         if (e != hipSuccess)
             return hip_status(e);
         lse = lse_ws;
+    } else {
+        if (lse == nullptr) {
+            e = mha_fwd_launch(Q, K, V, nullptr, lse_ws, iB, iS, iH, iD, s);
+            if (e != hipSuccess)
+                return hip_status(e);
+            lse = lse_ws;
+        }
+        e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
+        if (e != hipSuccess)
+            return hip_status(e);
     }
-    e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
-    if (e != hipSuccess)
-        return hip_status(e);
     return hip_status(mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s));
 }
 

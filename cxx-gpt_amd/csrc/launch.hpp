@@ -67,6 +67,13 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
                           const MhaRope* rope = nullptr);
 hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ,
                                int B, int S, int H, int Dh, hipStream_t st);
+// lse (the statistics pass) and the pre-pass's Di and dQ = 0 in one launch, for
+// the shapes mha_stats_prep_ok accepts (Dh <= 64, one round of jobs;
+// hipErrorInvalidValue otherwise: the two launches above then).
+bool mha_stats_prep_ok(int B, int S, int H, int Dh);
+hipError_t mha_stats_prep_launch(const float* Q, const float* K, const float* V, const float* O,
+                                 const float* dO, float* lse, float* Di, float* dQ, int B, int S,
+                                 int H, int Dh, hipStream_t st, const MhaRope* rope = nullptr);
 hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
                                const float* dO, const float* lse, const float* Di,
                                float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,

@@ -212,12 +212,18 @@ __device__ __forceinline__ int job_tid()
 // once the last key tile of a job has been through its math, requests the
 // next job's Q rows and first two K/V tiles, so that they arrive while the
 // current job merges its key splits and writes O.
-template <int DHP, int NSPLIT, bool VEC, bool WRITE_O, bool ROPE>
+//
+// PREP (statistics pass, DHP <= 64 only): the backward's pre-pass rides along,
+// Di = rowsum(dO * O) of the job's rows into Di and their dQ rows zeroed, so
+// the reference-signature backward needs no separate pre-pass launch.
+template <int DHP, int NSPLIT, bool VEC, bool WRITE_O, bool ROPE, bool PREP = false>
 __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
-    float qscale, int pair_cus, const MhaRope rope)
+    float qscale, int pair_cus, const MhaRope rope, const float* __restrict__ pO,
+    const float* __restrict__ pdO, float* __restrict__ pDi, float* __restrict__ pdQ)
 {
+    static_assert(!PREP || (!WRITE_O && DHP <= 64 && NSPLIT == 2), "pre-pass rides on 512-thread statistics passes");
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
     constexpr int KS = SM::KS, MS = SM::MS;
@@ -268,6 +274,13 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
     // pipeline, nothing more; the double-buffered one requests tiles 1 and 2
     // once tile 0 is in LDS, so that every workgroup's first tile arrives
     // ahead of the later ones).
+    // PREP: O and dO of the job's rows, 8 threads a row (row tid/8, f4 units
+    // tid%8 + 8i), loaded with the job's first loads; their dot products are
+    // formed once key tile 0 is in LDS, before the next job's loads reuse them.
+    constexpr int PUPR = DHP / 4;                  // f4 units per row
+    constexpr int PPU = PUPR >= 8 ? PUPR / 8 : 1;  // units per thread
+    f4 po[PREP ? PPU : 1], pd[PREP ? PPU : 1];
+    float pdot = 0.0f;
     auto load_first = [&](const Job& j) {
         const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4, qg = pair_group(wave);
@@ -277,6 +290,15 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         for (int dt = 0; dt < NDT; dt++)
             qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
         load_kv(kr, vr, j, 0);
+        if constexpr (PREP) {
+            const int prow = min(j.qb * MHA_BM + (tid >> 3), S - 1);
+            const long off = j.base + (long)prow * rs;
+#pragma unroll
+            for (int i = 0; i < PPU; i++) {
+                po[i] = load4c<VEC>(pO + off, 4 * ((tid & 7) + 8 * i), Dh);
+                pd[i] = load4c<VEC>(pdO + off, 4 * ((tid & 7) + 8 * i), Dh);
+            }
+        }
     };
 
     // The grid never exceeds the job count.  pair_cus > 0: one job per
@@ -414,6 +436,16 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             load_kv(kr1, vr1, jc, min(1, nkb - 1));
             load_kv(kr, vr, jc, min(2, nkb - 1));
             __syncthreads();
+            if constexpr (PREP) {
+                // this thread's part of Di (columns past Dh masked)
+                pdot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < PPU; i++) {
+                    const int c = 4 * ((tid & 7) + 8 * i);
+                    const f4 o = mask4(po[i], c, Dh, true), d = mask4(pd[i], c, Dh, true);
+                    pdot += o[0] * d[0] + o[1] * d[1] + o[2] * d[2] + o[3] * d[3];
+                }
+            }
             // Iteration kb < nkb-1: the math of tile kb (LDS buffer kb&1),
             // then registers (kx, vx), holding tile kb+1, go to buffer
             // (kb+1)&1 (last read in iteration kb-1) and are refilled with
@@ -520,6 +552,21 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             }
             if (lse != nullptr && g == 0)
                 lse[(long)bh * S + myq] = (m_run + fast_log2(l_tot)) * kLn2;
+        }
+        if constexpr (PREP) {
+            float dsum = pdot;
+            dsum += __shfl_xor(dsum, 1, 64);
+            dsum += __shfl_xor(dsum, 2, 64);
+            dsum += __shfl_xor(dsum, 4, 64);
+            const int prow = qb * MHA_BM + (tid >> 3);
+            if (prow < S) {
+                if ((tid & 7) == 0)
+                    pDi[(long)bh * S + prow] = dsum;
+                float* drow = pdQ + base + (long)prow * rs;
+#pragma unroll
+                for (int i = 0; i < PPU; i++)
+                    store4<VEC>(drow, 4 * ((tid & 7) + 8 * i), Dh, f4zero());
+            }
         }
         if (!more)
             break;
@@ -1097,10 +1144,18 @@ struct MhaSplits {
     static constexpr bool FWD_PAIR = DHP <= 64;
 };
 
+// The backward pre-pass riding on a statistics pass (mha_stats_prep_launch).
+struct MhaPrep {
+    const float* O;
+    const float* dO;
+    float* Di;
+    float* dQ;
+};
+
 template <int DHP, bool VEC, bool ROPE>
 static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, float* O,
                                 float* lse, int B, int S, int H, int Dh, hipStream_t st,
-                                const MhaRope& rope)
+                                const MhaRope& rope, const MhaPrep* prep = nullptr)
 {
     constexpr int NS = MhaSplits<DHP>::FWD;
     const int BH = B * H;
@@ -1117,11 +1172,22 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     if (O != nullptr) {
         ProfScope ps(st, ROPE ? "mha_rope_fwd" : "mha_fwd");
         CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, true, ROPE>), grid, block, 0, st, Q, K,
-                           V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
+                   V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr, nullptr,
+                   nullptr);
+    } else if (prep != nullptr) {
+        if constexpr (DHP <= 64) {
+            ProfScope ps(st, "mha_stats");
+            CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE, true>), grid, block, 0, st, Q,
+                       K, V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, prep->O, prep->dO,
+                       prep->Di, prep->dQ);
+        } else {
+            return hipErrorInvalidValue;   // the caller runs the separate pre-pass
+        }
     } else {
         ProfScope ps(st, "mha_stats");
         CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE>), grid, block, 0, st, Q, K,
-                           V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope);
+                   V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr, nullptr,
+                   nullptr);
     }
     return hipGetLastError();
 }
@@ -1129,19 +1195,21 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
 template <int DHP>
 static hipError_t fwd_dispatch(const float* Q, const float* K, const float* V, float* O,
                                float* lse, int B, int S, int H, int Dh, hipStream_t st,
-                               const MhaRope* rope)
+                               const MhaRope* rope, const MhaPrep* prep = nullptr)
 {
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
-                     (O == nullptr || aligned16(O));
+                     (O == nullptr || aligned16(O)) &&
+                     (prep == nullptr ||
+                      (aligned16(prep->O) && aligned16(prep->dO) && aligned16(prep->dQ)));
     if (rope != nullptr) {
         if (vec)
-            return fwd_dispatch2<DHP, true, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope);
-        return fwd_dispatch2<DHP, false, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope);
+            return fwd_dispatch2<DHP, true, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope, prep);
+        return fwd_dispatch2<DHP, false, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope, prep);
     }
     const MhaRope none{};
     if (vec)
-        return fwd_dispatch2<DHP, true, false>(Q, K, V, O, lse, B, S, H, Dh, st, none);
-    return fwd_dispatch2<DHP, false, false>(Q, K, V, O, lse, B, S, H, Dh, st, none);
+        return fwd_dispatch2<DHP, true, false>(Q, K, V, O, lse, B, S, H, Dh, st, none, prep);
+    return fwd_dispatch2<DHP, false, false>(Q, K, V, O, lse, B, S, H, Dh, st, none, prep);
 }
 
 void mha_rope_freqs(int Dh, MhaRope* r)
@@ -1163,6 +1231,36 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
     if (Dh <= 128)
         return fwd_dispatch<128>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     return fwd_dispatch<256>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
+}
+
+// The pre-pass rides on the statistics pass for heads up to 64 wide when the
+// pass's jobs fit one round of two workgroups per compute unit: the saved
+// launch (C2 legacy step 63.1 -> 61.2 us) outweighs each job's extra loads and
+// stores there, not over many rounds (B32 H64 S256 Dh8: statistics pass 56 ->
+// 66 us against an 11 us pre-pass).
+bool mha_stats_prep_ok(int B, int S, int H, int Dh)
+{
+    const long njobs = (long)B * H * ((S + MHA_BM - 1) / MHA_BM);
+    return Dh <= 64 && njobs <= 2L * device_cus();
+}
+
+// Statistics pass (lse) with the backward's pre-pass (Di, dQ = 0) in the same
+// launch (mha_stats_prep_ok shapes; others return hipErrorInvalidValue and
+// take mha_fwd_launch + mha_bwd_prep_launch).
+hipError_t mha_stats_prep_launch(const float* Q, const float* K, const float* V, const float* O,
+                                 const float* dO, float* lse, float* Di, float* dQ, int B, int S,
+                                 int H, int Dh, hipStream_t st, const MhaRope* rope)
+{
+    if (!mha_stats_prep_ok(B, S, H, Dh))
+        return hipErrorInvalidValue;
+    const MhaPrep prep{O, dO, Di, dQ};
+    if (Dh <= 16)
+        return fwd_dispatch<16>(Q, K, V, nullptr, lse, B, S, H, Dh, st, rope, &prep);
+    if (Dh <= 32)
+        return fwd_dispatch<32>(Q, K, V, nullptr, lse, B, S, H, Dh, st, rope, &prep);
+    if (Dh <= 64)
+        return fwd_dispatch<64>(Q, K, V, nullptr, lse, B, S, H, Dh, st, rope, &prep);
+    return hipErrorInvalidValue;
 }
 
 // The same for Dh = 4U (U = 1, 2, 4, 8, 16 lanes per (row, head) segment) with
