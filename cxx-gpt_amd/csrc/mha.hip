@@ -1266,10 +1266,10 @@ hipError_t mha_stats_prep_launch(const float* Q, const float* K, const float* V,
 // The same for Dh = 4U (U = 1, 2, 4, 8, 16 lanes per (row, head) segment) with
 // aligned rows: O and dO are read as one flat array of 16-byte units, thread
 // t taking units t + j*T (T threads in the grid, j < PREP_UNITS) with every
-// load issued before any arithmetic (one unit per thread ran at 3.8 TB/s at
-// Dh = 64 and 2 lanes of 16 busy at Dh = 8).  A segment's U units sit in U
+// load issued before any arithmetic (C2, 19.6 MB: 5.2 us at one or four units
+// per thread, 4.7 us at two, 6.4 us at eight).  A segment's U units sit in U
 // consecutive lanes; their partial dot products are summed by lane exchange.
-constexpr int PREP_UNITS = 4;
+constexpr int PREP_UNITS = 2;
 
 template <int U, bool ZERO>
 __global__ __launch_bounds__(256) void mha_bwd_prep_vec_kernel(
