@@ -1235,7 +1235,7 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
 
 // The pre-pass rides on the statistics pass for heads up to 64 wide when the
 // pass's jobs fit one round of two workgroups per compute unit: the saved
-// launch (C2 legacy step 63.1 -> 61.2 us) outweighs each job's extra loads and
+// launch (C2 legacy step 63.1 -> 58.8 us) outweighs each job's extra loads and
 // stores there, not over many rounds (B32 H64 S256 Dh8: statistics pass 56 ->
 // 66 us against an 11 us pre-pass).
 bool mha_stats_prep_ok(int B, int S, int H, int Dh)
