@@ -203,3 +203,25 @@ def test_error_paths(dev):
     assert cx.call_status("cxg_mha_bwd", p, p, p, p, p, None, p, p, p, 1, 8, 1, 8,
                           cx._ptr(ws_small), 4, st) == cx.CXG_ERR_WORKSPACE
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("B,S,H,Dh", [
+    (8, 256, 12, 64),    # C2: the pre-pass rides on the statistics pass
+    (2, 65, 3, 32), (1, 300, 4, 8), (3, 100, 2, 7),
+    (5, 130, 50, 16),    # 750 jobs: statistics pass and pre-pass as two launches
+    (2, 70, 2, 100),     # Dh > 64: two launches
+])
+def test_reference_signature_backward(dev, B, S, H, Dh):
+    """The backward without lse (the reference's signature) recomputes the
+    statistics; for Dh <= 64 and one round of jobs the pre-pass (Di, dQ = 0)
+    runs inside that launch.  Its gradients against the oracle and against
+    the lse path's (separate pre-pass), which differ only in the order of
+    Di's sum."""
+    Q, K, V, dO = normal_inputs((B * S, H * Dh), (B * S, H * Dh), 13 * S + H + Dh)
+    O, lse = _run_fwd(dev, Q, K, V, B, S, H, Dh, want_lse=True)
+    legacy = _run_bwd(dev, Q, K, V, O, dO, B, S, H, Dh)
+    with_lse = _run_bwd(dev, Q, K, V, O, dO, B, S, H, Dh, lse=lse)
+    ref = orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=8)
+    for name, a, b, r in zip(("dQ", "dK", "dV"), legacy, with_lse, ref):
+        assert_close(a, r, f"no-lse {name}")
+        assert_close(a, b, f"no-lse vs lse {name}", atol=2e-6, rtol=2e-5)
