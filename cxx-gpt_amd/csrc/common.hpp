@@ -200,4 +200,17 @@ __device__ __forceinline__ f4 buffer_load_f4(__amdgpu_buffer_rsrc_t r, unsigned 
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// Raw buffer over [base, base + bytes): reads at or past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const float* base, unsigned bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int)bytes, 0x00020000);
+}
+
+// 16-byte load at voff + soff, soff wave-uniform (a scalar operand, so a
+// tile's row offset costs no vector instruction).
+__device__ __forceinline__ f4 buffer_load_f4s(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff)
+{
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
 } // namespace cxg

@@ -41,6 +41,9 @@
 namespace cxg {
 
 constexpr int MHA_BM = 64;   // query rows per tile
+// Forward online softmax: the reference max moves when a score exceeds it by
+// more than this (log2 units), so unnormalised probabilities stay <= 2^8.
+constexpr float kLazyRescale = 8.0f;
 constexpr int MHA_BN = 64;   // key rows per tile
 
 // Rotary embedding of one f4 of a row at position pos, columns c .. c+3 of a
@@ -109,6 +112,30 @@ struct TileRegs {
             const int gr = min(row0 + row, S - 1);
             r[i] = load4c<VEC>(X + base + (long)gr * rs, c, Dh);
         }
+    }
+    // Whole-width heads (Dh == DHP, 16-byte aligned rows): the same units
+    // through a buffer descriptor whose range ends with row S-1 of the head,
+    // so rows past S read 0.  voff[i]: byte offset of unit i within a tile
+    // (tile-invariant, formed once); soff: the tile's first row, in bytes.
+    struct Offs {
+        unsigned v[UPT];
+    };
+    __device__ __forceinline__ static Offs offsets(long rs, int tid)
+    {
+        Offs o;
+#pragma unroll
+        for (int i = 0; i < UPT; i++) {
+            const int u = min(tid + i * NT, NU - 1);
+            const int row = u / CPR, c = 4 * (u - row * CPR);
+            o.v[i] = (unsigned)((row * rs + c) * 4);
+        }
+        return o;
+    }
+    __device__ __forceinline__ void loadb(__amdgpu_buffer_rsrc_t rsrc, const Offs& o, unsigned soff)
+    {
+#pragma unroll
+        for (int i = 0; i < UPT; i++)
+            r[i] = buffer_load_f4s(rsrc, o.v[i], soff);
     }
     // row-major [row][c] with row stride LD floats
     template <int LD>
@@ -216,7 +243,8 @@ __device__ __forceinline__ int job_tid()
 // PREP (statistics pass, DHP <= 64 only): the backward's pre-pass rides along,
 // Di = rowsum(dO * O) of the job's rows into Di and their dQ rows zeroed, so
 // the reference-signature backward needs no separate pre-pass launch.
-template <int DHP, int NSPLIT, bool VEC, bool WRITE_O, bool ROPE, bool PREP = false>
+template <int DHP, int NSPLIT, bool VEC, bool WRITE_O, bool ROPE, bool PREP = false,
+          bool BUF = false>
 __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int S, int H, int Dh, int BH, int nqb,
@@ -224,6 +252,7 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
     const float* __restrict__ pdO, float* __restrict__ pDi, float* __restrict__ pdQ)
 {
     static_assert(!PREP || (!WRITE_O && DHP <= 64 && NSPLIT == 2), "pre-pass rides on 512-thread statistics passes");
+    static_assert(!BUF || VEC, "buffer loads need aligned whole-width rows");
     using SM = FwdSmem<DHP, NSPLIT>;
     constexpr int NT = 256 * NSPLIT;
     constexpr int KS = SM::KS, MS = SM::MS;
@@ -242,6 +271,9 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         int bh, qb;
         long base;
     };
+    // BUF: descriptors over a head's rows 0..S-1 (built where used, in scalar
+    // registers: kept in the job record they would go to scratch memory)
+    const unsigned head_bytes = (unsigned)(((long)(S - 1) * rs + Dh) * 4);
     auto job_of = [&](int job) {
         Job j;
         const int qi = job / BH;
@@ -263,12 +295,23 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
     // Wider heads use one LDS buffer (two barriers per tile) and one register
     // stage (none for the widest).
     TileRegs<DHP, MHA_BN, NT, VEC> kr, vr, kr1, vr1;
+    using Offs = typename TileRegs<DHP, MHA_BN, NT, VEC>::Offs;
+    Offs koffs;
+    if constexpr (BUF)
+        koffs = TileRegs<DHP, MHA_BN, NT, VEC>::offsets(rs, threadIdx.x);
     auto load_kv = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx, TileRegs<DHP, MHA_BN, NT, VEC>& vx,
                        const Job& j, int kb) {
-        const int tid = job_tid();
-        kx.load(K, j.base, rs, kb * MHA_BN, S, Dh, tid);
-        if (WRITE_O)
-            vx.load(V, j.base, rs, kb * MHA_BN, S, Dh, tid);
+        if constexpr (BUF) {
+            const unsigned so = (unsigned)((long)kb * MHA_BN * rs * 4);
+            kx.loadb(buf_rsrc_n(K + j.base, head_bytes), koffs, so);
+            if (WRITE_O)
+                vx.loadb(buf_rsrc_n(V + j.base, head_bytes), koffs, so);
+        } else {
+            const int tid = job_tid();
+            kx.load(K, j.base, rs, kb * MHA_BN, S, Dh, tid);
+            if (WRITE_O)
+                vx.load(V, j.base, rs, kb * MHA_BN, S, Dh, tid);
+        }
     };
     // A job's first loads: Q rows and key tile 0 (and, for the single-stage
     // pipeline, nothing more; the double-buffered one requests tiles 1 and 2
@@ -284,11 +327,21 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
     auto load_first = [&](const Job& j) {
         const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4, qg = pair_group(wave);
-        const int q = min(j.qb * MHA_BM + qg * 16 + l16, S - 1);
-        const float* qrow = Q + j.base + (long)q * rs;
+        if constexpr (BUF) {
+            // rows past S read 0 (masked at the job start all the same)
+            const unsigned vo = (unsigned)(((qg * 16 + l16) * rs + 4 * g) * 4);
+            const unsigned so = (unsigned)((long)j.qb * MHA_BM * rs * 4);
+            const __amdgpu_buffer_rsrc_t rq = buf_rsrc_n(Q + j.base, head_bytes);
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
+            for (int dt = 0; dt < NDT; dt++)
+                qreg[dt] = buffer_load_f4s(rq, vo + 64 * dt, so);
+        } else {
+            const int q = min(j.qb * MHA_BM + qg * 16 + l16, S - 1);
+            const float* qrow = Q + j.base + (long)q * rs;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++)
+                qreg[dt] = load4c<VEC>(qrow, 16 * dt + 4 * g, Dh);
+        }
         load_kv(kr, vr, j, 0);
         if constexpr (PREP) {
             const int prow = min(j.qb * MHA_BM + (tid >> 3), S - 1);
@@ -324,6 +377,9 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++)
             oacc[dt] = f4zero();
+        // m_run: the lane's reference maximum (its query row's running max at
+        // the last rescale); l_run and oacc are relative to it.  A split that
+        // never sees a key keeps -1e30 and drops out of the merge.
         float m_run = -1e30f, l_run = 0.0f;
         // kb: the key tile held in (kx, vx); K is rotated on its way to LDS
         // under ROPE.
@@ -340,15 +396,19 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         // KS), over the first NA of the wave's NKT key blocks (the others lie
         // wholly above the causal diagonal).
         auto tile_math = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb,
-                             auto na) {
+                             auto na) __attribute__((always_inline)) {
             constexpr int NA = decltype(na)::value;
             const int k0 = kb * MHA_BN;
             // S^T block kt of this wave: lane holds query l16, keys k0 + 16*kt + 4*g + r.
-            // The NA key blocks run as interleaved accumulation chains.
+            // The NA key blocks run as interleaved accumulation chains.  The
+            // accumulators start at -m_run, so scores come out relative to
+            // the lane's reference (raw on the first tile, which sets it).
+            const bool first = kb == 0;   // wave-uniform
+            const f4 init = f4splat(first ? 0.0f : -m_run);
             f4 sacc[NA];
 #pragma unroll
             for (int kk = 0; kk < NA; kk++)
-                sacc[kk] = f4zero();
+                sacc[kk] = init;
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
@@ -374,26 +434,48 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     mloc = fmaxf(mloc, sacc[kk][r]);
-            mloc = xrow_max(mloc);
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = fast_exp2(m_run - m_new);
+            // Lazy rescaling: the reference moves only on the first tile or
+            // when a score of the wave exceeds its row's reference by more
+            // than 2^kLazyRescale (so p <= 2^8 and no sum can overflow).  The
+            // common case then needs no row max, no subtraction and no
+            // rescale of the accumulators; each VALU instruction here costs
+            // matrix-pipe time, since VALU and MFMA do not overlap on a SIMD.
             float psum = 0.0f;
+            if (first || __builtin_amdgcn_ballot_w64(mloc > kLazyRescale) != 0) {
+                mloc = xrow_max(mloc);   // every row has an unmasked key in a live block
+                const float d = first ? mloc : fmaxf(mloc, 0.0f);
+                const float alpha = first ? 0.0f : fast_exp2(-d);
+                m_run = (first ? 0.0f : m_run) + d;
 #pragma unroll
-            for (int kk = 0; kk < NA; kk++)
+                for (int kk = 0; kk < NA; kk++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float p = fast_exp2(sacc[kk][r] - m_new);
-                    sacc[kk][r] = p;
-                    psum += p;
-                }
-            l_run = l_run * alpha + psum;
-            m_run = m_new;
+                    for (int r = 0; r < 4; r++) {
+                        const float p = fast_exp2(sacc[kk][r] - d);
+                        sacc[kk][r] = p;
+                        psum += p;
+                    }
+                l_run = l_run * alpha + psum;
+                if (WRITE_O)
+#pragma unroll
+                    for (int dt = 0; dt < NDT; dt++)
+                        oacc[dt] = oacc[dt] * alpha;
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < NA; kk++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float p = fast_exp2(sacc[kk][r]);
+                        sacc[kk][r] = p;
+                        psum += p;
+                    }
+                l_run += psum;
+            }
             if (WRITE_O) {
                 // O^T += V^T P^T: A = V^T[d = 16dt + l16][key = 16kt + 4g + r], read
                 // as single floats from the row-major V tile; B = P^T from sacc.
 #pragma unroll
                 for (int dt = 0; dt < NDT; dt++) {
-                    f4 acc = oacc[dt] * alpha;
+                    f4 acc = oacc[dt];
 #pragma unroll
                     for (int kk = 0; kk < NA; kk++) {
                         const int kt = ks * NKT + kk;
@@ -410,7 +492,8 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         // the wave's blocks, and the rest are skipped (a block of scores that
         // are all masked leaves the online-softmax state unchanged), down to
         // the whole tile.
-        auto tile = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb) {
+        auto tile = [&](const float* __restrict__ Ks, const float* __restrict__ Vs, int kb)
+                        __attribute__((always_inline)) {
             if (NSPLIT == 1 || kb != qb) {
                 tile_math(Ks, Vs, kb, ic<NKT>{});
             } else {
@@ -423,7 +506,8 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         };
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            f4 q = mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok);
+            // BUF: rows past S were read as 0 and there are no columns past Dh
+            f4 q = BUF ? qreg[dt] : mask4(qreg[dt], 16 * dt + 4 * g, Dh, qok);
             if constexpr (ROPE)
                 q = rope4(q, min(myq, S - 1), 16 * dt + 4 * g, rope_w, 1.0f);
             qreg[dt] = q * qscale;
@@ -451,7 +535,7 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
             // (kb+1)&1 (last read in iteration kb-1) and are refilled with
             // tile kb+3.
             auto step = [&](TileRegs<DHP, MHA_BN, NT, VEC>& kx,
-                            TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) {
+                            TileRegs<DHP, MHA_BN, NT, VEC>& vx, int kb) __attribute__((always_inline)) {
                 const float* cur = smem + (kb & 1) * SM::TILES;
                 __builtin_amdgcn_s_setprio(1);
                 tile(cur, cur + MHA_BN * KS, kb);
@@ -1152,7 +1236,7 @@ struct MhaPrep {
     float* dQ;
 };
 
-template <int DHP, bool VEC, bool ROPE>
+template <int DHP, bool VEC, bool ROPE, bool BUF = false>
 static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, float* O,
                                 float* lse, int B, int S, int H, int Dh, hipStream_t st,
                                 const MhaRope& rope, const MhaPrep* prep = nullptr)
@@ -1171,23 +1255,23 @@ static hipError_t fwd_dispatch2(const float* Q, const float* K, const float* V, 
     }
     if (O != nullptr) {
         ProfScope ps(st, ROPE ? "mha_rope_fwd" : "mha_fwd");
-        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, true, ROPE>), grid, block, 0, st, Q, K,
-                   V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr, nullptr,
+        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, true, ROPE, false, BUF>), grid, block, 0, st, Q,
+                   K, V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr, nullptr,
                    nullptr);
     } else if (prep != nullptr) {
         if constexpr (DHP <= 64) {
             ProfScope ps(st, "mha_stats");
-            CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE, true>), grid, block, 0, st, Q,
-                       K, V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, prep->O, prep->dO,
-                       prep->Di, prep->dQ);
+            CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE, true, BUF>), grid, block, 0,
+                       st, Q, K, V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, prep->O,
+                       prep->dO, prep->Di, prep->dQ);
         } else {
             return hipErrorInvalidValue;   // the caller runs the separate pre-pass
         }
     } else {
         ProfScope ps(st, "mha_stats");
-        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE>), grid, block, 0, st, Q, K,
-                   V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr, nullptr,
-                   nullptr);
+        CXG_LAUNCH((mha_fwd_kernel<DHP, NS, VEC, false, ROPE, false, BUF>), grid, block, 0, st,
+                   Q, K, V, O, lse, S, H, Dh, BH, nqb, qscale, pair, rope, nullptr, nullptr,
+                   nullptr, nullptr);
     }
     return hipGetLastError();
 }
@@ -1201,12 +1285,21 @@ static hipError_t fwd_dispatch(const float* Q, const float* K, const float* V, f
                      (O == nullptr || aligned16(O)) &&
                      (prep == nullptr ||
                       (aligned16(prep->O) && aligned16(prep->dO) && aligned16(prep->dQ)));
+    // Whole-width heads take scalar-offset buffer loads (byte offsets within
+    // a head's S rows must fit 31 bits).
+    const bool buf = vec && Dh == DHP && (long)S * H * Dh * 4 < (1L << 31);
     if (rope != nullptr) {
+        if (buf)
+            return fwd_dispatch2<DHP, true, true, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope,
+                                                        prep);
         if (vec)
             return fwd_dispatch2<DHP, true, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope, prep);
         return fwd_dispatch2<DHP, false, true>(Q, K, V, O, lse, B, S, H, Dh, st, *rope, prep);
     }
     const MhaRope none{};
+    if (buf)
+        return fwd_dispatch2<DHP, true, false, true>(Q, K, V, O, lse, B, S, H, Dh, st, none,
+                                                     prep);
     if (vec)
         return fwd_dispatch2<DHP, true, false>(Q, K, V, O, lse, B, S, H, Dh, st, none, prep);
     return fwd_dispatch2<DHP, false, false>(Q, K, V, O, lse, B, S, H, Dh, st, none, prep);
