@@ -179,6 +179,13 @@ __device__ __forceinline__ void buffer_atomic_add_f32(__amdgpu_buffer_rsrc_t r, 
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)off, 0, 0);
 }
 
+// atomic add at voff + soff, soff wave-uniform
+__device__ __forceinline__ void buffer_atomic_add_f32s(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                       unsigned soff, float v)
+{
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)voff, (int)soff, 0);
+}
+
 __device__ __forceinline__ void buffer_store_f4(__amdgpu_buffer_rsrc_t r, unsigned off, f4 v)
 {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, (int)off, 0, 0);

@@ -716,7 +716,14 @@ struct BwdSmem {
 // job has been through its key-side work, requests the next job's K/V rows
 // and first query tiles, so that they arrive while the current job finishes
 // its dQ jobs and dK/dV reduction.
-template <int DHP, int BM, int NSPLIT, bool VEC, bool ROPE>
+//
+// The softmax scale is folded into V (so dP and dS come out scaled) and Di
+// once per job, which removes a multiply per dQ atomic and per dK element.
+// BUF (whole-width heads, double-buffered path): Q/dO/K/V rows through buffer
+// descriptors over the head's rows 0..S-1 with scalar row offsets, and dQ
+// atomics through one whose range drops rows past S, so neither loads nor
+// atomics spend vector instructions on addresses or masks.
+template <int DHP, int BM, int NSPLIT, bool VEC, bool ROPE, bool BUF = false>
 __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
@@ -724,6 +731,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     int BH, int nkb, float scale, float c2, const MhaRope rope)
 {
     using SM = BwdSmem<DHP, BM>;
+    static_assert(!BUF || (VEC && SM::DB), "buffer loads need the double-buffered aligned path");
     constexpr int NT = 256 * NSPLIT;
     constexpr int NW = NT / 64;
     constexpr int NDT = DHP / 16;
@@ -771,10 +779,22 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         TileRegs<DHP, BM, NT, VEC> q, d;
         float lse, di;
     };
+    // BUF: bytes from a head's first element to the end of its row S-1
+    const unsigned head_bytes = (unsigned)(((long)(S - 1) * rs + Dh) * 4);
+    using Offs = typename TileRegs<DHP, BM, NT, VEC>::Offs;
+    Offs qoffs;
+    if constexpr (BUF)
+        qoffs = TileRegs<DHP, BM, NT, VEC>::offsets(rs, threadIdx.x);
     auto load_q = [&](QTile& t, const Job& j, int q0) {
         const int tid = job_tid();
-        t.q.load(Q, j.base, rs, q0, S, Dh, tid);
-        t.d.load(dO, j.base, rs, q0, S, Dh, tid);
+        if constexpr (BUF) {
+            const unsigned so = (unsigned)((long)q0 * rs * 4);
+            t.q.loadb(buf_rsrc_n(Q + j.base, head_bytes), qoffs, so);
+            t.d.loadb(buf_rsrc_n(dO + j.base, head_bytes), qoffs, so);
+        } else {
+            t.q.load(Q, j.base, rs, q0, S, Dh, tid);
+            t.d.load(dO, j.base, rs, q0, S, Dh, tid);
+        }
         // Every thread loads (rows past S repeat row S-1, their P is masked to
         // 0); threads tid < BM store.  No use of the loaded data here (lse is
         // scaled at the LDS store), so the loads stay in flight.
@@ -795,12 +815,24 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     auto load_kv = [&](const Job& j) {
         const int tid = job_tid(), lane = tid & 63, wave = wave_id(tid);
         const int l16 = lane & 15, g = lane >> 4, kg = pair_group(wave);
-        const int key = min(j.k0 + kg * 16 + l16, S - 1);   // masked at job start
-        const long off = j.base + (long)key * rs;
+        if constexpr (BUF) {   // keys past S read 0
+            const unsigned vo = (unsigned)(((kg * 16 + l16) * rs + 4 * g) * 4);
+            const unsigned so = (unsigned)((long)j.k0 * rs * 4);
+            const __amdgpu_buffer_rsrc_t rk = buf_rsrc_n(K + j.base, head_bytes);
+            const __amdgpu_buffer_rsrc_t rv = buf_rsrc_n(V + j.base, head_bytes);
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            kreg[dt] = load4c<VEC>(K + off, 16 * dt + 4 * g, Dh);
-            vreg[dt] = load4c<VEC>(V + off, 16 * dt + 4 * g, Dh);
+            for (int dt = 0; dt < NDT; dt++) {
+                kreg[dt] = buffer_load_f4s(rk, vo + 64 * dt, so);
+                vreg[dt] = buffer_load_f4s(rv, vo + 64 * dt, so);
+            }
+        } else {
+            const int key = min(j.k0 + kg * 16 + l16, S - 1);   // masked at job start
+            const long off = j.base + (long)key * rs;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                kreg[dt] = load4c<VEC>(K + off, 16 * dt + 4 * g, Dh);
+                vreg[dt] = load4c<VEC>(V + off, 16 * dt + 4 * g, Dh);
+            }
         }
     };
     auto load_first_q = [&](const Job& j) {
@@ -841,7 +873,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             t.d.template store<QS>(st + BM * QS, tid);
             if (tid < BM) {
                 st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
-                st[2 * BM * QS + BM * TS + BM + tid] = t.di;
+                st[2 * BM * QS + BM * TS + BM + tid] = t.di * scale;   // scaled as dP is
             }
         };
         // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
@@ -967,13 +999,23 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     acc[r] = odd ? other * sn + acc[r] * cs : acc[r] * cs - other * sn;
                 }
             }
-            const __amdgpu_buffer_rsrc_t rq = buf_rsrc(dQ + base + (long)q0 * rs);
+            if constexpr (BUF) {
+                // rows past S fall outside the descriptor and are dropped
+                const __amdgpu_buffer_rsrc_t rq = buf_rsrc_n(dQ + base, head_bytes);
+                const unsigned vo = (unsigned)(((16 * qt + 4 * g) * rs + l16) * 4);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int qi = 16 * qt + 4 * g + r;
-                const unsigned off = (q0 + qi < S && d < Dh) ? (unsigned)(qi * rs + d) * 4u
-                                                             : kDropOffset;
-                buffer_atomic_add_f32(rq, off, acc[r] * scale);
+                for (int r = 0; r < 4; r++)
+                    buffer_atomic_add_f32s(rq, vo, (unsigned)(((long)(q0 + r) * rs + 16 * dt) * 4),
+                                           acc[r]);
+            } else {
+                const __amdgpu_buffer_rsrc_t rq = buf_rsrc(dQ + base + (long)q0 * rs);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int qi = 16 * qt + 4 * g + r;
+                    const unsigned off = (q0 + qi < S && d < Dh) ? (unsigned)(qi * rs + d) * 4u
+                                                                 : kDropOffset;
+                    buffer_atomic_add_f32(rq, off, acc[r]);
+                }
             }
         };
         const int dq_qt = SKIP ? pair_group(wave) : wave % NQT;
@@ -1034,13 +1076,15 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 query_side_f(st, q0, kend, std::false_type{});
         };
 
-        // Zero the K/V operands past S and Dh (their loads were clamped).
+        // Zero the K/V operands past S and Dh (their loads were clamped; BUF
+        // loads read 0 there already), and fold the softmax scale into V.
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            kreg[dt] = mask4(kreg[dt], 16 * dt + 4 * g, Dh, kok);
+            if constexpr (!BUF)
+                kreg[dt] = mask4(kreg[dt], 16 * dt + 4 * g, Dh, kok);
             if constexpr (ROPE)
                 kreg[dt] = rope4(kreg[dt], min(mykey, S - 1), 16 * dt + 4 * g, rope_w, 1.0f);
-            vreg[dt] = mask4(vreg[dt], 16 * dt + 4 * g, Dh, kok);
+            vreg[dt] = (BUF ? vreg[dt] : mask4(vreg[dt], 16 * dt + 4 * g, Dh, kok)) * scale;
         }
         // K^T tile for the dQ product, written from the K operand registers by
         // the waves of query split 0 (their key blocks kg cover the tile).
@@ -1163,7 +1207,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             for (int dt = 0; dt < NDT; dt++) {
                 if constexpr (ROPE)   // gradient w.r.t. the unrotated K: the inverse rotation
                     dk[dt] = rope4(dk[dt], mykey, 16 * dt + 4 * g, rope_w, -1.0f);
-                store4<VEC>(dK + off, 16 * dt + 4 * g, Dh, dk[dt] * scale);
+                store4<VEC>(dK + off, 16 * dt + 4 * g, Dh, dk[dt]);   // dS carries the scale
                 store4<VEC>(dV + off, 16 * dt + 4 * g, Dh, dv[dt]);
             }
         }
@@ -1484,6 +1528,15 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
     ProfScope ps(st, ROPE ? "mha_rope_bwd" : "mha_bwd");
+    // Whole-width heads on the double-buffered path take buffer loads and
+    // atomics (byte offsets within a head's S rows must fit 31 bits).
+    if constexpr (BwdSmem<DHP, BM>::DB) {
+        if (vec && Dh == DHP && aligned16(dQ) && (long)S * H * Dh * 4 < (1L << 31)) {
+            CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE, true>), grid, block, 0, st, Q, K,
+                       V, dO, lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
+            return hipGetLastError();
+        }
+    }
     if (vec)
         CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE>), grid, block, 0, st, Q, K, V, dO,
                            lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
