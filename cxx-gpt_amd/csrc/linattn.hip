@@ -431,7 +431,8 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             dpart += q[dt][0] * zR[dt][0] + q[dt][1] * zR[dt][1] + q[dt][2] * zR[dt][2] +
                      q[dt][3] * zR[dt][3];
         const float dn = xrow_sum(dpart);
-        const float inv = 1.0f / (dn + 1e-8f);
+        // hardware reciprocal (within 1 ulp) in place of a ten-instruction division
+        const float inv = __builtin_amdgcn_rcpf(dn + 1e-8f);
 
         f4 kC[4], vC[2];
         getC(bK, kC, l16, g);

@@ -152,7 +152,8 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
             }
             wv = 1.0f;
         } else {
-            const float inv = ok ? 1.0f / s.dn : 0.0f;
+            // the same reciprocal as the main backward's step 1
+            const float inv = ok ? __builtin_amdgcn_rcpf(s.dn) : 0.0f;
             const float dot = row16_sum(s.c[0] * s.b[0] + s.c[1] * s.b[1] + s.c[2] * s.b[2] +
                                         s.c[3] * s.b[3]);
 #pragma unroll
@@ -440,18 +441,23 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         float* bN = st + 3 * CHUNK;
         float* bd = st + 4 * CHUNK;
         {
-            // step 1 for this wave's four rows, phi, row masks; stage the chunk
+            // step 1 for this wave's four rows, phi, row masks; stage the chunk.
+            // 1/den through the hardware reciprocal (within 1 ulp; the exact
+            // division costs ten VALU instructions, which on gfx950 add to the
+            // chunk's MFMA time).  Rows past the end exist only in a
+            // sequence's last, partial chunk (a wave-uniform branch).
             const bool ok = t0 + lrow < tend;
-            const float inv = ok ? 1.0f / s.dn : 0.0f;
+            const float inv = ok ? __builtin_amdgcn_rcpf(s.dn) : 0.0f;
             const float dot = row16_sum(s.d[0] * s.o[0] + s.d[1] * s.o[1] + s.d[2] * s.o[2] +
                                         s.d[3] * s.o[3]);
-            f4 q, k, v;
-            const f4 pq = phi_row<PHI>(s.q, lane), pk = phi_row<PHI>(s.k, lane);
+            f4 q = phi_row<PHI>(s.q, lane), k = phi_row<PHI>(s.k, lane), v = s.v;
+            if (t0 + 16 > tend) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                q[i] = ok ? pq[i] : 0.0f;
-                k[i] = ok ? pk[i] : 0.0f;
-                v[i] = ok ? s.v[i] : 0.0f;
+                for (int i = 0; i < 4; i++) {
+                    q[i] = ok ? q[i] : 0.0f;
+                    k[i] = ok ? k[i] : 0.0f;
+                    v[i] = ok ? v[i] : 0.0f;
+                }
             }
             if (!FW) {
                 q = mask4(q, lcol, D, true);
@@ -594,11 +600,17 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             }
             // re-anchor: chunk 0 of the sequence starts from zero, an anchor chunk
             // from its forward-summed state; then request the next chunk's anchor
+            // (wave-uniform branches: taken at log2(S / 16) + 1 chunks)
             const int ca = cb + c;
-            const bool anc = is_anchor(ca);
+            if (ca == 0) {
 #pragma unroll
-            for (int et = 0; et < 4; et++)
-                StT[et] = ca == 0 ? f4zero() : (anc ? an[et] : StT[et]);
+                for (int et = 0; et < 4; et++)
+                    StT[et] = f4zero();
+            } else if (is_anchor(ca)) {
+#pragma unroll
+                for (int et = 0; et < 4; et++)
+                    StT[et] = an[et];
+            }
             fetch_anchor(ca - 1);
         }
         // dQ^T[d][t] = (z_t[d] dden_t + sum_e S[d][e] dnum_t[e]) phi'(Q_t[d]), with
