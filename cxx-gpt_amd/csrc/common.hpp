@@ -179,6 +179,12 @@ __device__ __forceinline__ void buffer_atomic_add_f32(__amdgpu_buffer_rsrc_t r, 
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r, (int)off, 0, 0);
 }
 
+// 4-byte load at voff + soff, soff wave-uniform
+__device__ __forceinline__ float buffer_load_f32s(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
 // atomic add at voff + soff, soff wave-uniform
 __device__ __forceinline__ void buffer_atomic_add_f32s(__amdgpu_buffer_rsrc_t r, unsigned voff,
                                                        unsigned soff, float v)

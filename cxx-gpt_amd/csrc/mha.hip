@@ -455,7 +455,7 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
                         psum += p;
                     }
                 l_run = l_run * alpha + psum;
-                if (WRITE_O)
+                if (WRITE_O && !first)   // the first tile's accumulators are still zero
 #pragma unroll
                     for (int dt = 0; dt < NDT; dt++)
                         oacc[dt] = oacc[dt] * alpha;
@@ -798,9 +798,19 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // Every thread loads (rows past S repeat row S-1, their P is masked to
         // 0); threads tid < BM store.  No use of the loaded data here (lse is
         // scaled at the LDS store), so the loads stay in flight.
-        const long i = (long)j.bh * S + min(q0 + (tid & (BM - 1)), S - 1);
-        t.lse = lse[i];
-        t.di = Di[i];
+        if constexpr (BUF) {
+            // [BH][S] arrays: rows past S read the next head's (or 0 past the
+            // end); their probabilities are masked
+            const unsigned n = (unsigned)((long)BH * S * 4);
+            const unsigned vo = (unsigned)((tid & (BM - 1)) * 4);
+            const unsigned so = (unsigned)(((long)j.bh * S + q0) * 4);
+            t.lse = buffer_load_f32s(buf_rsrc_n(lse, n), vo, so);
+            t.di = buffer_load_f32s(buf_rsrc_n(Di, n), vo, so);
+        } else {
+            const long i = (long)j.bh * S + min(q0 + (tid & (BM - 1)), S - 1);
+            t.lse = lse[i];
+            t.di = Di[i];
+        }
     };
     // Loads past the last query tile repeat it (clamped tile index), so the
     // job prologue issues the same memory operations on every path and the

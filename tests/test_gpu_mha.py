@@ -136,6 +136,9 @@ def test_config5_long_sequence(dev):
 @pytest.mark.parametrize("B,S,H,Dh", [
     (1, 1, 1, 64), (1, 5, 3, 8), (2, 65, 2, 16), (1, 130, 1, 24), (3, 100, 2, 7), (2, 33, 3, 4),
     (1, 200, 2, 100), (1, 96, 1, 128), (1, 70, 1, 200), (1, 129, 2, 256), (2, 64, 1, 1),
+    # whole-width heads with rows past S in the last tile and more than one
+    # batch element (the buffer loads' range must end with each head's row S-1)
+    (3, 100, 2, 64), (2, 77, 3, 32),
 ])
 def test_ragged_shapes(dev, B, S, H, Dh):
     """Ragged S (not a tile multiple), odd and wide head dims, S = 1."""
