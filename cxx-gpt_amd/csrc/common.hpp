@@ -62,12 +62,15 @@ __device__ __forceinline__ float xrow_max(float v)
     v = fmaxf(v, __shfl_xor(v, 32, 64));
     return v;
 }
-// Lane exchange within a 16-lane row through DPP (no LDS round trip).
+// Lane exchange within a 16-lane row through DPP (no LDS round trip).  The
+// patterns used here (quad_perm, row_ror, row_mirror, row_half_mirror) have a
+// source lane for every lane, so bound_ctrl is set: no old value to keep,
+// which lets the compiler fold the move into the instruction that uses it.
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v)
 {
     return __builtin_bit_cast(
-        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 
 // Sum over the 16 lanes of one row (lanes sharing l / 16): rotations by 8

@@ -1264,10 +1264,10 @@ __global__ __launch_bounds__(256) void phi_hexp_fwd_vec_kernel(const float* __re
         const long n = uc / upr;
         const int c = 4 * (int)(uc - n * upr);
         const bool tr = (c / 64) * 64 + 64 <= E;   // uniform over the 16-lane group
-        f4 y = fwht64_f4(v[k], lane);
+        f4 y = fwht64_f4(v[k], lane, 0.125f);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            y[i] = tr ? __expf(y[i] * 0.125f) : 0.0f;
+            y[i] = tr ? __expf(y[i]) : 0.0f;
         if (u < total)
             *reinterpret_cast<f4*>(phi + n * D + c) = y;
     }
@@ -1301,11 +1301,11 @@ __global__ __launch_bounds__(256) void phi_hexp_bwd_vec_kernel(const float* __re
         const long uc = min(u, total - 1);
         const long n = uc / upr;
         const int c = 4 * (int)(uc - n * upr);
-        f4 y = fwht64_f4(xv[k], lane);
+        f4 y = fwht64_f4(xv[k], lane, 0.125f);
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            y[i] = gv[k][i] * __expf(y[i] * 0.125f);
-        const f4 t = fwht64_f4(y, lane) * 0.125f;
+            y[i] = gv[k][i] * __expf(y[i]);
+        const f4 t = fwht64_f4(y, lane, 0.125f);
         if (u < total)
             *reinterpret_cast<f4*>(dx + n * E + c) = t;
     }

@@ -57,10 +57,11 @@ struct Phi<PHI_NONE> {
 
 // The value of lane l ^ M (M = 1, 2, 4, 8: within the lane's 16-lane row)
 // through DPP lane moves, which stay in the VALU (a shuffle through
-// ds_bpermute takes a round trip through the LDS unit).  Rotations are
-// row_ror: lane i receives lane (i - n) mod 16.
+// ds_bpermute takes a round trip through the LDS unit).  Lane l ^ 4 is two
+// moves: row_half_mirror (lane i of each 8 reads lane 7 - i, i.e. i ^ 7),
+// then quad_perm [3,2,1,0] (i ^ 3): i ^ 7 ^ 3 = i ^ 4.
 template <int M>
-__device__ __forceinline__ float lane_xor16(float v, int lane)
+__device__ __forceinline__ float lane_xor16(float v)
 {
     if constexpr (M == 1)
         return dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -70,9 +71,7 @@ __device__ __forceinline__ float lane_xor16(float v, int lane)
         return dpp_f<0x128>(v);   // row_ror:8
     else {
         static_assert(M == 4, "lane_xor16: M in {1, 2, 4, 8}");
-        const float up = dpp_f<0x12C>(v);   // row_ror:12: lane i + 4
-        const float dn = dpp_f<0x124>(v);   // row_ror:4: lane i - 4
-        return (lane & 4) ? dn : up;
+        return dpp_f<0x1B>(dpp_f<0x141>(v));   // row_half_mirror, quad_perm [3,2,1,0]
     }
 }
 
@@ -81,14 +80,14 @@ __device__ __forceinline__ float lane_xor16(float v, int lane)
 template <int M>
 __device__ __forceinline__ float bfly16(float v, int lane)
 {
-    const float u = lane_xor16<M>(v, lane);
+    const float u = lane_xor16<M>(v);
     return (lane & M) ? (u - v) : (v + u);
 }
 
 // Row-coalesced layout: a lane holds columns 4q .. 4q+3 (q = lane % 16) of a
 // row that the 16 lanes of its group share: bits 0-1 are in-lane, bits 2-5
-// exchanges within the 16-lane group.
-__device__ __forceinline__ f4 fwht64_f4(f4 v, int lane)
+// exchanges within the 16-lane group.  Returns (H v) * scale.
+__device__ __forceinline__ f4 fwht64_f4(f4 v, int lane, float scale)
 {
     f4 t;
     t[0] = v[0] + v[1];
@@ -111,15 +110,15 @@ __device__ __forceinline__ f4 fwht64_f4(f4 v, int lane)
 #pragma unroll
     for (int i = 0; i < 4; i++)
         v[i] = bfly16<8>(v[i], lane);
-    return v;
+    return v * scale;
 }
 
 __device__ __forceinline__ f4 hexp_row4(f4 v, int lane)
 {
-    f4 y = fwht64_f4(v, lane);
+    f4 y = fwht64_f4(v, lane, 0.125f);
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        y[i] = __expf(y[i] * 0.125f);
+        y[i] = __expf(y[i]);
     return y;
 }
 

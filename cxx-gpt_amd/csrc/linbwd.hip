@@ -424,8 +424,8 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     auto flush = [&]() __attribute__((always_inline)) {
         const f4 hq = *reinterpret_cast<const f4*>(&sH[lrow * CLD + lcol]);
         const f4 hk = *reinterpret_cast<const f4*>(&sH[CHUNK + lrow * CLD + lcol]);
-        const f4 tq = fwht64_f4(hq, lane) * 0.125f;
-        const f4 tk = fwht64_f4(hk, lane) * 0.125f;
+        const f4 tq = fwht64_f4(hq, lane, 0.125f);
+        const f4 tk = fwht64_f4(hk, lane, 0.125f);
         const unsigned off = (ht0 >= 0 && ht0 + lrow < tend)
                                  ? (unsigned)((ht0 + lrow) * 64 + lcol) * 4u
                                  : kDropOffset;
