@@ -62,6 +62,7 @@ __device__ __forceinline__ float xrow_max(float v)
     v = fmaxf(v, __shfl_xor(v, 32, 64));
     return v;
 }
+
 // Lane exchange within a 16-lane row through DPP (no LDS round trip).  The
 // patterns used here (quad_perm, row_ror, row_mirror, row_half_mirror) have a
 // source lane for every lane, so bound_ctrl is set: no old value to keep,
@@ -71,6 +72,26 @@ __device__ __forceinline__ float dpp_f(float v)
 {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// The value of lane l ^ M (M = 1, 2, 4, 8: within the lane's 16-lane row)
+// through DPP lane moves, which stay in the VALU (a shuffle through
+// ds_bpermute takes a round trip through the LDS unit).  Lane l ^ 4 is two
+// moves: row_half_mirror (lane i of each 8 reads lane 7 - i, i.e. i ^ 7),
+// then quad_perm [3,2,1,0] (i ^ 3): i ^ 7 ^ 3 = i ^ 4.
+template <int M>
+__device__ __forceinline__ float lane_xor16(float v)
+{
+    if constexpr (M == 1)
+        return dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    else if constexpr (M == 2)
+        return dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    else if constexpr (M == 8)
+        return dpp_f<0x128>(v);   // row_ror:8
+    else {
+        static_assert(M == 4, "lane_xor16: M in {1, 2, 4, 8}");
+        return dpp_f<0x1B>(dpp_f<0x141>(v));   // row_half_mirror, quad_perm [3,2,1,0]
+    }
 }
 
 // Sum over the 16 lanes of one row (lanes sharing l / 16): rotations by 8

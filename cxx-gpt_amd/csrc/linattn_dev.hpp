@@ -55,26 +55,6 @@ struct Phi<PHI_NONE> {
 // every layout gives the same roundings.
 // ---------------------------------------------------------------------------
 
-// The value of lane l ^ M (M = 1, 2, 4, 8: within the lane's 16-lane row)
-// through DPP lane moves, which stay in the VALU (a shuffle through
-// ds_bpermute takes a round trip through the LDS unit).  Lane l ^ 4 is two
-// moves: row_half_mirror (lane i of each 8 reads lane 7 - i, i.e. i ^ 7),
-// then quad_perm [3,2,1,0] (i ^ 3): i ^ 7 ^ 3 = i ^ 4.
-template <int M>
-__device__ __forceinline__ float lane_xor16(float v)
-{
-    if constexpr (M == 1)
-        return dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-    else if constexpr (M == 2)
-        return dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-    else if constexpr (M == 8)
-        return dpp_f<0x128>(v);   // row_ror:8
-    else {
-        static_assert(M == 4, "lane_xor16: M in {1, 2, 4, 8}");
-        return dpp_f<0x1B>(dpp_f<0x141>(v));   // row_half_mirror, quad_perm [3,2,1,0]
-    }
-}
-
 // One butterfly stage over lane bit M: lower lane a + b, upper lane a - b
 // (a the lower lane's value, b the upper's).
 template <int M>

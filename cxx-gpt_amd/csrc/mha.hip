@@ -639,9 +639,9 @@ __global__ __launch_bounds__(256 * NSPLIT, DHP <= 64 ? 4 : 1) void mha_fwd_kerne
         }
         if constexpr (PREP) {
             float dsum = pdot;
-            dsum += __shfl_xor(dsum, 1, 64);
-            dsum += __shfl_xor(dsum, 2, 64);
-            dsum += __shfl_xor(dsum, 4, 64);
+            dsum += lane_xor16<1>(dsum);
+            dsum += lane_xor16<2>(dsum);
+            dsum += lane_xor16<4>(dsum);
             const int prow = qb * MHA_BM + (tid >> 3);
             if (prow < S) {
                 if ((tid & 7) == 0)
@@ -1005,7 +1005,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     const int q = min(q0 + 16 * qt + 4 * g + r, S - 1);
                     float sn, cs;
                     sincos_rev(-(float)q * wv, &sn, &cs);
-                    const float other = __shfl_xor(acc[r], 1, 64);
+                    const float other = lane_xor16<1>(acc[r]);
                     acc[r] = odd ? other * sn + acc[r] * cs : acc[r] * cs - other * sn;
                 }
             }
@@ -1415,7 +1415,8 @@ hipError_t mha_stats_prep_launch(const float* Q, const float* K, const float* V,
 // t taking units t + j*T (T threads in the grid, j < PREP_UNITS) with every
 // load issued before any arithmetic (C2, 19.6 MB: 5.2 us at one or four units
 // per thread, 4.7 us at two, 6.4 us at eight).  A segment's U units sit in U
-// consecutive lanes; their partial dot products are summed by lane exchange.
+// consecutive lanes of one 16-lane row; their partial dot products are summed
+// by an xor butterfly of DPP lane moves.
 constexpr int PREP_UNITS = 2;
 
 template <int U, bool ZERO>
@@ -1437,9 +1438,14 @@ __global__ __launch_bounds__(256) void mha_bwd_prep_vec_kernel(
     for (int j = 0; j < PREP_UNITS; j++) {
         const long u = t0 + j * T;
         float acc = o[j][0] * d[j][0] + o[j][1] * d[j][1] + o[j][2] * d[j][2] + o[j][3] * d[j][3];
-#pragma unroll
-        for (int m = 1; m < U; m <<= 1)
-            acc += __shfl_xor(acc, m, 64);
+        if constexpr (U > 1)
+            acc += lane_xor16<1>(acc);
+        if constexpr (U > 2)
+            acc += lane_xor16<2>(acc);
+        if constexpr (U > 4)
+            acc += lane_xor16<4>(acc);
+        if constexpr (U > 8)
+            acc += lane_xor16<8>(acc);
         if (u < nunits) {
             if (ZERO)
                 *reinterpret_cast<f4*>(dQ + 4 * u) = f4zero();
