@@ -394,11 +394,13 @@ int cxg_mha_bwd_noalloc(const float* Q, const float* K, const float* V, const fl
     int st = mha_check(B, S, H, Dh, &empty);
     if (st != CXG_OK || empty)
         return st;
-    if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
-        return CXG_ERR_NULL;
+    // the capacity check comes first: a problem beyond the array is refused
+    // whatever else is wrong with the call
     const size_t rows = B * H * S;
     if (rows > (size_t)CXG_MHA_BWD_NOALLOC_MAX_ROWS)
         return CXG_ERR_WORKSPACE;
+    if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
     hipError_t e = hipSuccess;
     float* sp = scratch_ptr(&e);
     if (sp == nullptr)
@@ -572,24 +574,40 @@ static int lin_check(size_t B, size_t S, size_t D, size_t E, bool* empty)
     return CXG_OK;
 }
 
-// Contexts the forwards have written: device, shape and feature map per
-// context pointer, so that the fused backward refuses a context written for
-// another problem (whose records it would read at the wrong offsets) or by
-// another API's forward (whose sums use another feature map).
+// Contexts the forwards have written: device, shape, feature map and byte
+// span per context pointer, so that the fused backward refuses a context
+// written for another problem (whose records it would read at the wrong
+// offsets) or by another API's forward (whose sums use another feature map).
+// The check is on shape and feature map only: it cannot tell that a context's
+// memory was freed and reused for another context of the same shape.  A
+// forward that writes a context drops every tag on the same device whose span
+// overlaps it (that memory now holds the new context), and the table keeps at
+// most kCtxTagsMax tags, so it stays bounded by the contexts that are live.
 namespace {
 struct CtxTag {
     int dev, phi;
-    size_t B, S, D, E;
+    size_t B, S, D, E, bytes;
 };
+constexpr size_t kCtxTagsMax = 4096;
 std::mutex g_ctx_mu;
 std::unordered_map<const void*, CtxTag> g_ctx_tags;
 
-void ctx_record(const void* ctx, int phi, size_t B, size_t S, size_t D, size_t E)
+void ctx_record(const void* ctx, size_t bytes, int phi, size_t B, size_t S, size_t D, size_t E)
 {
     int dev = -1;
     (void)hipGetDevice(&dev);
+    const uintptr_t lo = (uintptr_t)ctx, hi = lo + bytes;
     std::lock_guard<std::mutex> lk(g_ctx_mu);
-    g_ctx_tags[ctx] = CtxTag{dev, phi, B, S, D, E};
+    for (auto it = g_ctx_tags.begin(); it != g_ctx_tags.end();) {
+        const uintptr_t a = (uintptr_t)it->first, b = a + it->second.bytes;
+        if (it->second.dev == dev && a < hi && lo < b)
+            it = g_ctx_tags.erase(it);
+        else
+            ++it;
+    }
+    if (g_ctx_tags.size() >= kCtxTagsMax)
+        g_ctx_tags.erase(g_ctx_tags.begin());
+    g_ctx_tags[ctx] = CtxTag{dev, phi, B, S, D, E, bytes};
 }
 
 bool ctx_matches(const void* ctx, int phi, size_t B, size_t S, size_t D, size_t E)
@@ -627,7 +645,7 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
             return CXG_ERR_NULL;
         if (ctx_bytes < need)
             return CXG_ERR_WORKSPACE;
-        ctx_record(ctx, phi, B, S, D, E);
+        ctx_record(ctx, need, phi, B, S, D, E);
         const LinCtx c = lin_ctx_split(ctx, (int)B, (int)S, (int)D, (int)E);
         return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de,
                                          den_eps, (int)B, (int)S, (int)D, (int)E, c.rec, s, c.tot,

@@ -182,7 +182,11 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
  * dimensions and feature map of the forward that last wrote it: a context
  * with no such record, or written for other dimensions, another device or
  * another API's forward (cxg_lin_fwd_ctx, cxg_lin_elu_fwd), is refused with
- * CXG_ERR_WORKSPACE before any launch.  D <= 64 and E <= 64 take the fused
+ * CXG_ERR_WORKSPACE before any launch.  The check compares dimensions, device
+ * and feature map only: it cannot see that a context's memory was freed and
+ * reused for another context of the same shape.  A forward that writes a
+ * context forgets every earlier record whose bytes it overlaps, and at most
+ * 4096 records are kept.  D <= 64 and E <= 64 take the fused
  * kernels (sequences of up to 128 rows the quadratic form); widths up to 512
  * run step 1 and one quadratic-form backward launch (dnum, dden in the
  * library's scratch); wider ones the split kernels; ctx is not read on these

@@ -7,7 +7,9 @@
 // fromTensor()/toTensor(), and host Tensor<float>(shape, vector) with a
 // shared data vector and operator[] (uses at two_stage_cuda_kernels.cu:853,
 // :1751, two_stage_gpt.hpp:105, :577, kernel_test.cpp:198, :225, :231).
-// Include this header only where the real TensorN is absent.
+// Include this header only where the real TensorN is absent.  It also
+// provides the two macros of TensorN's that those call sites rely on,
+// TENSORN_CUDA_AVAILABLE and CHECK_CUDA_ERROR.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -28,6 +30,22 @@
             throw std::runtime_error(std::string("HIP error: ") + hipGetErrorString(cxg_e_) + \
                                      " at " + __FILE__ + ":" + std::to_string(__LINE__));    \
     } while (0)
+
+// TensorN defines TENSORN_CUDA_AVAILABLE when it is built with its GPU
+// backend; the reference's GPU call sites compile only under it
+// (two_stage_gpt.hpp:7, linear_gpt.hpp:6, gpt_gpt.hpp:21).  This stand-in is
+// the GPU backend, so it defines it.
+#ifndef TENSORN_CUDA_AVAILABLE
+#define TENSORN_CUDA_AVAILABLE 1
+#endif
+
+// TensorN's status check, used after launches as CHECK_CUDA_ERROR(<status>)
+// (linear_cuda_kernels.cu:98, gpt_cuda_kernels.cu:30): here it takes a
+// hipError_t (e.g. hipGetLastError()) and throws std::runtime_error naming the
+// error and the call site when it is not hipSuccess.
+#ifndef CHECK_CUDA_ERROR
+#define CHECK_CUDA_ERROR(expr) CXG_HIP_CHECK(expr)
+#endif
 
 namespace TensorN {
 

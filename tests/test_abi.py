@@ -72,6 +72,44 @@ def test_status_strings_and_version():
     ("cxg_lin_bwd_dKdV", (None,) * 7 + (1, 4, 4, 4, None), cx.CXG_ERR_NULL),
     ("cxg_phi_hexp_fwd", (None, None, 2, 64, 32, None), cx.CXG_ERR_DIMS),
     ("cxg_phi_elu_fwd", (None, None, 2, 4, 8, None), cx.CXG_ERR_DIMS),
+    # the allocation-free backward's capacity check precedes its pointer checks
+    ("cxg_mha_bwd_noalloc", (None,) * 9 + (1, cx.MHA_BWD_NOALLOC_MAX_ROWS + 1, 1, 64, None),
+     cx.CXG_ERR_WORKSPACE),
+    ("cxg_mha_bwd_noalloc", (None,) * 9 + (1, cx.MHA_BWD_NOALLOC_MAX_ROWS, 1, 64, None),
+     cx.CXG_ERR_NULL),
 ])
 def test_argument_checks_without_gpu(call, args, want):
     assert cx.call_status(call, *args) == want
+
+
+ERR_BIN = os.path.join(ROOT, "tests", "cpp", "dropin_errors")
+
+
+@pytest.fixture(scope="module")
+def dropin_errors():
+    """tests/cpp/dropin_errors, built by build() (made here if missing)."""
+    if not os.path.exists(ERR_BIN):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp"), ERR_BIN], check=True,
+                       capture_output=True)
+    return ERR_BIN
+
+
+@pytest.mark.parametrize("mode,fn,dh", [("abort_fwd", "fused_mha_fwd", 300),
+                                        ("abort_bwd", "fused_mha_bwd", 257)])
+def test_dropin_aborts_above_256(dropin_errors, mode, fn, dh):
+    """The C++ wrappers keep the reference's fprintf + std::abort() for head_dim
+    > 256 (two_stage_cuda_kernels.cu:316-321, :867-872); the check happens
+    before any HIP call, so this runs without a GPU."""
+    r = subprocess.run([dropin_errors, mode], capture_output=True, text=True, timeout=60)
+    assert r.returncode == -6, (r.returncode, r.stdout, r.stderr)   # SIGABRT
+    assert f"two_stage_cuda::{fn}: head_dim {dh} > 256" in r.stderr
+    assert "returned without aborting" not in r.stdout
+
+
+@pytest.mark.parametrize("mode", ["throw_null", "macros"])
+def test_dropin_throws_and_shim_macros(dropin_errors, mode):
+    """Other failures throw std::runtime_error (the reference's CHECK_CUDA_ERROR);
+    the stand-in defines TENSORN_CUDA_AVAILABLE and CHECK_CUDA_ERROR."""
+    r = subprocess.run([dropin_errors, mode], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, (r.returncode, r.stdout, r.stderr)
+    assert r.stdout.startswith("caught: ")

@@ -50,7 +50,12 @@ def test_noalloc_rejects_oversize(dev):
     st = cx.call_status("cxg_mha_bwd_noalloc", *[P(t)] * 9, 1, rows + 1, 1, 64,
                         cx._stream(None))
     assert st == cx.CXG_ERR_WORKSPACE
-    # at the limit the size check passes (argument checks only: NULL outputs)
+    # the capacity check precedes the pointer checks: NULL outputs give
+    # CXG_ERR_WORKSPACE one row past the limit and CXG_ERR_NULL at it, so the
+    # limit itself is accepted by the size check (no launch either way)
+    st = cx.call_status("cxg_mha_bwd_noalloc", *[P(t)] * 6, None, None, None, 1, rows + 1, 1,
+                        64, cx._stream(None))
+    assert st == cx.CXG_ERR_WORKSPACE
     st = cx.call_status("cxg_mha_bwd_noalloc", *[P(t)] * 6, None, None, None, 1, rows, 1, 64,
                         cx._stream(None))
     assert st == cx.CXG_ERR_NULL
