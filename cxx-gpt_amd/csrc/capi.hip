@@ -221,6 +221,31 @@ int cxg_last_hip_error(void) { return t_last_hip; }
 
 const char* cxg_version(void) { return "cxxgpt-attn-gfx950 0.1"; }
 
+int cxg_release_scratch(cxg_stream_t stream)
+{
+    const hipStream_t s = (hipStream_t)stream;
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return hip_status(e);
+    std::unique_ptr<StreamScratch> victim;
+    {
+        std::lock_guard<std::mutex> lk(g_scratch_map_mu);
+        auto it = g_scratch_map.find(std::make_pair(dev, s));
+        if (it == g_scratch_map.end())
+            return CXG_OK;
+        victim = std::move(it->second);
+        g_scratch_map.erase(it);
+    }
+    std::lock_guard<std::mutex> held(victim->mu);   // a call holding it finishes first
+    e = hipStreamSynchronize(s);
+    if (e == hipSuccess && victim->p != nullptr)
+        e = hipFree(victim->p);
+    victim->p = nullptr;
+    victim->n = 0;
+    return hip_status(e);
+}
+
 // ---------------------------------------------------------------------------
 // softmax MHA
 // ---------------------------------------------------------------------------
@@ -451,7 +476,7 @@ static int gpt_check(size_t B, size_t S, size_t E, bool* empty)
         return CXG_OK;
     if (E > (size_t)MHA_WIDE_MAX_DH) {
         // scores in memory: S x S floats per sequence (S <= 16384: 1 GiB), GEMM
-        // shapes in int
+        // shapes in int; any S, E a multiple of 4
         if (!fits_int(B) || !fits_int(E) || S > 16384 || B * S * E > ((size_t)1 << 40))
             return CXG_ERR_DIMS;
         return gpt_mat_ok((int)S, (int)E) ? CXG_OK : CXG_ERR_ALIGN;
@@ -480,7 +505,8 @@ int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, f
         if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(O))
             return CXG_ERR_ALIGN;
         Scratch ws;
-        st = ws.acquire(nullptr, 0, gpt_mat_ws_floats((int)B, (int)S, (int)E) * sizeof(float), s);
+        st = ws.acquire(nullptr, 0, gpt_mat_fwd_ws_floats((int)B, (int)S, (int)E) * sizeof(float),
+                        s);
         if (st != CXG_OK)
             return st;
         return hip_status(gpt_mat_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)E,

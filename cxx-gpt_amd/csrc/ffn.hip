@@ -37,7 +37,9 @@
 // products like any other tiles.
 //
 // Requires E, F multiples of 4 and 16-byte aligned tensors (checked at the C
-// ABI); any M.
+// ABI); any M.  Callers with other shapes (GPT's score matrices, whose
+// sequence length S need not be a multiple of 4) store into padded rows and
+// bound the operand reads separately (FfnGemm::Mc, Nc, Kc).
 #include "common.hpp"
 #include "gelu_dev.hpp"
 #include "launch.hpp"
@@ -61,6 +63,7 @@ struct GemmArgs {
     float* part;       // 2 * P partial tiles of GT * GT floats (slot 0, 1 per workgroup)
     long lda, ldb, ldc;
     int M, N, K;
+    int Mc, Nc, Kc;    // read extents (FfnGemm)
     int tn;            // tiles along N
     int Tb;            // tiles per product of the batch
     long sA, sB, sC;   // batch strides (elements)
@@ -111,11 +114,13 @@ __device__ __forceinline__ void epi_apply(f4 v, long off, float* C, const float*
 }
 
 // One operand's 128 x 32 k-tile, 4 float4 per thread.  KC: element (row, k)
-// at P[row*ld + k].  Rows past the end are clamped onto the last row (their
-// products land in C rows/columns that are never stored); k past K reads 0.
+// at P[row*ld + k].  Rows past `rows` are clamped onto the last row (KC) or
+// the last 4-row group (their products land in C rows/columns that are never
+// stored, or are multiplied by zeros of the other operand); k past K reads 0,
+// and a row-contiguous operand's k-rows are clamped below Kc.
 template <bool KC>
 __device__ __forceinline__ void tile_fetch(const float* __restrict__ P, long ld, int r0, int rows,
-                                           int k0, int K, f4 (&v)[4])
+                                           int k0, int K, int Kc, f4 (&v)[4])
 {
     const int t = threadIdx.x;
 #pragma unroll
@@ -129,7 +134,7 @@ __device__ __forceinline__ void tile_fetch(const float* __restrict__ P, long ld,
         } else {
             const int k = k0 + (idx >> 5);
             const int r = min(r0 + (idx & 31) * 4, rows - 4);
-            const f4 x = *reinterpret_cast<const f4*>(P + (long)min(k, K - 1) * ld + r);
+            const f4 x = *reinterpret_cast<const f4*>(P + (long)min(k, Kc - 1) * ld + r);
             v[q] = k < K ? x : f4zero();
         }
     }
@@ -197,8 +202,8 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
         // (LDS is free here: the previous segment's last reads precede its
         // final barrier.)
         f4 ra[4], rb[4];
-        tile_fetch<AK>(Ab, a.lda, m0, a.M, ka * GKT, a.K, ra);
-        tile_fetch<BK>(Bb, a.ldb, n0, a.N, ka * GKT, a.K, rb);
+        tile_fetch<AK>(Ab, a.lda, m0, a.Mc, ka * GKT, a.K, a.Kc, ra);
+        tile_fetch<BK>(Bb, a.ldb, n0, a.Nc, ka * GKT, a.K, a.Kc, rb);
         tile_put<AK>(lds[0][0], ra);
         tile_put<BK>(lds[0][1], rb);
         __syncthreads();
@@ -207,8 +212,8 @@ __global__ __launch_bounds__(256, 2) void ffn_gemm_kernel(GemmArgs a)
             const int st = kt & 1;
             // Next k-tile in flight during this one's MFMAs (past the
             // segment's end it reads valid memory that is never used).
-            tile_fetch<AK>(Ab, a.lda, m0, a.M, (ka + kt + 1) * GKT, a.K, ra);
-            tile_fetch<BK>(Bb, a.ldb, n0, a.N, (ka + kt + 1) * GKT, a.K, rb);
+            tile_fetch<AK>(Ab, a.lda, m0, a.Mc, (ka + kt + 1) * GKT, a.K, a.Kc, ra);
+            tile_fetch<BK>(Bb, a.ldb, n0, a.Nc, (ka + kt + 1) * GKT, a.K, a.Kc, rb);
             const float* LA = lds[st][0];
             const float* LB = lds[st][1];
 #pragma unroll
@@ -371,6 +376,9 @@ hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st)
     a.M = op.M;
     a.N = op.N;
     a.K = op.K;
+    a.Mc = op.Mc > 0 ? op.Mc : op.M;
+    a.Nc = op.Nc > 0 ? op.Nc : op.N;
+    a.Kc = op.Kc > 0 ? op.Kc : op.K;
     a.tn = (op.N + GT - 1) / GT;
     a.Tb = ((op.M + GT - 1) / GT) * a.tn;
     a.sA = op.sA;

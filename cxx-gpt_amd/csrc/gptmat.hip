@@ -14,32 +14,36 @@
 //             dS = P (dP - rowsum(P dP)) / sqrt(E);
 //             dV = P^T dO;  dQ = dS K;  dK = dS^T Q
 // The masked entries' probabilities are exactly 0, as exp(-1e10 - max) is in
-// the reference, so the full-width products give the causal result.  The
-// GEMM needs S and E multiples of 4 and 16-byte aligned rows.
+// the reference, so the full-width products give the causal result.  A
+// sequence's score matrix has S rows of Sp = S rounded up to 4 floats; the
+// padding columns hold probability 0, so every product can run its
+// contraction over Sp (or S) with 16-byte aligned rows whatever S is.  The
+// GEMM needs E a multiple of 4 and 16-byte aligned Q, K, V, O rows.
 #include "common.hpp"
 #include "launch.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace cxg {
 
 // Row softmax of a group's scores in place (one wave per row of a sequence's
-// S x S matrix, row stride S, sequence blockIdx.y of the group): P[i][j] =
-// 2^(Sc[i][j] c - L_i) for j <= i, else 0, with L_i the base-2 log-sum-exp of
-// the row's unmasked scaled scores (c = log2(e) / sqrt(E)).  lse_in (natural
-// log, nullable): use it instead of forming L_i; lse_out (nullable): store
-// L_i ln 2.
+// S x Sp matrix, row stride Sp, sequence blockIdx.y of the group): P[i][j] =
+// 2^(Sc[i][j] c - L_i) for j <= i, else 0 (the padding columns j >= S
+// included), with L_i the base-2 log-sum-exp of the row's unmasked scaled
+// scores (c = log2(e) / sqrt(E)).  lse_in (natural log, nullable): use it
+// instead of forming L_i; lse_out (nullable): store L_i ln 2.
 __global__ __launch_bounds__(256) void gpt_softmax_kernel(float* __restrict__ P,
                                                          const float* __restrict__ lse_in,
                                                          float* __restrict__ lse_out, int S,
-                                                         float c)
+                                                         int Sp, float c)
 {
     const int lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= S)
         return;
     const long sq = blockIdx.y;
-    float* r = P + (sq * S + i) * S;
+    float* r = P + (sq * S + i) * Sp;
     float L;
     if (lse_in != nullptr) {
         L = lse_in[sq * S + i] * kLog2e;
@@ -60,57 +64,84 @@ __global__ __launch_bounds__(256) void gpt_softmax_kernel(float* __restrict__ P,
         if (lse_out != nullptr && lane == 0)
             lse_out[sq * S + i] = L * kLn2;
     }
-    for (int j = lane; j < S; j += 64)
+    for (int j = lane; j < Sp; j += 64)
         r[j] = j <= i ? fast_exp2(r[j] * c - L) : 0.0f;
 }
 
 // dS[i][j] = P[i][j] (dP[i][j] - sum_j P[i][j] dP[i][j]) * scale, in place
-// over dP (one wave per row; sequence blockIdx.y of the group).
+// over dP (one wave per row, row stride Sp, padding columns included;
+// sequence blockIdx.y of the group).
 __global__ __launch_bounds__(256) void gpt_softmax_bwd_kernel(const float* __restrict__ P,
                                                              float* __restrict__ dP, int S,
-                                                             float scale)
+                                                             int Sp, float scale)
 {
     const int lane = threadIdx.x & 63;
     const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= S)
         return;
     const long row = (long)blockIdx.y * S + i;
-    const float* p = P + row * S;
-    float* d = dP + row * S;
+    const float* p = P + row * Sp;
+    float* d = dP + row * Sp;
     float di = 0.0f;
     for (int j = lane; j <= i; j += 64)
         di += p[j] * d[j];
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1)
         di += __shfl_xor(di, o, 64);
-    for (int j = lane; j < S; j += 64)
+    for (int j = lane; j < Sp; j += 64)
         d[j] = p[j] * (d[j] - di) * scale;
 }
 
-bool gpt_mat_ok(int S, int E) { return S % 4 == 0 && E % 4 == 0; }
-
-// Sequences per group: as many as keep the group's two score matrices within
-// 2^25 floats (128 MiB), at least one.
-static int gpt_group(int B, int S)
+bool gpt_mat_ok(int S, int E)
 {
-    const long per = 2L * S * S;
-    return (int)std::max<long>(1, std::min<long>(B, (1L << 25) / per));
+    (void)S;
+    return E % 4 == 0;
 }
 
-// Scratch: the group's two score matrices and the GEMM's partial tiles (the
+static int pad4(int S) { return (S + 3) & ~3; }
+
+// Score-matrix floats a group may hold: 2^25 (128 MiB), or the value of the
+// environment variable CXXGPT_GPT_SCORE_FLOATS when it is set to a positive
+// number (read at each call; callers short of memory lower it, and tests use
+// it to force several groups on small problems).
+static long score_budget()
+{
+    const char* v = std::getenv("CXXGPT_GPT_SCORE_FLOATS");
+    if (v != nullptr) {
+        const long n = std::atol(v);
+        if (n > 0)
+            return n;
+    }
+    return 1L << 25;
+}
+
+// Sequences per group: as many as keep the group's score matrices (`mats` of
+// S x Sp floats per sequence: one forward, two backward) within the budget,
+// at least one.
+static int gpt_group(int B, int S, int mats)
+{
+    const long per = (long)mats * S * pad4(S);
+    return (int)std::max<long>(1, std::min<long>(B, score_budget() / per));
+}
+
+// Scratch: the group's score matrices and the GEMM's partial tiles (the
 // largest of the products' needs).
-size_t gpt_mat_ws_floats(int B, int S, int E)
+static size_t ws_floats(int B, int S, int E, int mats)
 {
-    const int nb = gpt_group(B, S);
-    const size_t g = std::max({ffn_gemm_ws_floats(S, S, E, nb), ffn_gemm_ws_floats(S, E, S, nb)});
-    return 2 * (size_t)nb * S * S + g;
+    const int nb = gpt_group(B, S, mats), Sp = pad4(S);
+    const size_t g = std::max({ffn_gemm_ws_floats(S, Sp, E, nb), ffn_gemm_ws_floats(S, E, Sp, nb),
+                               ffn_gemm_ws_floats(S, E, S, nb)});
+    return (size_t)mats * nb * S * Sp + g;
 }
+
+size_t gpt_mat_fwd_ws_floats(int B, int S, int E) { return ws_floats(B, S, E, 1); }
+size_t gpt_mat_ws_floats(int B, int S, int E) { return ws_floats(B, S, E, 2); }
 
 // C_b = A_b B_b for the nb sequences of a group (A, B, C at sequence strides
-// sA, sB, sC).
+// sA, sB, sC), C stored over M x N; operand reads bounded by Mc, Nc, Kc.
 static hipError_t gemm(const float* A, long lda, bool ak, long sA, const float* B, long ldb,
-                       bool bk, long sB, float* C, long ldc, long sC, int M, int N, int K, int nb,
-                       float* ws, hipStream_t st)
+                       bool bk, long sB, float* C, long ldc, long sC, int M, int N, int K,
+                       int Mc, int Nc, int Kc, int nb, float* ws, hipStream_t st)
 {
     FfnGemm op{};
     op.A = A;
@@ -122,6 +153,9 @@ static hipError_t gemm(const float* A, long lda, bool ak, long sA, const float* 
     op.M = M;
     op.N = N;
     op.K = K;
+    op.Mc = Mc;
+    op.Nc = Nc;
+    op.Kc = Kc;
     op.epi = FFN_EPI_STORE;
     op.C = C;
     op.ldc = ldc;
@@ -138,26 +172,33 @@ static hipError_t softmax(float* P, const float* lse_in, float* lse_out, int S, 
     ProfScope ps(st, "gpt_softmax");
     const float c = kLog2e / sqrtf((float)E);
     CXG_LAUNCH(gpt_softmax_kernel, dim3((unsigned)((S + 3) / 4), (unsigned)nb), dim3(256), 0, st,
-               P, lse_in, lse_out, S, c);
+               P, lse_in, lse_out, S, pad4(S), c);
     return hipGetLastError();
 }
 
+// The products, per group, with Sp = S rounded up to 4 (score rows padded):
+//   scores  Q K^T    stored S x Sp; K's rows read below S
+//   O       P V      summed over Sp (P's padding is 0); V's rows read below S
+//   dV      P^T dO   summed over the S query rows; P's columns read below Sp
+//   dQ      dS K     as O
+//   dK      dS^T Q   as dV
 hipError_t gpt_mat_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                               float* lse, int B, int S, int E, float* ws, hipStream_t st)
 {
-    const int G = gpt_group(B, S);
-    const long SE = (long)S * E, SS = (long)S * S;
+    const int G = gpt_group(B, S, 1), Sp = pad4(S);
+    const long SE = (long)S * E, SS = (long)S * Sp;
     float* Sc = ws;
-    float* gws = ws + 2 * (size_t)G * SS;
+    float* gws = ws + (size_t)G * SS;
     for (int b0 = 0; b0 < B; b0 += G) {
         const int nb = std::min(G, B - b0);
         const long r0 = (long)b0 * SE;
-        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, Sc, S, SS, S, S, E, nb,
-                            gws, st);
+        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, Sc, Sp, SS, S, Sp, E, S, S,
+                            E, nb, gws, st);
         if (e == hipSuccess)
             e = softmax(Sc, nullptr, lse != nullptr ? lse + (long)b0 * S : nullptr, S, E, nb, st);
         if (e == hipSuccess && O != nullptr)
-            e = gemm(Sc, S, true, SS, V + r0, E, false, SE, O + r0, E, SE, S, E, S, nb, gws, st);
+            e = gemm(Sc, Sp, true, SS, V + r0, E, false, SE, O + r0, E, SE, S, E, Sp, S, E, S, nb,
+                     gws, st);
         if (e != hipSuccess)
             return e;
     }
@@ -168,8 +209,8 @@ hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, co
                               const float* lse, float* dQ, float* dK, float* dV, int B, int S,
                               int E, float* ws, hipStream_t st)
 {
-    const int G = gpt_group(B, S);
-    const long SE = (long)S * E, SS = (long)S * S;
+    const int G = gpt_group(B, S, 2), Sp = pad4(S);
+    const long SE = (long)S * E, SS = (long)S * Sp;
     float* P = ws;
     float* dS = ws + (size_t)G * SS;
     float* gws = ws + 2 * (size_t)G * SS;
@@ -177,26 +218,28 @@ hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, co
     for (int b0 = 0; b0 < B; b0 += G) {
         const int nb = std::min(G, B - b0);
         const long r0 = (long)b0 * SE;
-        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, P, S, SS, S, S, E, nb, gws,
-                            st);
+        hipError_t e = gemm(Q + r0, E, true, SE, K + r0, E, true, SE, P, Sp, SS, S, Sp, E, S, S,
+                            E, nb, gws, st);
         if (e == hipSuccess)
             e = softmax(P, lse != nullptr ? lse + (long)b0 * S : nullptr, nullptr, S, E, nb, st);
         if (e == hipSuccess)   // dP = dO V^T
-            e = gemm(dO + r0, E, true, SE, V + r0, E, true, SE, dS, S, SS, S, S, E, nb, gws, st);
+            e = gemm(dO + r0, E, true, SE, V + r0, E, true, SE, dS, Sp, SS, S, Sp, E, S, S, E, nb,
+                     gws, st);
         if (e == hipSuccess) {
             ProfScope ps(st, "gpt_softmax_bwd");
             CXG_LAUNCH(gpt_softmax_bwd_kernel, dim3((unsigned)((S + 3) / 4), (unsigned)nb),
-                       dim3(256), 0, st, P, dS, S, scale);
+                       dim3(256), 0, st, P, dS, S, Sp, scale);
             e = hipGetLastError();
         }
         if (e == hipSuccess)   // dV = P^T dO
-            e = gemm(P, S, false, SS, dO + r0, E, false, SE, dV + r0, E, SE, S, E, S, nb, gws,
-                     st);
+            e = gemm(P, Sp, false, SS, dO + r0, E, false, SE, dV + r0, E, SE, S, E, S, Sp, E, S,
+                     nb, gws, st);
         if (e == hipSuccess)   // dQ = dS K
-            e = gemm(dS, S, true, SS, K + r0, E, false, SE, dQ + r0, E, SE, S, E, S, nb, gws, st);
+            e = gemm(dS, Sp, true, SS, K + r0, E, false, SE, dQ + r0, E, SE, S, E, Sp, S, E, S,
+                     nb, gws, st);
         if (e == hipSuccess)   // dK = dS^T Q
-            e = gemm(dS, S, false, SS, Q + r0, E, false, SE, dK + r0, E, SE, S, E, S, nb, gws,
-                     st);
+            e = gemm(dS, Sp, false, SS, Q + r0, E, false, SE, dK + r0, E, SE, S, E, S, Sp, E, S,
+                     nb, gws, st);
         if (e != hipSuccess)
             return e;
     }

@@ -97,11 +97,13 @@ hipError_t mha_wide_bwd_launch(const float* Q, const float* K, const float* V, c
                                hipStream_t st);
 
 // GPT's attention for E > 512 (gptmat.hip): a group of sequences' S x S
-// scores in memory, products on the FP32 GEMM below, batched over the group.
-// S and E multiples of 4 and 16-byte aligned rows; scratch
-// gpt_mat_ws_floats(B, S, E) floats.  O may be null (statistics only); lse
-// [B][S] natural log, nullable in both.
+// scores in memory (rows padded to a multiple of 4), products on the FP32
+// GEMM below, batched over the group.  Any S; E a multiple of 4 and 16-byte
+// aligned rows; scratch gpt_mat_fwd_ws_floats(B, S, E) floats for the
+// forward, gpt_mat_ws_floats(B, S, E) for the backward.  O may be null
+// (statistics only); lse [B][S] natural log, nullable in both.
 bool gpt_mat_ok(int S, int E);
+size_t gpt_mat_fwd_ws_floats(int B, int S, int E);
 size_t gpt_mat_ws_floats(int B, int S, int E);
 hipError_t gpt_mat_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                               float* lse, int B, int S, int E, float* ws, hipStream_t st);
@@ -138,6 +140,12 @@ struct FfnGemm {
     // C (G, pre) + b sC (element strides)
     int batch = 1;
     long sA = 0, sB = 0, sC = 0;
+    // extents that bound the operand reads, when they differ from the stored
+    // extents M, N and the summed K (0: the same).  Rows i >= Mc of A and
+    // j >= Nc of B read row Mc-1 / Nc-1 instead (k-contiguous operands) or the
+    // last aligned 4-row group below Mc / Nc (row-contiguous ones); a
+    // row-contiguous operand's k >= Kc reads k-row Kc-1 (k >= K reads 0).
+    int Mc = 0, Nc = 0, Kc = 0;
 };
 size_t ffn_gemm_ws_floats(int M, int N, int K, int batch = 1);
 hipError_t ffn_gemm_launch(const FfnGemm& op, float* ws, hipStream_t st);

@@ -28,6 +28,7 @@ SIGNATURES = {
     "cxg_status_str": [ctypes.c_int],
     "cxg_last_hip_error": [],
     "cxg_version": [],
+    "cxg_release_scratch": [_vp],
     "cxg_mha_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_mha_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz,
                     _vp],
@@ -182,6 +183,11 @@ def mha_bwd_workspace_size(B, S, H, Dh):
 
 
 # ------------------------------------------------------------------ GPT's attention (H = 1)
+def release_scratch(stream=None):
+    """Free the library's cached scratch buffer of (current device, stream)."""
+    _call("cxg_release_scratch", _stream(stream))
+
+
 def gpt_attn_fwd(Q, K, V, O, B, S, E, lse=None, stream=None):
     _call("cxg_gpt_attn_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(lse), B, S, E,
           _stream(stream))

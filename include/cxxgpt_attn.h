@@ -55,6 +55,13 @@ const char *cxg_status_str(int status);
 int cxg_last_hip_error(void);
 /* Library version string. */
 const char *cxg_version(void);
+/* Frees the scratch buffer the library keeps for (current device, stream),
+ * e.g. after a one-off call with large sizes; the next call that needs
+ * scratch on that stream allocates it again.  Waits for the stream's work
+ * first.  Not for use while another thread calls into the library on the
+ * same stream, nor under stream capture.  No counterpart in the reference
+ * (it allocates its temporaries per call). */
+int cxg_release_scratch(cxg_stream_t stream);
 
 /* ===================== fused causal softmax MHA =====================
  * Q/K/V/O/dO/dQ/dK/dV: (B*S, H*Dh); head h of row r at [(r*H+h)*Dh, +Dh).
@@ -124,11 +131,15 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * cxg_gpt_attn_bwd_workspace_size counts them for the backward's statistics
  * pass (lse == NULL), as well as the partial sums of the backward's own
  * chunked jobs.  Above E = 512 (the reference has no limit) each sequence's
- * S x S scores are kept in scratch and the products run as FP32 MFMA GEMMs;
- * S and E must be multiples of 4 and the tensors 16-byte aligned
- * (CXG_ERR_ALIGN otherwise), S <= 16384 (CXG_ERR_DIMS); the forward takes the
- * library's scratch and the backward's workspace holds two S x S matrices
- * and the GEMMs' partial tiles. */
+ * S x S scores (rows padded to a multiple of 4 floats) are kept in scratch
+ * and the products run as FP32 MFMA GEMMs; any S up to 16384 (CXG_ERR_DIMS
+ * beyond), E a multiple of 4 and the tensors 16-byte aligned (CXG_ERR_ALIGN
+ * otherwise).  The forward takes the library's scratch for one score matrix
+ * per sequence of a group, the backward's workspace holds two per sequence of
+ * a group and the GEMMs' partial tiles; a group is as many sequences as keep
+ * its score matrices within 2^25 floats (128 MiB), or within the value of the
+ * environment variable CXXGPT_GPT_SCORE_FLOATS when it is set (read at each
+ * call, so workspace size and call must see the same value). */
 int cxg_gpt_attn_fwd(const float *Q, const float *K, const float *V, float *O, float *lse,
                      size_t B, size_t S, size_t E, cxg_stream_t stream);
 int cxg_gpt_attn_bwd(const float *Q, const float *K, const float *V, const float *O,

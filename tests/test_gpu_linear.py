@@ -95,7 +95,8 @@ def test_config3_elu(dev, S):
     (5, 333, 16, 8), (2, 40, 64, 1), (300, 16, 64, 64), (1, 50, 128, 64), (2, 20, 64, 96),
 ])
 def test_ragged_shapes(dev, B, S, D, E):
-    """Partial chunks, single and multi-segment plans, narrow and wide (generic) D/E."""
+    """Partial chunks, single and multi-segment plans, narrow D/E (the chunked scan) and
+    widths in (64, 512] (the quadratic form); widths above 512 are in test_gpu_lingeneric."""
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 13 * S + D + E)
     check_kattn(dev, Q, K, V, dO, B, S, D, E, literal=(S <= 40), tag=f"B{B}S{S}D{D}E{E}")
 

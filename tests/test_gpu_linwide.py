@@ -118,7 +118,8 @@ def test_state_outputs_wide(dev):
         assert_close(_np(zb2)[b], pK[sl].sum(0), f"two_stage z_buf seq{b}")
 
 
-@pytest.mark.parametrize("B,S,E", [(8, 256, 512), (2, 100, 300), (3, 31, 96)])
+@pytest.mark.parametrize("B,S,E", [(8, 256, 512), (2, 100, 300), (3, 31, 96),
+                                   (2, 60, 768)])   # above 512: the recurrence kernels
 def test_linear_gpt_wide(dev, B, S, E):
     """LinearGPT's attention at its width (D = next_pow2(E), zero-padded phi):
     the linear_cuda chain and the fused block (cxg_lin_elu_*) on raw inputs."""
