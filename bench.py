@@ -40,6 +40,10 @@ them can be made the reported workload with --workload NAME):
             (two_stage_train.cpp:168-170), two_stage API chain; c3widefused
             through the fused pair; lgptwide LinearGPT's shape (8 sequences,
             S256, D=E=512, linear_train.cpp:168-172) through cxg_lin_elu_*
+  c3widerope, c3wideropesep
+            c3wide's shape with stage 2's RoPE (two_stage_gpt.hpp:113, :160) fused
+            into the kernels (cxg_kattn_rope_fwd/bwd) / as separate passes around
+            the fused pair; c3rope, c3ropesep the same at C3's S4096 D=E=64 shape
   c5        long-sequence MHA, B2 H12 S4096 Dh64, fwd+bwd
   rope      RoPE fwd + bwd on the stage-1 q/k heads at the C2 shape (in place),
             GB/s of compulsory I/O (each tensor read and written once)
@@ -203,7 +207,7 @@ def attribute(cx, step, steps):
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state",
-              "phi_hexp_fwd", "phi_hexp_bwd",
+              "phi_hexp_fwd", "phi_hexp_bwd", "lin_rope_feat",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",
               "ffn_fixup"):
@@ -601,6 +605,65 @@ def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
                 frac=value / HBM_PEAK_GBS, cpu_inputs=(Q, K, V, dO, Bq, S, D, E))
 
 
+def _kattn_rope(c, name, Bq, S, D, seed, steps, warmup, fused):
+    """TwoStageGPT's stage 2 with its RoPE (two_stage_gpt.hpp:113-122, :149-160):
+    fused, cxg_kattn_rope_fwd -> cxg_kattn_rope_bwd (q, k rotated inside the
+    kernels); otherwise RoPE as separate in-place passes around the fused pair
+    (cxg_rope_fwd, cxg_kattn_fwd_ctx, cxg_kattn_bwd, cxg_rope_bwd).  GB/s of the
+    compulsory linear-attention I/O, as c3."""
+    g = c.gen(seed)
+    E, N = D, Bq * S
+    Q, K, V, dO = c.randn(g, N, D), c.randn(g, N, D), c.randn(g, N, E), c.randn(g, N, E)
+    O, den = c.empty(N, E), c.empty(N)
+    dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
+    nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+    ctx = c.empty(max(1, nctx // 4)) if nctx else None
+    P = _ptr
+    if fused:
+        calls = [("cxg_kattn_rope_fwd", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, D,
+                                         E, c.sp)),
+                 ("cxg_kattn_rope_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ),
+                                         P(dK), P(dV), Bq, S, D, E, c.sp))]
+        desc = "RoPE fused (cxg_kattn_rope_fwd -> cxg_kattn_rope_bwd)"
+    else:
+        calls = [("cxg_rope_fwd", (P(Q), P(K), Bq, S, D, D, c.sp)),
+                 ("cxg_kattn_fwd_ctx", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, D,
+                                        E, c.sp)),
+                 ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ), P(dK),
+                                    P(dV), Bq, S, D, E, c.sp)),
+                 ("cxg_rope_bwd", (P(dQ), P(dK), Bq, S, D, D, c.sp))]
+        desc = "RoPE as separate passes around the fused pair (cxg_rope_fwd, " \
+               "cxg_kattn_fwd_ctx, cxg_kattn_bwd, cxg_rope_bwd)"
+    step = Stepper(c.cx.lib(), calls)
+    ms = timed(step, steps, warmup, c.stream, c.windows, c.spread)
+    att = attribute(c.cx, step, ("seconds", ms))
+    total = lin_bytes(Bq, S, D)
+    value = total / (ms * 1e-3) / 1e9
+    kt = {k: round(v[0], 5) for k, v in att.items()}
+    if D > 64 or S <= 128:   # the quadratic form: MFMA-bound
+        kf = lin_wide_flops(Bq, S, D, E)
+        dom = max((k for k in att if k in kf), key=lambda k: att[k][0])
+        ach = kf[dom] / (att[dom][0] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+                "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+                "traffic": c.traffic.get(f"{name}/{dom}"), "flops_per_launch": kf[dom],
+                "kernel_ms": kt}
+    else:
+        kb = lin_kernel_bytes(Bq, S, D, True)
+        dom = max((k for k in att if k in kb), key=lambda k: att[k][0])
+        ach = kb[dom] / (att[dom][0] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                "traffic": c.traffic.get(f"{name}/{dom}"), "bytes_per_launch": kb[dom],
+                "kernel_ms": kt}
+    return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
+                config={"workload": f"{name}: stage-2 ELU+1 linear attention fwd+bwd with RoPE "
+                                    f"over the full width, {desc}",
+                        "B_seq": Bq, "S": S, "D": D, "E": E, "bytes_per_step": total},
+                frac=value / HBM_PEAK_GBS, cpu_inputs=None)
+
+
 def _hexp(c, name, Bq, S, seed, steps, warmup, fused=False, inside=False):
     """fused: the feature maps around the fused pair (cxg_lin_fwd_ctx ->
     cxg_lin_bwd with the context) instead of the four-call linear_cuda chain;
@@ -782,6 +845,16 @@ def run_workload(c, name, steps, warmup):
         return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "chain")
     if name == "c3widefused":
         return _linwide(c, name, 32, 256, 512, 83, steps, warmup, "fused")
+    if name == "c3widerope":   # stage 2 with its RoPE fused (two_stage_gpt.hpp:113, :160)
+        return _kattn_rope(c, name, 32, 256, 512, 85, steps, warmup, True)
+    if name == "c3wideropesep":
+        return _kattn_rope(c, name, 32, 256, 512, 85, steps, warmup, False)
+    if name == "c3rope":
+        return _kattn_rope(c, name, 96, 4096, 64, 86, max(20, steps // 4), max(5, warmup // 2),
+                           True)
+    if name == "c3ropesep":
+        return _kattn_rope(c, name, 96, 4096, 64, 86, max(20, steps // 4), max(5, warmup // 2),
+                           False)
     if name == "lgptwide":   # LinearGPT (linear_train.cpp:168-172, 191)
         return _linwide(c, name, 8, 256, 512, 84, steps, warmup, "lgpt")
     raise ValueError(f"unknown workload {name}")
@@ -847,7 +920,8 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 # of the printed line -- what a reader of only its tail sees -- carries it.
 SECONDARY = ("c2legacy", "c2dropin", "c5", "mhats", "gen1", "gen64", "gen256", "rope", "c2rope",
              "c2ropesep", "gpt", "gpt768", "gelu", "ffn", "c3s256", "c3fuseds256", "c3lgpt",
-             "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c4hexp", "c3fused", "c3")
+             "c3wide", "c3widefused", "c3widerope", "c3wideropesep", "c3rope", "c3ropesep",
+             "lgptwide", "c4", "c4fused", "c4hexp", "c3fused", "c3")
 
 
 def main():
@@ -857,7 +931,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2",
                     choices=["c2", "c2legacy", "c2dropin", "c2graph", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
-                             "c3wide", "c3widefused", "lgptwide", "c4", "c4fused", "c4hexp", "c5",
+                             "c3wide", "c3widefused", "c3widerope", "c3wideropesep", "c3rope",
+                             "c3ropesep", "lgptwide", "c4", "c4fused", "c4hexp", "c5",
                              "mhats", "gen1",
                              "gen64", "gen256", "gpt768", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])

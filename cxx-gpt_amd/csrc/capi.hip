@@ -811,6 +811,128 @@ int cxg_kattn_bwd(const float* Q, const float* K, const float* V, const float* O
                           stream);
 }
 
+// TwoStageGPT's stage 2 with RoPE fused (two_stage_gpt.hpp:113-122 forward,
+// :149-160 backward): Q and K are read unrotated and rotated over their whole
+// width (head_dim = D).  The chunked scan (D, E <= 64, longer sequences)
+// rotates rows as its kernels stage them and rotates dQ, dK back before their
+// stores.  The quadratic form (widths up to 512) would rotate every streamed
+// block again in each job that reads it, so a pre-pass forms the features
+// phi(rot(Q)), phi(rot(K)) once (library scratch), the forward runs on them,
+// and the backward streams them and applies phi' and the inverse rotation in
+// its output stage.  Wider heads rotate copies of Q and K in scratch, run the
+// ELU+1 kernels and rotate dQ and dK back in place.
+static int rope_lin_check(size_t B, size_t S, size_t D, size_t E, bool* empty)
+{
+    int st = lin_check(B, S, D, E, empty);
+    if (st != CXG_OK)
+        return st;
+    if (D % 2 != 0 || D > (size_t)ROPE_MAX_HEAD_DIM)
+        return CXG_ERR_DIMS;
+    return CXG_OK;
+}
+
+int cxg_kattn_rope_fwd(const float* Q, const float* K, const float* V, float* O,
+                       float* den_cache, void* ctx, size_t ctx_bytes, size_t B, size_t S,
+                       size_t D, size_t E, cxg_stream_t stream)
+{
+    bool empty;
+    int st = rope_lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (lin_bwd_fused_ok((int)D, (int)E, (long)S))   // the chunked scan
+        return lin_fwd_common(PHI_ELU1_ROPE, 0, 0, Q, K, V, O, den_cache, nullptr, nullptr,
+                              nullptr, B, S, D, E, stream, ctx, ctx_bytes);
+    if (!Q || !K || !V || !O || !den_cache)
+        return CXG_ERR_NULL;
+    hipStream_t s = (hipStream_t)stream;
+    const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_FWD);
+    const size_t t = round_up(B * S * D * sizeof(float), 256);
+    if (p.quad) {
+        Scratch ws;
+        st = ws.acquire(nullptr, 0, 2 * t + lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
+        if (st != CXG_OK)
+            return st;
+        float* fq = (float*)ws.p;
+        float* fk = (float*)((char*)ws.p + t);
+        hipError_t e = lin_rope_feat_launch(Q, K, fq, fk, (int)B, (int)S, (int)D, s);
+        if (e == hipSuccess)
+            e = lin_wide_fwd_launch(PHI_NONE, fq, fk, V, O, den_cache, nullptr, 0, (int)B,
+                                    (int)S, (int)D, (int)E, (char*)ws.p + 2 * t, s);
+        return hip_status(e);
+    }
+    Scratch ws;
+    st = ws.acquire(nullptr, 0, 2 * t + lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
+    if (st != CXG_OK)
+        return st;
+    float* rq = (float*)ws.p;
+    float* rk = (float*)((char*)ws.p + t);
+    hipError_t e = hipMemcpyAsync(rq, Q, B * S * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(rk, K, B * S * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = rope_launch(rq, rk, (long)B, (int)S, (int)D, (int)D, 1.0f, s);
+    if (e == hipSuccess)
+        e = lin_fwd_launch(PHI_ELU1, rq, rk, V, O, den_cache, nullptr, nullptr, nullptr, 0, 0,
+                           (int)B, (int)S, (int)D, (int)E, (char*)ws.p + 2 * t, s);
+    return hip_status(e);
+}
+
+int cxg_kattn_rope_bwd(const float* Q, const float* K, const float* V, const float* O,
+                       const float* dO, const float* den_cache, const void* ctx, float* dQ,
+                       float* dK, float* dV, size_t B, size_t S, size_t D, size_t E,
+                       cxg_stream_t stream)
+{
+    bool empty;
+    int st = rope_lin_check(B, S, D, E, &empty);
+    if (st != CXG_OK || empty)
+        return st;
+    if (lin_bwd_fused_ok((int)D, (int)E, (long)S))   // the chunked scan
+        return lin_bwd_common(PHI_ELU1_ROPE, Q, K, V, O, dO, den_cache, ctx, dQ, dK, dV, B, S, D,
+                              E, stream);
+    if (!Q || !K || !V || !O || !dO || !den_cache || !dQ || !dK || !dV)
+        return CXG_ERR_NULL;
+    if (B * S > ((size_t)1 << 34) / (D + E + 1))
+        return CXG_ERR_DIMS;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t t = round_up(B * S * D * sizeof(float), 256);
+    if (lin_quad_ok((int)D, (int)E, (long)S)) {
+        const size_t N = B * S, tn = round_up(N * E * sizeof(float), 256);
+        Scratch ws;
+        st = ws.acquire(nullptr, 0, 2 * t + tn + round_up(N * sizeof(float), 256), s);
+        if (st != CXG_OK)
+            return st;
+        float* fq = (float*)ws.p;
+        float* fk = (float*)((char*)ws.p + t);
+        float* dnum = (float*)((char*)ws.p + 2 * t);
+        float* dden = (float*)((char*)ws.p + 2 * t + tn);
+        hipError_t e = lin_rope_feat_launch(Q, K, fq, fk, (int)B, (int)S, (int)D, s);
+        if (e == hipSuccess)
+            e = lin_step1_launch(O, dO, den_cache, dnum, dden, (long)N, (int)E, s);
+        if (e == hipSuccess)
+            e = lin_wide_bwd_launch(PHI_ELU1_ROPE, fq, fk, V, dnum, dden, dQ, dK, dV, (int)B,
+                                    (int)S, (int)D, (int)E, 3, s, Q, K);
+        return hip_status(e);
+    }
+    Scratch ws;
+    st = ws.acquire(nullptr, 0,
+                    2 * t + lin_bwd_split_ws_bytes((int)B, (int)S, (int)D, (int)E), s);
+    if (st != CXG_OK)
+        return st;
+    float* rq = (float*)ws.p;
+    float* rk = (float*)((char*)ws.p + t);
+    hipError_t e = hipMemcpyAsync(rq, Q, B * S * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(rk, K, B * S * D * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = rope_launch(rq, rk, (long)B, (int)S, (int)D, (int)D, 1.0f, s);
+    if (e == hipSuccess)
+        e = lin_bwd_split_launch(PHI_ELU1, rq, rk, V, O, dO, den_cache, dQ, dK, dV, (int)B,
+                                 (int)S, (int)D, (int)E, (char*)ws.p + 2 * t, s);
+    if (e == hipSuccess)
+        e = rope_launch(dQ, dK, (long)B, (int)S, (int)D, (int)D, -1.0f, s);
+    return hip_status(e);
+}
+
 size_t cxg_lin_ctx_size(size_t B, size_t S, size_t D, size_t E)
 {
     bool empty;

@@ -66,9 +66,14 @@ constexpr int AGG_STAGE = 2 * CHUNK + 16;
 template <int PHI, bool VEC, bool FW>
 __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))) void lin_agg_kernel(
     const float* __restrict__ X, const float* __restrict__ Y, const float* __restrict__ w,
-    float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L)
+    float* __restrict__ ws, int Bq, int S, int D, int E, int nseg, int L,
+    const LinRopeArg<PHI> rope)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * AGG_STAGE];
+    __shared__ float rope_w[phi_rope(PHI) ? 32 : 1];   // RoPE maps: X rows rotated first
+    rope_tab_lds<PHI, 32>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int h = wv & 1, half = wv >> 1;
     const int l16 = lane & 15, g = lane >> 4;
@@ -139,6 +144,7 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
                     ay[i][e] = ok ? ay[i][e] : 0.0f;
                 }
             } else {
+                ax[i] = rot_row<PHI>(ax[i], t0 + crow + 4 * i, ccol, rope_w);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const float xv = Phi<PHI>::f(ax[i][e]);
@@ -286,9 +292,13 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     float* __restrict__ O, float* __restrict__ den, float* __restrict__ zcache,
     const float* __restrict__ ws, float* __restrict__ Sfin, float* __restrict__ zfin,
     float* __restrict__ ctot, float* __restrict__ ztab, float* __restrict__ anch, int sfin_de,
-    int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L)
+    int den_incl_eps, int Bq, int S, int D, int E, int nseg, int L, const LinRopeArg<PHI> rope)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * FWD_STAGE + CHUNK];
+    __shared__ float rope_w[phi_rope(PHI) ? 32 : 1];   // RoPE maps: Q, K rows rotated first
+    rope_tab_lds<PHI, 32>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();
     const int lane = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x;
@@ -393,6 +403,12 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                 *reinterpret_cast<f4*>(&bK[row * CLD + 4 * l16]) = ok ? hk : f4zero();
             }
         } else {
+            if constexpr (phi_rope(PHI))
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    aq[i] = rot_row<PHI>(aq[i], t0 + l16, 16 * (2 * h + i) + 4 * g, rope_w);
+                    ak[i] = rot_row<PHI>(ak[i], t0 + l16, 16 * (2 * h + i) + 4 * g, rope_w);
+                }
             finRp<PHI, true, FW, 2>(aq, full, rok, D, g, 2 * h);
             finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
             putRp(bQ, aq, l16, g, 2 * h);
@@ -1406,23 +1422,26 @@ static hipError_t agg_and_scan(const LinPlan& p, const float* X, const float* Y,
                                float* ws, int Bq, int S, int D, int E, int reverse, int mode,
                                hipStream_t st)
 {
-    // short sequences: one launch forms the scanned records
-    if (lin_seq_cpw((S + 15) / 16, p.L / 16) > 0)
-        return lin_seqrec_launch<PHI>(X, Y, w, ws, Bq, S, D, E, p.L, p.nseg, reverse, st);
+    // short sequences: one launch forms the scanned records (its column-layout
+    // loads split RoPE's pairs across lanes, so the RoPE map takes the pair)
+    if constexpr (!phi_rope(PHI))
+        if (lin_seq_cpw((S + 15) / 16, p.L / 16) > 0)
+            return lin_seqrec_launch<PHI>(X, Y, w, ws, Bq, S, D, E, p.L, p.nseg, reverse, st);
+    const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
     dim3 grid((unsigned)(Bq * p.nseg)), block(AGG_THREADS);
     {
         ProfScope ps(st, "lin_agg");
         if (mode == 2)
             CXG_LAUNCH((lin_agg_kernel<PHI, true, true>), grid, block, 0, st, X, Y, w, ws,
-                               Bq, S, D, E, p.nseg, p.L);
+                               Bq, S, D, E, p.nseg, p.L, rope);
         else if constexpr (PHI == PHI_HEXP)
             return hipErrorInvalidValue;   // D = E = 64 only
         else if (mode == 1)
             CXG_LAUNCH((lin_agg_kernel<PHI, true, false>), grid, block, 0, st, X, Y, w, ws,
-                               Bq, S, D, E, p.nseg, p.L);
+                               Bq, S, D, E, p.nseg, p.L, rope);
         else
             CXG_LAUNCH((lin_agg_kernel<PHI, false, false>), grid, block, 0, st, X, Y, w,
-                               ws, Bq, S, D, E, p.nseg, p.L);
+                               ws, Bq, S, D, E, p.nseg, p.L, rope);
     }
     {
         ProfScope ps(st, "lin_scan");
@@ -1450,12 +1469,17 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         if (p.quad || !p.fast || mode != 2)
             return hipErrorInvalidValue;
     } else if (p.quad) {
+        if (phi_rope(PHI))   // the callers form the features (lin_rope_feat_launch)
+            return hipErrorInvalidValue;
         hipError_t e = lin_wide_fwd_launch(PHI, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, ws,
                                            st);
         if (e == hipSuccess && Sfin != nullptr)
             e = lin_wide_state_launch(PHI, K, V, Sfin, zfin, sfin_de, Bq, S, D, E, st);
         return e;
     } else if (!p.fast) {
+        if constexpr (phi_rope(PHI))
+            return hipErrorInvalidValue;   // widths above 512: the callers rotate outside
+        else {
         float* state = (float*)ws;
         const size_t sm = (size_t)(3 * D + 256) * sizeof(float);
         {
@@ -1469,6 +1493,7 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
                                0, st, state, Sfin, (long)Bq, D, E, sfin_de);
         }
         return hipGetLastError();
+        }
     }
     float* wsf = (float*)ws;
     if (p.nseg > 1) {
@@ -1479,21 +1504,22 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         wsf = nullptr;
     }
     dim3 grid((unsigned)(Bq * p.nseg)), block(FWD_THREADS);
+    const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
     ProfScope ps(st, "lin_fwd");
     if (mode == 2)
         CXG_LAUNCH((lin_fwd_kernel<PHI, true, true>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
-                           p.L);
+                           p.L, rope);
     else if constexpr (PHI == PHI_HEXP)
         return hipErrorInvalidValue;
     else if (mode == 1)
         CXG_LAUNCH((lin_fwd_kernel<PHI, true, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
-                           p.L);
+                           p.L, rope);
     else
         CXG_LAUNCH((lin_fwd_kernel<PHI, false, false>), grid, block, 0, st, Q, K, V, O, den, zc,
                            wsf, Sfin, zfin, ctot, ztab, anch, sfin_de, den_eps, Bq, S, D, E, p.nseg,
-                           p.L);
+                           p.L, rope);
     return hipGetLastError();
 }
 
@@ -1511,6 +1537,9 @@ hipError_t lin_fwd_launch(int phi, const float* Q, const float* K, const float* 
     if (phi == PHI_HEXP)
         return fwd_impl<PHI_HEXP>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
                                   den_eps, Bq, S, D, E, ws, st);
+    if (phi == PHI_ELU1_ROPE)
+        return fwd_impl<PHI_ELU1_ROPE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch,
+                                       sfin_de, den_eps, Bq, S, D, E, ws, st);
     return fwd_impl<PHI_NONE>(Q, K, V, O, den, zc, Sfin, zfin, ctot, ztab, anch, sfin_de,
                               den_eps, Bq, S, D, E, ws, st);
 }

@@ -2,16 +2,41 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stddef.h>
 
 namespace cxg {
 
 // Feature map applied inside the kernels: ELU+1 as two_stage computes it, none
 // (inputs are features already: linear_cuda), ELU+1 in linear_cuda's
-// phi_elu form (LinearGPT's feature map fused into the scans), or
+// phi_elu form (LinearGPT's feature map fused into the scans),
 // Hadamard+Exp (exp(H x / 8) per 64-column row, phi_hexp fused into the
-// fused pair's kernels; D = E = 64 only).
-enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2, PHI_HEXP = 3 };
+// fused pair's kernels; D = E = 64 only), or two_stage's ELU+1 of q and k
+// rotated by RoPE over their whole width first (head_dim = D: TwoStageGPT's
+// stage 2, two_stage_gpt.hpp:113; D even, D <= 512, the fused pair's kernels
+// and the quadratic form only).
+enum { PHI_ELU1 = 0, PHI_NONE = 1, PHI_ELU1_LG = 2, PHI_HEXP = 3, PHI_ELU1_ROPE = 4 };
+
+__host__ __device__ constexpr bool phi_rope(int phi) { return phi == PHI_ELU1_ROPE; }
+
+// Rotary frequencies for the PHI_ELU1_ROPE kernels, passed by value:
+// w[i] = 10000^(-2i/D), i < D/2 (one float for the other maps).
+constexpr int LIN_ROPE_MAX_D = 512;
+template <int PHI>
+struct LinRopeArg {
+    float w[phi_rope(PHI) ? LIN_ROPE_MAX_D / 2 : 1];
+};
+template <int PHI>
+inline LinRopeArg<PHI> lin_rope_arg(int D)
+{
+    LinRopeArg<PHI> a{};
+    if constexpr (phi_rope(PHI)) {
+        // kernel_test.cpp:453 (the reference's CPU RoPE): powf of the same float exponent
+        for (int i = 0; i < D / 2 && i < LIN_ROPE_MAX_D / 2; i++)
+            a.w[i] = powf(10000.0f, -2.0f * (float)i / (float)D);
+    }
+    return a;
+}
 
 // floats per segment record in the scan workspace: 64x64 state [d][e] + z[64]
 constexpr int LIN_WS = 64 * 64 + 64;
@@ -133,7 +158,14 @@ hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const fl
                                void* ws, hipStream_t st);
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                                const float* dnum, const float* dden, float* dQ, float* dK,
-                               float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st);
+                               float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st,
+                               const float* Qx = nullptr, const float* Kx = nullptr);
+// The RoPE map's features for the quadratic form: Fq = phi(rot(Q)), Fk =
+// phi(rot(K)) (B' x S rows of width D, D even, D <= LIN_ROPE_MAX_D).  The
+// forward then runs with PHI_NONE on them; the backward (lin_wide_bwd_launch
+// with phi = PHI_ELU1_ROPE) streams them and takes the raw Q, K as Qx, Kx.
+hipError_t lin_rope_feat_launch(const float* Q, const float* K, float* Fq, float* Fk, int Bq,
+                                int S, int D, hipStream_t st);
 hipError_t lin_wide_state_launch(int phi, const float* K, const float* V, float* Sfin,
                                  float* zfin, int sfin_de, int Bq, int S, int D, int E,
                                  hipStream_t st);

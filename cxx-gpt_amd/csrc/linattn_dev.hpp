@@ -37,6 +37,11 @@ struct Phi<PHI_ELU1_LG> {
     // 2^-25 of expf(x)
     static __device__ __forceinline__ float d_from_f(float p) { return fminf(p, 1.0f); }
 };
+// ELU+1 of rotated inputs: the elementwise part is two_stage's ELU+1; the
+// rotation is applied to the raw row before it (rot_row below).
+template <>
+struct Phi<PHI_ELU1_ROPE> : Phi<PHI_ELU1> {
+};
 // PHI_HEXP has no elementwise form: the kernels apply it to whole rows
 // (hexp_row4, hexp_colC below) and leave Phi<PHI_HEXP> undefined, so that no
 // elementwise site can take it by mistake.
@@ -124,6 +129,53 @@ __device__ __forceinline__ void hexp_colC(float (&x)[4], int lane)
     x[1] = __expf((a1 + a3) * 0.125f);
     x[2] = __expf((a0 - a2) * 0.125f);
     x[3] = __expf((a1 - a3) * 0.125f);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE of the PHI_ELU1_ROPE maps.  The frequency table goes to LDS at kernel
+// start (one lane, uniform indices, so the argument is read with scalar
+// loads; the caller synchronises before the first use).  rot_row rotates an
+// f4 holding columns c .. c+3 of the row at sequence position pos; other maps
+// leave it unchanged.
+// ---------------------------------------------------------------------------
+template <int PHI, int N>
+__device__ __forceinline__ void rope_tab_lds(float* __restrict__ dst, const LinRopeArg<PHI>& a)
+{
+    if constexpr (phi_rope(PHI)) {
+        static_assert(N <= LIN_ROPE_MAX_D / 2, "rope table");
+        for (int i = threadIdx.x; i < N; i += blockDim.x)
+            dst[i] = a.w[i];
+    }
+}
+
+template <int PHI>
+__device__ __forceinline__ f4 rot_row(f4 v, int pos, int c, const float* __restrict__ rw,
+                                      float sign = 1.0f)
+{
+    if constexpr (phi_rope(PHI))
+        return rope4(v, pos, c, rw, sign);
+    return v;
+}
+
+// Gradient with respect to the raw row x of a RoPE map's feature row
+// phi(rot(x)): g (columns c .. c+3, gradient w.r.t. the features) times
+// phi'(rot(x)), rotated back; one sin/cos per pair serves both rotations.
+template <int PHI>
+__device__ __forceinline__ f4 rope_phi_grad4(f4 g, f4 x, int pos, int c,
+                                             const float* __restrict__ rw)
+{
+    f4 o;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float sn, cs;
+        sincos_rev((float)pos * rw[(c >> 1) + h], &sn, &cs);
+        const float x0 = x[2 * h], x1 = x[2 * h + 1];
+        const float g0 = g[2 * h] * Phi<PHI>::d(x0 * cs - x1 * sn);
+        const float g1 = g[2 * h + 1] * Phi<PHI>::d(x0 * sn + x1 * cs);
+        o[2 * h] = g0 * cs + g1 * sn;
+        o[2 * h + 1] = -g0 * sn + g1 * cs;
+    }
+    return o;
 }
 
 // ---------------------------------------------------------------------------

@@ -94,7 +94,8 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
     float* __restrict__ rec, float* __restrict__ ztab_seg, float* __restrict__ anch_seq,
-    float* __restrict__ lds, int seq, int seg, int S, int D, int E, int L)
+    float* __restrict__ lds, int seq, int seg, int S, int D, int E, int L,
+    const float* __restrict__ rope_w)
 {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int l16 = lane & 15, g = lane >> 4;
@@ -143,7 +144,7 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
         const bool ok = t0 + lrow < tend;
         f4 x, y;
         float wv;
-        const f4 px = phi_row<PHI>(s.a, lane);
+        const f4 px = phi_row<PHI>(rot_row<PHI>(s.a, t0 + lrow, lcol, rope_w), lane);
         if constexpr (!SUF) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -227,9 +228,13 @@ __global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ den,
     float* __restrict__ wsP, float* __restrict__ wsB, float* __restrict__ ztab,
     float* __restrict__ anch, int nanch, int Bq, int S, int D, int E, int nseg, int L, int nchs,
-    int with_prefix)
+    int with_prefix, const LinRopeArg<PHI> rope)
 {
     __shared__ __attribute__((aligned(16))) float lds[2 * BAGG_STAGE];
+    __shared__ float rope_w[phi_rope(PHI) ? 32 : 1];   // RoPE maps: Q, K rows rotated first
+    rope_tab_lds<PHI, 32>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();
     const int nP = with_prefix ? Bq * nseg : 0;
     if ((int)blockIdx.x < nP) {
         const int seq = blockIdx.x / nseg, seg = blockIdx.x - seq * nseg;
@@ -237,13 +242,13 @@ __global__ __launch_bounds__(BAGG_THREADS) void lin_bagg_kernel(
                                        ztab + ((long)seq * nchs + seg * (L / 16)) * 64,
                                        seg == 0 && nanch > 0 ? anch + (long)seq * nanch * LIN_ANCH
                                                              : nullptr,
-                                       lds, seq, seg, S, D, E, L);
+                                       lds, seq, seg, S, D, E, L, rope_w);
     } else {
         const int b = blockIdx.x - nP;
         const int seq = b / (nseg - 1), seg = 1 + (b - seq * (nseg - 1));
         bagg_body<PHI, VEC, FW, true>(Q, K, V, O, dO, den,
                                       wsB + ((long)seq * nseg + seg) * LIN_WS, nullptr, nullptr,
-                                      lds, seq, seg, S, D, E, L);
+                                      lds, seq, seg, S, D, E, L, rope_w);
     }
 }
 
@@ -315,12 +320,19 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV,
     const float* __restrict__ wsP, const float* __restrict__ wsB, const float* __restrict__ ztab,
     const float* __restrict__ crec, const float* __restrict__ ctot, const float* __restrict__ anch,
-    int nanch, int mf, int nsegf, int S, int D, int E, int nseg, int L, int nchs)
+    int nanch, int mf, int nsegf, int S, int D, int E, int nseg, int L, int nchs,
+    const LinRopeArg<PHI> rope)
 {
     // Hadamard+Exp: the chunk's dphi(Q) * phi(Q) and dphi(K) * phi(K), [t][d],
     // for the row transform that turns them into dQ and dK (see flush below)
     constexpr int HEXP_LDS = PHI == PHI_HEXP ? 2 * CHUNK : 0;
     __shared__ __attribute__((aligned(16))) float lds[BWD_LDS + HEXP_LDS];
+    // RoPE maps: Q, K rows rotated as they are staged; dQ, dK (gradients with
+    // respect to the rotated rows) rotated back before their stores
+    __shared__ float rope_w[phi_rope(PHI) ? 32 : 1];
+    rope_tab_lds<PHI, 32>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();
     float* sS = lds + 2 * BWD_STAGE;   // S* [d][e]
     float* sP = sS + 64 * SLD;         // partial products [wave][M1, X, X^T][lane * 4 + r]
     float* sH = lds + BWD_LDS;         // Hadamard+Exp only
@@ -450,7 +462,9 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             const float inv = ok ? __builtin_amdgcn_rcpf(s.dn) : 0.0f;
             const float dot = row16_sum(s.d[0] * s.o[0] + s.d[1] * s.o[1] + s.d[2] * s.o[2] +
                                         s.d[3] * s.o[3]);
-            f4 q = phi_row<PHI>(s.q, lane), k = phi_row<PHI>(s.k, lane), v = s.v;
+            f4 q = phi_row<PHI>(rot_row<PHI>(s.q, t0 + lrow, lcol, rope_w), lane);
+            f4 k = phi_row<PHI>(rot_row<PHI>(s.k, t0 + lrow, lcol, rope_w), lane);
+            f4 v = s.v;
             if (t0 + 16 > tend) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -576,6 +590,7 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     dk[i] *= Phi<PHI>::d_from_f(kRw[i]);
+                dk = rot_row<PHI>(dk, t0 + l16, 16 * w + 4 * g, rope_w, -1.0f);
             }
             if constexpr (PHI == PHI_HEXP) {
             } else if constexpr (FW) {
@@ -636,6 +651,7 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     dq[i] *= Phi<PHI>::d_from_f(qRw[i]);
+                dq = rot_row<PHI>(dq, t0 + l16, 16 * w + 4 * g, rope_w, -1.0f);
             }
             if constexpr (PHI == PHI_HEXP) {
             } else if constexpr (FW) {
@@ -764,11 +780,12 @@ static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const
     // those lin_bagg forms inside the first segment
     const int nanch = pre ? bwd_nanch_noctx(p, S) : lin_nanch(nchs);
     const unsigned nb = (unsigned)((pre ? Bq * p.nseg : 0) + Bq * (p.nseg - 1));
+    const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
     if (nb > 0) {
         ProfScope ps(st, "lin_bagg");
         CXG_LAUNCH((lin_bagg_kernel<PHI, VEC, FW>), dim3(nb), dim3(BAGG_THREADS), 0, st,
                            Q, K, V, O, dO, den, a.wsP, a.wsB, a.zt, a.anch, pre ? nanch : 0, Bq,
-                           S, D, E, p.nseg, p.L, nchs, pre ? 1 : 0);
+                           S, D, E, p.nseg, p.L, nchs, pre ? 1 : 0, rope);
     }
     {
         ProfScope ps(st, "lin_bscan");
@@ -780,7 +797,7 @@ static void bwd_launch_t(const LinPlan& p, const float* Q, const float* K, const
     CXG_LAUNCH((lin_bwd_kernel<PHI, VEC, FW>), dim3((unsigned)(Bq * p.nseg)),
                        dim3(BWD_THREADS), 0, st, Q, K, V, O, dO, den, dQ, dK, dV, a.wsP, a.wsB,
                        pre ? a.zt : a.c.zt, a.c.rec, a.c.tot, pre ? a.anch : a.c.anch, nanch,
-                       a.mf, a.nsegf, S, D, E, p.nseg, p.L, nchs);
+                       a.mf, a.nsegf, S, D, E, p.nseg, p.L, nchs, rope);
 }
 
 template <int PHI>
@@ -840,6 +857,8 @@ hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const f
         bwd_dispatch<PHI_ELU1_LG>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else if (phi == PHI_HEXP)
         bwd_dispatch<PHI_HEXP>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
+    else if (phi == PHI_ELU1_ROPE)
+        bwd_dispatch<PHI_ELU1_ROPE>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     else
         bwd_dispatch<PHI_NONE>(p, Q, K, V, O, dO, den, dQ, dK, dV, a, Bq, S, D, E, st);
     return hipGetLastError();

@@ -80,6 +80,7 @@ template <int NW, int PHI, bool APPLY>
 __device__ __forceinline__ void lw_store(float* __restrict__ dst, const LwRegs<NW>& R, int n,
                                          int tid)
 {
+    static_assert(!phi_rope(PHI), "RoPE maps stream features (lin_rope_feat_kernel)");
     constexpr int UPR = LW<NW>::DP / 4;
 #pragma unroll
     for (int k = 0; k < LW<NW>::U; k++) {
@@ -297,10 +298,19 @@ template <int PHI, int NW, bool VEC>
 __global__ __launch_bounds__(64 * NW) void lin_wide_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dnum, const float* __restrict__ dden, float* __restrict__ dQ,
-    float* __restrict__ dK, float* __restrict__ dV, int S, int D, int E, int Bq, int kinds)
+    float* __restrict__ dK, float* __restrict__ dV, int S, int D, int E, int Bq, int kinds,
+    const float* __restrict__ Qx, const float* __restrict__ Kx, const LinRopeArg<PHI> rope)
 {
+    // RoPE maps: Q and K are the features phi(rot(x)) (lin_rope_feat_kernel),
+    // streamed as they are; Qx, Kx the raw inputs, for phi' and the inverse
+    // rotation of dQ, dK at the end.  Other maps: Qx = Q, Kx = K.
+    constexpr int PS = phi_rope(PHI) ? PHI_NONE : PHI;   // the map applied to streamed rows
     using P = LW<NW>;
     __shared__ __attribute__((aligned(16))) float lds[4 * P::TILE + 2 * NW * 256 + LWB];
+    __shared__ float rope_w[phi_rope(PHI) ? 32 * NW : 1];
+    rope_tab_lds<PHI, 32 * NW>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();
     float* Ks = lds;
     float* Vs = Ks + P::TILE;
     float* Qs = Vs + P::TILE;
@@ -327,13 +337,13 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_bwd_kernel(
     if (kjob) {
         LwRegs<NW> t;
         lw_fetch<NW, VEC>(t, K + rb * D, D, x0, S, D, tid);
-        lw_store<NW, PHI, true>(Ks, t, D, tid);
+        lw_store<NW, PS, true>(Ks, t, D, tid);
         lw_fetch<NW, VEC>(t, V + rb * E, E, x0, S, E, tid);
-        lw_store<NW, PHI, false>(Vs, t, E, tid);
+        lw_store<NW, PS, false>(Vs, t, E, tid);
     } else {
         LwRegs<NW> t;
         lw_fetch<NW, VEC>(t, dnum + rb * E, E, x0, S, E, tid);
-        lw_store<NW, PHI, false>(Ns, t, E, tid);
+        lw_store<NW, PS, false>(Ns, t, E, tid);
         if (tid < LWB)
             dd[tid] = dden[rb + min(x0 + tid, S - 1)];
     }
@@ -356,8 +366,8 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_bwd_kernel(
     float ddn = (kjob && tid < LWB) ? dden[rb + min(sbeg * LWB + tid, S - 1)] : 0.0f;
     for (int sb = sbeg; sb < send; sb++) {
         const int y0 = sb * LWB;
-        lw_store<NW, PHI, true>(d1, r1, n1, tid);
-        lw_store<NW, PHI, false>(d2, r2, n2, tid);
+        lw_store<NW, PS, true>(d1, r1, n1, tid);
+        lw_store<NW, PS, false>(d2, r2, n2, tid);
         if (kjob && tid < LWB)
             dd[tid] = ddn;
         __builtin_amdgcn_sched_barrier(0);
@@ -440,14 +450,17 @@ __global__ __launch_bounds__(64 * NW) void lin_wide_bwd_kernel(
     // row x0 + l16 of this job's outputs: phi' from the raw inputs
     const int row = x0 + l16;
     if (row < S) {
-        const float* xr = (kjob ? K : Q) + (rb + row) * D;
+        const float* xr = (kjob ? Kx : Qx) + (rb + row) * D;
         float* g1 = (kjob ? dK : dQ) + (rb + row) * D;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int c = c0 + 16 * t + 4 * g;
             if (c < D) {
                 f4 v = acc1[t];
-                if constexpr (PHI != PHI_NONE) {
+                if constexpr (phi_rope(PHI)) {
+                    // phi' at the rotated input, then the gradient rotated back
+                    v = rope_phi_grad4<PHI>(v, load4c<VEC>(xr, c, D), row, c, rope_w);
+                } else if constexpr (PHI != PHI_NONE) {
                     const f4 xv = load4c<VEC>(xr, c, D);
 #pragma unroll
                     for (int i = 0; i < 4; i++)
@@ -667,17 +680,19 @@ static hipError_t wide_fwd_t(const float* Q, const float* K, const float* V, flo
 template <int PHI, int NW>
 static hipError_t wide_bwd_t(const float* Q, const float* K, const float* V, const float* dnum,
                              const float* dden, float* dQ, float* dK, float* dV, int Bq, int S,
-                             int D, int E, int kinds, bool vec, hipStream_t st)
+                             int D, int E, int kinds, bool vec, hipStream_t st, const float* Qx,
+                             const float* Kx)
 {
     const int nb = (S + LWB - 1) / LWB;
     dim3 grid((unsigned)((long)(kinds == 3 ? 2 : 1) * nb * Bq)), block(64 * NW);
     ProfScope ps(st, kinds == 3 ? "lin_wide_bwd" : kinds == 1 ? "lin_wide_dkdv" : "lin_wide_dq");
+    const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
     if (vec)
         CXG_LAUNCH((lin_wide_bwd_kernel<PHI, NW, true>), grid, block, 0, st, Q, K, V,
-                           dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds);
+                           dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds, Qx, Kx, rope);
     else
         CXG_LAUNCH((lin_wide_bwd_kernel<PHI, NW, false>), grid, block, 0, st, Q, K, V,
-                           dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds);
+                           dnum, dden, dQ, dK, dV, S, D, E, Bq, kinds, Qx, Kx, rope);
     return hipGetLastError();
 }
 
@@ -699,16 +714,21 @@ static hipError_t wide_fwd_p(const float* Q, const float* K, const float* V, flo
 template <int PHI>
 static hipError_t wide_bwd_p(const float* Q, const float* K, const float* V, const float* dnum,
                              const float* dden, float* dQ, float* dK, float* dV, int Bq, int S,
-                             int D, int E, int kinds, bool vec, hipStream_t st)
+                             int D, int E, int kinds, bool vec, hipStream_t st, const float* Qx,
+                             const float* Kx)
 {
     const int m = std::max(D, E);
     if (m <= 64)
-        return wide_bwd_t<PHI, 1>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
+        return wide_bwd_t<PHI, 1>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st,
+                                  Qx, Kx);
     if (m <= 128)
-        return wide_bwd_t<PHI, 2>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
+        return wide_bwd_t<PHI, 2>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st,
+                                  Qx, Kx);
     if (m <= 256)
-        return wide_bwd_t<PHI, 4>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
-    return wide_bwd_t<PHI, 8>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
+        return wide_bwd_t<PHI, 4>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st,
+                                  Qx, Kx);
+    return wide_bwd_t<PHI, 8>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st, Qx,
+                              Kx);
 }
 
 hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
@@ -725,16 +745,101 @@ hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const fl
 
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                                const float* dnum, const float* dden, float* dQ, float* dK,
-                               float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st)
+                               float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st,
+                               const float* Qx, const float* Kx)
 {
+    if (phi_rope(phi) != (Qx != nullptr && Kx != nullptr))
+        return hipErrorInvalidValue;   // RoPE maps: features plus raw inputs; others: no raw
+    if (Qx == nullptr) {
+        Qx = Q;
+        Kx = K;
+    }
     const bool vec = D % 4 == 0 && E % 4 == 0 && al16x(Q) && al16x(K) && al16x(V) &&
-                     al16x(dnum) && al16x(dQ) && al16x(dK) && al16x(dV);
+                     al16x(dnum) && al16x(dQ) && al16x(dK) && al16x(dV) && al16x(Qx) && al16x(Kx);
     if (phi == PHI_ELU1)
-        return wide_bwd_p<PHI_ELU1>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
+        return wide_bwd_p<PHI_ELU1>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st,
+                                    Qx, Kx);
     if (phi == PHI_ELU1_LG)
         return wide_bwd_p<PHI_ELU1_LG>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec,
-                                       st);
-    return wide_bwd_p<PHI_NONE>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st);
+                                       st, Qx, Kx);
+    if (phi == PHI_ELU1_ROPE)
+        return wide_bwd_p<PHI_ELU1_ROPE>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds,
+                                         vec, st, Qx, Kx);
+    return wide_bwd_p<PHI_NONE>(Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, vec, st, Qx,
+                                Kx);
+}
+
+// ---------------------------------------------------------------------------
+// Features of the RoPE map for the quadratic form: F = phi(rot(X)) for Q and K
+// (rows of B' sequences of S, width D even; pair i of row t rotated by
+// t * 10000^(-2i/D), then two_stage's ELU+1).  Each row is rotated once here,
+// where the quadratic-form kernels would rotate every streamed block again in
+// each job that reads it.  A thread takes one column pair of FEAT_ROWS
+// consecutive rows of both tensors (the pair's frequency read once, pairs
+// moved as 8-byte loads when aligned).
+// ---------------------------------------------------------------------------
+constexpr int FEAT_ROWS = 4;   // rows per thread: the pair's frequency is read once
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void lin_rope_feat_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, float* __restrict__ Fq,
+    float* __restrict__ Fk, long rows, int S, int D, const LinRopeArg<PHI_ELU1_ROPE> rope)
+{
+    const int np = D / 2;
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+    const long rblk = idx / np;
+    const int i = (int)(idx - rblk * np);
+    const long r0 = rblk * FEAT_ROWS;
+    if (r0 >= rows)
+        return;
+    const float w = rope.w[i];
+    using F = Phi<PHI_ELU1_ROPE>;
+    auto ld = [&](const float* a) {
+        if constexpr (VEC)
+            return *reinterpret_cast<const float2*>(a);
+        return make_float2(a[0], a[1]);
+    };
+    auto st = [&](float* a, float2 v) {
+        if constexpr (VEC) {
+            *reinterpret_cast<float2*>(a) = v;
+        } else {
+            a[0] = v.x;
+            a[1] = v.y;
+        }
+    };
+    int pos = (int)(r0 % S);
+#pragma unroll
+    for (int k = 0; k < FEAT_ROWS; k++) {
+        if (r0 + k < rows) {
+            float sn, cs;
+            sincos_rev((float)pos * w, &sn, &cs);
+            const long off = (r0 + k) * D + 2 * i;
+            const float2 q = ld(Q + off), kk = ld(K + off);
+            st(Fq + off, make_float2(F::f(q.x * cs - q.y * sn), F::f(q.x * sn + q.y * cs)));
+            st(Fk + off, make_float2(F::f(kk.x * cs - kk.y * sn), F::f(kk.x * sn + kk.y * cs)));
+        }
+        pos = (pos + 1 == S) ? 0 : pos + 1;
+    }
+}
+
+hipError_t lin_rope_feat_launch(const float* Q, const float* K, float* Fq, float* Fk, int Bq,
+                                int S, int D, hipStream_t st)
+{
+    if (D % 2 != 0 || D > LIN_ROPE_MAX_D)
+        return hipErrorInvalidValue;
+    const long rows = (long)Bq * S;
+    const long n = (rows + FEAT_ROWS - 1) / FEAT_ROWS * (D / 2);
+    const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    const bool vec = (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)Fq | (uintptr_t)Fk) & 7u) == 0;
+    const LinRopeArg<PHI_ELU1_ROPE> rope = lin_rope_arg<PHI_ELU1_ROPE>(D);
+    ProfScope ps(st, "lin_rope_feat");
+    if (vec)
+        CXG_LAUNCH(lin_rope_feat_kernel<true>, grid, block, 0, st, Q, K, Fq, Fk, rows, S, D,
+                   rope);
+    else
+        CXG_LAUNCH(lin_rope_feat_kernel<false>, grid, block, 0, st, Q, K, Fq, Fk, rows, S, D,
+                   rope);
+    return hipGetLastError();
 }
 
 hipError_t lin_wide_state_launch(int phi, const float* K, const float* V, float* Sfin,

@@ -46,6 +46,8 @@ SIGNATURES = {
     "cxg_kattn_bwd_dKdV": [_vp] * 7 + [_sz] * 4 + [_vp],
     "cxg_kattn_bwd": [_vp] * 10 + [_sz] * 4 + [_vp],
     "cxg_kattn_fwd_ctx": [_vp] * 6 + [_sz] * 5 + [_vp],
+    "cxg_kattn_rope_fwd": [_vp] * 6 + [_sz] * 5 + [_vp],
+    "cxg_kattn_rope_bwd": [_vp] * 10 + [_sz] * 4 + [_vp],
     "cxg_lin_ctx_size": [_sz] * 4,
     "cxg_lin_fwd": [_vp] * 8 + [_sz] * 4 + [_vp],
     "cxg_lin_bwd_step1": [_vp] * 5 + [_sz] * 2 + [_vp],
@@ -235,6 +237,19 @@ def kattn_fwd_ctx(Q, K, V, O, den, ctx, B, S, D, E, stream=None):
     nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
     _call("cxg_kattn_fwd_ctx", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
           B, S, D, E, _stream(stream))
+
+
+def kattn_rope_fwd(Q, K, V, O, den, B, S, D, E, ctx=None, stream=None):
+    """Stage 2 with RoPE fused: Q, K unrotated (rotated over width D as loaded)."""
+    nbytes = 0 if ctx is None else ctx.numel() * ctx.element_size()
+    _call("cxg_kattn_rope_fwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(den), _ptr(ctx), nbytes,
+          B, S, D, E, _stream(stream))
+
+
+def kattn_rope_bwd(Q, K, V, O, dO, den, dQ, dK, dV, B, S, D, E, ctx=None, stream=None):
+    """Backward of kattn_rope_fwd: dQ, dK with respect to the unrotated Q, K."""
+    _call("cxg_kattn_rope_bwd", _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(dO), _ptr(den),
+          _ptr(ctx), _ptr(dQ), _ptr(dK), _ptr(dV), B, S, D, E, _stream(stream))
 
 
 # ------------------------------------------------------------------ linear_cuda API

@@ -220,6 +220,37 @@ int cxg_kattn_fwd_ctx(const float *Q, const float *K, const float *V, float *O,
                       float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
                       size_t D, size_t E, cxg_stream_t stream);
 
+/* TwoStageGPT's stage 2 with its RoPE fused into the linear-attention
+ * kernels: cxg_kattn_rope_fwd replaces two_stage_cuda::rope_fwd(lqc, lkc, B,
+ * S, E, E) followed by kernel_attn_fwd (two_stage_gpt.hpp:113-122), and
+ * cxg_kattn_rope_bwd replaces kernel_attn_bwd_step1 + _bwd_dQ + _bwd_dKdV
+ * followed by rope_bwd(dlq, dlk, B, S, E, E) (:149-160; the rotation is
+ * two_stage_cuda_kernels.cu:1810-1878).  No single counterpart in the
+ * reference.  Q and K are read unrotated and left unchanged: each row t of a
+ * sequence is rotated over its whole width (head_dim = D, pair i by
+ * t * 10000^(-2i/D)) as it is loaded, phi = ELU+1 is applied to the rotated
+ * row, and dQ, dK are the gradients with respect to the unrotated Q, K.  The
+ * forward writes O and den_cache as cxg_kattn_fwd (no z_cache: the backward
+ * here does not need it) and, like cxg_kattn_fwd_ctx, the context ctx for the
+ * backward when cxg_lin_ctx_size(B, S, D, E) is not 0 (ctx may be NULL with
+ * ctx_bytes 0 otherwise, and for the backward).  A context written by
+ * another forward is refused (CXG_ERR_WORKSPACE).  D even and at most 1024
+ * (CXG_ERR_DIMS).  The chunked scan (D, E <= 64, more than 128 rows) rotates
+ * rows inside its kernels as it stages them and rotates dQ, dK back before
+ * storing them; the quadratic form (widths up to 512, and shorter sequences)
+ * forms phi(rot(Q)), phi(rot(K)) once in a pre-pass into the library's
+ * scratch (its jobs would otherwise rotate each streamed block again), and
+ * its backward applies phi' and the inverse rotation as it stores dQ, dK;
+ * wider heads rotate copies of Q and K in the library's scratch and rotate
+ * dQ, dK back in place. */
+int cxg_kattn_rope_fwd(const float *Q, const float *K, const float *V, float *O,
+                       float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
+                       size_t D, size_t E, cxg_stream_t stream);
+int cxg_kattn_rope_bwd(const float *Q, const float *K, const float *V, const float *O,
+                       const float *dO, const float *den_cache, const void *ctx, float *dQ,
+                       float *dK, float *dV, size_t B, size_t S, size_t D, size_t E,
+                       cxg_stream_t stream);
+
 /* ============ causal linear attention, linear_cuda API (phi outside) ==========
  * Inputs are feature-mapped already: Q_phi/K_phi (B*S, D), V/O (B*S, E).
  * State layout [d][e]; den_cache includes eps (den = phiQ.z + 1e-8).
