@@ -128,6 +128,41 @@ std::mutex g_scratch_map_mu;
 std::map<std::pair<int, hipStream_t>, std::unique_ptr<StreamScratch>> g_scratch_map;
 } // namespace
 
+// Three device words per (device, stream) for the backward's in-kernel
+// pre-pass (MhaIPrep::sync): allocated and zeroed at the first eligible call
+// on the stream, left zero by every launch, held until the process ends (a
+// graph captured on the stream keeps pointing at them).  Under stream capture
+// no new words are allocated (the call takes the separate pre-pass instead).
+namespace {
+std::mutex g_sync_mu;
+std::map<std::pair<int, hipStream_t>, unsigned*> g_sync_map;
+
+unsigned* stream_sync(hipStream_t s, bool create)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return nullptr;
+    std::lock_guard<std::mutex> lk(g_sync_mu);
+    auto it = g_sync_map.find(std::make_pair(dev, s));
+    if (it != g_sync_map.end())
+        return it->second;
+    if (!create)
+        return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, 256) != hipSuccess)
+        return nullptr;
+    if (hipMemset(p, 0, 256) != hipSuccess) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    g_sync_map[std::make_pair(dev, s)] = (unsigned*)p;
+    return (unsigned*)p;
+}
+} // namespace
+
 // Scratch for one call: caller memory if provided; else the stream's cached
 // buffer; under stream capture, stream-ordered memory for the duration of the
 // call (hipMallocAsync, which capture records as graph memory nodes).
@@ -347,11 +382,36 @@ static int mha_bwd_common(const float* Q, const float* K, const float* V, const 
                 return hip_status(e);
             lse = lse_ws;
         }
+        // Di and dQ = 0 inside the backward kernel where it can take them
+        unsigned* sync = rope == nullptr &&
+                                 mha_bwd_iprep_ok(iB, iS, iH, iD, Q, K, V, dO, O, dQ, dK, dV)
+                             ? stream_sync(s, true)
+                             : nullptr;
+        if (sync != nullptr) {
+            const MhaIPrep ip{O, sync};
+            return hip_status(mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH,
+                                                  iD, s, nullptr, &ip));
+        }
         e = mha_bwd_prep_launch(O, dO, Di, dQ, iB, iS, iH, iD, s);
         if (e != hipSuccess)
             return hip_status(e);
     }
     e = mha_bwd_main_launch(Q, K, V, dO, lse, Di, dQ, dK, dV, iB, iS, iH, iD, s, rope);
+    return hip_status(e);
+}
+
+int cxg_wait_timeouts(cxg_stream_t stream, unsigned* count)
+{
+    if (count == nullptr)
+        return CXG_ERR_NULL;
+    *count = 0;
+    hipStream_t s = (hipStream_t)stream;
+    unsigned* p = stream_sync(s, false);
+    if (p == nullptr)
+        return CXG_OK;
+    hipError_t e = hipStreamSynchronize(s);
+    if (e == hipSuccess)
+        e = hipMemcpy(count, p + 2, sizeof(unsigned), hipMemcpyDeviceToHost);
     return hip_status(e);
 }
 

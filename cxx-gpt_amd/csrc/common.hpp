@@ -237,6 +237,37 @@ __device__ __forceinline__ f4 buffer_load_f4(__amdgpu_buffer_rsrc_t r, unsigned 
     return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// Device-coherent accesses (cache policy sc1 on gfx950): a store is written
+// through to where every compute unit of the device reads it, and a load does
+// not take a copy that another XCD's L2 may have made stale.  Data shared
+// between workgroups inside one launch moves this way, so that no
+// device-scope fence (an L2-wide write-back or invalidate) is needed.
+constexpr int kCPolDevice = 16;
+
+__device__ __forceinline__ void buffer_store_f4_dev(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                    unsigned soff, f4 v)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, (int)voff, (int)soff,
+                                           kCPolDevice);
+}
+
+__device__ __forceinline__ void buffer_store_f32_dev(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                     unsigned soff, float v)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)voff,
+                                          (int)soff, kCPolDevice);
+}
+
+__device__ __forceinline__ float buffer_load_f32s_dev(__amdgpu_buffer_rsrc_t r, unsigned voff,
+                                                      unsigned soff)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff,
+                                                                          kCPolDevice));
+}
+
+// Wait until this wave's vector memory operations (loads and stores) are done.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Raw buffer over [base, base + bytes): reads at or past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_n(const float* base, unsigned bytes)
 {

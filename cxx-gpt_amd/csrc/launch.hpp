@@ -62,6 +62,23 @@ struct MhaRope {
     float w[128];
 };
 void mha_rope_freqs(int Dh, MhaRope* r);
+
+// The backward's pre-pass inside the backward kernel (mha_bwd_main_launch
+// with ip != nullptr, see mha_bwd_iprep_ok): each job forms Di = rowsum(O dO)
+// of the query tiles it visits from their O rows (ip.O), and the persistent
+// workgroups zero dQ for the query tiles they own before their first job,
+// post their arrival on sync[0] and, before their first atomic into another
+// workgroup's tile, wait for all arrivals.  sync: three device words, zero
+// before the launch and left zero after it (sync[1] counts departures and the
+// last one resets both); sync[2] counts waits that gave up (a workgroup that
+// never arrived), so the host can report them.
+struct MhaIPrep {
+    const float* O;
+    unsigned* sync;
+};
+bool mha_bwd_iprep_ok(int B, int S, int H, int Dh, const float* Q, const float* K,
+                      const float* V, const float* dO, const float* O, const float* dQ,
+                      const float* dK, const float* dV);
 hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float* O,
                           float* lse, int B, int S, int H, int Dh, hipStream_t st,
                           const MhaRope* rope = nullptr);
@@ -77,7 +94,8 @@ hipError_t mha_stats_prep_launch(const float* Q, const float* K, const float* V,
 hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V,
                                const float* dO, const float* lse, const float* Di,
                                float* dQ, float* dK, float* dV, int B, int S, int H, int Dh,
-                               hipStream_t st, const MhaRope* rope = nullptr);
+                               hipStream_t st, const MhaRope* rope = nullptr,
+                               const MhaIPrep* ip = nullptr);
 
 // Causal softmax attention for 256 < Dh <= 512 (same layout, lse and backward
 // contract as the launchers above; O may be null: statistics only).

@@ -689,15 +689,19 @@ struct BwdSmem {
 // descriptors over the head's rows 0..S-1 with scalar row offsets, and dQ
 // atomics through one whose range drops rows past S, so neither loads nor
 // atomics spend vector instructions on addresses or masks.
-template <int DHP, int BM, int NSPLIT, bool VEC, bool ROPE, bool BUF = false>
+template <int DHP, int BM, int NSPLIT, bool VEC, bool ROPE, bool BUF = false, bool IPREP = false>
 __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ Di,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
-    int BH, int nkb, float scale, float c2, const MhaRope rope)
+    int BH, int nkb, float scale, float c2, const MhaRope rope, const MhaIPrep ip)
 {
     using SM = BwdSmem<DHP, BM>;
     static_assert(!BUF || (VEC && SM::DB), "buffer loads need the double-buffered aligned path");
+    // The pre-pass inside the kernel: query tiles and key tiles coincide (a
+    // job's first query tile is its own key tile) and the grid is persistent.
+    static_assert(!IPREP || (BUF && BM == MHA_BN && NSPLIT == 2 && DHP == 64 && !ROPE),
+                  "in-kernel pre-pass: whole-width Dh = 64 heads, 64-row tiles");
     constexpr int NT = 256 * NSPLIT;
     constexpr int NW = NT / 64;
     constexpr int NDT = DHP / 16;
@@ -743,6 +747,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     // tile's lse and Di entries (lse is scaled by log2 e on its way to LDS).
     struct QTile {
         TileRegs<DHP, BM, NT, VEC> q, d;
+        TileRegs<DHP, BM, NT, VEC> o;   // in-kernel pre-pass: O rows, for the tile's Di
         float lse, di;
     };
     // BUF: bytes from a head's first element to the end of its row S-1
@@ -771,7 +776,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             const unsigned vo = (unsigned)((tid & (BM - 1)) * 4);
             const unsigned so = (unsigned)(((long)j.bh * S + q0) * 4);
             t.lse = buffer_load_f32s(buf_rsrc_n(lse, n), vo, so);
-            t.di = buffer_load_f32s(buf_rsrc_n(Di, n), vo, so);
+            if constexpr (!IPREP)   // in-kernel pre-pass: Di from the O and dO rows
+                t.di = buffer_load_f32s(buf_rsrc_n(Di, n), vo, so);
         } else {
             const long i = (long)j.bh * S + min(q0 + (tid & (BM - 1)), S - 1);
             t.lse = lse[i];
@@ -782,6 +788,13 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     // job prologue issues the same memory operations on every path and the
     // compiler's waits for its register stages stay tight.
     auto tile_q0 = [&](int qb) { return min(qb, nqb - 1) * BM; };
+    // In-kernel pre-pass: a tile's O rows, for its Di.  Requested one pipeline
+    // step after its Q and dO rows (once the other stage's O rows have been
+    // consumed), so that only one register stage holds O rows at a time.
+    auto load_o = [&](QTile& t, const Job& j, int q0) {
+        if constexpr (IPREP)
+            t.o.loadb(buf_rsrc_n(ip.O + j.base, head_bytes), qoffs, (unsigned)((long)q0 * rs * 4));
+    };
 
     // B operands for S = Q K^T and dP = dO V^T: K/V[key][16dt + 4g + r] for the
     // lane's key (zeroed past S and Dh at the start of the job); and the
@@ -813,6 +826,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     };
     auto load_first_q = [&](const Job& j) {
         load_q(t0, j, j.qb0 * BM);
+        load_o(t0, j, j.qb0 * BM);
         if (SM::DB)
             load_q(t1, j, tile_q0(j.qb0 + 1));
     };
@@ -820,6 +834,88 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     Job jc = job_of(snake_job(0));   // the grid never exceeds the job count
     load_kv(jc);
     load_first_q(jc);
+    // In-kernel pre-pass.  Every job forms the Di of each query tile it
+    // visits from the tile's O and dO rows (loaded with its Q rows).  The dQ
+    // rows are zeroed before any atomic reaches them: query tile t = qb*BH + bh
+    // (numbered like the jobs, so a workgroup's first job w starts on its own
+    // tile w) belongs to workgroup t mod G, which zeroes it before its first
+    // job, with device-coherent stores, and then posts its arrival; before its
+    // first atomic into a tile of another workgroup (after its first tile's
+    // key-side work), a workgroup waits until all have arrived.
+    if constexpr (IPREP) {
+        const int tid = threadIdx.x, u = tid & 15, rr = tid >> 4;
+        const int G = gridDim.x, ntiles = nqb * BH;
+        for (int t = blockIdx.x; t < ntiles; t += G) {
+            const int qb = t / BH, bh = t - qb * BH;
+            const int b = bh / H, h = bh - b * H;
+            const __amdgpu_buffer_rsrc_t rq =
+                buf_rsrc_n(dQ + (long)b * S * rs + (long)h * Dh, head_bytes);
+#pragma unroll
+            for (int k = 0; k < 2; k++) {   // thread: rows rr, rr + 32, columns 4u .. 4u+3
+                const long s0 = (long)qb * BM + rr + 32 * k;
+                // rows past S fall outside the descriptor and are dropped
+                buffer_store_f4_dev(rq, (unsigned)(min(s0, (long)S) * rs + 4 * u) * 4u, 0u,
+                                    f4zero());
+            }
+        }
+        // Arrival: every wave's device-coherent stores are complete before the
+        // count moves (no fence: a device-scope one writes back the whole L2;
+        // the dQ atomics are performed past the L2).
+        wait_vmem();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(ip.sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Wait until every workgroup has arrived (thread 0, bounded: a workgroup
+    // that never arrives is counted in sync[2] and the wait gives up).  A
+    // workgroup's first query tile is its own (zeroed by itself), so the wait
+    // comes before its second tile's dQ atomics; the count is requested after
+    // its first tile's key-side work (arrivals come within the first
+    // microseconds of the launch) and checked a tile later, so that the check
+    // rarely waits for a round trip.  phase: 0 before the first key side, 1
+    // count requested, 2 first query side done, 3 waited.
+    int phase = IPREP ? 0 : 3;
+    unsigned arrived = 0;
+    auto first_wait = [&]() {
+        if constexpr (IPREP) {
+            if (threadIdx.x == 0) {
+                const unsigned G = gridDim.x;
+                unsigned n = arrived;
+                for (int spin = 0; n < G && spin < (1 << 20); spin++) {
+                    __builtin_amdgcn_s_sleep(2);
+                    n = __hip_atomic_load(ip.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (n < G)
+                    __hip_atomic_fetch_add(ip.sync + 2, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+        }
+    };
+    auto after_key_side = [&]() {
+        if constexpr (IPREP) {
+            if (phase == 0) {
+                if (threadIdx.x == 0)
+                    arrived =
+                        __hip_atomic_load(ip.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                phase = 1;
+            }
+        }
+    };
+    auto before_query_side = [&]() {
+        if constexpr (IPREP) {
+            if (phase == 2) {
+                first_wait();
+                phase = 3;
+            }
+        }
+    };
+    auto after_query_side = [&]() {
+        if constexpr (IPREP) {
+            if (phase == 1)
+                phase = 2;
+        }
+    };
 #pragma nounroll
     for (int r = 0;; r++) {
         const int jn = snake_job(r + 1);
@@ -849,7 +945,24 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             t.d.template store<QS>(st + BM * QS, tid);
             if (tid < BM) {
                 st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
-                st[2 * BM * QS + BM * TS + BM + tid] = t.di * scale;   // scaled as dP is
+                if constexpr (!IPREP)
+                    st[2 * BM * QS + BM * TS + BM + tid] = t.di * scale;   // scaled as dP is
+            }
+            if constexpr (IPREP) {
+                // Di of rows tid/16 + 32i: a row's 16 units are the 16 lanes of a
+                // row group, summed in the separate pre-pass's order
+                // (mha_bwd_prep_vec_kernel), so both paths give the same Di
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const f4 o = t.o.r[i], d = t.d.r[i];
+                    float di = o[0] * d[0] + o[1] * d[1] + o[2] * d[2] + o[3] * d[3];
+                    di += lane_xor16<1>(di);
+                    di += lane_xor16<2>(di);
+                    di += lane_xor16<4>(di);
+                    di += lane_xor16<8>(di);
+                    if ((tid & 15) == 0)
+                        st[2 * BM * QS + BM * TS + BM + (tid >> 4) + 32 * i] = di * scale;
+                }
             }
         };
         // S = Q K^T and dP = dO V^T for this wave's query blocks (lane holds key
@@ -1085,29 +1198,34 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             // the wait for its registers.
             store_q(t0, stage(qb0 & 1), qb0 * BM);
             load_q(t0, jc, tile_q0(qb0 + 2));
+            load_o(t1, jc, tile_q0(qb0 + 1));
             __syncthreads();
             // Iteration qb < nqb-1: registers tx hold tile qb+1 and are
-            // refilled with qb+3.
-            auto step = [&](QTile& tx, int qb) {
+            // refilled with qb+3; ty hold tile qb+2 (its O rows requested here).
+            auto step = [&](QTile& tx, QTile& ty, int qb) {
                 const int q0 = qb * BM;
                 float* cur = stage(qb & 1);
                 key_side(cur, q0);
+                after_key_side();
                 store_q(tx, stage((qb + 1) & 1), (qb + 1) * BM);
                 // Keep the refill below the LDS writes: issued earlier, the
                 // wait for the old data would include the new loads.
                 __builtin_amdgcn_sched_barrier(0);
                 if (qb + 3 < nqb)
                     load_q(tx, jc, q0 + 3 * BM);
+                load_o(ty, jc, tile_q0(qb + 2));
                 __syncthreads();
+                before_query_side();
                 query_side(cur, q0);
+                after_query_side();
             };
             int qb = qb0;
             for (; qb + 2 < nqb; qb += 2) {
-                step(t1, qb);
-                step(t0, qb + 1);
+                step(t1, t0, qb);
+                step(t0, t1, qb + 1);
             }
             if (qb + 1 < nqb)
-                step(t1, qb++);
+                step(t1, t0, qb++);
             // The last query tile: once its key-side work is issued the next
             // job's K/V rows and first query tiles are requested (all register
             // stages are free by then), ahead of this tile's dQ atomics.
@@ -1115,6 +1233,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 const int q0 = qb * BM;
                 float* cur = stage(qb & 1);
                 key_side(cur, q0);
+                after_key_side();
                 // Not above the key-side work: the loads overwrite its operands.
                 __builtin_amdgcn_sched_barrier(0);
                 if (more) {
@@ -1122,7 +1241,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     load_first_q(jnext);
                 }
                 __syncthreads();
+                before_query_side();
                 query_side(cur, q0);
+                after_query_side();
             }
         } else {
             constexpr bool PREFETCH = DHP <= 128;
@@ -1191,6 +1312,16 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             break;
         jc = jnext;
         __syncthreads();   // the reduction records and K^T tile are consumed
+    }
+    // In-kernel pre-pass: the last workgroup to finish resets the counters
+    // for the next launch (every workgroup has passed its wait by now).
+    if constexpr (IPREP) {
+        if (threadIdx.x == 0 &&
+            __hip_atomic_fetch_add(ip.sync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                gridDim.x - 1) {
+            __hip_atomic_store(ip.sync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ip.sync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -1483,19 +1614,13 @@ hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float
     return hipGetLastError();
 }
 
+// Resident backward workgroups per compute unit for the persistent grid: what
+// the kernel's registers and LDS allow (two for Dh <= 16, one above), found
+// once; jobs are claimed by index, so any grid size is correct.
 template <int DHP, bool ROPE>
-static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, const float* dO,
-                               const float* lse, const float* Di, float* dQ, float* dK,
-                               float* dV, int B, int S, int H, int Dh, hipStream_t st,
-                               const MhaRope& rope)
+static int bwd_per_cu()
 {
     constexpr int NS = MhaSplits<DHP>::BWD, BM = MhaSplits<DHP>::BWD_BM;
-    const int BH = B * H;
-    const int nkb = (S + MHA_BN - 1) / MHA_BN;
-    const float scale = 1.0f / sqrtf((float)Dh);
-    // Resident workgroups per compute unit for the persistent grid: what the
-    // kernel's registers and LDS allow (two for Dh <= 16, one above), found
-    // once; jobs are claimed by index, so any grid size is correct.
     static int per_cu = 0;
     if (per_cu <= 0) {
         int n = 0;
@@ -1506,39 +1631,95 @@ static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, c
             n = MhaSplits<DHP>::BWD_PER_CU;
         per_cu = n;
     }
+    return per_cu;
+}
+
+// Byte offsets within a head's S rows fit 31 bits (the buffer-descriptor path).
+static bool bwd_buf_ok(int S, int H, int Dh) { return (long)S * H * Dh * 4 < (1L << 31); }
+
+template <int DHP, bool ROPE>
+static hipError_t bwd_dispatch(const float* Q, const float* K, const float* V, const float* dO,
+                               const float* lse, const float* Di, float* dQ, float* dK,
+                               float* dV, int B, int S, int H, int Dh, hipStream_t st,
+                               const MhaRope& rope, const MhaIPrep* ip)
+{
+    constexpr int NS = MhaSplits<DHP>::BWD, BM = MhaSplits<DHP>::BWD_BM;
+    const int BH = B * H;
+    const int nkb = (S + MHA_BN - 1) / MHA_BN;
+    const float scale = 1.0f / sqrtf((float)Dh);
+    const int per_cu = bwd_per_cu<DHP, ROPE>();
     dim3 grid(job_grid((long)nkb * BH, per_cu, true)), block(256 * NS);
     const bool vec = (Dh % 4 == 0) && aligned16(Q) && aligned16(K) && aligned16(V) &&
                      aligned16(dO) && aligned16(dK) && aligned16(dV);
+    const MhaIPrep noip{};
     ProfScope ps(st, ROPE ? "mha_rope_bwd" : "mha_bwd");
     // Whole-width heads on the double-buffered path take buffer loads and
     // atomics (byte offsets within a head's S rows must fit 31 bits).
     if constexpr (BwdSmem<DHP, BM>::DB) {
-        if (vec && Dh == DHP && aligned16(dQ) && (long)S * H * Dh * 4 < (1L << 31)) {
+        if (vec && Dh == DHP && aligned16(dQ) && bwd_buf_ok(S, H, Dh)) {
+            if constexpr (DHP == 64 && !ROPE) {
+                if (ip != nullptr) {   // the caller checked mha_bwd_iprep_ok
+                    CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE, true, true>), grid, block,
+                               0, st, Q, K, V, dO, lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale,
+                               scale * kLog2e, rope, *ip);
+                    return hipGetLastError();
+                }
+            }
             CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE, true>), grid, block, 0, st, Q, K,
-                       V, dO, lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
+                       V, dO, lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope,
+                       noip);
             return hipGetLastError();
         }
     }
+    if (ip != nullptr)
+        return hipErrorInvalidValue;
     if (vec)
         CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, true, ROPE>), grid, block, 0, st, Q, K, V, dO,
-                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope,
+                           noip);
     else
         CXG_LAUNCH((mha_bwd_kernel<DHP, BM, NS, false, ROPE>), grid, block, 0, st, Q, K, V, dO,
-                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope);
+                           lse, Di, dQ, dK, dV, S, H, Dh, BH, nkb, scale, scale * kLog2e, rope,
+                           noip);
     return hipGetLastError();
+}
+
+// The in-kernel pre-pass (MhaIPrep) applies to whole-width Dh = 64 heads on
+// the buffer-descriptor path whose grid is persistent (every workgroup
+// resident at once, so the wait for all arrivals ends), for sequences of up
+// to 8 query tiles: each job forms the Di of every tile it visits, which pays
+// where a tile has few visitors and the separate pre-pass's launch is a large
+// share of the step (C2: 49.7 -> 48.5 us a step), and costs more than that
+// pass at long sequences (C5, 64 tiles: 1.48 -> 1.52 ms).
+bool mha_bwd_iprep_ok(int B, int S, int H, int Dh, const float* Q, const float* K,
+                      const float* V, const float* dO, const float* O, const float* dQ,
+                      const float* dK, const float* dV)
+{
+    if (Dh != 64 || S > 8 * MHA_BN || !bwd_buf_ok(S, H, Dh))
+        return false;
+    if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(dO) || !aligned16(O) ||
+        !aligned16(dQ) || !aligned16(dK) || !aligned16(dV))
+        return false;
+    const long njobs = (long)((S + MHA_BN - 1) / MHA_BN) * B * H;
+    const long slots = (long)device_cus() * bwd_per_cu<64, false>();
+    return (long)job_grid(njobs, bwd_per_cu<64, false>(), true) <= slots;
 }
 
 hipError_t mha_bwd_main_launch(const float* Q, const float* K, const float* V, const float* dO,
                                const float* lse, const float* Di, float* dQ, float* dK,
                                float* dV, int B, int S, int H, int Dh, hipStream_t st,
-                               const MhaRope* rope)
+                               const MhaRope* rope, const MhaIPrep* ip)
 {
     const MhaRope none{};
     const MhaRope& rp = rope != nullptr ? *rope : none;
+    if (ip != nullptr && (rope != nullptr || Dh != 64))
+        return hipErrorInvalidValue;
 #define CXG_BWD(D)                                                                            \
     return rope != nullptr                                                                    \
-               ? bwd_dispatch<D, true>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp)  \
-               : bwd_dispatch<D, false>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp)
+               ? bwd_dispatch<D, true>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp,  \
+                                       nullptr)                                               \
+               : bwd_dispatch<D, false>(Q, K, V, dO, lse, Di, dQ, dK, dV, B, S, H, Dh, st, rp, \
+                                        ip)
     if (Dh <= 16)
         CXG_BWD(16);
     if (Dh <= 32)

@@ -29,6 +29,7 @@ SIGNATURES = {
     "cxg_last_hip_error": [],
     "cxg_version": [],
     "cxg_release_scratch": [_vp],
+    "cxg_wait_timeouts": [_vp, ctypes.POINTER(ctypes.c_uint)],
     "cxg_mha_fwd": [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp],
     "cxg_mha_bwd": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp, _sz,
                     _vp],
@@ -185,6 +186,13 @@ def mha_bwd_workspace_size(B, S, H, Dh):
 
 
 # ------------------------------------------------------------------ GPT's attention (H = 1)
+def wait_timeouts(stream=None):
+    """Count of the backward's in-kernel waits that gave up on this stream (0 normally)."""
+    n = ctypes.c_uint(0)
+    _call("cxg_wait_timeouts", _stream(stream), ctypes.byref(n))
+    return n.value
+
+
 def release_scratch(stream=None):
     """Free the library's cached scratch buffer of (current device, stream)."""
     _call("cxg_release_scratch", _stream(stream))

@@ -84,6 +84,18 @@ int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
                 const float *dO, const float *lse, float *dQ, float *dK, float *dV,
                 size_t B, size_t S, size_t H, size_t Dh, void *workspace,
                 size_t workspace_bytes, cxg_stream_t stream);
+
+/* Waits inside cxg_mha_bwd that gave up (0 normally).  With lse, head_dim 64
+ * and 16-byte aligned tensors, the backward kernel forms Di = rowsum(O dO)
+ * and zeroes dQ itself: each of its workgroups (one per compute unit or
+ * fewer, all resident at once) does so for the query tiles it owns, then,
+ * before it reads another's, waits until all have done theirs.  That wait is
+ * bounded (about half a second); a wait that gives up is counted per
+ * (device, stream), and the backward results of that call are then not
+ * reliable.  *count receives the stream's count (it waits for the stream's
+ * work first).  Without such calls on the stream the count is 0.  No
+ * counterpart in the reference. */
+int cxg_wait_timeouts(cxg_stream_t stream, unsigned *count);
 size_t cxg_mha_bwd_workspace_size(size_t B, size_t S, size_t H, size_t Dh);
 
 /* Allocation-free cxg_mha_bwd.  No counterpart in the reference: for callers

@@ -228,3 +228,33 @@ def test_reference_signature_backward(dev, B, S, H, Dh):
     for name, a, b, r in zip(("dQ", "dK", "dV"), legacy, with_lse, ref):
         assert_close(a, r, f"no-lse {name}")
         assert_close(a, b, f"no-lse vs lse {name}", atol=2e-6, rtol=2e-5)
+
+
+@pytest.mark.parametrize("B,S,H", [
+    (8, 256, 12),    # C2: 384 jobs, 256 persistent workgroups (second round)
+    (1, 64, 3),      # three one-tile jobs
+    (2, 300, 5),     # ragged last tile, 50 jobs
+    (4, 1000, 16),   # 1024 jobs: four rounds on the persistent grid
+])
+def test_backward_in_kernel_prepass(dev, B, S, H):
+    """With lse and Dh = 64 the backward kernel forms Di and zeroes dQ itself
+    (its workgroups each own some query tiles and wait, once, until every
+    workgroup has done its part).  Several calls in a row on the same inputs
+    and outputs (dQ holds the previous call's result, so a missed zeroing
+    would double it; the arrival counters must reset after every launch),
+    checked against the oracle, and no wait may have given up."""
+    import torch
+    import cxxgpt_attn as cx
+    Dh = 64
+    Q, K, V, dO = normal_inputs((B * S, H * Dh), (B * S, H * Dh), 900 + S + H)
+    O, lse = _run_fwd(dev, Q, K, V, B, S, H, Dh, want_lse=True)
+    rQ, rK, rV = orc.mha_bwd(Q, K, V, O, dO, B, S, H, Dh, nthreads=8)
+    ts = [_t(a, dev) for a in (Q, K, V, O, dO)]
+    tl = _t(lse, dev)
+    outs = [torch.full_like(ts[0], float("nan")) for _ in range(3)]
+    for it in range(3):
+        cx.mha_bwd(*ts, *outs, B, S, H, Dh, lse=tl)
+        torch.cuda.synchronize()
+        for name, g, r in zip(("dQ", "dK", "dV"), outs, (rQ, rK, rV)):
+            assert_close(g.cpu().numpy(), r, f"in-kernel pre-pass B{B}S{S}H{H} call {it} {name}")
+    assert cx.wait_timeouts() == 0
