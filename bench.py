@@ -206,7 +206,8 @@ def attribute(cx, step, steps):
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
-              "lin_wide_state",
+              "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
+              "lin_qs_grad",
               "phi_hexp_fwd", "phi_hexp_bwd", "lin_rope_feat",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",
@@ -542,7 +543,27 @@ def lin_wide_flops(Bq, S, D, E):
     recomputed there, not credited)."""
     P = S * (S + 1) // 2
     f = 2 * P * (D + E) * Bq
-    return {"lin_wide_fwd": f, "lin_wide_dq": f, "lin_wide_dkdv": f, "lin_wide_bwd": 2 * f}
+    # per step: the one-workgroup-per-block kernels (one launch of each a step),
+    # and the block-score kernels, whose credit is summed over a step's launches
+    # (forward: scores A, products A V; backward: X = dnum V^T in the score
+    # launches, the three gradient products in the product launches)
+    return {"lin_wide_fwd": f, "lin_wide_dq": f, "lin_wide_dkdv": f, "lin_wide_bwd": 2 * f,
+            "lin_qs_score": 2 * P * D * Bq, "lin_qs_out": 2 * P * E * Bq,
+            "lin_qs_bscore": 2 * P * E * Bq, "lin_qs_grad": (4 * P * D + 2 * P * E) * Bq}
+
+
+def wide_roofline(c, name, att, kf):
+    """MFMA roofline of the quadratic form's dominant kernel tag (most time per
+    step): its credited FLOPs per step over its time per step."""
+    dom = max((k for k in att if k in kf), key=lambda k: att[k][0] * att[k][1])
+    per_step_ms = att[dom][0] * att[dom][1]
+    ach = kf[dom] / (per_step_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": c.traffic.get(f"{name}/{dom}"),
+            "flops_per_launch": int(round(kf[dom] / att[dom][1])),
+            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()},
+            "launches_per_step": {k: round(v[1], 2) for k, v in att.items() if v[1] != 1}}
 
 
 def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
@@ -588,14 +609,8 @@ def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
     total = lin_bytes(Bq, S, D)
     value = total / (ms * 1e-3) / 1e9
     kf = lin_wide_flops(Bq, S, D, E)
-    dom = max((k for k in att if k in kf), key=lambda k: att[k][0])
-    ach = kf[dom] / (att[dom][0] * 1e-3) / 1e12
+    roof = wide_roofline(c, name, att, kf)
     step_flops = 3 * kf["lin_wide_fwd"]
-    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
-            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": c.traffic.get(f"{name}/{dom}"),
-            "flops_per_launch": kf[dom],
-            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="GB/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: ELU+1 linear attention fwd+bwd, wide heads "
                                     f"(quadratic form), {desc}",
@@ -641,14 +656,7 @@ def _kattn_rope(c, name, Bq, S, D, seed, steps, warmup, fused):
     value = total / (ms * 1e-3) / 1e9
     kt = {k: round(v[0], 5) for k, v in att.items()}
     if D > 64 or S <= 128:   # the quadratic form: MFMA-bound
-        kf = lin_wide_flops(Bq, S, D, E)
-        dom = max((k for k in att if k in kf), key=lambda k: att[k][0])
-        ach = kf[dom] / (att[dom][0] * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
-                "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
-                "traffic": c.traffic.get(f"{name}/{dom}"), "flops_per_launch": kf[dom],
-                "kernel_ms": kt}
+        roof = wide_roofline(c, name, att, lin_wide_flops(Bq, S, D, E))
     else:
         kb = lin_kernel_bytes(Bq, S, D, True)
         dom = max((k for k in att if k in kb), key=lambda k: att[k][0])

@@ -957,8 +957,9 @@ int cxg_kattn_rope_bwd(const float* Q, const float* K, const float* V, const flo
     const size_t t = round_up(B * S * D * sizeof(float), 256);
     if (lin_quad_ok((int)D, (int)E, (long)S)) {
         const size_t N = B * S, tn = round_up(N * E * sizeof(float), 256);
+        const size_t tq = lin_wide_bwd_ws_bytes((int)B, (int)S, (int)D, (int)E, 3);
         Scratch ws;
-        st = ws.acquire(nullptr, 0, 2 * t + tn + round_up(N * sizeof(float), 256), s);
+        st = ws.acquire(nullptr, 0, 2 * t + tn + round_up(N * sizeof(float), 256) + tq, s);
         if (st != CXG_OK)
             return st;
         float* fq = (float*)ws.p;
@@ -969,8 +970,10 @@ int cxg_kattn_rope_bwd(const float* Q, const float* K, const float* V, const flo
         if (e == hipSuccess)
             e = lin_step1_launch(O, dO, den_cache, dnum, dden, (long)N, (int)E, s);
         if (e == hipSuccess)
-            e = lin_wide_bwd_launch(PHI_ELU1_ROPE, fq, fk, V, dnum, dden, dQ, dK, dV, (int)B,
-                                    (int)S, (int)D, (int)E, 3, s, Q, K);
+            e = lin_wide_bwd_launch(
+                PHI_ELU1_ROPE, fq, fk, V, dnum, dden, dQ, dK, dV, (int)B, (int)S, (int)D, (int)E,
+                3, s, Q, K,
+                tq ? (char*)ws.p + 2 * t + tn + round_up(N * sizeof(float), 256) : nullptr);
         return hip_status(e);
     }
     Scratch ws;

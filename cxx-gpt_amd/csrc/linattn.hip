@@ -1377,7 +1377,7 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 {
     LinPlan p;
     p.pass = pass;
-    p.quad = lin_quad_ok(D, E, S);
+    p.quad = lin_quad_any(Bq, S, D, E);
     p.fast = !p.quad && (D <= 64 && E <= 64);
     p.nseg = 1;
     p.L = S;
@@ -1404,8 +1404,11 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
 
 size_t lin_ws_bytes(const LinPlan& p, int Bq, int D, int E)
 {
-    if (p.quad)   // the forward's key parts (p.L = S)
-        return p.pass == LIN_PASS_FWD ? lin_wide_ws_bytes(Bq, p.L, D, E) : 0;
+    if (p.quad)   // the forward's key parts or score blocks (p.L = S)
+        return p.pass == LIN_PASS_FWD    ? lin_wide_ws_bytes(Bq, p.L, D, E)
+               : p.pass == LIN_PASS_DQ   ? lin_wide_bwd_ws_bytes(Bq, p.L, D, E, 2)
+               : p.pass == LIN_PASS_DKDV ? lin_wide_bwd_ws_bytes(Bq, p.L, D, E, 1)
+                                         : lin_wide_bwd_ws_bytes(Bq, p.L, D, E, 3);
     if (!p.fast)
         return (size_t)Bq * D * E * sizeof(float);
     if (p.nseg <= 1)
@@ -1567,7 +1570,7 @@ static hipError_t dq_impl(const float* K, const float* V, const float* dnum, con
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DQ);
     if (p.quad)   // the quadratic form needs no z_cache
         return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, dQ, nullptr, nullptr, Bq, S, D, E, 2,
-                                   st);
+                                   st, nullptr, nullptr, ws);
     if (!p.fast) {
         ProfScope ps(st, "lin_dq_generic");
         CXG_LAUNCH((lin_dq_generic_kernel<PHI>), dim3(Bq), dim3(256), 0, st, K, V, dnum,
@@ -1617,7 +1620,8 @@ static hipError_t dkdv_impl(const float* Q, const float* K, const float* V, cons
 {
     const LinPlan p = lin_plan(Bq, S, D, E, LIN_PASS_DKDV);
     if (p.quad)
-        return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, nullptr, dK, dV, Bq, S, D, E, 1, st);
+        return lin_wide_bwd_launch(PHI, Q, K, V, dnum, dden, nullptr, dK, dV, Bq, S, D, E, 1, st,
+                                   nullptr, nullptr, ws);
     if (!p.fast) {
         ProfScope ps(st, "lin_dkdv_generic");
         CXG_LAUNCH((lin_dkdv_generic_kernel<PHI>), dim3(Bq), dim3(256),
@@ -1669,8 +1673,8 @@ static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E)
 {
     const size_t N = (size_t)Bq * S;
-    if (lin_quad_ok(D, E, S))   // dnum and dden only
-        return al256(N * E * 4) + al256(N * 4);
+    if (lin_quad_any(Bq, S, D, E))   // dnum, dden and the quadratic form's scratch
+        return al256(N * E * 4) + al256(N * 4) + lin_wide_bwd_ws_bytes(Bq, S, D, E, 3);
     const size_t a = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DQ), Bq, D, E);
     const size_t b = lin_ws_bytes(lin_plan(Bq, S, D, E, LIN_PASS_DKDV), Bq, D, E);
     return al256(N * D * 4) + al256(N * E * 4) + al256(N * 4) + (a > b ? a : b);
@@ -1683,14 +1687,16 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
 {
     const size_t N = (size_t)Bq * S;
     char* p = (char*)ws;
-    if (lin_quad_ok(D, E, S)) {
-        // step 1, then every gradient from one launch of the quadratic-form
-        // backward
+    if (lin_quad_any(Bq, S, D, E)) {
+        // step 1, then every gradient from the quadratic-form backward
         float* dnum = (float*)p;
         float* dden = (float*)(p + al256(N * E * 4));
+        char* qws = p + al256(N * E * 4) + al256(N * 4);
         hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);
         if (e == hipSuccess)
-            e = lin_wide_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, st);
+            e = lin_wide_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, st,
+                                    nullptr, nullptr,
+                                    lin_wide_bwd_ws_bytes(Bq, S, D, E, 3) ? qws : nullptr);
         return e;
     }
     float* zc = (float*)p;

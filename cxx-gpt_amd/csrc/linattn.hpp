@@ -156,10 +156,30 @@ size_t lin_wide_ws_bytes(int Bq, int S, int D, int E);
 hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                                float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
                                void* ws, hipStream_t st);
+// ws: lin_wide_bwd_ws_bytes(.., kinds) of scratch, or null (then only widths
+// up to LIN_WIDE_MAX, through the one-workgroup-per-block kernels).
+size_t lin_wide_bwd_ws_bytes(int Bq, int S, int D, int E, int kinds);
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                                const float* dnum, const float* dden, float* dQ, float* dK,
                                float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st,
-                               const float* Qx = nullptr, const float* Kx = nullptr);
+                               const float* Qx = nullptr, const float* Kx = nullptr,
+                               void* ws = nullptr);
+// The quadratic form through block score matrices in scratch (linquad.hip):
+// widths multiples of 16, any size, while the scratch (lin_qs_bytes; kinds
+// 0 = forward, else as lin_wide_bwd_launch) stays within the path's budget.
+// The wide launchers take it whenever they are given the scratch.
+bool lin_qs_ok(int Bq, int S, int D, int E);
+size_t lin_qs_bytes(int Bq, int S, int D, int E, int kinds);
+hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
+                             float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
+                             void* ws, hipStream_t st);
+hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const float* V,
+                             const float* dnum, const float* dden, float* dQ, float* dK,
+                             float* dV, int Bq, int S, int D, int E, int kinds, void* ws,
+                             hipStream_t st, const float* Qx, const float* Kx);
+// The quadratic form for any width: lin_quad_ok, or widths above LIN_WIDE_MAX
+// when lin_qs_ok.
+bool lin_quad_any(int Bq, int S, int D, int E);
 // The RoPE map's features for the quadratic form: Fq = phi(rot(Q)), Fk =
 // phi(rot(K)) (B' x S rows of width D, D even, D <= LIN_ROPE_MAX_D).  The
 // forward then runs with PHI_NONE on them; the backward (lin_wide_bwd_launch

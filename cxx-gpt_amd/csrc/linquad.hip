@@ -1,0 +1,644 @@
+// linquad.hip -- causal linear attention in the quadratic form with the block
+// score matrices in scratch memory (gfx950, FP32 MFMA).
+//
+// Same algebra as linwide.hip (per sequence, 16-row blocks i, j):
+//   A[t][s] = phi(Q_t) . phi(K_s)            (s <= t)
+//   den_t = sum_s A[t][s],   O_t = (sum_s A[t][s] V_s) / (den_t + 1e-8)
+//   G[t][s] = dnum_t . V_s + dden_t          (s <= t)
+//   dQ_t = (sum_s G[t][s] phi(K_s)) * phi'(Q_t)
+//   dK_s = (sum_t G[t][s] phi(Q_t)) * phi'(K_s)
+//   dV_s = sum_t A[t][s] dnum_t
+// the forms two_stage_cuda::kernel_attn_fwd / _bwd_dQ / _bwd_dKdV
+// (src/TwoStage/two_stage_cuda_kernels.cu:988-1809) and
+// linear_cuda::causal_linear_attention_fwd / _bwd_dQ / _bwd_dKdV
+// (src/LinearAttention/linear_cuda_kernels.cu:10-298) compute with a running
+// state.  linwide.hip gives each 16-row block to one workgroup that streams
+// every other block of its sequence through LDS: at LinearGPT's shape (8
+// sequences of 256 rows, D = E = 512) 256 jobs for 256 compute units whose 16
+// block steps run one after another.  Here the work is cut into small
+// independent jobs instead:
+//   0. features Fq = phi(Q), Fk = phi(K) into scratch (ELU+1 maps; PHI_NONE
+//      reads Q and K as they are; the RoPE map's callers pass its features);
+//   1. scores: one workgroup per (sequence, pair of 32-row tiles) forms the
+//      16x16 blocks A_ij and/or G_ij (j <= i), masked to s <= t, into scratch,
+//      the rows staged through LDS a 32-column chunk at a time;
+//   2. products: one wave per (sequence, block, 64-column slice of one
+//      output) -- O and z_cache over the query blocks' keys, dQ likewise, dK
+//      and dV over the key blocks' queries -- then the epilogue (1/(den +
+//      1e-8), or phi' and the RoPE map's inverse rotation).
+// Every job owns its outputs: no atomics, no ordering between workgroups.
+// Scratch: B' * nb(nb+1)/2 blocks of 256 floats per score matrix (nb =
+// ceil(S/16)) and the features; the path is taken when that fits
+// kQsBudget.
+#include "common.hpp"
+#include "launch.hpp"
+#include "linattn.hpp"
+#include "linattn_dev.hpp"
+
+#include <algorithm>
+
+namespace cxg {
+
+constexpr size_t kQsBudget = (size_t)512 << 20;   // bytes of scratch the path may take
+
+enum { QS_O = 0, QS_Z = 1, QS_DQ = 2, QS_DK = 3, QS_DV = 4 };
+
+struct QsArgs {
+    const float* Fq;     // phi(Q) (or Q / the RoPE features)
+    const float* Fk;     // phi(K)
+    const float* V;
+    const float* dnum;
+    const float* dden;
+    float* Ab;           // score blocks: [seq][pair][16 * 16], pair = i(i+1)/2 + j
+    float* Gb;
+    float* O;
+    float* den;
+    float* zc;
+    float* dQ;
+    float* dK;
+    float* dV;
+    const float* Qx;     // raw inputs for phi'
+    const float* Kx;
+    int S, D, E, Bq, nb, npairs;
+    int ntp;             // pairs of 32-row tiles per sequence
+    int den_eps;
+    int units;           // product units (output slices) per (sequence, block)
+    int nslD, nslE;      // 64-column slices of the widths
+    int kinds;           // backward: 1 = dK, dV; 2 = dQ; 3 = both
+};
+
+__host__ __device__ inline int qs_slices(int W) { return (W + 63) / 64; }
+
+// Raw buffer over a sequence's rows of width W: reads past the last row return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qs_rows(const float* X, long rb, int S, int W)
+{
+    return buf_rsrc_n(X + rb * W, (unsigned)((long)S * W * 4));
+}
+
+// Workgroup b's job among B' sequences of n jobs each (jobs numbered in the
+// order they should start).  The dispatcher places workgroup b on XCD b % 8,
+// and each XCD has its own L2: spread over all eight, every XCD would fetch
+// nearly every row of every sequence.  So each XCD gets whole sequences
+// (B' >= 8: sequences [x B'/8, (x+1) B'/8), their jobs interleaved in job
+// order) or, with fewer sequences than XCDs, a share of one sequence (sequence
+// floor(x B'/8), every m-th of its jobs, m = its XCD count).  False for the
+// grid's spare slots (qs_grid rounds up).
+__device__ __forceinline__ bool qs_xcd_job(int b, int Bq, int n, int& seq, int& job)
+{
+    const int x = b & 7, k = b >> 3;
+    if (Bq >= 8) {
+        const int s0 = x * Bq / 8, ns = (x + 1) * Bq / 8 - s0;
+        job = k / ns;
+        seq = s0 + k % ns;
+        return job < n;
+    }
+    seq = x * Bq / 8;
+    const int x0 = (8 * seq + Bq - 1) / Bq, x1 = (8 * (seq + 1) + Bq - 1) / Bq;
+    job = (x - x0) + k * (x1 - x0);
+    return job < n;
+}
+
+// ---------------------------------------------------------------------------
+// phase 0: features (ELU+1 maps)
+// ---------------------------------------------------------------------------
+template <int PHI>
+__global__ __launch_bounds__(256) void lin_qs_feat_kernel(const f4* __restrict__ Q,
+                                                          const f4* __restrict__ K,
+                                                          f4* __restrict__ Fq, f4* __restrict__ Fk,
+                                                          long n4)
+{
+    // Q null: phi(K) only
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n4; i += (long)gridDim.x * 256) {
+        f4 k = K[i];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            k[r] = Phi<PHI>::f(k[r]);
+        Fk[i] = k;
+        if (Q != nullptr) {
+            f4 q = Q[i];
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                q[r] = Phi<PHI>::f(q[r]);
+            Fq[i] = q;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// phase 1: score blocks.  Workgroup = (sequence, pair of 32-row tiles J <= I);
+// wave w forms block (2I + w/2, 2J + w%2) of it (blocks above the diagonal are
+// formed and dropped).  The contraction runs in 32-column chunks staged in
+// LDS by whole 128-byte rows (thread t: row t/8, columns 4(t%8)..+3 of the
+// chunk), double-buffered, one barrier a chunk; a wave reads its operands
+// from LDS as 16-byte pieces, lane (l16, g) taking row l16 of its block at
+// columns 16h + 4g .. +3, the same k order for both operands, in two
+// accumulation chains (h = 0, 1).  MODE: 1 = A, 2 = G, 3 = both.  Lane
+// (l16, g), element r of a block <-> [t = 4g + r][s = l16].
+// ---------------------------------------------------------------------------
+constexpr int QS_TR = 32;            // score tile rows
+constexpr int QS_KC = 32;            // contraction chunk (columns)
+constexpr int QS_LD = QS_KC + 4;     // LDS row stride
+
+__device__ __forceinline__ f4 qs_tile_dot(float (*xs)[2][QS_TR * QS_LD], const float* X1,
+                                          const float* X2, long rb, int S, int W, int I, int J,
+                                          int tid, int bi, int bj, int l16, int g)
+{
+    const __amdgpu_buffer_rsrc_t b1 = qs_rows(X1, rb, S, W), b2 = qs_rows(X2, rb, S, W);
+    const int sr = tid >> 3, sc = 4 * (tid & 7);
+    const unsigned o1 = (unsigned)(((QS_TR * I + sr) * W + sc) * 4);
+    const unsigned o2 = (unsigned)(((QS_TR * J + sr) * W + sc) * 4);
+    const int nch = (W + QS_KC - 1) / QS_KC;
+    auto fetch = [&](int c, f4& r1, f4& r2) __attribute__((always_inline)) {
+        const bool ok = QS_KC * c + sc < W;   // W % 16 == 0: a chunk's 16-col halves
+        const f4 v1 = buffer_load_f4(b1, o1 + (unsigned)(4 * QS_KC * c));
+        const f4 v2 = buffer_load_f4(b2, o2 + (unsigned)(4 * QS_KC * c));
+        r1 = ok ? v1 : f4zero();
+        r2 = ok ? v2 : f4zero();
+    };
+    f4 r1, r2;
+    fetch(0, r1, r2);
+    f4 c0 = f4zero(), c1 = f4zero();
+    for (int c = 0; c < nch; c++) {
+        float* s1 = xs[c & 1][0];
+        float* s2 = xs[c & 1][1];
+        *reinterpret_cast<f4*>(&s1[sr * QS_LD + sc]) = r1;
+        *reinterpret_cast<f4*>(&s2[sr * QS_LD + sc]) = r2;
+        if (c + 1 < nch)
+            fetch(c + 1, r1, r2);
+        __syncthreads();
+        const float* pa = &s1[(16 * bi + l16) * QS_LD + 4 * g];
+        const float* pb = &s2[(16 * bj + l16) * QS_LD + 4 * g];
+        const f4 a0 = *reinterpret_cast<const f4*>(pa), a1 = *reinterpret_cast<const f4*>(pa + 16);
+        const f4 e0 = *reinterpret_cast<const f4*>(pb), e1 = *reinterpret_cast<const f4*>(pb + 16);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            c0 = mfma16(a0[r], e0[r], c0);
+            c1 = mfma16(a1[r], e1[r], c1);
+        }
+    }
+    return c0 + c1;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void lin_qs_score_kernel(const QsArgs a)
+{
+    __shared__ __attribute__((aligned(16))) float xs[2][2][QS_TR * QS_LD];
+    int seq, tp;
+    if (!qs_xcd_job((int)blockIdx.x, a.Bq, a.ntp, seq, tp))
+        return;   // the whole workgroup
+    // tp = I(I+1)/2 + J
+    int I = (int)((sqrtf(8.0f * (float)tp + 1.0f) - 1.0f) * 0.5f);
+    while ((I + 1) * (I + 2) / 2 <= tp)
+        I++;
+    while (I * (I + 1) / 2 > tp)
+        I--;
+    const int J = tp - I * (I + 1) / 2;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int bi = w >> 1, bj = w & 1;
+    const int i = 2 * I + bi, j = 2 * J + bj;
+    const long rb = (long)seq * a.S;
+    f4 sa = f4zero(), sg = f4zero();
+    if (MODE & 1)
+        sa = qs_tile_dot(xs, a.Fq, a.Fk, rb, a.S, a.D, I, J, tid, bi, bj, l16, g);
+    if (MODE == 3)
+        __syncthreads();   // the last chunk's buffers are read before they are refilled
+    if (MODE & 2)
+        sg = qs_tile_dot(xs, a.dnum, a.V, rb, a.S, a.E, I, J, tid, bi, bj, l16, g);
+    if (j > i || i >= a.nb)
+        return;
+    const long blk = ((long)seq * a.npairs + i * (i + 1) / 2 + j) * 256;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int t = 16 * i + 4 * g + r, s = 16 * j + l16;
+        const bool ok = s <= t && t < a.S;
+        const int e = (4 * g + r) * 16 + l16;
+        if (MODE & 1)
+            a.Ab[blk + e] = ok ? sa[r] : 0.0f;
+        if (MODE & 2)
+            a.Gb[blk + e] = ok ? sg[r] + a.dden[rb + min(t, a.S - 1)] : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// phase 2: products.  Unit = (kind, 64-column slice) of one (sequence, block),
+// worked by `split` waves (1, 2 or 4, so that short launches still fill the
+// SIMDs), wave part p taking block steps p, p + split, ..., with the loads of
+// its next two steps in flight; the parts are summed through LDS.  A
+// workgroup takes 4 / split consecutive units of one (sequence, step count
+// L).  Query-side kinds (O, z_cache, dQ) run over key blocks j = 0..i,
+// key-side kinds (dK, dV) over query blocks i = j..nb-1.  Results are
+// transposed: MFMA q (q = 0..3) covers the output columns c0 + 4m + q,
+// m = 0..15, so acc[q] element r is column c0 + 16g + 4r + q of row
+// 16 blk + l16 and each lane ends with four 16-byte pieces of its own row.
+// Per step: A operand X[16 b + 4g + r][c0 + 4 l16 + q] (X = V, phi(K), phi(Q)
+// or dnum at block row b; one 16-byte load per r, so a load instruction reads
+// 4 rows of 256 contiguous bytes), B operand the score block read by rows
+// (query side: lane row l16, columns 4g + r) or by columns (key side: row
+// 4g + r, column l16).
+// ---------------------------------------------------------------------------
+template <int PHI, bool BWD>
+__global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
+                                                          const LinRopeArg<PHI> rope, int split)
+{
+    __shared__ __attribute__((aligned(16))) float red[4][17 * 64];   // parts > 0: acc + dp
+    __shared__ float rope_w[phi_rope(PHI) ? LIN_ROPE_MAX_D / 2 : 1];
+    rope_tab_lds<PHI, LIN_ROPE_MAX_D / 2>(rope_w, rope);
+    if constexpr (phi_rope(PHI))
+        __syncthreads();   // the rope table
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    // heaviest units first: job = (nb - L) * groups + group for L block steps
+    const int upw = 4 / split, groups = (a.units + upw - 1) / upw;
+    int seq, job;
+    if (!qs_xcd_job((int)blockIdx.x, a.Bq, a.nb * groups, seq, job))
+        return;   // the whole workgroup
+    const int L = a.nb - job / groups, unit = upw * (job % groups) + w / split;
+    const int part = w % split;
+    if (unit >= a.units) {
+        if (split > 1)
+            __syncthreads();   // the other units' reduction
+        return;
+    }
+    int kind, sl;
+    if (!BWD) {
+        kind = unit < a.nslE ? QS_O : QS_Z;
+        sl = unit < a.nslE ? unit : unit - a.nslE;
+    } else {
+        int u = unit;
+        kind = -1;
+        sl = 0;
+        if (a.kinds & 2) {
+            if (u < a.nslD) {
+                kind = QS_DQ;
+                sl = u;
+            }
+            u -= a.nslD;
+        }
+        if (kind < 0) {
+            if (u < a.nslD) {
+                kind = QS_DK;
+                sl = u;
+            } else {
+                kind = QS_DV;
+                sl = u - a.nslD;
+            }
+        }
+    }
+    const bool qside = kind == QS_O || kind == QS_Z || kind == QS_DQ;
+    const int blk = qside ? L - 1 : a.nb - L;
+    const int W = (kind == QS_O || kind == QS_DV) ? a.E : a.D;
+    const float* X = kind == QS_O ? a.V : kind == QS_DK ? a.Fq : kind == QS_DV ? a.dnum : a.Fk;
+    const float* Sb = (kind == QS_O || kind == QS_DV) ? a.Ab : a.Gb;
+    const long rb = (long)seq * a.S;
+    const int c0 = 64 * sl;
+    const __amdgpu_buffer_rsrc_t bx = qs_rows(X, rb, a.S, W);
+    const float* sbase = Sb != nullptr ? Sb + (long)seq * a.npairs * 256 : nullptr;
+
+    f4 acc[4] = {f4zero(), f4zero(), f4zero(), f4zero()};
+    float dp = 0.0f;   // O: this lane's partial row sum of A (row l16, columns 4g..4g+3)
+    // step k: block row b of X and score block p
+    auto load = [&](int k, f4 (&xa)[4], f4& sb) __attribute__((always_inline)) {
+        const int b = qside ? k : blk + k;                 // key block (query side) / query block
+        const int i = qside ? blk : b, j = qside ? b : blk;
+        const unsigned xo = (unsigned)(((16 * b + 4 * g) * W + c0 + 4 * l16) * 4);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            xa[r] = buffer_load_f4(bx, xo + (unsigned)(r * W * 4));
+        if (kind == QS_Z) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                sb[r] = (j < i || 4 * g + r <= l16) ? 1.0f : 0.0f;
+        } else {
+            const float* sp = sbase + (long)(i * (i + 1) / 2 + j) * 256;
+            if (qside) {
+                sb = *reinterpret_cast<const f4*>(sp + l16 * 16 + 4 * g);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    sb[r] = sp[(4 * g + r) * 16 + l16];
+            }
+        }
+    };
+    auto math = [&](const f4 (&xa)[4], const f4& sb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                acc[q] = mfma16(xa[r][q], sb[r], acc[q]);
+        dp += (sb[0] + sb[1]) + (sb[2] + sb[3]);
+    };
+    // three register stages: step k + 2 is requested before step k's products
+    // (steps part + split n, n < nk)
+    const int nk = (L - part + split - 1) / split;
+    auto ld = [&](int n, f4 (&xa)[4], f4& sb) __attribute__((always_inline)) {
+        load(part + split * n, xa, sb);
+    };
+    if (nk > 0) {
+        f4 x0[4], x1[4], x2[4];
+        f4 s0, s1, s2;
+        ld(0, x0, s0);
+        if (nk > 1)
+            ld(1, x1, s1);
+        for (int n = 0;; n += 3) {
+            if (n + 2 < nk)
+                ld(n + 2, x2, s2);
+            math(x0, s0);
+            if (n + 1 >= nk)
+                break;
+            if (n + 3 < nk)
+                ld(n + 3, x0, s0);
+            math(x1, s1);
+            if (n + 2 >= nk)
+                break;
+            if (n + 4 < nk)
+                ld(n + 4, x1, s1);
+            math(x2, s2);
+            if (n + 3 >= nk)
+                break;
+        }
+    }
+    if (split > 1) {
+        if (part > 0) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                *reinterpret_cast<f4*>(&red[w][(4 * q) * 64 + lane * 4]) = acc[q];
+            red[w][16 * 64 + lane] = dp;
+        }
+        __syncthreads();
+        if (part > 0)
+            return;
+        for (int u = 1; u < split; u++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                acc[q] += *reinterpret_cast<const f4*>(&red[w + u][(4 * q) * 64 + lane * 4]);
+            dp += red[w + u][16 * 64 + lane];
+        }
+    }
+    const int row = 16 * blk + l16;
+    // piece r: columns c0 + 16g + 4r .. +3 of this lane's row
+    f4 out[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        out[r] = f4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    if (kind == QS_O) {
+        const float d = xrow_sum(dp);   // row l16's sum over every key
+        if (row < a.S) {
+            const float inv = 1.0f / (d + 1e-8f);
+            float* orow = a.O + (rb + row) * a.E;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                store4<true>(orow, c0 + 16 * g + 4 * r, a.E, out[r] * inv);
+            if (sl == 0 && g == 0)
+                a.den[rb + row] = a.den_eps ? d + 1e-8f : d;
+        }
+        return;
+    }
+    if (row >= a.S)
+        return;
+    if (kind == QS_Z || kind == QS_DV) {
+        float* orow = (kind == QS_Z ? a.zc + (rb + row) * a.D : a.dV + (rb + row) * a.E);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            store4<true>(orow, c0 + 16 * g + 4 * r, W, out[r]);
+        return;
+    }
+    // dQ, dK: phi' at the raw input (the RoPE map: then the inverse rotation)
+    const float* xr = (kind == QS_DQ ? a.Qx : a.Kx) + (rb + row) * a.D;
+    float* orow = (kind == QS_DQ ? a.dQ : a.dK) + (rb + row) * a.D;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int c = c0 + 16 * g + 4 * r;
+        if (c < a.D) {
+            f4 v = out[r];
+            if constexpr (phi_rope(PHI)) {
+                v = rope_phi_grad4<PHI>(v, *reinterpret_cast<const f4*>(xr + c), row, c, rope_w);
+            } else if constexpr (PHI != PHI_NONE) {
+                const f4 xv = *reinterpret_cast<const f4*>(xr + c);
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    v[i] *= Phi<PHI>::d(xv[i]);
+            }
+            *reinterpret_cast<f4*>(orow + c) = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static size_t qs_al(size_t b) { return (b + 255) / 256 * 256; }
+
+static bool qs_needs_feat(int phi) { return phi == PHI_ELU1 || phi == PHI_ELU1_LG; }
+
+static long qs_npairs(int S)
+{
+    const long nb = (S + 15) / 16;
+    return nb * (nb + 1) / 2;
+}
+
+// kinds: 0 forward (A); backward 1 = dK, dV (A, G), 2 = dQ (G), 3 = all (A, G)
+static size_t qs_bytes(bool feat, int Bq, int S, int D, int kinds)
+{
+    const size_t N = (size_t)Bq * S;
+    const size_t blocks = qs_al((size_t)Bq * qs_npairs(S) * 256 * sizeof(float));
+    const int nmat = kinds == 0 ? 1 : kinds == 2 ? 1 : 2;
+    return (feat ? 2 * qs_al(N * D * sizeof(float)) : 0) + nmat * blocks;
+}
+
+size_t lin_qs_bytes(int Bq, int S, int D, int E, int kinds)
+{
+    (void)E;
+    return qs_bytes(true, Bq, S, D, kinds);
+}
+
+bool lin_qs_ok(int Bq, int S, int D, int E)
+{
+    if (Bq < 1 || S < 1 || D < 16 || E < 16 || D % 16 != 0 || E % 16 != 0)
+        return false;
+    const long nb = (S + 15) / 16;
+    if ((long)S * std::max(D, E) * 4 >= (1L << 31) || (Bq + 8L) * qs_npairs(S) >= (1L << 31) ||
+        nb * qs_slices(std::max(D, E)) * 3 * (Bq + 8L) >= (1L << 31))
+        return false;
+    return lin_qs_bytes(Bq, S, D, E, 3) <= kQsBudget;
+}
+
+static inline bool qs_al16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+// Compute units of the current device (cached per device).
+static int qs_cus()
+{
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// Grid of qs_xcd_job for B' sequences of n jobs each.
+static unsigned qs_grid(int Bq, long n)
+{
+    if (Bq >= 8)
+        return (unsigned)(8L * ((Bq + 7) / 8) * n);
+    const long m = 8 / Bq;   // the fewest XCDs a sequence gets
+    return (unsigned)(8L * ((n + m - 1) / m));
+}
+
+static QsArgs qs_base(int Bq, int S, int D, int E)
+{
+    QsArgs a{};
+    a.S = S;
+    a.D = D;
+    a.E = E;
+    a.Bq = Bq;
+    a.nb = (S + 15) / 16;
+    a.npairs = (int)qs_npairs(S);
+    const int nt = (S + QS_TR - 1) / QS_TR;
+    a.ntp = nt * (nt + 1) / 2;
+    a.nslD = qs_slices(D);
+    a.nslE = qs_slices(E);
+    return a;
+}
+
+// Features into ws (ELU+1 maps) or the inputs as they are; returns the bytes
+// of ws taken.
+// need_q false: phi(K) only (the dQ-only backward); Fq then stays Q, unused.
+static size_t qs_features(int phi, const float* Q, const float* K, bool need_q, QsArgs& a,
+                          char* ws, hipError_t& e, hipStream_t st)
+{
+    a.Fq = Q;
+    a.Fk = K;
+    e = hipSuccess;
+    if (!qs_needs_feat(phi))
+        return 0;
+    const size_t N = (size_t)a.Bq * a.S, t = qs_al(N * a.D * sizeof(float));
+    float* fq = (float*)ws;
+    float* fk = (float*)(ws + t);
+    const long n4 = (long)(N * a.D / 4);
+    const unsigned grid = (unsigned)std::min<long>((n4 + 255) / 256, 4096);
+    ProfScope ps(st, "lin_qs_feat");
+    const f4* q4 = need_q ? (const f4*)Q : nullptr;
+    if (phi == PHI_ELU1)
+        CXG_LAUNCH(lin_qs_feat_kernel<PHI_ELU1>, dim3(grid), dim3(256), 0, st, q4, (const f4*)K,
+                   (f4*)fq, (f4*)fk, n4);
+    else
+        CXG_LAUNCH(lin_qs_feat_kernel<PHI_ELU1_LG>, dim3(grid), dim3(256), 0, st, q4,
+                   (const f4*)K, (f4*)fq, (f4*)fk, n4);
+    e = hipGetLastError();
+    if (need_q)
+        a.Fq = fq;
+    a.Fk = fk;
+    return 2 * t;
+}
+
+template <int MODE>
+static void qs_scores(const QsArgs& a, hipStream_t st)
+{
+    ProfScope ps(st, MODE == 1 ? "lin_qs_score" : "lin_qs_bscore");
+    CXG_LAUNCH(lin_qs_score_kernel<MODE>, dim3(qs_grid(a.Bq, a.ntp)), dim3(256), 0, st, a);
+}
+
+// Waves per product unit: the fewest that give every SIMD four waves (4 SIMDs
+// per compute unit), at most 4.  The forward counts its O units only, so that
+// O and den do not depend on whether z_cache is requested.
+static int qs_split(const QsArgs& a, bool bwd)
+{
+    const long units = (long)a.Bq * a.nb * (bwd ? a.units : a.nslE), want = 4L * 4 * qs_cus();
+    return units >= want ? 1 : 2 * units >= want ? 2 : 4;
+}
+
+template <int PHI, bool BWD>
+static void qs_prod(const QsArgs& a, int D, hipStream_t st)
+{
+    ProfScope ps(st, BWD ? "lin_qs_grad" : "lin_qs_out");
+    const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
+    const int split = qs_split(a, BWD), upw = 4 / split;
+    CXG_LAUNCH((lin_qs_prod_kernel<PHI, BWD>),
+               dim3(qs_grid(a.Bq, (long)a.nb * ((a.units + upw - 1) / upw))), dim3(256), 0, st, a,
+               rope, split);
+}
+
+hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
+                             float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
+                             void* ws, hipStream_t st)
+{
+    if (ws == nullptr || !lin_qs_ok(Bq, S, D, E) || phi_rope(phi) || phi == PHI_HEXP ||
+        !qs_al16(Q) || !qs_al16(K) || !qs_al16(V) || !qs_al16(O) || !qs_al16(zc))
+        return hipErrorInvalidValue;
+    QsArgs a = qs_base(Bq, S, D, E);
+    hipError_t e;
+    char* p = (char*)ws;
+    p += qs_features(phi, Q, K, true, a, p, e, st);
+    if (e != hipSuccess)
+        return e;
+    a.Ab = (float*)p;
+    a.V = V;
+    a.O = O;
+    a.den = den;
+    a.zc = zc;
+    a.den_eps = den_eps;
+    a.units = a.nslE + (zc != nullptr ? a.nslD : 0);
+    qs_scores<1>(a, st);
+    qs_prod<PHI_NONE, false>(a, D, st);
+    return hipGetLastError();
+}
+
+template <int PHI>
+static void qs_bwd_t(const QsArgs& a, int D, hipStream_t st)
+{
+    if (a.kinds == 2)
+        qs_scores<2>(a, st);
+    else
+        qs_scores<3>(a, st);
+    qs_prod<PHI, true>(a, D, st);
+}
+
+hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const float* V,
+                             const float* dnum, const float* dden, float* dQ, float* dK,
+                             float* dV, int Bq, int S, int D, int E, int kinds, void* ws,
+                             hipStream_t st, const float* Qx, const float* Kx)
+{
+    if (ws == nullptr || !lin_qs_ok(Bq, S, D, E) || phi == PHI_HEXP || kinds < 1 || kinds > 3 ||
+        (phi_rope(phi) && D > LIN_ROPE_MAX_D))
+        return hipErrorInvalidValue;
+    if (!qs_al16(Q) || !qs_al16(K) || !qs_al16(V) || !qs_al16(dnum) || !qs_al16(dQ) ||
+        !qs_al16(dK) || !qs_al16(dV) || !qs_al16(Qx) || !qs_al16(Kx))
+        return hipErrorInvalidValue;
+    QsArgs a = qs_base(Bq, S, D, E);
+    hipError_t e;
+    char* p = (char*)ws;
+    p += qs_features(phi, Q, K, kinds != 2, a, p, e, st);
+    if (e != hipSuccess)
+        return e;
+    const size_t blocks = qs_al((size_t)Bq * a.npairs * 256 * sizeof(float));
+    a.Gb = (float*)p;
+    a.Ab = kinds == 2 ? nullptr : (float*)(p + blocks);
+    a.V = V;
+    a.dnum = dnum;
+    a.dden = dden;
+    a.dQ = dQ;
+    a.dK = dK;
+    a.dV = dV;
+    a.Qx = Qx != nullptr ? Qx : Q;
+    a.Kx = Kx != nullptr ? Kx : K;
+    a.kinds = kinds;
+    a.units = ((kinds & 2) ? a.nslD : 0) + ((kinds & 1) ? a.nslD + a.nslE : 0);
+    if (phi == PHI_ELU1)
+        qs_bwd_t<PHI_ELU1>(a, D, st);
+    else if (phi == PHI_ELU1_LG)
+        qs_bwd_t<PHI_ELU1_LG>(a, D, st);
+    else if (phi == PHI_ELU1_ROPE)
+        qs_bwd_t<PHI_ELU1_ROPE>(a, D, st);
+    else
+        qs_bwd_t<PHI_NONE>(a, D, st);
+    return hipGetLastError();
+}
+
+}  // namespace cxg

@@ -636,14 +636,33 @@ static size_t wide_fwd_ws(int Bq, int S, int E)
     return (size_t)pmax * N * ((size_t)E + 1) * sizeof(float);
 }
 
+// The block-score path (linquad.hip) takes every width above 64 whose scratch
+// fits its budget; narrow heads keep the one-wave kernels here.
+static bool wide_qs(int Bq, int S, int D, int E)
+{
+    return std::max(D, E) > 64 && lin_qs_ok(Bq, S, D, E);
+}
+
+bool lin_quad_any(int Bq, int S, int D, int E)
+{
+    return lin_quad_ok(D, E, S) || (std::max(D, E) > LIN_WIDE_MAX && lin_qs_ok(Bq, S, D, E));
+}
+
 size_t lin_wide_ws_bytes(int Bq, int S, int D, int E)
 {
+    if (wide_qs(Bq, S, D, E))
+        return lin_qs_bytes(Bq, S, D, E, 0);
     if (!lin_wide_ok(D, E))
         return 0;
     const int m = std::max(D, E);
     if (m <= 128)
         return 0;
     return m <= 256 ? wide_fwd_ws<4>(Bq, S, E) : wide_fwd_ws<8>(Bq, S, E);
+}
+
+size_t lin_wide_bwd_ws_bytes(int Bq, int S, int D, int E, int kinds)
+{
+    return wide_qs(Bq, S, D, E) ? lin_qs_bytes(Bq, S, D, E, kinds) : 0;
 }
 
 // ws: lin_wide_ws_bytes of scratch, or null (whole query blocks); z_cache
@@ -735,6 +754,11 @@ hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const fl
                                float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
                                void* ws, hipStream_t st)
 {
+    if (ws != nullptr && wide_qs(Bq, S, D, E) && phi != PHI_HEXP && !phi_rope(phi) && al16x(Q) &&
+        al16x(K) && al16x(V) && al16x(O) && al16x(zc))
+        return lin_qs_fwd_launch(phi, Q, K, V, O, den, zc, den_eps, Bq, S, D, E, ws, st);
+    if (!lin_quad_ok(D, E, S))
+        return hipErrorInvalidValue;   // above LIN_WIDE_MAX: the block-score path only
     const bool vec = D % 4 == 0 && E % 4 == 0 && al16x(Q) && al16x(K) && al16x(V) && al16x(O);
     if (phi == PHI_ELU1)
         return wide_fwd_p<PHI_ELU1>(Q, K, V, O, den, zc, den_eps, Bq, S, D, E, vec, ws, st);
@@ -746,7 +770,7 @@ hipError_t lin_wide_fwd_launch(int phi, const float* Q, const float* K, const fl
 hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                                const float* dnum, const float* dden, float* dQ, float* dK,
                                float* dV, int Bq, int S, int D, int E, int kinds, hipStream_t st,
-                               const float* Qx, const float* Kx)
+                               const float* Qx, const float* Kx, void* ws)
 {
     if (phi_rope(phi) != (Qx != nullptr && Kx != nullptr))
         return hipErrorInvalidValue;   // RoPE maps: features plus raw inputs; others: no raw
@@ -754,6 +778,12 @@ hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const fl
         Qx = Q;
         Kx = K;
     }
+    if (ws != nullptr && wide_qs(Bq, S, D, E) && phi != PHI_HEXP && al16x(Q) && al16x(K) &&
+        al16x(V) && al16x(dnum) && al16x(dQ) && al16x(dK) && al16x(dV) && al16x(Qx) && al16x(Kx))
+        return lin_qs_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, kinds, ws, st,
+                                 Qx, Kx);
+    if (!lin_quad_ok(D, E, S))
+        return hipErrorInvalidValue;   // above LIN_WIDE_MAX: the block-score path only
     const bool vec = D % 4 == 0 && E % 4 == 0 && al16x(Q) && al16x(K) && al16x(V) &&
                      al16x(dnum) && al16x(dQ) && al16x(dK) && al16x(dV) && al16x(Qx) && al16x(Kx);
     if (phi == PHI_ELU1)

@@ -196,16 +196,22 @@ def _launches(name):
     return cx.prof_query(name)[1]
 
 
-# at most a few hundred jobs when split (one or two resident workgroups per CU)
-@pytest.mark.parametrize("B,S,D,E", [(1, 256, 512, 512), (8, 256, 512, 512), (6, 200, 512, 512),
-                                     (4, 333, 256, 192), (2, 17, 512, 512)])
-def test_forward_key_split(dev, B, S, D, E):
-    """Forwards that return no z_cache split the keys of each query block into
-    parts when B' x S/16 jobs would leave resident workgroups idle (widths above
-    128), and add the parts' numerators and denominators in a second launch.
-    Both forwards (two_stage with phi inside, linear_cuda with phi outside)
-    against the oracle, and against the same call with z_cache requested (whole
-    query blocks), which differs only in the order of the key sums."""
+# Widths multiples of 16 take the block-score kernels (linquad.hip); others
+# above 128 the one-workgroup-per-block kernels, whose forward splits the keys
+# of each query block when the jobs would leave resident workgroups idle (at
+# most a few hundred jobs: one or two resident workgroups per CU).
+@pytest.mark.parametrize("B,S,D,E,path", [
+    (1, 256, 512, 512, "qs"), (8, 256, 512, 512, "qs"), (6, 200, 512, 512, "qs"),
+    (4, 333, 256, 192, "qs"), (2, 17, 512, 512, "qs"),
+    (1, 256, 508, 508, "split"), (8, 256, 500, 500, "split"), (4, 333, 260, 196, "split"),
+    (2, 17, 504, 504, "split")])
+def test_forward_paths(dev, B, S, D, E, path):
+    """Forwards with and without z_cache, both APIs (two_stage with phi inside,
+    linear_cuda with phi outside), against the oracle.  Block-score path: the
+    launches are the score and product kernels, and O, den do not depend on
+    whether z_cache is requested (its columns are separate jobs).  Key-split
+    path: without z_cache the keys are split and the parts added in a second
+    launch, which changes only the order of the key sums."""
     import torch
     import cxxgpt_attn as cx
     N = B * S
@@ -225,10 +231,14 @@ def test_forward_key_split(dev, B, S, D, E):
             fn(q, k, tV, O, den, zc, None, None, B, S, D, E)
             torch.cuda.synchronize()
             fin = _launches("lin_wide_fin")
+            qs = _launches("lin_qs_out")
+            old = _launches("lin_wide_fwd")
             cx.prof_enable(False)
             cx.prof_reset()
-            if not split:
-                assert fin == 0
+            if path == "qs":
+                assert qs == 1 and old == 0 and fin == 0, f"{api}: B{B} S{S} D{D} E{E} path"
+            elif not split:
+                assert fin == 0 and qs == 0
             elif S > 16:
                 assert fin == 1, f"{api}: the keys of B{B} S{S} were not split"
             out[api, split] = (_np(O), _np(den))
@@ -239,7 +249,11 @@ def test_forward_key_split(dev, B, S, D, E):
             o, d = out[api, split]
             assert_close(o, ro, f"{api} split={split} O")
             assert_close(d, rd, f"{api} split={split} den")
-        assert_close(out[api, True][0], out[api, False][0], f"{api} O split vs whole",
-                     atol=1e-6, rtol=1e-5)
-        assert_close(out[api, True][1], out[api, False][1], f"{api} den split vs whole",
-                     atol=1e-6, rtol=1e-5)
+        if path == "qs":
+            assert (out[api, True][0] == out[api, False][0]).all(), f"{api} O with z_cache"
+            assert (out[api, True][1] == out[api, False][1]).all(), f"{api} den with z_cache"
+        else:
+            assert_close(out[api, True][0], out[api, False][0], f"{api} O split vs whole",
+                         atol=1e-6, rtol=1e-5)
+            assert_close(out[api, True][1], out[api, False][1], f"{api} den split vs whole",
+                         atol=1e-6, rtol=1e-5)
