@@ -1,8 +1,12 @@
 """GPU parity tests of linear attention at feature widths above 512.
 
-Widths up to 512 take the quadratic-form kernels (linwide.hip) or the chunked
-scan; D or E above 512 take the one-workgroup-per-sequence recurrence kernels
-(lin_fwd_generic / lin_dq_generic / lin_dkdv_generic in linattn.hip).
+Widths up to 512 take the quadratic-form kernels (linwide.hip, or the
+block-score kernels of linquad.hip for widths that are multiples of 16) or the
+chunked scan.  D or E above 512 take the block-score kernels when both widths
+are multiples of 16 and their scratch fits the path's budget (the first shape
+below), and otherwise the one-workgroup-per-sequence recurrence kernels
+(lin_fwd_generic / lin_dq_generic / lin_dkdv_generic in linattn.hip: the
+other shapes).
 LinearGPT reaches them for any n_embd above 512: it runs the linear_cuda API
 at D = next_pow2(n_embd) (linear_gpt.hpp:232), and n_embd comes from the
 checkpoint's metadata.  Each API is checked against its oracle restatement:
