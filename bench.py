@@ -577,21 +577,26 @@ def _linwide(c, name, Bq, S, D, seed, steps, warmup, mode):
     O, den = c.empty(N, E), c.empty(N)
     dQ, dK, dV = c.empty(N, D), c.empty(N, D), c.empty(N, E)
     P = _ptr
+    # the forward-to-backward context (the block-score path keeps its features
+    # and score blocks there; 0 bytes for shapes that write none)
+    nctx = c.cx.lin_ctx_size(Bq, S, D, E)
+    ctx = c.empty(max(1, nctx // 4)) if nctx else None
     if mode == "lgpt":
         step = Stepper(c.cx.lib(), [
-            ("cxg_lin_elu_fwd", (P(Q), P(K), P(V), P(O), P(den), None, 0, Bq, S, E, c.sp)),
-            ("cxg_lin_elu_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), None, P(dQ), P(dK),
+            ("cxg_lin_elu_fwd", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, E, c.sp)),
+            ("cxg_lin_elu_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ), P(dK),
                                  P(dV), Bq, S, E, c.sp)),
         ])
-        desc = "LinearGPT block, phi_elu fused (cxg_lin_elu_fwd -> cxg_lin_elu_bwd)"
+        desc = ("LinearGPT block, phi_elu fused (cxg_lin_elu_fwd -> cxg_lin_elu_bwd with the "
+                "context)")
     elif mode == "fused":
         step = Stepper(c.cx.lib(), [
-            ("cxg_kattn_fwd", (P(Q), P(K), P(V), P(O), P(den), None, None, None, Bq, S, D, E,
-                               c.sp)),
-            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), None, P(dQ), P(dK),
+            ("cxg_kattn_fwd_ctx", (P(Q), P(K), P(V), P(O), P(den), P(ctx), nctx, Bq, S, D, E,
+                                   c.sp)),
+            ("cxg_kattn_bwd", (P(Q), P(K), P(V), P(O), P(dO), P(den), P(ctx), P(dQ), P(dK),
                                P(dV), Bq, S, D, E, c.sp)),
         ])
-        desc = "two_stage API forward then the one-call backward (cxg_kattn_bwd)"
+        desc = "two_stage fused pair (cxg_kattn_fwd_ctx -> cxg_kattn_bwd with the context)"
     else:
         zc, dnum, dden = c.empty(N, D), c.empty(N, E), c.empty(N)
         step = Stepper(c.cx.lib(), [

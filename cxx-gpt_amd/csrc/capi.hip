@@ -732,6 +732,9 @@ static int lin_fwd_common(int phi, int den_eps, int sfin_de, const float* Q, con
         if (ctx_bytes < need)
             return CXG_ERR_WORKSPACE;
         ctx_record(ctx, need, phi, B, S, D, E);
+        if (lin_qs_path((int)B, (int)S, (int)D, (int)E))   // features and score blocks
+            return hip_status(lin_qs_fwd_launch(phi, Q, K, V, O, den, zc, den_eps, (int)B,
+                                                (int)S, (int)D, (int)E, nullptr, s, ctx));
         const LinCtx c = lin_ctx_split(ctx, (int)B, (int)S, (int)D, (int)E);
         return hip_status(lin_fwd_launch(phi, Q, K, V, O, den, zc, S_buf, z_buf, sfin_de,
                                          den_eps, (int)B, (int)S, (int)D, (int)E, c.rec, s, c.tot,
@@ -818,11 +821,19 @@ static int lin_bwd_common(int phi, const float* Q, const float* K, const float* 
         // stream-ordered scratch
         if (B * S > ((size_t)1 << 34) / (D + E + 1))
             return CXG_ERR_DIMS;
+        // the block-score path takes the forward's context; other shapes write
+        // none and ignore it
+        const void* qctx = nullptr;
+        if (ctx != nullptr && lin_qs_path((int)B, (int)S, (int)D, (int)E)) {
+            if (!ctx_matches(ctx, phi, B, S, D, E))
+                return CXG_ERR_WORKSPACE;
+            qctx = ctx;
+        }
         st = ws.acquire(nullptr, 0, lin_bwd_split_ws_bytes((int)B, (int)S, (int)D, (int)E), s);
         if (st != CXG_OK)
             return st;
         return hip_status(lin_bwd_split_launch(phi, Q, K, V, O, dO, den, dQ, dK, dV, (int)B,
-                                               (int)S, (int)D, (int)E, ws.p, s));
+                                               (int)S, (int)D, (int)E, ws.p, s, qctx));
     }
     if (ctx != nullptr && !ctx_matches(ctx, phi, B, S, D, E))
         return CXG_ERR_WORKSPACE;
@@ -907,6 +918,25 @@ int cxg_kattn_rope_fwd(const float* Q, const float* K, const float* V, float* O,
     hipStream_t s = (hipStream_t)stream;
     const LinPlan p = lin_plan((int)B, (int)S, (int)D, (int)E, LIN_PASS_FWD);
     const size_t t = round_up(B * S * D * sizeof(float), 256);
+    // (the RoPE features are formed up to LIN_ROPE_MAX_D wide; wider, the
+    // rotated copies below take the split kernels and the context is unused)
+    const size_t need = (ctx_bytes > 0 || ctx != nullptr) && D <= (size_t)LIN_ROPE_MAX_D
+                            ? lin_ctx_bytes((int)B, (int)S, (int)D, (int)E) : 0;
+    if (need > 0) {
+        // the block-score path's context: the RoPE features and the score blocks
+        if (ctx == nullptr)
+            return CXG_ERR_NULL;
+        if (ctx_bytes < need)
+            return CXG_ERR_WORKSPACE;
+        ctx_record(ctx, need, PHI_ELU1_ROPE, B, S, D, E);
+        float* fq = lin_qs_ctx_features(ctx, (int)B, (int)S, (int)D, 0);
+        float* fk = lin_qs_ctx_features(ctx, (int)B, (int)S, (int)D, 1);
+        hipError_t e = lin_rope_feat_launch(Q, K, fq, fk, (int)B, (int)S, (int)D, s);
+        if (e == hipSuccess)
+            e = lin_qs_fwd_launch(PHI_NONE, fq, fk, V, O, den_cache, nullptr, 0, (int)B, (int)S,
+                                  (int)D, (int)E, nullptr, s, ctx);
+        return hip_status(e);
+    }
     if (p.quad) {
         Scratch ws;
         st = ws.acquire(nullptr, 0, 2 * t + lin_ws_bytes(p, (int)B, (int)D, (int)E), s);
@@ -955,6 +985,29 @@ int cxg_kattn_rope_bwd(const float* Q, const float* K, const float* V, const flo
         return CXG_ERR_DIMS;
     hipStream_t s = (hipStream_t)stream;
     const size_t t = round_up(B * S * D * sizeof(float), 256);
+    if (ctx != nullptr && D <= (size_t)LIN_ROPE_MAX_D &&
+        lin_qs_path((int)B, (int)S, (int)D, (int)E)) {
+        // the forward's context: its RoPE features and score blocks
+        if (!ctx_matches(ctx, PHI_ELU1_ROPE, B, S, D, E))
+            return CXG_ERR_WORKSPACE;
+        const size_t N = B * S, tn = round_up(N * E * sizeof(float), 256);
+        const size_t tq = lin_wide_bwd_ws_bytes((int)B, (int)S, (int)D, (int)E, 3);
+        Scratch ws;
+        st = ws.acquire(nullptr, 0, tn + round_up(N * sizeof(float), 256) + tq, s);
+        if (st != CXG_OK)
+            return st;
+        float* dnum = (float*)ws.p;
+        float* dden = (float*)((char*)ws.p + tn);
+        float* fq = lin_qs_ctx_features(const_cast<void*>(ctx), (int)B, (int)S, (int)D, 0);
+        float* fk = lin_qs_ctx_features(const_cast<void*>(ctx), (int)B, (int)S, (int)D, 1);
+        hipError_t e = lin_step1_launch(O, dO, den_cache, dnum, dden, (long)N, (int)E, s);
+        if (e == hipSuccess)
+            e = lin_qs_bwd_launch(PHI_ELU1_ROPE, fq, fk, V, dnum, dden, dQ, dK, dV, (int)B,
+                                  (int)S, (int)D, (int)E, 3,
+                                  (char*)ws.p + tn + round_up(N * sizeof(float), 256), s, Q, K,
+                                  ctx);
+        return hip_status(e);
+    }
     if (lin_quad_ok((int)D, (int)E, (long)S)) {
         const size_t N = B * S, tn = round_up(N * E * sizeof(float), 256);
         const size_t tq = lin_wide_bwd_ws_bytes((int)B, (int)S, (int)D, (int)E, 3);

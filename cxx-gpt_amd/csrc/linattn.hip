@@ -1683,7 +1683,7 @@ size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E)
 hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const float* V,
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
-                                hipStream_t st)
+                                hipStream_t st, const void* ctx)
 {
     const size_t N = (size_t)Bq * S;
     char* p = (char*)ws;
@@ -1693,11 +1693,14 @@ hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const f
         float* dden = (float*)(p + al256(N * E * 4));
         char* qws = p + al256(N * E * 4) + al256(N * 4);
         hipError_t e = lin_step1_launch(O, dO, den, dnum, dden, (long)N, E, st);
-        if (e == hipSuccess)
-            e = lin_wide_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, st,
-                                    nullptr, nullptr,
-                                    lin_wide_bwd_ws_bytes(Bq, S, D, E, 3) ? qws : nullptr);
-        return e;
+        if (e != hipSuccess)
+            return e;
+        if (ctx != nullptr)   // the block-score path with the forward's context
+            return lin_qs_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, qws,
+                                     st, nullptr, nullptr, ctx);
+        return lin_wide_bwd_launch(phi, Q, K, V, dnum, dden, dQ, dK, dV, Bq, S, D, E, 3, st,
+                                   nullptr, nullptr,
+                                   lin_wide_bwd_ws_bytes(Bq, S, D, E, 3) ? qws : nullptr);
     }
     float* zc = (float*)p;
     p += al256(N * D * 4);

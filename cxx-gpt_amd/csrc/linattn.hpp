@@ -111,7 +111,10 @@ struct LinCtx {
     float* zt;     // Bq * ceil(S / 16) * 64
     float* anch;   // Bq * lin_nanch(ceil(S / 16)) anchors of LIN_ANCH floats
 };
-size_t lin_ctx_bytes(int Bq, int S, int D, int E);   // 0: shapes the fused kernels do not take
+// 0: shapes neither the fused kernels nor the block-score path take; for the
+// block-score path the context is lin_qs_ctx_bytes (features and score blocks
+// A), and lin_ctx_split does not apply.
+size_t lin_ctx_bytes(int Bq, int S, int D, int E);
 LinCtx lin_ctx_split(void* ctx, int Bq, int S, int D, int E);
 // ctx (nullable): as written by the forward with the same dimensions; the
 // backward then takes the prefix state and z from it instead of recomputing them.
@@ -122,10 +125,15 @@ hipError_t lin_bwd_fused_launch(int phi, const float* Q, const float* K, const f
 // The same for other widths, through the split kernels (workspace: zc, dnum,
 // dden and the scan scratch).
 size_t lin_bwd_split_ws_bytes(int Bq, int S, int D, int E);
+// ctx (nullable): the block-score path's context from the forward (then the
+// quadratic form's backward takes its features and score blocks).
 hipError_t lin_bwd_split_launch(int phi, const float* Q, const float* K, const float* V,
                                 const float* O, const float* dO, const float* den, float* dQ,
                                 float* dK, float* dV, int Bq, int S, int D, int E, void* ws,
-                                hipStream_t st);
+                                hipStream_t st, const void* ctx = nullptr);
+// Whether the block-score path serves these dimensions (and so writes and
+// takes a context).
+bool lin_qs_path(int Bq, int S, int D, int E);
 // Segment records of short sequences in one launch (linseq.hip): one pass
 // with two workgroups per sequence forms the records the aggregate + scan
 // pair writes (reverse = 0: exclusive prefix over segments of
@@ -170,13 +178,21 @@ hipError_t lin_wide_bwd_launch(int phi, const float* Q, const float* K, const fl
 // The wide launchers take it whenever they are given the scratch.
 bool lin_qs_ok(int Bq, int S, int D, int E);
 size_t lin_qs_bytes(int Bq, int S, int D, int E, int kinds);
+// ctx (nullable, lin_qs_ctx_bytes): the forward leaves phi(Q), phi(K) (ELU+1
+// maps) and the score blocks A there, and the backward (kinds 3) takes them
+// instead of forming them again.  The RoPE map's callers write its features
+// into the context's feature buffers (lin_qs_ctx_features: 0 = Q, 1 = K) and
+// pass them as Q, K.
+size_t lin_qs_ctx_bytes(int Bq, int S, int D, int E);
+float* lin_qs_ctx_features(void* ctx, int Bq, int S, int D, int which);
 hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                              float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                             void* ws, hipStream_t st);
+                             void* ws, hipStream_t st, void* ctx = nullptr);
 hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                              const float* dnum, const float* dden, float* dQ, float* dK,
                              float* dV, int Bq, int S, int D, int E, int kinds, void* ws,
-                             hipStream_t st, const float* Qx, const float* Kx);
+                             hipStream_t st, const float* Qx, const float* Kx,
+                             const void* ctx = nullptr);
 // The quadratic form for any width: lin_quad_ok, or widths above LIN_WIDE_MAX
 // when lin_qs_ok.
 bool lin_quad_any(int Bq, int S, int D, int E);

@@ -739,6 +739,8 @@ size_t lin_bwd_ws_bytes(const LinPlan& p, int Bq, int S)
 
 size_t lin_ctx_bytes(int Bq, int S, int D, int E)
 {
+    if (lin_qs_path(Bq, S, D, E))
+        return lin_qs_ctx_bytes(Bq, S, D, E);
     if (!lin_bwd_fused_ok(D, E, S))
         return 0;
     const LinPlan pf = lin_plan(Bq, S, D, E, LIN_PASS_FWD);

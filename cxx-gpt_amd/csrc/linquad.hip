@@ -446,6 +446,35 @@ static size_t qs_bytes(bool feat, int Bq, int S, int D, int kinds)
     return (feat ? 2 * qs_al(N * D * sizeof(float)) : 0) + nmat * blocks;
 }
 
+// Forward -> backward context of the path: phi(Q), phi(K) (ELU+1 maps; the
+// RoPE map's callers put its features there) and the score blocks A.
+struct QsCtx {
+    float* fq;
+    float* fk;
+    float* ab;
+};
+
+static QsCtx qs_ctx_split(const void* ctx, int Bq, int S, int D)
+{
+    const size_t N = (size_t)Bq * S, t = qs_al(N * D * sizeof(float));
+    char* c = (char*)const_cast<void*>(ctx);
+    return QsCtx{(float*)c, (float*)(c + t), (float*)(c + 2 * t)};
+}
+
+size_t lin_qs_ctx_bytes(int Bq, int S, int D, int E)
+{
+    (void)E;
+    const size_t N = (size_t)Bq * S;
+    return 2 * qs_al(N * D * sizeof(float)) +
+           qs_al((size_t)Bq * qs_npairs(S) * 256 * sizeof(float));
+}
+
+float* lin_qs_ctx_features(void* ctx, int Bq, int S, int D, int which)
+{
+    const QsCtx c = qs_ctx_split(ctx, Bq, S, D);
+    return which == 0 ? c.fq : c.fk;
+}
+
 size_t lin_qs_bytes(int Bq, int S, int D, int E, int kinds)
 {
     (void)E;
@@ -510,8 +539,9 @@ static QsArgs qs_base(int Bq, int S, int D, int E)
 // Features into ws (ELU+1 maps) or the inputs as they are; returns the bytes
 // of ws taken.
 // need_q false: phi(K) only (the dQ-only backward); Fq then stays Q, unused.
+// dst (nullable): a context's feature buffers instead of ws.
 static size_t qs_features(int phi, const float* Q, const float* K, bool need_q, QsArgs& a,
-                          char* ws, hipError_t& e, hipStream_t st)
+                          char* ws, hipError_t& e, hipStream_t st, const QsCtx* dst = nullptr)
 {
     a.Fq = Q;
     a.Fk = K;
@@ -519,8 +549,8 @@ static size_t qs_features(int phi, const float* Q, const float* K, bool need_q, 
     if (!qs_needs_feat(phi))
         return 0;
     const size_t N = (size_t)a.Bq * a.S, t = qs_al(N * a.D * sizeof(float));
-    float* fq = (float*)ws;
-    float* fk = (float*)(ws + t);
+    float* fq = dst ? dst->fq : (float*)ws;
+    float* fk = dst ? dst->fk : (float*)(ws + t);
     const long n4 = (long)(N * a.D / 4);
     const unsigned grid = (unsigned)std::min<long>((n4 + 255) / 256, 4096);
     ProfScope ps(st, "lin_qs_feat");
@@ -535,7 +565,7 @@ static size_t qs_features(int phi, const float* Q, const float* K, bool need_q, 
     if (need_q)
         a.Fq = fq;
     a.Fk = fk;
-    return 2 * t;
+    return dst ? 0 : 2 * t;
 }
 
 template <int MODE>
@@ -567,18 +597,25 @@ static void qs_prod(const QsArgs& a, int D, hipStream_t st)
 
 hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const float* V, float* O,
                              float* den, float* zc, int den_eps, int Bq, int S, int D, int E,
-                             void* ws, hipStream_t st)
+                             void* ws, hipStream_t st, void* ctx)
 {
-    if (ws == nullptr || !lin_qs_ok(Bq, S, D, E) || phi_rope(phi) || phi == PHI_HEXP ||
-        !qs_al16(Q) || !qs_al16(K) || !qs_al16(V) || !qs_al16(O) || !qs_al16(zc))
+    if ((ws == nullptr && ctx == nullptr) || !lin_qs_ok(Bq, S, D, E) || phi_rope(phi) ||
+        phi == PHI_HEXP || !qs_al16(Q) || !qs_al16(K) || !qs_al16(V) || !qs_al16(O) ||
+        !qs_al16(zc))
         return hipErrorInvalidValue;
     QsArgs a = qs_base(Bq, S, D, E);
     hipError_t e;
-    char* p = (char*)ws;
-    p += qs_features(phi, Q, K, true, a, p, e, st);
+    if (ctx != nullptr) {   // features and score blocks into the context
+        const QsCtx c = qs_ctx_split(ctx, Bq, S, D);
+        qs_features(phi, Q, K, true, a, nullptr, e, st, &c);
+        a.Ab = c.ab;
+    } else {
+        char* p = (char*)ws;
+        p += qs_features(phi, Q, K, true, a, p, e, st);
+        a.Ab = (float*)p;
+    }
     if (e != hipSuccess)
         return e;
-    a.Ab = (float*)p;
     a.V = V;
     a.O = O;
     a.den = den;
@@ -590,10 +627,11 @@ hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const floa
     return hipGetLastError();
 }
 
+// with_a: A is already in a.Ab (the forward's context): G only.
 template <int PHI>
-static void qs_bwd_t(const QsArgs& a, int D, hipStream_t st)
+static void qs_bwd_t(const QsArgs& a, int D, bool with_a, hipStream_t st)
 {
-    if (a.kinds == 2)
+    if (a.kinds == 2 || with_a)
         qs_scores<2>(a, st);
     else
         qs_scores<3>(a, st);
@@ -603,23 +641,32 @@ static void qs_bwd_t(const QsArgs& a, int D, hipStream_t st)
 hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const float* V,
                              const float* dnum, const float* dden, float* dQ, float* dK,
                              float* dV, int Bq, int S, int D, int E, int kinds, void* ws,
-                             hipStream_t st, const float* Qx, const float* Kx)
+                             hipStream_t st, const float* Qx, const float* Kx, const void* ctx)
 {
     if (ws == nullptr || !lin_qs_ok(Bq, S, D, E) || phi == PHI_HEXP || kinds < 1 || kinds > 3 ||
-        (phi_rope(phi) && D > LIN_ROPE_MAX_D))
+        (phi_rope(phi) && D > LIN_ROPE_MAX_D) || (ctx != nullptr && kinds != 3))
         return hipErrorInvalidValue;
     if (!qs_al16(Q) || !qs_al16(K) || !qs_al16(V) || !qs_al16(dnum) || !qs_al16(dQ) ||
         !qs_al16(dK) || !qs_al16(dV) || !qs_al16(Qx) || !qs_al16(Kx))
         return hipErrorInvalidValue;
     QsArgs a = qs_base(Bq, S, D, E);
-    hipError_t e;
+    hipError_t e = hipSuccess;
     char* p = (char*)ws;
-    p += qs_features(phi, Q, K, kinds != 2, a, p, e, st);
-    if (e != hipSuccess)
-        return e;
-    const size_t blocks = qs_al((size_t)Bq * a.npairs * 256 * sizeof(float));
-    a.Gb = (float*)p;
-    a.Ab = kinds == 2 ? nullptr : (float*)(p + blocks);
+    if (ctx != nullptr) {
+        // the forward's features (ELU+1 maps) and score blocks A
+        const QsCtx c = qs_ctx_split(ctx, Bq, S, D);
+        a.Fq = qs_needs_feat(phi) ? c.fq : Q;
+        a.Fk = qs_needs_feat(phi) ? c.fk : K;
+        a.Ab = c.ab;
+        a.Gb = (float*)p;
+    } else {
+        p += qs_features(phi, Q, K, kinds != 2, a, p, e, st);
+        if (e != hipSuccess)
+            return e;
+        const size_t blocks = qs_al((size_t)Bq * a.npairs * 256 * sizeof(float));
+        a.Gb = (float*)p;
+        a.Ab = kinds == 2 ? nullptr : (float*)(p + blocks);
+    }
     a.V = V;
     a.dnum = dnum;
     a.dden = dden;
@@ -631,13 +678,13 @@ hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const floa
     a.kinds = kinds;
     a.units = ((kinds & 2) ? a.nslD : 0) + ((kinds & 1) ? a.nslD + a.nslE : 0);
     if (phi == PHI_ELU1)
-        qs_bwd_t<PHI_ELU1>(a, D, st);
+        qs_bwd_t<PHI_ELU1>(a, D, ctx != nullptr, st);
     else if (phi == PHI_ELU1_LG)
-        qs_bwd_t<PHI_ELU1_LG>(a, D, st);
+        qs_bwd_t<PHI_ELU1_LG>(a, D, ctx != nullptr, st);
     else if (phi == PHI_ELU1_ROPE)
-        qs_bwd_t<PHI_ELU1_ROPE>(a, D, st);
+        qs_bwd_t<PHI_ELU1_ROPE>(a, D, ctx != nullptr, st);
     else
-        qs_bwd_t<PHI_NONE>(a, D, st);
+        qs_bwd_t<PHI_NONE>(a, D, ctx != nullptr, st);
     return hipGetLastError();
 }
 

@@ -643,6 +643,11 @@ static bool wide_qs(int Bq, int S, int D, int E)
     return std::max(D, E) > 64 && lin_qs_ok(Bq, S, D, E);
 }
 
+bool lin_qs_path(int Bq, int S, int D, int E)
+{
+    return lin_quad_any(Bq, S, D, E) && wide_qs(Bq, S, D, E);
+}
+
 bool lin_quad_any(int Bq, int S, int D, int E)
 {
     return lin_quad_ok(D, E, S) || (std::max(D, E) > LIN_WIDE_MAX && lin_qs_ok(Bq, S, D, E));

@@ -255,16 +255,20 @@ def test_error_paths(dev):
         assert cx.call_status(fn, *([None] + p[1:]), 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
         assert cx.call_status(fn, *p[:5], None, *p[6:], 1, 4, 8, 8, st) == cx.CXG_ERR_NULL
         assert cx.call_status(fn, *([None] * 10), 0, 4, 8, 8, st) == cx.CXG_OK   # empty
-    # the context: none for heads wider than 64 or for sequences short enough
-    # for the quadratic form; a short buffer is refused
-    assert cx.lin_ctx_size(2, 300, 128, 64) == 0
+    # the context: none for narrow heads on sequences short enough for the
+    # quadratic form or for wide heads whose widths are not multiples of 16;
+    # the chunked scan's records, or the block-score path's features and score
+    # blocks, otherwise; a short buffer is refused
     assert cx.lin_ctx_size(2, 100, 64, 64) == 0
-    n = cx.lin_ctx_size(2, 300, 64, 64)
-    assert n > 0
-    for fn in ("cxg_kattn_fwd_ctx", "cxg_lin_fwd_ctx"):
-        assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 300, 64, 64, st) == \
-            cx.CXG_ERR_WORKSPACE
-        assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 300, 64, 64, st) == cx.CXG_ERR_NULL
+    assert cx.lin_ctx_size(2, 300, 100, 64) == 0
+    for D in (64, 128):
+        n = cx.lin_ctx_size(2, 300, D, 64)
+        assert n > 0
+        for fn in ("cxg_kattn_fwd_ctx", "cxg_lin_fwd_ctx"):
+            assert cx.call_status(fn, *[P(t)] * 5, P(t), n - 4, 2, 300, D, 64, st) == \
+                cx.CXG_ERR_WORKSPACE
+            assert cx.call_status(fn, *[P(t)] * 5, None, n, 2, 300, D, 64, st) == \
+                cx.CXG_ERR_NULL
 
 
 # ---------------------------------------------------------------------------

@@ -75,9 +75,14 @@ def check_rope_pair(dev, Q, K, V, dO, B, S, D, E, tag, use_ctx=False):
     (2, 77, 96, 64),      # D != E
     (1, 33, 258, 130),    # widths not multiples of 4
 ])
-def test_rope_quadratic_form(dev, B, S, D, E):
+@pytest.mark.parametrize("use_ctx", [False, True])
+def test_rope_quadratic_form(dev, B, S, D, E, use_ctx):
+    """With the context, the block-score path's forward leaves the RoPE
+    features and score blocks there for the backward (widths multiples of 16
+    above 64; other shapes have no context to write)."""
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 41 * S + D + E)
-    check_rope_pair(dev, Q, K, V, dO, B, S, D, E, tag=f"rope quad B{B}S{S}D{D}E{E}")
+    check_rope_pair(dev, Q, K, V, dO, B, S, D, E, tag=f"rope quad B{B}S{S}D{D}E{E}",
+                    use_ctx=use_ctx)
 
 
 @pytest.mark.parametrize("use_ctx", [False, True])

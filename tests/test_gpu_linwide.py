@@ -143,6 +143,20 @@ def test_linear_gpt_wide(dev, B, S, E):
     cx.lin_elu_fwd(_t(Xq, dev), _t(Xk, dev), tv, eO, eden, None, B, S, E)
     dXq, dXk, edV = _nan(dev, N, E), _nan(dev, N, E), _nan(dev, N, E)
     cx.lin_elu_bwd(_t(Xq, dev), _t(Xk, dev), tv, eO, tdo, eden, dXq, dXk, edV, B, S, E)
+    # with the forward's context (block-score path: features and score blocks
+    # kept): the same kernels on the same values, so the same bits
+    nctx = cx.lin_ctx_size(B, S, E, E)
+    if nctx:
+        ctx = torch.full((nctx // 4,), float("nan"), device=dev)
+        cO, cden = _nan(dev, N, E), _nan(dev, N)
+        cx.lin_elu_fwd(_t(Xq, dev), _t(Xk, dev), tv, cO, cden, ctx, B, S, E)
+        cdXq, cdXk, cdV = _nan(dev, N, E), _nan(dev, N, E), _nan(dev, N, E)
+        cx.lin_elu_bwd(_t(Xq, dev), _t(Xk, dev), tv, cO, tdo, cden, cdXq, cdXk, cdV, B, S, E,
+                       ctx=ctx)
+        torch.cuda.synchronize()
+        for name, a, b in (("O", cO, eO), ("den", cden, eden), ("dXq", cdXq, dXq),
+                           ("dXk", cdXk, dXk), ("dV", cdV, edV)):
+            assert np.array_equal(_np(a), _np(b)), f"lin_elu with context: {name}"
     torch.cuda.synchronize()
     seqs = [0, B - 1] if B > 2 else list(range(B))
     for s in seqs:
