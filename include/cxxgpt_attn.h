@@ -210,10 +210,14 @@ int cxg_kattn_bwd_dKdV(const float *Q, const float *K, const float *V,
  * reused for another context of the same shape.  A forward that writes a
  * context forgets every earlier record whose bytes it overlaps, and at most
  * 4096 records are kept.  D <= 64 and E <= 64 take the fused
- * kernels (sequences of up to 128 rows the quadratic form); widths up to 512
- * run step 1 and one quadratic-form backward launch (dnum, dden in the
- * library's scratch); wider ones the split kernels; ctx is not read on these
- * paths (the forward wrote none: cxg_lin_ctx_size is 0 for them). */
+ * kernels (sequences of up to 128 rows the quadratic form); wider heads run
+ * step 1 and the quadratic-form backward (dnum, dden in the library's
+ * scratch): with both widths multiples of 16 through block score matrices,
+ * and then the context holds the forward's phi(Q), phi(K) and score blocks,
+ * which the backward takes instead of forming them again; other widths up to
+ * 512 through the one-workgroup-per-block kernels and wider ones through the
+ * split kernels, where the forward writes no context (cxg_lin_ctx_size is 0)
+ * and ctx is not read. */
 int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O,
                   const float *dO, const float *den_cache, const void *ctx, float *dQ,
                   float *dK, float *dV, size_t B, size_t S, size_t D, size_t E,
@@ -224,9 +228,12 @@ int cxg_kattn_bwd(const float *Q, const float *K, const float *V, const float *O
  * cxg_lin_ctx_size() bytes) the per-segment prefix states, each sequence's
  * final state and z before every 16-row chunk.  No counterpart in the
  * reference (its forward hands the backward z_cache, B*S*D floats; the context
- * is about a fifth of that at B' = 96, S = 4096, D = E = 64).  For shapes the
- * fused kernels do not take, cxg_lin_ctx_size() is 0, ctx may be NULL and
- * nothing is written to it. */
+ * is about a fifth of that at B' = 96, S = 4096, D = E = 64).  Wider heads
+ * whose widths are multiples of 16 (the block-score quadratic form) keep
+ * phi(Q), phi(K) and the causal 16x16 score blocks there instead:
+ * 2*B*S*D + B*nb(nb+1)/2*256 floats, nb = ceil(S/16) (9.4 MB at B = 8,
+ * S = 256, D = E = 512).  For shapes neither takes, cxg_lin_ctx_size() is 0,
+ * ctx may be NULL and nothing is written to it. */
 size_t cxg_lin_ctx_size(size_t B, size_t S, size_t D, size_t E);
 int cxg_kattn_fwd_ctx(const float *Q, const float *K, const float *V, float *O,
                       float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
@@ -251,10 +258,11 @@ int cxg_kattn_fwd_ctx(const float *Q, const float *K, const float *V, float *O,
  * rows inside its kernels as it stages them and rotates dQ, dK back before
  * storing them; the quadratic form (widths up to 512, and shorter sequences)
  * forms phi(rot(Q)), phi(rot(K)) once in a pre-pass into the library's
- * scratch (its jobs would otherwise rotate each streamed block again), and
- * its backward applies phi' and the inverse rotation as it stores dQ, dK;
- * wider heads rotate copies of Q and K in the library's scratch and rotate
- * dQ, dK back in place. */
+ * scratch, or into the context when it has one (the block-score path: the
+ * backward then takes them and the score blocks from there), and its backward
+ * applies phi' and the inverse rotation as it stores dQ, dK; heads wider than
+ * 512 rotate copies of Q and K in the library's scratch and rotate dQ, dK
+ * back in place, and use no context. */
 int cxg_kattn_rope_fwd(const float *Q, const float *K, const float *V, float *O,
                        float *den_cache, void *ctx, size_t ctx_bytes, size_t B, size_t S,
                        size_t D, size_t E, cxg_stream_t stream);
