@@ -43,6 +43,8 @@ constexpr size_t kQsBudget = (size_t)512 << 20;   // bytes of scratch the path m
 
 enum { QS_O = 0, QS_Z = 1, QS_DQ = 2, QS_DK = 3, QS_DV = 4 };
 
+constexpr int kQsStages = 2;   // register stages of the product kernels' operand loads
+
 struct QsArgs {
     const float* Fq;     // phi(Q) (or Q / the RoPE features)
     const float* Fk;     // phi(K)
@@ -328,34 +330,64 @@ __global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
                 acc[q] = mfma16(xa[r][q], sb[r], acc[q]);
         dp += (sb[0] + sb[1]) + (sb[2] + sb[3]);
     };
-    // three register stages: step k + 2 is requested before step k's products
-    // (steps part + split n, n < nk)
+    // The epilogue's phi' operands (dQ, dK units of the first part), requested
+    // now so that they arrive during the block steps.
+    const int row = 16 * blk + l16;
+    const float* raw = kind == QS_DQ ? a.Qx : a.Kx;
+    const float* fea = kind == QS_DQ ? a.Fq : a.Fk;
+    const bool from_f = !phi_rope(PHI) && fea != raw;
+    f4 xe[4] = {f4zero(), f4zero(), f4zero(), f4zero()};
+    if (BWD && PHI != PHI_NONE && part == 0 && (kind == QS_DQ || kind == QS_DK)) {
+        const __amdgpu_buffer_rsrc_t be = qs_rows(from_f ? fea : raw, rb, a.S, a.D);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            xe[r] = buffer_load_f4(be, (unsigned)((row * a.D + c0 + 16 * g + 4 * r) * 4));
+    }
+    // register stages: with three, step n + 2 is requested before step n's
+    // products (steps part + split n, n < nk); with two, step n + 1
     const int nk = (L - part + split - 1) / split;
     auto ld = [&](int n, f4 (&xa)[4], f4& sb) __attribute__((always_inline)) {
         load(part + split * n, xa, sb);
     };
     if (nk > 0) {
-        f4 x0[4], x1[4], x2[4];
-        f4 s0, s1, s2;
+        f4 x0[4], x1[4];
+        f4 s0, s1;
         ld(0, x0, s0);
-        if (nk > 1)
-            ld(1, x1, s1);
-        for (int n = 0;; n += 3) {
-            if (n + 2 < nk)
-                ld(n + 2, x2, s2);
-            math(x0, s0);
-            if (n + 1 >= nk)
-                break;
-            if (n + 3 < nk)
-                ld(n + 3, x0, s0);
-            math(x1, s1);
-            if (n + 2 >= nk)
-                break;
-            if (n + 4 < nk)
-                ld(n + 4, x1, s1);
-            math(x2, s2);
-            if (n + 3 >= nk)
-                break;
+        if constexpr (kQsStages == 3) {
+            f4 x2[4];
+            f4 s2;
+            if (nk > 1)
+                ld(1, x1, s1);
+            for (int n = 0;; n += 3) {
+                if (n + 2 < nk)
+                    ld(n + 2, x2, s2);
+                math(x0, s0);
+                if (n + 1 >= nk)
+                    break;
+                if (n + 3 < nk)
+                    ld(n + 3, x0, s0);
+                math(x1, s1);
+                if (n + 2 >= nk)
+                    break;
+                if (n + 4 < nk)
+                    ld(n + 4, x1, s1);
+                math(x2, s2);
+                if (n + 3 >= nk)
+                    break;
+            }
+        } else {
+            for (int n = 0;; n += 2) {
+                if (n + 1 < nk)
+                    ld(n + 1, x1, s1);
+                math(x0, s0);
+                if (n + 1 >= nk)
+                    break;
+                if (n + 2 < nk)
+                    ld(n + 2, x0, s0);
+                math(x1, s1);
+                if (n + 2 >= nk)
+                    break;
+            }
         }
     }
     if (split > 1) {
@@ -375,7 +407,6 @@ __global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
             dp += red[w + u][16 * 64 + lane];
         }
     }
-    const int row = 16 * blk + l16;
     // piece r: columns c0 + 16g + 4r .. +3 of this lane's row
     f4 out[4];
 #pragma unroll
@@ -403,8 +434,10 @@ __global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
             store4<true>(orow, c0 + 16 * g + 4 * r, W, out[r]);
         return;
     }
-    // dQ, dK: phi' at the raw input (the RoPE map: then the inverse rotation)
-    const float* xr = (kind == QS_DQ ? a.Qx : a.Kx) + (rb + row) * a.D;
+    // dQ, dK: phi' (ELU+1 maps: min(phi, 1) from the features, which is
+    // exp(x) for x <= 0 as phi is, or at the raw input where no features were
+    // formed (the dQ-only backward's Q); the RoPE map: at the raw input, then
+    // the inverse rotation); the operands were requested at the unit's start
     float* orow = (kind == QS_DQ ? a.dQ : a.dK) + (rb + row) * a.D;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -412,12 +445,18 @@ __global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
         if (c < a.D) {
             f4 v = out[r];
             if constexpr (phi_rope(PHI)) {
-                v = rope_phi_grad4<PHI>(v, *reinterpret_cast<const f4*>(xr + c), row, c, rope_w);
+                v = rope_phi_grad4<PHI>(v, xe[r], row, c, rope_w);
             } else if constexpr (PHI != PHI_NONE) {
-                const f4 xv = *reinterpret_cast<const f4*>(xr + c);
+                const f4 xv = xe[r];
+                if (from_f) {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    v[i] *= Phi<PHI>::d(xv[i]);
+                    for (int i = 0; i < 4; i++)
+                        v[i] *= Phi<PHI>::d_from_f(xv[i]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        v[i] *= Phi<PHI>::d(xv[i]);
+                }
             }
             *reinterpret_cast<f4*>(orow + c) = v;
         }
