@@ -207,7 +207,7 @@ def attribute(cx, step, steps):
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
-              "lin_qs_grad",
+              "lin_qs_grad", "lin_qs_zc",
               "phi_hexp_fwd", "phi_hexp_bwd", "lin_rope_feat",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",

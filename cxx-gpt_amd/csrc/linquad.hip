@@ -126,6 +126,40 @@ __global__ __launch_bounds__(256) void lin_qs_feat_kernel(const f4* __restrict__
     }
 }
 
+// z_cache = inclusive column sums of phi(K) over each sequence's rows (the
+// forwards that return it): workgroup = (sequence, 64-column slice), wave w
+// of 16 walking a sixteenth of the rows twice (its column sums, then the
+// running sums from the earlier waves' totals), lane = column, so every load
+// and store is a row's 256 contiguous bytes.
+constexpr int QS_ZC_WAVES = 16;
+
+__global__ __launch_bounds__(64 * QS_ZC_WAVES) void lin_qs_zc_kernel(
+    const float* __restrict__ Fk, float* __restrict__ zc, int S, int D, int nsl)
+{
+    __shared__ float tot[QS_ZC_WAVES][64];
+    const int seq = (int)(blockIdx.x / (unsigned)nsl), sl = (int)(blockIdx.x % (unsigned)nsl);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = 64 * sl + lane;
+    const bool cok = c < D;
+    const long base = (long)seq * S * D + (cok ? c : 0);
+    const int q = (S + QS_ZC_WAVES - 1) / QS_ZC_WAVES, r0 = min(S, w * q), r1 = min(S, r0 + q);
+    float sum = 0.0f;
+#pragma unroll 16
+    for (int t = r0; t < r1; t++)
+        sum += Fk[base + (long)t * D];
+    tot[w][lane] = sum;
+    __syncthreads();
+    float z = 0.0f;
+    for (int u = 0; u < w; u++)
+        z += tot[u][lane];
+#pragma unroll 16
+    for (int t = r0; t < r1; t++) {
+        z += Fk[base + (long)t * D];
+        if (cok)
+            zc[base + (long)t * D] = z;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // phase 1: score blocks.  Workgroup = (sequence, pair of 32-row tiles J <= I);
 // wave w forms block (2I + w/2, 2J + w%2) of it (blocks above the diagonal are
@@ -658,11 +692,16 @@ hipError_t lin_qs_fwd_launch(int phi, const float* Q, const float* K, const floa
     a.V = V;
     a.O = O;
     a.den = den;
-    a.zc = zc;
+    a.zc = nullptr;   // z_cache: lin_qs_zc_kernel below
     a.den_eps = den_eps;
-    a.units = a.nslE + (zc != nullptr ? a.nslD : 0);
+    a.units = a.nslE;
     qs_scores<1>(a, st);
     qs_prod<PHI_NONE, false>(a, D, st);
+    if (zc != nullptr) {
+        ProfScope ps(st, "lin_qs_zc");
+        CXG_LAUNCH(lin_qs_zc_kernel, dim3((unsigned)((long)Bq * a.nslD)),
+                   dim3(64 * QS_ZC_WAVES), 0, st, a.Fk, zc, S, D, a.nslD);
+    }
     return hipGetLastError();
 }
 
