@@ -51,7 +51,7 @@ them can be made the reported workload with --workload NAME):
   c2ropesep C2 with RoPE as separate passes, the reference's call sequence
   gpt       GPT's attention at its training shape (B8 S256, one head of E=512,
             gpt_train.cpp:139/156): cxg_gpt_attn_fwd -> cxg_gpt_attn_bwd
-  gpt768    the same at E=768 (scores kept in memory, FP32 MFMA GEMMs)
+  gpt768    the same at E=768 (causal score blocks kept in memory)
   gelu      exact GELU + derivative over the q/k/v expander FFN activations at
             the C2 shape (3 x 2048 x 6144 floats; two_stage_gpt.hpp:86-99), GB/s
   ffn       one expander FFN fwd+bwd (X [2048][768], W1 [6144][768], W2
@@ -207,7 +207,8 @@ def attribute(cx, step, steps):
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
-              "lin_qs_grad", "lin_qs_zc",
+              "lin_qs_grad", "lin_qs_zc", "gpt_qs_score", "gpt_qs_softmax", "gpt_qs_out",
+              "gpt_qs_bscore", "gpt_qs_grad",
               "phi_hexp_fwd", "phi_hexp_bwd", "lin_rope_feat",
               "rope_fwd", "rope_bwd", "mha_rope_fwd", "mha_rope_bwd", "mha_wide_fwd",
               "mha_wide_stats", "mha_wide_bwd", "mha_wide_merge", "mha_wide_bsum", "gelu", "gelu_deriv", "ffn_gemm",
@@ -462,13 +463,21 @@ def _gpt(c, name, B, S, E, seed, steps, warmup):
               # matrices per sequence within 2^25 floats), credited with its
               # causal half (S^2 E of the 2 S^2 E executed)
               "ffn_gemm": 1.0 * min(B, max(1, (1 << 25) // (2 * S * S))) * S * S * E}
-    dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
-    ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
-    roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
-            "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
-            "traffic": c.traffic.get(f"{name}/{dom}"), "flops_per_launch": kflops[dom],
-            "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
+    if any(k.startswith("gpt_qs") for k in att):
+        # causal score blocks: credit per step (P = S(S+1)/2 causal pairs per
+        # sequence): QK^T and PV forward, dP (S recomputed, not credited) and
+        # dQ, dK, dV backward
+        P2 = S * (S + 1) // 2 * B * 2 * E
+        roof = wide_roofline(c, name, att, {"gpt_qs_score": P2, "gpt_qs_out": P2,
+                                            "gpt_qs_bscore": P2, "gpt_qs_grad": 3 * P2})
+    else:
+        dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
+        ach = kflops[dom] / (att[dom][0] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dom, "achieved": round(ach, 3),
+                "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / FP32_MFMA_PEAK_TFLOPS, 4),
+                "traffic": c.traffic.get(f"{name}/{dom}"), "flops_per_launch": kflops[dom],
+                "kernel_ms": {k: round(v[0], 5) for k, v in att.items()}}
     return dict(value=value, unit="TFLOP/s", ms=ms, roofline=roof,
                 config={"workload": f"{name}: GPT attention (one head over the embedding, "
                                     "gpt_gpt.hpp:365-438) via cxg_gpt_attn_fwd -> "

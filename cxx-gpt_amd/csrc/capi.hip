@@ -535,8 +535,9 @@ static int gpt_check(size_t B, size_t S, size_t E, bool* empty)
     if (*empty)
         return CXG_OK;
     if (E > (size_t)MHA_WIDE_MAX_DH) {
-        // scores in memory: S x S floats per sequence (S <= 16384: 1 GiB), GEMM
-        // shapes in int; any S, E a multiple of 4
+        // scores in memory: causal score blocks (E a multiple of 16, within the
+        // block-score scratch budget), else S x S floats per sequence (S <=
+        // 16384: 1 GiB) with GEMM shapes in int; any S, E a multiple of 4
         if (!fits_int(B) || !fits_int(E) || S > 16384 || B * S * E > ((size_t)1 << 40))
             return CXG_ERR_DIMS;
         return gpt_mat_ok((int)S, (int)E) ? CXG_OK : CXG_ERR_ALIGN;
@@ -547,6 +548,15 @@ static int gpt_check(size_t B, size_t S, size_t E, bool* empty)
     if (E > 256 && S * E > ((size_t)1 << 28))
         return CXG_ERR_DIMS;
     return CXG_OK;
+}
+
+// Widths above 256 that are multiples of 16 take the causal score blocks
+// (faster than the wide-head kernels at E = 512: 58 against 81 us a B8 S256
+// step) whenever their scratch fits; others the wide-head kernels (up to 512)
+// or the S x S scores and GEMMs.
+static bool gpt_blocks(size_t B, size_t S, size_t E)
+{
+    return E > 256 && E % 16 == 0 && gpt_qs_ok((int)B, (int)S, (int)E);
 }
 
 int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, float* lse,
@@ -561,9 +571,17 @@ int cxg_gpt_attn_fwd(const float* Q, const float* K, const float* V, float* O, f
     if (!Q || !K || !V || !O)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
-    if (E > (size_t)MHA_WIDE_MAX_DH) {
+    if (E > (size_t)MHA_WIDE_MAX_DH || gpt_blocks(B, S, E)) {
         if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(O))
             return CXG_ERR_ALIGN;
+        if (gpt_blocks(B, S, E)) {
+            Scratch ws;
+            st = ws.acquire(nullptr, 0, gpt_qs_ws_bytes((int)B, (int)S, (int)E, false), s);
+            if (st != CXG_OK)
+                return st;
+            return hip_status(
+                gpt_qs_fwd_launch(Q, K, V, O, lse, (int)B, (int)S, (int)E, ws.p, s));
+        }
         Scratch ws;
         st = ws.acquire(nullptr, 0, gpt_mat_fwd_ws_floats((int)B, (int)S, (int)E) * sizeof(float),
                         s);
@@ -587,7 +605,9 @@ size_t cxg_gpt_attn_bwd_workspace_size(size_t B, size_t S, size_t E)
     bool empty;
     if (gpt_check(B, S, E, &empty) != CXG_OK || empty)
         return 0;
-    if (E > (size_t)MHA_WIDE_MAX_DH)   // the scores of one sequence, and GEMM partial tiles
+    if (gpt_blocks(B, S, E))   // P and dS blocks, Di and lse
+        return gpt_qs_ws_bytes((int)B, (int)S, (int)E, true);
+    if (E > (size_t)MHA_WIDE_MAX_DH)   // the scores of a group of sequences, GEMM partials
         return gpt_mat_ws_floats((int)B, (int)S, (int)E) * sizeof(float);
     // Di, lse, and the partial records of the statistics pass and of the
     // backward (used one after the other)
@@ -616,10 +636,13 @@ int cxg_gpt_attn_bwd(const float* Q, const float* K, const float* V, const float
     st = ws.acquire(workspace, workspace_bytes, cxg_gpt_attn_bwd_workspace_size(B, S, E), s);
     if (st != CXG_OK)
         return st;
-    if (E > (size_t)MHA_WIDE_MAX_DH) {
+    if (E > (size_t)MHA_WIDE_MAX_DH || gpt_blocks(B, S, E)) {
         if (!al16c(Q) || !al16c(K) || !al16c(V) || !al16c(dO) || !al16c(dQ) || !al16c(dK) ||
             !al16c(dV) || !al16c(ws.p))
             return CXG_ERR_ALIGN;
+        if (gpt_blocks(B, S, E))
+            return hip_status(gpt_qs_bwd_launch(Q, K, V, O, dO, lse, dQ, dK, dV, (int)B, (int)S,
+                                                (int)E, ws.p, s));
         return hip_status(gpt_mat_bwd_launch(Q, K, V, dO, lse, dQ, dK, dV, (int)B, (int)S,
                                              (int)E, (float*)ws.p, s));
     }

@@ -129,6 +129,21 @@ hipError_t gpt_mat_bwd_launch(const float* Q, const float* K, const float* V, co
                               const float* lse, float* dQ, float* dK, float* dV, int B, int S,
                               int E, float* ws, hipStream_t st);
 
+// GPT's attention through block score matrices in scratch (linquad.hip):
+// E a multiple of 16 and the scratch within the block-score budget
+// (CXXGPT_GPT_PATH=mat in the environment keeps the GEMM path above).  The
+// forward forms the scaled causal 16x16 score blocks, their row softmax (P
+// over the scores, lse) and O = P V; the backward P and dS = P (dP - Di) /
+// sqrt(E) from S and dP = dO V^T, then dQ = dS K, dK = dS^T Q, dV = P^T dO.
+// O may be null (statistics only); lse nullable in both (recomputed).
+bool gpt_qs_ok(int B, int S, int E);
+size_t gpt_qs_ws_bytes(int B, int S, int E, bool bwd);
+hipError_t gpt_qs_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                             float* lse, int B, int S, int E, void* ws, hipStream_t st);
+hipError_t gpt_qs_bwd_launch(const float* Q, const float* K, const float* V, const float* O,
+                             const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                             int B, int S, int E, void* ws, hipStream_t st);
+
 // Exact (erf) GELU or its derivative over n elements (C may alias A).
 hipError_t gelu_launch(const float* A, float* C, long n, bool deriv, hipStream_t st);
 

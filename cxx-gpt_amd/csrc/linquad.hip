@@ -36,6 +36,8 @@
 #include "linattn_dev.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 namespace cxg {
 
@@ -67,6 +69,15 @@ struct QsArgs {
     int units;           // product units (output slices) per (sequence, block)
     int nslD, nslE;      // 64-column slices of the widths
     int kinds;           // backward: 1 = dK, dV; 2 = dQ; 3 = both
+    int norm;            // O divided by den + 1e-8 (linear attention; 0: P is normalised)
+    // softmax attention (GPT's, one head of width E): scores are formed as
+    // q . k * qk_scale (scale * log2 e, the exp2 domain); the backward takes
+    // lse (natural log) and Di = rowsum(dO * O) per row and stores
+    // dS = P (dP - Di) * sm_scale
+    float qk_scale, sm_scale;
+    const float* lse_in;
+    const float* Di;
+    float* lse_out;
 };
 
 __host__ __device__ inline int qs_slices(int W) { return (W + 63) / 64; }
@@ -215,7 +226,10 @@ __device__ __forceinline__ f4 qs_tile_dot(float (*xs)[2][QS_TR * QS_LD], const f
     return c0 + c1;
 }
 
-template <int MODE>
+// SM: 0 linear attention (A, G as above); 1 softmax forward (A = the scaled
+// scores, exp2 domain, for lin_qs_softmax_kernel); 2 softmax backward (MODE 3:
+// A = P = exp2(S - lse log2 e), G = dS).
+template <int MODE, int SM = 0>
 __global__ __launch_bounds__(256) void lin_qs_score_kernel(const QsArgs a)
 {
     __shared__ __attribute__((aligned(16))) float xs[2][2][QS_TR * QS_LD];
@@ -249,11 +263,74 @@ __global__ __launch_bounds__(256) void lin_qs_score_kernel(const QsArgs a)
         const int t = 16 * i + 4 * g + r, s = 16 * j + l16;
         const bool ok = s <= t && t < a.S;
         const int e = (4 * g + r) * 16 + l16;
-        if (MODE & 1)
-            a.Ab[blk + e] = ok ? sa[r] : 0.0f;
-        if (MODE & 2)
-            a.Gb[blk + e] = ok ? sg[r] + a.dden[rb + min(t, a.S - 1)] : 0.0f;
+        if constexpr (SM == 0) {
+            if (MODE & 1)
+                a.Ab[blk + e] = ok ? sa[r] : 0.0f;
+            if (MODE & 2)
+                a.Gb[blk + e] = ok ? sg[r] + a.dden[rb + min(t, a.S - 1)] : 0.0f;
+        } else if constexpr (SM == 1) {
+            a.Ab[blk + e] = ok ? sa[r] * a.qk_scale : 0.0f;
+        } else {
+            const long rt = rb + min(t, a.S - 1);
+            const float p = ok ? fast_exp2(sa[r] * a.qk_scale - a.lse_in[rt] * kLog2e) : 0.0f;
+            a.Ab[blk + e] = p;
+            a.Gb[blk + e] = p * (sg[r] - a.Di[rt]) * a.sm_scale;
+        }
     }
+}
+
+// Row softmax of the scaled score blocks of one (sequence, query block i) per
+// workgroup: the blocks (i, 0..i) are consecutive in the packed layout; wave w
+// takes blocks j = w, w+4, ..., lane (l16, g) reading row l16 at columns
+// 4g..4g+3 of each.  Three passes, the first two combined across the waves
+// through LDS: the row maximum, the sum of exp2(S - max), then P = exp2(S -
+// max) / sum written over the scores (0 above the diagonal and in rows past
+// S), and lse = (max + log2 sum) ln 2 when lse_out is given.
+__global__ __launch_bounds__(256) void lin_qs_softmax_kernel(const QsArgs a)
+{
+    __shared__ float red[2][4][16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int seq = (int)(blockIdx.x / (unsigned)a.nb), i = (int)(blockIdx.x % (unsigned)a.nb);
+    float* base = a.Ab + ((long)seq * a.npairs + (long)i * (i + 1) / 2) * 256 + l16 * 16 + 4 * g;
+    const int t = 16 * i + l16;
+    float m = -INFINITY;
+    for (int j = w; j <= i; j += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(base + j * 256);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (16 * j + 4 * g + r <= t)
+                m = fmaxf(m, v[r]);
+    }
+    m = xrow_max(m);
+    if (g == 0)
+        red[0][w][l16] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0][0][l16], red[0][1][l16]), fmaxf(red[0][2][l16], red[0][3][l16]));
+    float l = 0.0f;   // every row has its diagonal entry, so m is finite
+    for (int j = w; j <= i; j += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(base + j * 256);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (16 * j + 4 * g + r <= t)
+                l += fast_exp2(v[r] - m);
+    }
+    l = xrow_sum(l);
+    if (g == 0)
+        red[1][w][l16] = l;
+    __syncthreads();
+    l = (red[1][0][l16] + red[1][1][l16]) + (red[1][2][l16] + red[1][3][l16]);
+    const float inv = 1.0f / l;
+    const bool rok = t < a.S;
+    for (int j = w; j <= i; j += 4) {
+        f4 v = *reinterpret_cast<const f4*>(base + j * 256);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            v[r] = (rok && 16 * j + 4 * g + r <= t) ? fast_exp2(v[r] - m) * inv : 0.0f;
+        *reinterpret_cast<f4*>(base + j * 256) = v;
+    }
+    if (a.lse_out != nullptr && rok && w == 0 && g == 0)
+        a.lse_out[(long)seq * a.S + t] = (m + fast_log2(l)) * kLn2;
 }
 
 // ---------------------------------------------------------------------------
@@ -449,12 +526,12 @@ __global__ __launch_bounds__(256) void lin_qs_prod_kernel(const QsArgs a,
     if (kind == QS_O) {
         const float d = xrow_sum(dp);   // row l16's sum over every key
         if (row < a.S) {
-            const float inv = 1.0f / (d + 1e-8f);
+            const float inv = a.norm ? 1.0f / (d + 1e-8f) : 1.0f;
             float* orow = a.O + (rb + row) * a.E;
 #pragma unroll
             for (int r = 0; r < 4; r++)
                 store4<true>(orow, c0 + 16 * g + 4 * r, a.E, out[r] * inv);
-            if (sl == 0 && g == 0)
+            if (a.norm && sl == 0 && g == 0)
                 a.den[rb + row] = a.den_eps ? d + 1e-8f : d;
         }
         return;
@@ -596,6 +673,7 @@ static unsigned qs_grid(int Bq, long n)
 static QsArgs qs_base(int Bq, int S, int D, int E)
 {
     QsArgs a{};
+    a.norm = 1;
     a.S = S;
     a.D = D;
     a.E = E;
@@ -641,11 +719,12 @@ static size_t qs_features(int phi, const float* Q, const float* K, bool need_q, 
     return dst ? 0 : 2 * t;
 }
 
-template <int MODE>
+template <int MODE, int SM = 0>
 static void qs_scores(const QsArgs& a, hipStream_t st)
 {
-    ProfScope ps(st, MODE == 1 ? "lin_qs_score" : "lin_qs_bscore");
-    CXG_LAUNCH(lin_qs_score_kernel<MODE>, dim3(qs_grid(a.Bq, a.ntp)), dim3(256), 0, st, a);
+    ProfScope ps(st, SM != 0 ? (SM == 1 ? "gpt_qs_score" : "gpt_qs_bscore")
+                             : (MODE == 1 ? "lin_qs_score" : "lin_qs_bscore"));
+    CXG_LAUNCH((lin_qs_score_kernel<MODE, SM>), dim3(qs_grid(a.Bq, a.ntp)), dim3(256), 0, st, a);
 }
 
 // Waves per product unit: the fewest that give every SIMD four waves (4 SIMDs
@@ -660,7 +739,8 @@ static int qs_split(const QsArgs& a, bool bwd)
 template <int PHI, bool BWD>
 static void qs_prod(const QsArgs& a, int D, hipStream_t st)
 {
-    ProfScope ps(st, BWD ? "lin_qs_grad" : "lin_qs_out");
+    ProfScope ps(st, a.norm ? (BWD ? "lin_qs_grad" : "lin_qs_out")
+                            : (BWD ? "gpt_qs_grad" : "gpt_qs_out"));
     const LinRopeArg<PHI> rope = lin_rope_arg<PHI>(D);
     const int split = qs_split(a, BWD), upw = 4 / split;
     CXG_LAUNCH((lin_qs_prod_kernel<PHI, BWD>),
@@ -763,6 +843,106 @@ hipError_t lin_qs_bwd_launch(int phi, const float* Q, const float* K, const floa
         qs_bwd_t<PHI_ELU1_ROPE>(a, D, ctx != nullptr, st);
     else
         qs_bwd_t<PHI_NONE>(a, D, ctx != nullptr, st);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// GPT's attention (softmax, one head of width E) through the same blocks
+// ---------------------------------------------------------------------------
+static bool qs_gpt_forced_mat()
+{
+    const char* v = getenv("CXXGPT_GPT_PATH");
+    return v != nullptr && strcmp(v, "mat") == 0;
+}
+
+bool gpt_qs_ok(int B, int S, int E)
+{
+    return !qs_gpt_forced_mat() && lin_qs_ok(B, S, E, E);
+}
+
+// forward: the score blocks; backward: P and dS blocks, Di and lse rows
+size_t gpt_qs_ws_bytes(int B, int S, int E, bool bwd)
+{
+    (void)E;
+    const size_t blocks = qs_al((size_t)B * qs_npairs(S) * 256 * sizeof(float));
+    const size_t rows = qs_al((size_t)B * S * sizeof(float));
+    return bwd ? 2 * blocks + 2 * rows : blocks;
+}
+
+static QsArgs gpt_args(const float* Q, const float* K, const float* V, int B, int S, int E)
+{
+    QsArgs a = qs_base(B, S, E, E);
+    a.Fq = Q;
+    a.Fk = K;
+    a.V = V;
+    a.norm = 0;
+    const float scale = 1.0f / sqrtf((float)E);
+    a.qk_scale = scale * kLog2e;
+    a.sm_scale = scale;
+    return a;
+}
+
+hipError_t gpt_qs_fwd_launch(const float* Q, const float* K, const float* V, float* O,
+                             float* lse, int B, int S, int E, void* ws, hipStream_t st)
+{
+    if (ws == nullptr || !lin_qs_ok(B, S, E, E) || !qs_al16(Q) || !qs_al16(K) || !qs_al16(V) ||
+        !qs_al16(O))
+        return hipErrorInvalidValue;
+    QsArgs a = gpt_args(Q, K, V, B, S, E);
+    a.Ab = (float*)ws;
+    a.O = O;
+    a.lse_out = lse;
+    a.units = a.nslE;
+    qs_scores<1, 1>(a, st);
+    {
+        ProfScope ps(st, "gpt_qs_softmax");
+        CXG_LAUNCH(lin_qs_softmax_kernel, dim3((unsigned)((long)B * a.nb)), dim3(256), 0, st,
+                   a);
+    }
+    if (O != nullptr)
+        qs_prod<PHI_NONE, false>(a, E, st);
+    return hipGetLastError();
+}
+
+hipError_t gpt_qs_bwd_launch(const float* Q, const float* K, const float* V, const float* O,
+                             const float* dO, const float* lse, float* dQ, float* dK, float* dV,
+                             int B, int S, int E, void* ws, hipStream_t st)
+{
+    if (ws == nullptr || !lin_qs_ok(B, S, E, E) || !qs_al16(Q) || !qs_al16(K) || !qs_al16(V) ||
+        !qs_al16(dO) || !qs_al16(dQ) || !qs_al16(dK) || !qs_al16(dV))
+        return hipErrorInvalidValue;
+    const size_t blocks = qs_al((size_t)B * qs_npairs(S) * 256 * sizeof(float));
+    const size_t rows = qs_al((size_t)B * S * sizeof(float));
+    char* p = (char*)ws;
+    float* Ab = (float*)p;
+    float* Gb = (float*)(p + blocks);
+    float* Di = (float*)(p + 2 * blocks);
+    float* lse_ws = (float*)(p + 2 * blocks + rows);
+    hipError_t e;
+    if (lse == nullptr) {   // the forward's statistics again
+        e = gpt_qs_fwd_launch(Q, K, V, nullptr, lse_ws, B, S, E, Ab, st);
+        if (e != hipSuccess)
+            return e;
+        lse = lse_ws;
+    }
+    e = mha_bwd_prep_launch(O, dO, Di, nullptr, B, S, 1, E, st);
+    if (e != hipSuccess)
+        return e;
+    QsArgs a = gpt_args(Q, K, V, B, S, E);
+    a.Ab = Ab;
+    a.Gb = Gb;
+    a.dnum = dO;
+    a.lse_in = lse;
+    a.Di = Di;
+    a.dQ = dQ;
+    a.dK = dK;
+    a.dV = dV;
+    a.Qx = Q;
+    a.Kx = K;
+    a.kinds = 3;
+    a.units = 2 * a.nslD + a.nslE;
+    qs_scores<3, 2>(a, st);
+    qs_prod<PHI_NONE, true>(a, E, st);
     return hipGetLastError();
 }
 

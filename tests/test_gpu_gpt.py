@@ -5,8 +5,9 @@ attention with whole-matrix TensorN calls: scores = Q K^T / sqrt(E) over all
 B*S rows, gpt_cuda::attention_mask (gpt_cuda_kernels.cu:458-480: -1e10 on
 cross-batch and future entries), softmax, times V; the backward goes through
 gpt_cuda::softmax_backward (:131-173) and three products.  The entry points
-compute it as causal attention with H = 1, Dh = E (above E = 512 with each
-sequence's scores in memory and FP32 MFMA GEMMs).  Each case is checked
+compute it as causal attention with H = 1, Dh = E (above E = 512 with the
+scores in memory: causal 16x16 score blocks when E is a multiple of 16, else
+each sequence's S x S scores and FP32 MFMA GEMMs).  Each case is checked
 against the C oracle's MHA (ref_mha_fwd / ref_mha_bwd restated, H = 1) and,
 for small B*S, against a float64 restatement of the reference's whole-matrix
 formulation itself (mask value -1e10, row softmax, softmax_backward's
@@ -53,15 +54,15 @@ def gpt_whole_matrix(Q, K, V, dO, B, S, E):
 
 @pytest.mark.parametrize("B,S,E", [
     (2, 64, 128),     # gpt_gpt.hpp:322 default n_embd (the fused MHA kernels, H = 1)
-    (2, 100, 512),    # gpt_train.cpp:139 n_embd: the wide-head kernels
+    (2, 100, 512),    # gpt_train.cpp:139 n_embd: causal score blocks
     (1, 257, 384),    # ragged S, a mid width
     (3, 33, 260),     # just past 256
     (1, 16, 512),     # one tile
     (2, 50, 258),     # width not a multiple of 4 (scalar loads)
     (1, 130, 258),    # chunked backward and split-KV forward with scalar stores
     (4, 128, 512),
-    (2, 64, 768),     # wider than 512: scores in memory, FP32 MFMA GEMMs
-    (3, 100, 516),
+    (2, 64, 768),     # wider than 512, a multiple of 16: causal score blocks in memory
+    (3, 100, 516),    # not a multiple of 16: S x S scores and FP32 MFMA GEMMs
     (1, 256, 1024),
     (2, 12, 2048),
     # generate()'s pattern (gpt_gpt.hpp:672-693): every context length, so S
@@ -115,6 +116,7 @@ def test_gpt_attention_groups(dev, B, S, E, budget, monkeypatch):
     the batched GEMM's sequence strides are exercised, with and without lse."""
     import torch
     import cxxgpt_attn as cx
+    monkeypatch.setenv("CXXGPT_GPT_PATH", "mat")   # the GEMM path, not the score blocks
     monkeypatch.setenv("CXXGPT_GPT_SCORE_FLOATS", str(budget))
     N = B * S
     Q, K, V, dO = normal_inputs((N, E), (N, E), 11 * S + E + B)
@@ -136,6 +138,41 @@ def test_gpt_attention_groups(dev, B, S, E, budget, monkeypatch):
         torch.cuda.synchronize()
         for name, g, r in zip(("dQ", "dK", "dV"), outs, (rdQ, rdK, rdV)):
             assert_close(_np(g), r, f"gpt groups {name} B{B}S{S}E{E} lse={use_lse}")
+    cx.release_scratch()
+
+
+@pytest.mark.parametrize("B,S,E", [(2, 100, 512), (1, 77, 384), (2, 64, 768)])
+def test_gpt_attention_without_blocks(dev, B, S, E, monkeypatch):
+    """Widths above 256 that are multiples of 16 take the causal score blocks;
+    with CXXGPT_GPT_PATH=mat the same shapes run the wide-head kernels (up to
+    512) or the S x S scores and GEMMs, which other widths still use.  Both
+    against the oracle, and against each other."""
+    import torch
+    import cxxgpt_attn as cx
+    N = B * S
+    Q, K, V, dO = normal_inputs((N, E), (N, E), 13 * S + E + B)
+    tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
+    res = {}
+    for path in ("blocks", "mat"):
+        if path == "mat":
+            monkeypatch.setenv("CXXGPT_GPT_PATH", "mat")
+        O = torch.full((N, E), float("nan"), device=dev)
+        lse = torch.full((N,), float("nan"), device=dev)
+        cx.gpt_attn_fwd(tQ, tK, tV, O, B, S, E, lse=lse)
+        outs = [torch.full((N, E), float("nan"), device=dev) for _ in range(3)]
+        cx.gpt_attn_bwd(tQ, tK, tV, O, tdO, *outs, B, S, E, lse=lse)
+        torch.cuda.synchronize()
+        res[path] = [_np(O), _np(lse)] + [_np(t) for t in outs]
+    rO, rlse = orc.mha_fwd(Q, K, V, B, S, 1, E, nthreads=8, want_lse=True)
+    rdQ, rdK, rdV = orc.mha_bwd(Q, K, V, res["blocks"][0], dO, B, S, 1, E, nthreads=8)
+    for path, (gO, glse, gdQ, gdK, gdV) in res.items():
+        assert_close(gO, rO, f"gpt {path} O B{B}S{S}E{E}")
+        assert_close(glse, rlse, f"gpt {path} lse B{B}S{S}E{E}")
+        assert_close(gdQ, rdQ, f"gpt {path} dQ B{B}S{S}E{E}")
+        assert_close(gdK, rdK, f"gpt {path} dK B{B}S{S}E{E}")
+        assert_close(gdV, rdV, f"gpt {path} dV B{B}S{S}E{E}")
+    for k, (a, b) in enumerate(zip(res["blocks"], res["mat"])):
+        assert_close(a, b, f"gpt blocks vs mat output {k}", atol=2e-5, rtol=2e-4)
     cx.release_scratch()
 
 
