@@ -135,9 +135,14 @@ int cxg_mha_rope_bwd(const float *Q, const float *K, const float *V, const float
  * softmax, times V, and the backward through gpt_cuda::softmax_backward.  No
  * single counterpart in the reference (it is matmuls, a mask, a softmax and
  * transposes).  Q, K, V, O (B*S, E) row-major; lse [B][S] natural log; the
- * same as cxg_mha_fwd / cxg_mha_bwd with H = 1, Dh = E, which serve E <= 256;
- * 256 < E <= 512 (the reference GPT's training configuration has E = 512)
- * takes wider-head kernels.  There, shapes with few 16-row query blocks
+ * same as cxg_mha_fwd / cxg_mha_bwd with H = 1, Dh = E, which serve E <= 256.
+ * Above 256, widths that are multiples of 16 keep the causal 16x16 score
+ * blocks in scratch (B * nb(nb+1)/2 KB per matrix, nb = ceil(S/16): the
+ * forward one matrix, the backward two plus Di and lse rows) whenever that
+ * fits the library's 512 MB budget for them, and run every product per
+ * 64-column slice; the environment variable CXXGPT_GPT_PATH=mat (read at
+ * each call) turns this off.  Otherwise 256 < E <= 512 (the reference GPT's
+ * training configuration has E = 512) takes wider-head kernels.  There, shapes with few 16-row query blocks
  * split the forward's key range over more workgroups and merge the partial
  * softmax states: the forward then takes the library's scratch for them, and
  * cxg_gpt_attn_bwd_workspace_size counts them for the backward's statistics
