@@ -24,6 +24,9 @@ pytestmark = pytest.mark.gpu
     (2, 256, 512, 512),   # the stage-2 shape, two sequences
     (3, 77, 256, 256), (2, 300, 128, 128), (1, 33, 100, 200), (2, 16, 512, 300),
     (4, 1, 96, 96), (1, 700, 192, 192), (2, 40, 65, 64), (1, 19, 512, 8),
+    # batches of 8 and more that are not multiples of 8 (sequences dealt to
+    # XCDs unevenly by the block-score kernels), one and two row blocks
+    (9, 48, 128, 128), (20, 17, 96, 64), (11, 16, 64, 96),
 ])
 def test_two_stage_chain_wide(dev, B, S, D, E):
     """fwd (O, den, z_cache) -> step1 -> dQ -> dKdV through the two_stage API."""
