@@ -190,37 +190,50 @@ __device__ __forceinline__ f4 qs_tile_dot(float (*xs)[2][QS_TR * QS_LD], const f
                                           const float* X2, long rb, int S, int W, int I, int J,
                                           int tid, int bi, int bj, int l16, int g)
 {
+    constexpr int NU = QS_KC / 32;   // 16-byte pieces a thread stages per operand and chunk
     const __amdgpu_buffer_rsrc_t b1 = qs_rows(X1, rb, S, W), b2 = qs_rows(X2, rb, S, W);
     const int sr = tid >> 3, sc = 4 * (tid & 7);
     const unsigned o1 = (unsigned)(((QS_TR * I + sr) * W + sc) * 4);
     const unsigned o2 = (unsigned)(((QS_TR * J + sr) * W + sc) * 4);
     const int nch = (W + QS_KC - 1) / QS_KC;
-    auto fetch = [&](int c, f4& r1, f4& r2) __attribute__((always_inline)) {
-        const bool ok = QS_KC * c + sc < W;   // W % 16 == 0: a chunk's 16-col halves
-        const f4 v1 = buffer_load_f4(b1, o1 + (unsigned)(4 * QS_KC * c));
-        const f4 v2 = buffer_load_f4(b2, o2 + (unsigned)(4 * QS_KC * c));
-        r1 = ok ? v1 : f4zero();
-        r2 = ok ? v2 : f4zero();
+    auto fetch = [&](int c, f4 (&r1)[NU], f4 (&r2)[NU]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            const int col = QS_KC * c + 32 * u;
+            const bool ok = col + sc < W;   // W % 16 == 0: whole 16-column groups
+            const f4 v1 = buffer_load_f4(b1, o1 + (unsigned)(4 * col));
+            const f4 v2 = buffer_load_f4(b2, o2 + (unsigned)(4 * col));
+            r1[u] = ok ? v1 : f4zero();
+            r2[u] = ok ? v2 : f4zero();
+        }
     };
-    f4 r1, r2;
+    f4 r1[NU], r2[NU];
     fetch(0, r1, r2);
     f4 c0 = f4zero(), c1 = f4zero();
     for (int c = 0; c < nch; c++) {
         float* s1 = xs[c & 1][0];
         float* s2 = xs[c & 1][1];
-        *reinterpret_cast<f4*>(&s1[sr * QS_LD + sc]) = r1;
-        *reinterpret_cast<f4*>(&s2[sr * QS_LD + sc]) = r2;
+#pragma unroll
+        for (int u = 0; u < NU; u++) {
+            *reinterpret_cast<f4*>(&s1[sr * QS_LD + sc + 32 * u]) = r1[u];
+            *reinterpret_cast<f4*>(&s2[sr * QS_LD + sc + 32 * u]) = r2[u];
+        }
         if (c + 1 < nch)
             fetch(c + 1, r1, r2);
         __syncthreads();
         const float* pa = &s1[(16 * bi + l16) * QS_LD + 4 * g];
         const float* pb = &s2[(16 * bj + l16) * QS_LD + 4 * g];
-        const f4 a0 = *reinterpret_cast<const f4*>(pa), a1 = *reinterpret_cast<const f4*>(pa + 16);
-        const f4 e0 = *reinterpret_cast<const f4*>(pb), e1 = *reinterpret_cast<const f4*>(pb + 16);
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            c0 = mfma16(a0[r], e0[r], c0);
-            c1 = mfma16(a1[r], e1[r], c1);
+        for (int h = 0; h < QS_KC / 16; h += 2) {
+            const f4 a0 = *reinterpret_cast<const f4*>(pa + 16 * h);
+            const f4 a1 = *reinterpret_cast<const f4*>(pa + 16 * h + 16);
+            const f4 e0 = *reinterpret_cast<const f4*>(pb + 16 * h);
+            const f4 e1 = *reinterpret_cast<const f4*>(pb + 16 * h + 16);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                c0 = mfma16(a0[r], e0[r], c0);
+                c1 = mfma16(a1[r], e1[r], c1);
+            }
         }
     }
     return c0 + c1;
