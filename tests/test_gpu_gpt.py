@@ -73,6 +73,7 @@ def gpt_whole_matrix(Q, K, V, dO, B, S, E):
     (2, 130, 1024),
     (3, 3, 516),
     (9, 40, 384),     # score blocks with a batch of 8 and more, not a multiple of 8
+    (20, 200, 768),   # a large batch, an odd block count
 ])
 def test_gpt_attention(dev, B, S, E):
     import torch

@@ -74,6 +74,7 @@ def check_rope_pair(dev, Q, K, V, dO, B, S, D, E, tag, use_ctx=False):
     (3, 100, 64, 64),     # short sequences: the quadratic form at narrow width
     (2, 77, 96, 64),      # D != E
     (1, 33, 258, 130),    # widths not multiples of 4
+    (50, 112, 512, 512),  # a large batch, an odd block count
 ])
 @pytest.mark.parametrize("use_ctx", [False, True])
 def test_rope_quadratic_form(dev, B, S, D, E, use_ctx):

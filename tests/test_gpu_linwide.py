@@ -27,6 +27,8 @@ pytestmark = pytest.mark.gpu
     # batches of 8 and more that are not multiples of 8 (sequences dealt to
     # XCDs unevenly by the block-score kernels), one and two row blocks
     (9, 48, 128, 128), (20, 17, 96, 64), (11, 16, 64, 96),
+    # a batch large enough for one wave per product unit, an odd block count
+    (48, 240, 256, 256),
 ])
 def test_two_stage_chain_wide(dev, B, S, D, E):
     """fwd (O, den, z_cache) -> step1 -> dQ -> dKdV through the two_stage API."""
@@ -35,12 +37,17 @@ def test_two_stage_chain_wide(dev, B, S, D, E):
                 tag=f"wide B{B}S{S}D{D}E{E}")
 
 
-def test_two_stage_reference_shape(dev):
-    """TwoStageGPT stage 2 at its training shape: B = 32, S = 256, D = E = 512
-    (the oracle checks a sample of sequences; each is independent)."""
+@pytest.mark.parametrize("B,S,D", [
+    (32, 256, 512),   # the training shape
+    (70, 240, 512),   # one wave per product unit in every pass, an odd block count
+])
+def test_two_stage_reference_shape(dev, B, S, D):
+    """TwoStageGPT stage 2 at its training shape, B = 32, S = 256, D = E = 512,
+    and at a batch large enough that the block-score forward, like the
+    backward, runs one wave per product unit (the oracle checks a sample of
+    sequences; each is independent)."""
     import torch
     import cxxgpt_attn as cx
-    B, S, D = 32, 256, 512
     N = B * S
     Q, K, V, dO = normal_inputs((N, D), (N, D), 4242)
     tQ, tK, tV, tdO = _t(Q, dev), _t(K, dev), _t(V, dev), _t(dO, dev)
@@ -57,7 +64,7 @@ def test_two_stage_reference_shape(dev):
     torch.cuda.synchronize()
     g = {k: _np(v) for k, v in dict(O=O, den=den, zc=zc, dnum=dnum, dden=dden, dQ=dQ, dK=dK,
                                     dV=dV, fQ=fQ, fK=fK, fV=fV).items()}
-    for s in (0, 17, 31):
+    for s in (0, 17, B - 1):
         sl = slice(s * S, (s + 1) * S)
         q, k, v = Q[sl], K[sl], V[sl]
         rO, rden, rzc = orc.kattn_fwd(q, k, v, 1, S, D, D)
