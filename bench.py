@@ -203,7 +203,8 @@ def attribute(cx, step, steps):
     torch.cuda.synchronize()
     cx.prof_enable(False)
     out = {}
-    for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "lin_agg", "lin_scan",
+    for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "mha_nar_fwd", "mha_nar_stats",
+              "mha_nar_bwd", "lin_agg", "lin_scan",
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
@@ -326,6 +327,8 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only
     value = flops / (ms * 1e-3) / 1e12
     kflops = {"mha_fwd": mha_flops(B, S, H, Dh, bwd=False),
               "mha_bwd": mha_flops(B, S, H, Dh, fwd=False),
+              "mha_nar_fwd": mha_flops(B, S, H, Dh, bwd=False),
+              "mha_nar_bwd": mha_flops(B, S, H, Dh, fwd=False),
               "mha_rope_fwd": mha_flops(B, S, H, Dh, bwd=False),
               "mha_rope_bwd": mha_flops(B, S, H, Dh, fwd=False)}
     dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])

@@ -359,6 +359,14 @@ static int mha_bwd_common(const float* Q, const float* K, const float* V, const 
     if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
+    const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
+    if (rope == nullptr && mha_nar_ok(iB, iS, iH, iD)) {
+        // one launch that uses no scratch; a caller's workspace is still
+        // checked against the documented size, whichever kernels run
+        if (workspace != nullptr && workspace_bytes < cxg_mha_bwd_workspace_size(B, S, H, Dh))
+            return CXG_ERR_WORKSPACE;
+        return hip_status(mha_nar_bwd_launch(Q, K, V, O, dO, lse, dQ, dK, dV, iB, iS, iH, iD, s));
+    }
     const size_t half = round_up(B * H * S * sizeof(float), 256);
     Scratch ws;
     st = ws.acquire(workspace, workspace_bytes, cxg_mha_bwd_workspace_size(B, S, H, Dh), s);
@@ -366,7 +374,6 @@ static int mha_bwd_common(const float* Q, const float* K, const float* V, const 
         return st;
     float* Di = (float*)ws.p;
     float* lse_ws = (float*)((char*)ws.p + half);
-    const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
     hipError_t e;
     if (lse == nullptr && mha_stats_prep_ok(iB, iS, iH, iD)) {
         // statistics-only forward pass (the reference recomputes them too),
@@ -486,6 +493,9 @@ int cxg_mha_bwd_noalloc(const float* Q, const float* K, const float* V, const fl
         return CXG_ERR_WORKSPACE;
     if (!Q || !K || !V || !O || !dO || !dQ || !dK || !dV)
         return CXG_ERR_NULL;
+    if (mha_nar_ok((int)B, (int)S, (int)H, (int)Dh))   // its kernel uses no scratch
+        return hip_status(mha_nar_bwd_launch(Q, K, V, O, dO, lse, dQ, dK, dV, (int)B, (int)S,
+                                             (int)H, (int)Dh, (hipStream_t)stream));
     hipError_t e = hipSuccess;
     float* sp = scratch_ptr(&e);
     if (sp == nullptr)
