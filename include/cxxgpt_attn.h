@@ -79,7 +79,11 @@ int cxg_mha_fwd(const float *Q, const float *K, const float *V, float *O, float 
  * two_stage_cuda_kernels.cu:830-882).  lse: as written by cxg_mha_fwd, or NULL
  * to recompute it (the reference's signature has no lse).  workspace: at least
  * cxg_mha_bwd_workspace_size() bytes of device memory, or NULL for the
- * library's scratch (see the conventions above). */
+ * library's scratch (see the conventions above).  Narrow heads on short
+ * sequences (Dh <= 16, and S rounded up to 16 times 8 columns for Dh <= 8, or
+ * 16 columns otherwise, at most 4096) run as one kernel per call that uses no
+ * scratch: a workspace passed is still checked for size and left unused, and
+ * NULL allocates nothing. */
 int cxg_mha_bwd(const float *Q, const float *K, const float *V, const float *O,
                 const float *dO, const float *lse, float *dQ, float *dK, float *dV,
                 size_t B, size_t S, size_t H, size_t Dh, void *workspace,
