@@ -17,7 +17,8 @@ them can be made the reported workload with --workload NAME):
             the library's cached per-stream scratch)
   c2graph   c2 captured once in a HIP graph and replayed (not in the default run)
   mhats     TwoStageGPT's stage-1 shape, B32 H64 S256 Dh8, legacy signatures
-            (two_stage_train.cpp:168-170)
+            (two_stage_train.cpp:168-170); mhatsrope with its RoPE fused
+            (cxg_mha_rope_fwd/bwd), mhatsropesep with RoPE as separate passes
   gen1, gen64, gen256
             generate()'s forward at B = 1, S = 1 / 64 / 256, probe heads H8 Dh32
             (two_stage_gpt.hpp:453-470), latency per call
@@ -204,7 +205,7 @@ def attribute(cx, step, steps):
     cx.prof_enable(False)
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "mha_nar_fwd", "mha_nar_stats",
-              "mha_nar_bwd", "lin_agg", "lin_scan",
+              "mha_nar_bwd", "mha_nar_rope_fwd", "mha_nar_rope_bwd", "lin_agg", "lin_scan",
               "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
@@ -329,6 +330,8 @@ def _mha(c, name, B, S, H, Dh, use_lse, seed, steps, warmup, rope=None, fwd_only
               "mha_bwd": mha_flops(B, S, H, Dh, fwd=False),
               "mha_nar_fwd": mha_flops(B, S, H, Dh, bwd=False),
               "mha_nar_bwd": mha_flops(B, S, H, Dh, fwd=False),
+              "mha_nar_rope_fwd": mha_flops(B, S, H, Dh, bwd=False),
+              "mha_nar_rope_bwd": mha_flops(B, S, H, Dh, fwd=False),
               "mha_rope_fwd": mha_flops(B, S, H, Dh, bwd=False),
               "mha_rope_bwd": mha_flops(B, S, H, Dh, fwd=False)}
     dom = max((k for k in att if k in kflops), key=lambda k: att[k][0])
@@ -838,6 +841,10 @@ def run_workload(c, name, steps, warmup):
                     max(3, warmup // 4))
     if name == "mhats":      # TwoStageGPT stage 1 (two_stage_train.cpp:168-170, 193): legacy calls
         return _mha(c, name, 32, 256, 64, 8, False, 1301, steps, warmup)
+    if name == "mhatsrope":   # stage 1 with its RoPE (two_stage_gpt.hpp:102-106, :171-174) fused
+        return _mha(c, name, 32, 256, 64, 8, False, 1303, steps, warmup, rope="fused")
+    if name == "mhatsropesep":   # the same as the reference's four calls
+        return _mha(c, name, 32, 256, 64, 8, False, 1303, steps, warmup, rope="separate")
     if name in ("gen1", "gen64", "gen256"):   # generate() forward at B = 1 (probe shape H8 Dh32)
         return _mha(c, name, 1, int(name[3:]), 8, 32, True, 1302, steps, warmup, fwd_only=True)
     if name == "c3":
@@ -943,7 +950,7 @@ def cpu_baseline(name, inputs, nthreads, budget_s):
 # The linear-attention half of the metric (C3 S4096: the fused pair, then the
 # reference-signature chain with its CPU baseline) goes last, so that the end
 # of the printed line -- what a reader of only its tail sees -- carries it.
-SECONDARY = ("c2legacy", "c2dropin", "c5", "mhats", "gen1", "gen64", "gen256", "rope", "c2rope",
+SECONDARY = ("c2legacy", "c2dropin", "c5", "mhats", "mhatsrope", "mhatsropesep", "gen1", "gen64", "gen256", "rope", "c2rope",
              "c2ropesep", "gpt", "gpt768", "gelu", "ffn", "c3s256", "c3fuseds256", "c3lgpt",
              "c3wide", "c3widefused", "c3widerope", "c3wideropesep", "c3rope", "c3ropesep",
              "lgptwide", "c4", "c4fused", "c4hexp", "c3fused", "c3")
@@ -958,7 +965,7 @@ def main():
                     choices=["c2", "c2legacy", "c2dropin", "c2graph", "c3", "c3s256", "c3fused", "c3fuseds256", "c3lgpt",
                              "c3wide", "c3widefused", "c3widerope", "c3wideropesep", "c3rope",
                              "c3ropesep", "lgptwide", "c4", "c4fused", "c4hexp", "c5",
-                             "mhats", "gen1",
+                             "mhats", "mhatsrope", "mhatsropesep", "gen1",
                              "gen64", "gen256", "gpt768", "rope", "c2rope",
                              "c2ropesep", "gpt", "gelu", "ffn", "copy"])
     ap.add_argument("--no-secondary", action="store_true", help="only the reported workload")

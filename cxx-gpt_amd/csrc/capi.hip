@@ -360,12 +360,13 @@ static int mha_bwd_common(const float* Q, const float* K, const float* V, const 
         return CXG_ERR_NULL;
     hipStream_t s = (hipStream_t)stream;
     const int iB = (int)B, iS = (int)S, iH = (int)H, iD = (int)Dh;
-    if (rope == nullptr && mha_nar_ok(iB, iS, iH, iD)) {
+    if (mha_nar_ok(iB, iS, iH, iD)) {
         // one launch that uses no scratch; a caller's workspace is still
         // checked against the documented size, whichever kernels run
         if (workspace != nullptr && workspace_bytes < cxg_mha_bwd_workspace_size(B, S, H, Dh))
             return CXG_ERR_WORKSPACE;
-        return hip_status(mha_nar_bwd_launch(Q, K, V, O, dO, lse, dQ, dK, dV, iB, iS, iH, iD, s));
+        return hip_status(
+            mha_nar_bwd_launch(Q, K, V, O, dO, lse, dQ, dK, dV, iB, iS, iH, iD, s, rope));
     }
     const size_t half = round_up(B * H * S * sizeof(float), 256);
     Scratch ws;

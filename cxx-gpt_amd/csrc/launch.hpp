@@ -86,14 +86,17 @@ hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float*
 // rows staged in LDS (S rounded up to 16, times 8 or 16 columns, at most 4096
 // floats); one workgroup per head, no scratch.  The backward takes lse or,
 // when it is null, recomputes the statistics itself; O (forward) may be null
-// (lse only).  mha_fwd_launch routes plain (no RoPE) forwards of these shapes
-// here; the C ABI's backward does the same.
+// (lse only).  rope (Dh even): Q and K rotated inside, dQ and dK rotated
+// back.  mha_fwd_launch routes forwards of these shapes here; the C ABI's
+// backward does the same.
 bool mha_nar_ok(int B, int S, int H, int Dh);
 hipError_t mha_nar_fwd_launch(const float* Q, const float* K, const float* V, float* O,
-                              float* lse, int B, int S, int H, int Dh, hipStream_t st);
+                              float* lse, int B, int S, int H, int Dh, hipStream_t st,
+                              const MhaRope* rope = nullptr);
 hipError_t mha_nar_bwd_launch(const float* Q, const float* K, const float* V, const float* O,
                               const float* dO, const float* lse, float* dQ, float* dK, float* dV,
-                              int B, int S, int H, int Dh, hipStream_t st);
+                              int B, int S, int H, int Dh, hipStream_t st,
+                              const MhaRope* rope = nullptr);
 hipError_t mha_bwd_prep_launch(const float* O, const float* dO, float* Di, float* dQ,
                                int B, int S, int H, int Dh, hipStream_t st);
 // lse (the statistics pass) and the pre-pass's Di and dQ = 0 in one launch, for

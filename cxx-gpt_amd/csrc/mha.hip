@@ -1466,8 +1466,8 @@ void mha_rope_freqs(int Dh, MhaRope* r)
 hipError_t mha_fwd_launch(const float* Q, const float* K, const float* V, float* O, float* lse,
                           int B, int S, int H, int Dh, hipStream_t st, const MhaRope* rope)
 {
-    if (rope == nullptr && mha_nar_ok(B, S, H, Dh))
-        return mha_nar_fwd_launch(Q, K, V, O, lse, B, S, H, Dh, st);
+    if (mha_nar_ok(B, S, H, Dh))
+        return mha_nar_fwd_launch(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     if (Dh <= 16)
         return fwd_dispatch<16>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
     if (Dh <= 32)

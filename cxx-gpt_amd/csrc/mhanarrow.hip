@@ -107,6 +107,38 @@ __device__ __forceinline__ void lds_kw(float (&o)[KW], const float* p)
     }
 }
 
+// RoPE (the fused entry points): the head's rotary frequencies, w[i] for the
+// pairs (2i, 2i+1) of at most 16 columns, copied into LDS by one lane with
+// uniform indices (scalar reads of the kernel argument); the caller
+// synchronises.
+template <bool ROPE>
+__device__ __forceinline__ void nar_rope_table(float* rw, const MhaRope& rp)
+{
+    if (ROPE && threadIdx.x == 0)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            rw[i] = rp.w[i];
+}
+
+// Rotation of the pair (a, b) at position pos by sign * pos * w.
+__device__ __forceinline__ void rope2(float& a, float& b, int pos, float w, float sign)
+{
+    float sn, cs;
+    sincos_rev(sign * (float)pos * w, &sn, &cs);
+    const float x = a;
+    a = x * cs - b * sn;
+    b = x * sn + b * cs;
+}
+
+// The KW columns d0 .. d0+KW-1 (d0 even) of a row at position pos, rotated.
+template <int KW>
+__device__ __forceinline__ void rope_kw(float (&o)[KW], int pos, int d0, const float* rw)
+{
+#pragma unroll
+    for (int s = 0; s < KW; s += 2)
+        rope2(o[s], o[s + 1], pos, rw[(d0 + s) >> 1], 1.0f);
+}
+
 constexpr int NAR_CH = 4;   // forward: key blocks per score chunk
 constexpr int NAR_CH_STATS = 8;   // the backward's statistics (its registers are shared with dQ)
 
@@ -185,13 +217,17 @@ __device__ __forceinline__ f4 xrow_sum4(f4 v)
 // accumulators a lane).
 constexpr int nar_fwd_waves(int dhp) { return dhp > 8 ? 4 : 5; }
 
-template <int DHP, bool VEC, bool WRITE_O>
+template <int DHP, bool VEC, bool WRITE_O, bool ROPE>
 __global__ __launch_bounds__(NAR_THREADS) __attribute__((amdgpu_waves_per_eu(nar_fwd_waves(DHP))))
 void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K,
                    const float* __restrict__ V, float* __restrict__ O, float* __restrict__ lse,
-                   int S, int H, int Dh, int BH, float qscale)
+                   int S, int H, int Dh, int BH, float qscale, const MhaRope rope)
 {
     extern __shared__ __attribute__((aligned(16))) float nar_lds[];
+    __shared__ float rw[ROPE ? 8 : 1];   // RoPE: Q and K rotated as they are read
+    nar_rope_table<ROPE>(rw, rope);
+    if (ROPE)
+        __syncthreads();
     constexpr int KW = DHP / 4;   // score k-slots per lane (d = KW g + s); 4-column groups of d
     const int nb = (S + 15) >> 4, SP = nb * 16, VLD = SP + 4;
     float* Ks = nar_lds;             // [SP][DHP]
@@ -205,8 +241,10 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
         const int row = u / KW, c = 4 * (u - row * KW);
         const bool ok = row < S;
         const long ro = base + (long)min(row, S - 1) * rs;
-        const f4 k4 = ld_c4<VEC>(K + ro, ok, c, Dh);
+        f4 k4 = ld_c4<VEC>(K + ro, ok, c, Dh);
         const f4 v4 = ld_c4<VEC>(V + ro, ok, c, Dh);
+        if (ROPE)
+            k4 = rope4(k4, row, c, rw, 1.0f);
         *reinterpret_cast<f4*>(&Ks[row * DHP + c]) = k4;
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -228,6 +266,8 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
             const bool qok = qrow < S;
             float qo[KW];
             ld_kw<KW, VEC>(qo, Q + base + (long)min(qrow, S - 1) * rs, qok, KW * g, Dh);
+            if (ROPE)
+                rope_kw<KW>(qo, qrow, KW * g, rw);
 #pragma unroll
             for (int s = 0; s < KW; s++)
                 qo[s] *= qscale;
@@ -318,15 +358,21 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
 // take 4 NBM registers, so 32 blocks (S > 256) leave room for two waves.
 constexpr int nar_bwd_waves(int dhp, int nbm) { return nbm > 16 ? 2 : dhp > 8 ? 3 : 4; }
 
-template <int DHP, bool VEC, bool STATS, int NBM>
+template <int DHP, bool VEC, bool STATS, int NBM, bool ROPE>
 __global__ __launch_bounds__(NAR_THREADS)
 __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ O, const float* __restrict__ dO, const float* __restrict__ lse,
     float* __restrict__ dQ, float* __restrict__ dK, float* __restrict__ dV, int S, int H, int Dh,
-    int BH, float qscale, float scale)
+    int BH, float qscale, float scale, const MhaRope rope)
 {
     extern __shared__ __attribute__((aligned(16))) float nar_lds[];
+    // RoPE: Q and K rotated as they are staged, dQ and dK rotated back as
+    // they are written
+    __shared__ float rw[ROPE ? 8 : 1];
+    nar_rope_table<ROPE>(rw, rope);
+    if (ROPE)
+        __syncthreads();
     constexpr int KW = DHP / 4;
     const int nb = (S + 15) >> 4, SP = nb * 16;
     // Q (pre-scaled) and dO transposed, [d][query] with row stride QLD, and a
@@ -348,14 +394,20 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
         const int row = u / KW, c = 4 * (u - row * KW);
         const bool ok = row < S;
         const long ro = base + (long)min(row, S - 1) * rs;
-        const f4 q4 = ld_c4<VEC>(Q + ro, ok, c, Dh) * qscale;
+        f4 q4 = ld_c4<VEC>(Q + ro, ok, c, Dh);
+        if (ROPE)
+            q4 = rope4(q4, row, c, rw, 1.0f);
+        q4 *= qscale;
         const f4 o4 = ld_c4<VEC>(dO + ro, ok, c, Dh);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             Qt[(c + i) * QLD + row] = q4[i];
             dOt[(c + i) * QLD + row] = o4[i];
         }
-        *reinterpret_cast<f4*>(&Ks[row * DHP + c]) = ld_c4<VEC>(K + ro, ok, c, Dh);
+        f4 k4 = ld_c4<VEC>(K + ro, ok, c, Dh);
+        if (ROPE)
+            k4 = rope4(k4, row, c, rw, 1.0f);
+        *reinterpret_cast<f4*>(&Ks[row * DHP + c]) = k4;
     }
     for (int col = tid; col < SP; col += NAR_THREADS) {
         Qt[DHP * QLD + col] = 0.0f;
@@ -489,11 +541,19 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
                     dqp[I] = mfma16(kt[r], dst[r], dqp[I]);   // dQ^T[d 4g+r][query l16]
             }
             // dK, dV rows of key block j: lane (d = l16, g) holds keys 4g + r
+            // (RoPE: dK rotated back, the pair's other column from lane l16 ^ 1)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int kr = 16 * j + 4 * g + r;
+                float kv = dk[r];
+                if (ROPE) {
+                    const float other = lane_xor16<1>(kv);
+                    float sn, cs;
+                    sincos_rev(-(float)kr * rw[min(l16, DHP - 1) >> 1], &sn, &cs);
+                    kv = (l16 & 1) ? other * sn + kv * cs : kv * cs - other * sn;
+                }
                 if (kr < S && l16 < Dh) {
-                    dK[base + (long)kr * rs + l16] = dk[r] * kLn2;
+                    dK[base + (long)kr * rs + l16] = kv * kLn2;
                     dV[base + (long)kr * rs + l16] = dv[r];
                 }
             }
@@ -523,9 +583,11 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
         const int row = u / KW, c = 4 * (u - row * KW);
         if (c >= Dh)
             continue;
-        const f4 v = (*reinterpret_cast<const f4*>(&Qt[row * DHP + c]) +
-                      *reinterpret_cast<const f4*>(&dOt[row * DHP + c])) *
-                     scale;
+        f4 v = (*reinterpret_cast<const f4*>(&Qt[row * DHP + c]) +
+                *reinterpret_cast<const f4*>(&dOt[row * DHP + c])) *
+               scale;
+        if (ROPE)
+            v = rope4(v, row, c, rw, -1.0f);
         float* qrow = dQ + base + (long)row * rs;
         if (VEC) {
             *reinterpret_cast<f4*>(qrow + c) = v;
@@ -556,40 +618,66 @@ bool mha_nar_ok(int B, int S, int H, int Dh)
 
 template <int DHP, bool VEC>
 static hipError_t nar_fwd_t(const float* Q, const float* K, const float* V, float* O, float* lse,
-                            int B, int S, int H, int Dh, hipStream_t st)
+                            int B, int S, int H, int Dh, hipStream_t st, const MhaRope* rope)
 {
     const int sp = (S + 15) / 16 * 16;
     const size_t lds = ((size_t)sp * DHP + (size_t)DHP * (sp + 4)) * sizeof(float);
     const float qscale = (1.0f / sqrtf((float)Dh)) * kLog2e;
     const dim3 grid((unsigned)(B * H)), block(NAR_THREADS);
     const int BH = B * H;
-    ProfScope ps(st, O != nullptr ? "mha_nar_fwd" : "mha_nar_stats");
-    if (O == nullptr)
-        CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, false>), grid, block, lds, st, Q, K, V, O, lse,
-                   S, H, Dh, BH, qscale);
-    else
-        CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, true>), grid, block, lds, st, Q, K, V, O, lse,
-                   S, H, Dh, BH, qscale);
+    const MhaRope rp = rope != nullptr ? *rope : MhaRope{};
+    ProfScope ps(st, rope != nullptr ? (O != nullptr ? "mha_nar_rope_fwd" : "mha_nar_rope_stats")
+                                     : (O != nullptr ? "mha_nar_fwd" : "mha_nar_stats"));
+    if (rope != nullptr) {
+        if (O == nullptr)
+            CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, false, true>), grid, block, lds, st, Q, K, V,
+                       O, lse, S, H, Dh, BH, qscale, rp);
+        else
+            CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, true, true>), grid, block, lds, st, Q, K, V,
+                       O, lse, S, H, Dh, BH, qscale, rp);
+    } else if (O == nullptr) {
+        CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, false, false>), grid, block, lds, st, Q, K, V, O,
+                   lse, S, H, Dh, BH, qscale, rp);
+    } else {
+        CXG_LAUNCH((mha_nar_fwd_kernel<DHP, VEC, true, false>), grid, block, lds, st, Q, K, V, O,
+                   lse, S, H, Dh, BH, qscale, rp);
+    }
     return hipGetLastError();
 }
 
 hipError_t mha_nar_fwd_launch(const float* Q, const float* K, const float* V, float* O,
-                              float* lse, int B, int S, int H, int Dh, hipStream_t st)
+                              float* lse, int B, int S, int H, int Dh, hipStream_t st,
+                              const MhaRope* rope)
 {
-    if (!mha_nar_ok(B, S, H, Dh))
+    if (!mha_nar_ok(B, S, H, Dh) || (rope != nullptr && Dh % 2 != 0))
         return hipErrorInvalidValue;
     const bool vec = Dh % 4 == 0 && nar_al16(Q) && nar_al16(K) && nar_al16(V) && nar_al16(O);
     if (Dh <= 8)
-        return vec ? nar_fwd_t<8, true>(Q, K, V, O, lse, B, S, H, Dh, st)
-                   : nar_fwd_t<8, false>(Q, K, V, O, lse, B, S, H, Dh, st);
-    return vec ? nar_fwd_t<16, true>(Q, K, V, O, lse, B, S, H, Dh, st)
-               : nar_fwd_t<16, false>(Q, K, V, O, lse, B, S, H, Dh, st);
+        return vec ? nar_fwd_t<8, true>(Q, K, V, O, lse, B, S, H, Dh, st, rope)
+                   : nar_fwd_t<8, false>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
+    return vec ? nar_fwd_t<16, true>(Q, K, V, O, lse, B, S, H, Dh, st, rope)
+               : nar_fwd_t<16, false>(Q, K, V, O, lse, B, S, H, Dh, st, rope);
+}
+
+template <int DHP, bool VEC, int NBM, bool ROPE>
+static void nar_bwd_go(const float* Q, const float* K, const float* V, const float* O,
+                       const float* dO, const float* lse, float* dQ, float* dK, float* dV, int S,
+                       int H, int Dh, int BH, float qscale, float scale, const MhaRope& rp,
+                       size_t lds, hipStream_t st)
+{
+    const dim3 grid((unsigned)BH), block(NAR_THREADS);
+    if (lse == nullptr)
+        CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, true, NBM, ROPE>), grid, block, lds, st, Q, K, V,
+                   O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale, rp);
+    else
+        CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, false, NBM, ROPE>), grid, block, lds, st, Q, K,
+                   V, O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale, rp);
 }
 
 template <int DHP, bool VEC>
 static hipError_t nar_bwd_t(const float* Q, const float* K, const float* V, const float* O,
                             const float* dO, const float* lse, float* dQ, float* dK, float* dV,
-                            int B, int S, int H, int Dh, hipStream_t st)
+                            int B, int S, int H, int Dh, hipStream_t st, const MhaRope* rope)
 {
     const int sp = (S + 15) / 16 * 16;
     const size_t lds = ((size_t)2 * (DHP + 1) * (sp + 4) + (size_t)sp * DHP + 2 * (size_t)sp +
@@ -597,23 +685,23 @@ static hipError_t nar_bwd_t(const float* Q, const float* K, const float* V, cons
                        sizeof(float);
     const float scale = 1.0f / sqrtf((float)Dh);
     const float qscale = scale * kLog2e;
-    const dim3 grid((unsigned)(B * H)), block(NAR_THREADS);
     const int BH = B * H;
-    ProfScope ps(st, "mha_nar_bwd");
+    const MhaRope rp = rope != nullptr ? *rope : MhaRope{};
+    ProfScope ps(st, rope != nullptr ? "mha_nar_rope_bwd" : "mha_nar_bwd");
     if (sp <= 256) {
-        if (lse == nullptr)
-            CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, true, 16>), grid, block, lds, st, Q, K, V, O,
-                       dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale);
+        if (rope != nullptr)
+            nar_bwd_go<DHP, VEC, 16, true>(Q, K, V, O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale,
+                                           scale, rp, lds, st);
         else
-            CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, false, 16>), grid, block, lds, st, Q, K, V,
-                       O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale);
+            nar_bwd_go<DHP, VEC, 16, false>(Q, K, V, O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale,
+                                            scale, rp, lds, st);
     } else if constexpr (DHP == 8) {   // S_pad * DHP <= 4096: 32 blocks at most
-        if (lse == nullptr)
-            CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, true, 32>), grid, block, lds, st, Q, K, V, O,
-                       dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale);
+        if (rope != nullptr)
+            nar_bwd_go<DHP, VEC, 32, true>(Q, K, V, O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale,
+                                           scale, rp, lds, st);
         else
-            CXG_LAUNCH((mha_nar_bwd_kernel<DHP, VEC, false, 32>), grid, block, lds, st, Q, K, V,
-                       O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale, scale);
+            nar_bwd_go<DHP, VEC, 32, false>(Q, K, V, O, dO, lse, dQ, dK, dV, S, H, Dh, BH, qscale,
+                                            scale, rp, lds, st);
     } else {
         return hipErrorInvalidValue;   // excluded by mha_nar_ok
     }
@@ -622,17 +710,17 @@ static hipError_t nar_bwd_t(const float* Q, const float* K, const float* V, cons
 
 hipError_t mha_nar_bwd_launch(const float* Q, const float* K, const float* V, const float* O,
                               const float* dO, const float* lse, float* dQ, float* dK, float* dV,
-                              int B, int S, int H, int Dh, hipStream_t st)
+                              int B, int S, int H, int Dh, hipStream_t st, const MhaRope* rope)
 {
-    if (!mha_nar_ok(B, S, H, Dh))
+    if (!mha_nar_ok(B, S, H, Dh) || (rope != nullptr && Dh % 2 != 0))
         return hipErrorInvalidValue;
     const bool vec = Dh % 4 == 0 && nar_al16(Q) && nar_al16(K) && nar_al16(V) && nar_al16(O) &&
                      nar_al16(dO) && nar_al16(dQ) && nar_al16(dK) && nar_al16(dV);
     if (Dh <= 8)
-        return vec ? nar_bwd_t<8, true>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st)
-                   : nar_bwd_t<8, false>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st);
-    return vec ? nar_bwd_t<16, true>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st)
-               : nar_bwd_t<16, false>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st);
+        return vec ? nar_bwd_t<8, true>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st, rope)
+                   : nar_bwd_t<8, false>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st, rope);
+    return vec ? nar_bwd_t<16, true>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st, rope)
+               : nar_bwd_t<16, false>(Q, K, V, O, dO, lse, dQ, dK, dV, B, S, H, Dh, st, rope);
 }
 
 } // namespace cxg

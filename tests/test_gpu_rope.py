@@ -124,6 +124,9 @@ def _fused_refs(Q, K, V, B, S, H, Dh):
     (8, 256, 12, 64),    # the C2 shape (stage-1 heads of two_stage_gpt.hpp)
     (1, 1000, 2, 64),    # positions up to 999
     (2, 65, 2, 16), (1, 100, 3, 32), (1, 130, 2, 128), (1, 70, 1, 256), (3, 7, 2, 8),
+    # narrow heads (one workgroup per head): TwoStageGPT's stage 1, the
+    # longest sequence at Dh <= 8, Dh not a multiple of 4, 16-column padding
+    (32, 256, 64, 8), (1, 512, 2, 8), (2, 100, 3, 6), (2, 250, 2, 12),
 ])
 def test_fused_mha_rope(dev, B, S, H, Dh):
     """cxg_mha_rope_fwd/bwd == rope_fwd; fused_mha_fwd; fused_mha_bwd; rope_bwd
