@@ -28,6 +28,9 @@
 //             whose per-query-block partials stay in the wave's registers
 //             until the four waves add theirs through LDS at the end.  dQ
 //             leaves once: no atomics, no zeroing pass, no scratch.
+// The fused RoPE calls (cxg_mha_rope_fwd/bwd, two_stage_gpt.hpp:102-106,
+// :171-174) take the same kernels: Q and K rows are rotated as they are read
+// or staged, dQ and dK rotated back as they are written.
 // Products run on FP32 MFMA: the score contractions (S, dP) as 16x16x4 over
 // DHP/4 steps, dQ, dV and dK as 16x16x4 with the head columns padded to 16
 // (4x4x1 blocks for dV and dK measured no faster: their registers cost a wave
