@@ -119,9 +119,11 @@ def lin_kernel_bytes(Bq, S, D, fused=False):
             "lin_wide_bwd": 4 * T + r + 3 * T}   # Q, K, V, dnum, dden -> dQ, dK, dV
     if fused:
         return {"lin_fwd": 3 * T + T + r,        # Q,K,V -> O, den
+                "lin_seqfwd": 3 * T + T + r,     # the same forward in one launch (S <= 256)
                 "lin_bwd": 5 * T + r + 3 * T,    # Q,K,V,O,dO, den -> dQ, dK, dV
                 "lin_wide_fwd": 3 * T + T + r, **quad}
     return {"lin_fwd": 3 * T + 2 * T + r,        # Q,K,V -> O, z_cache, den
+            "lin_seqfwd": 3 * T + 2 * T + r,
             "lin_step1": 2 * T + r + T + r,      # O, dO, den -> dnum, dden
             "lin_dq": 5 * T + r + T,             # K, V, dnum, z_cache, Q, dden -> dQ
             "lin_dkdv": 4 * T + r + 2 * T,       # Q, K, V, dnum, dden -> dK, dV
@@ -206,7 +208,7 @@ def attribute(cx, step, steps):
     out = {}
     for n in ("mha_fwd", "mha_stats", "mha_bwd_prep", "mha_bwd", "mha_nar_fwd", "mha_nar_stats",
               "mha_nar_bwd", "mha_nar_rope_fwd", "mha_nar_rope_bwd", "lin_agg", "lin_scan",
-              "lin_seqrec", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
+              "lin_seqrec", "lin_seqfwd", "lin_fwd", "lin_step1", "lin_dq", "lin_dkdv", "lin_bagg", "lin_bscan", "lin_bwd",
               "lin_wide_fwd", "lin_wide_fin", "lin_wide_dq", "lin_wide_dkdv", "lin_wide_bwd",
               "lin_wide_state", "lin_qs_feat", "lin_qs_score", "lin_qs_bscore", "lin_qs_out",
               "lin_qs_grad", "lin_qs_zc", "gpt_qs_score", "gpt_qs_softmax", "gpt_qs_out",

@@ -1499,6 +1499,14 @@ static hipError_t fwd_impl(const float* Q, const float* K, const float* V, float
         }
     }
     float* wsf = (float*)ws;
+    if constexpr (PHI == PHI_ELU1 || PHI == PHI_ELU1_LG || PHI == PHI_NONE) {
+        // short sequences at D = E = 64: records and outputs in one launch
+        // (the segment records still go to ws, where a context takes them)
+        if (mode == 2 && lin_seqfwd_ok(S))
+            return lin_seqfwd_launch<PHI>(Q, K, V, O, den, zc, p.nseg > 1 ? wsf : nullptr, p.nseg,
+                                          p.L, Sfin, zfin, sfin_de, ctot, ztab, anch, den_eps, Bq,
+                                          S, st);
+    }
     if (p.nseg > 1) {
         hipError_t e = agg_and_scan<PHI>(p, K, V, nullptr, wsf, Bq, S, D, E, 0, mode, st);
         if (e != hipSuccess)

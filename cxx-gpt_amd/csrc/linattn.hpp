@@ -143,6 +143,17 @@ int lin_seq_cpw(int nch, int cps);
 template <int PHI>
 hipError_t lin_seqrec_launch(const float* X, const float* Y, const float* w, float* ws, int Bq,
                              int S, int D, int E, int L, int nseg, int reverse, hipStream_t st);
+// The whole forward of short sequences (S <= 256) at D = E = 64 in one launch
+// (linseq.hip): O, den, z_cache (nullable) and the outputs lin_fwd_launch
+// documents (Sfin/zfin, ctot/ztab/anch, nullable); rec (nullable) receives the
+// prefix records of the plan's segments (nseg segments of L rows), as the
+// records pass would have written them.  No RoPE or Hadamard+Exp map.
+bool lin_seqfwd_ok(int S);
+template <int PHI>
+hipError_t lin_seqfwd_launch(const float* Q, const float* K, const float* V, float* O, float* den,
+                             float* zc, float* rec, int nseg, int L, float* Sfin, float* zfin,
+                             int sfin_de, float* ctot, float* ztab, float* anch, int den_eps,
+                             int Bq, int S, hipStream_t st);
 // Wide heads (64 < max(D, E) <= LIN_WIDE_MAX, linwide.hip): the quadratic
 // form on FP32 MFMA.  Forward: O, den (den_eps as lin_fwd_launch) and
 // z_cache (nullable).

@@ -9,7 +9,8 @@ every API whose scans use those records at shapes that take that path
 with the oracle: the two_stage chain (kernel_attn_fwd -> step1 -> dQ ->
 dKdV, two_stage_cuda_kernels.cu:1133-1809), the fused pair (its forward) with
 and without the forward's context, and the linear_cuda pair (phi applied
-outside, linear_cuda_kernels.cu:10-298).  Shapes cover one and two chunks per
+outside, linear_cuda_kernels.cu:10-298).  At D = E = 64 and S <= 256 the
+whole forward (records, outputs and context) is one launch (lin_seqfwd).  Shapes cover one and two chunks per
 wave, partial last chunks and segments, widths below 64, and mean-shifted V
 at S = 256.
 """
@@ -27,6 +28,12 @@ pytestmark = pytest.mark.gpu
 # 200 end in a partial chunk and a partial segment
 SHAPES = [(96, 256, 64, 64), (5, 200, 64, 64), (2, 129, 64, 64), (7, 384, 64, 64),
           (3, 512, 48, 40), (4, 256, 20, 64)]
+
+
+def _one_launch_fwd(S, D, E):
+    """The forward's records and outputs in one launch (lin_seqfwd): D = E =
+    64, at most 16 chunks."""
+    return D == 64 and E == 64 and S <= 256
 
 
 def _count(name):
@@ -47,7 +54,7 @@ class _Launches:
         import torch
         import cxxgpt_attn as cx
         torch.cuda.synchronize()
-        self.n = {k: _count(k) for k in ("lin_seqrec", "lin_agg", "lin_scan")}
+        self.n = {k: _count(k) for k in ("lin_seqrec", "lin_seqfwd", "lin_agg", "lin_scan")}
         cx.prof_enable(False)
         cx.prof_reset()
         return False
@@ -59,7 +66,9 @@ def test_chain(dev, B, S, D, E):
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 40 * S + D + E)
     with _Launches() as L:
         check_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"chain B{B}S{S}D{D}E{E}")
-    assert L.n["lin_seqrec"] == 3 and L.n["lin_agg"] == 0 and L.n["lin_scan"] == 0, L.n
+    one = _one_launch_fwd(S, D, E)
+    assert L.n["lin_seqrec"] == 3 - one and L.n["lin_seqfwd"] == one, L.n
+    assert L.n["lin_agg"] == 0 and L.n["lin_scan"] == 0, L.n
 
 
 @pytest.mark.parametrize("use_ctx", [False, True])
@@ -71,7 +80,9 @@ def test_fused(dev, B, S, D, E, use_ctx):
     with _Launches() as L:
         check_fused_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"fused B{B}S{S}D{D}E{E}",
                           use_ctx=use_ctx)
-    assert L.n["lin_seqrec"] == 1 and L.n["lin_agg"] == 0 and L.n["lin_scan"] == 0, L.n
+    one = _one_launch_fwd(S, D, E)
+    assert L.n["lin_seqrec"] == 1 - one and L.n["lin_seqfwd"] == one, L.n
+    assert L.n["lin_agg"] == 0 and L.n["lin_scan"] == 0, L.n
 
 
 @pytest.mark.parametrize("B,S,D,E", [(96, 256, 64, 64), (5, 200, 64, 64), (3, 512, 48, 40)])
@@ -82,7 +93,8 @@ def test_linear_cuda_pair(dev, B, S, D, E):
     for use_ctx in (False, True):
         with _Launches() as L:
             fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu B{B}S{S}", use_ctx=use_ctx)
-        assert L.n["lin_seqrec"] == 1, L.n
+        one = _one_launch_fwd(S, D, E)
+        assert L.n["lin_seqrec"] == 1 - one and L.n["lin_seqfwd"] == one, L.n
 
 
 @pytest.mark.parametrize("use_ctx", [False, True])
@@ -114,7 +126,7 @@ def test_records_match_two_launch_path(dev):
             g = check_kattn(dev, Q, K, V, dO, B, S, D, E, tag=f"B{B}S{S}")
         outs.append(g)
         if S == 256:
-            assert L.n["lin_seqrec"] == 3, L.n
+            assert L.n["lin_seqrec"] == 2 and L.n["lin_seqfwd"] == 1, L.n
         else:
             assert L.n["lin_seqrec"] == 0 and L.n["lin_agg"] == 3, L.n
     # rows 0..255 are the first sequence in both splits: dQ of a row depends
