@@ -1,4 +1,5 @@
-// linseq.hip -- segment records of short sequences in one pass (gfx950).
+// linseq.hip -- segment records of short sequences in one pass, and the whole
+// forward of sequences of at most 16 chunks in one launch (gfx950).
 //
 // The chunked linear-attention scans of the forward, dQ and dK/dV passes
 // (linattn.hip) start each segment of a sequence from a record of the
