@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle as orc
-from helpers import normal_inputs
+from helpers import assert_close, normal_inputs
 from test_gpu_linbwd import check_fused_kattn, fused_lcu
 from test_gpu_linear import check_kattn
 
@@ -132,3 +132,47 @@ def test_records_match_two_launch_path(dev):
     # rows 0..255 are the first sequence in both splits: dQ of a row depends
     # only on the rows up to it
     np.testing.assert_allclose(outs[0]["dQ"][:256], outs[1]["dQ"][:256], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("S", [256, 200, 137])
+def test_state_outputs_one_launch(dev, S):
+    """The one-launch forward's final-state outputs: S_buf ([d][e] for
+    linear_cuda, [e][d] for two_stage) and z_buf, with O, den and z_cache,
+    at D = E = 64 (full, partial-chunk and partial-segment lengths)."""
+    import torch
+    import cxxgpt_attn as cx
+    from test_gpu_linwide import _state_bound_check
+    B, D, E = 3, 64, 64
+    N = B * S
+    Q, K, V, _ = normal_inputs((N, D), (N, E), 1200 + S)
+    Qp, Kp = orc.phi_elu_forward(Q, D, D), orc.phi_elu_forward(K, D, D)
+
+    def nan(*shape):
+        return torch.full(shape, float("nan"), device=dev)
+
+    def t(a):
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+
+    O, den, zc, Sb, zb = nan(N, E), nan(N), nan(N, D), nan(B * D, E), nan(B, D)
+    O2, den2, zc2, Sb2, zb2 = nan(N, E), nan(N), nan(N, D), nan(B * E, D), nan(B, D)
+    with _Launches() as L:
+        cx.lin_fwd(t(Qp), t(Kp), t(V), O, den, zc, Sb, zb, B, S, D, E)
+        cx.kattn_fwd(t(Q), t(K), t(V), O2, den2, zc2, Sb2, zb2, B, S, D, E)
+    assert L.n["lin_seqfwd"] == 2 and L.n["lin_seqrec"] == 0, L.n
+    rO, rden, rzc, rSb, rzb = orc.lcu_fwd(Qp, Kp, V, B, S, D, E, nthreads=8)
+    np_ = lambda x: x.cpu().numpy()   # noqa: E731
+    assert_close(np_(O), rO, "lcu O")
+    assert_close(np_(den), rden, "lcu den_cache")
+    assert_close(np_(zc), rzc, "lcu z_cache")
+    assert_close(np_(zb), rzb, "lcu z_buf")
+    kO, kden, kzc = orc.kattn_fwd(Q, K, V, B, S, D, E, nthreads=8)
+    assert_close(np_(O2), kO, "two_stage O")
+    assert_close(np_(den2), kden, "two_stage den")
+    assert_close(np_(zc2), kzc, "two_stage z_cache")
+    pK = np.where(K > 0, K + 1.0, np.exp(K.astype(np.float64)))
+    for b in range(B):
+        sl = slice(b * S, (b + 1) * S)
+        _state_bound_check(np_(Sb)[b * D:(b + 1) * D], Kp[sl], V[sl], f"lcu S_buf seq{b}")
+        _state_bound_check(np_(Sb2)[b * E:(b + 1) * E], pK[sl], V[sl],
+                           f"two_stage S_buf [e][d] seq{b}", transpose=True)
+        assert_close(np_(zb2)[b], pK[sl].sum(0), f"two_stage z_buf seq{b}")
