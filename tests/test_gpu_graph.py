@@ -68,6 +68,45 @@ def test_mha_fwd_bwd_graph_replay(dev):
         assert_close(gdQ.cpu().numpy(), edQ.cpu().numpy(), f"replay {rep}: dQ")
 
 
+@pytest.mark.parametrize("use_lse", [True, False])
+def test_mha_narrow_graph_replay(dev, use_lse):
+    """Narrow heads (one workgroup per head, no atomics): every output of every
+    replay bit-identical to the eager run, with the forward's lse and with
+    the reference's signature (statistics recomputed in the backward), RoPE
+    fused."""
+    import torch
+    import cxxgpt_attn as cx
+    B, S, H, Dh = 3, 200, 8, 8
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    shp = (B * S, H * Dh)
+    Q, K, V, dO = [torch.empty(shp, device=dev) for _ in range(4)]
+
+    def outs():
+        return ([torch.empty(shp, device=dev) for _ in range(4)],
+                torch.empty(B * H * S, device=dev))
+
+    def chain(O, dQ, dK, dV, lse, stream):
+        cx.mha_rope_fwd(Q, K, V, O, B, S, H, Dh, lse=lse, stream=stream)
+        cx.mha_rope_bwd(Q, K, V, O, dO, dQ, dK, dV, B, S, H, Dh,
+                        lse=lse if use_lse else None, stream=stream)
+
+    _refill(torch, gen, (Q, K, V, dO))
+    (gO, gdQ, gdK, gdV), glse = outs()
+    graph = _capture(torch, lambda s: chain(gO, gdQ, gdK, gdV, glse, s))
+    (eO, edQ, edK, edV), e_lse = outs()
+    for rep in range(3):
+        _refill(torch, gen, (Q, K, V, dO))
+        torch.cuda.synchronize()
+        chain(eO, edQ, edK, edV, e_lse, None)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b, name in ((gO, eO, "O"), (glse, e_lse, "lse"), (gdQ, edQ, "dQ"),
+                           (gdK, edK, "dK"), (gdV, edV, "dV")):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager run"
+
+
 def test_linear_two_stage_graph_replay(dev):
     import torch
     import cxxgpt_attn as cx
