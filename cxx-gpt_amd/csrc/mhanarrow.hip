@@ -143,19 +143,22 @@ __device__ __forceinline__ void rope_kw(float (&o)[KW], int pos, int d0, const f
 }
 
 constexpr int NAR_CH = 4;   // forward: key blocks per score chunk
+// The softmax reference moves when a score passes it by more than this (log2
+// units): probabilities stay below 2^8, so no sum can overflow.
+constexpr float kNarHead = 8.0f;
 constexpr int NAR_CH_STATS = 8;   // the backward's statistics (its registers are shared with dQ)
 
 // S^T block (i, j) from Ks ([SP][DHP] rows) and the query operand qo (query
-// l16, columns KW g + s, pre-scaled to log2 units): lane (l16, g) element r
-// is key 16j + 4g + r.  DIAG (j == i): the keys after the lane's query -inf.
+// l16, columns KW g + s, pre-scaled to log2 units), added to a: lane (l16, g)
+// element r is key 16j + 4g + r.  DIAG (j == i): the keys after the lane's
+// query -inf.
 template <int DHP, bool DIAG>
 __device__ __forceinline__ f4 nar_score(const float* Ks, const float (&qo)[DHP / 4], int j,
-                                        int l16, int g)
+                                        int l16, int g, f4 a)
 {
     constexpr int KW = DHP / 4;
     float ka[KW];
     lds_kw<KW>(ka, &Ks[(16 * j + l16) * DHP + KW * g]);
-    f4 a = f4zero();
 #pragma unroll
     for (int s = 0; s < KW; s++)
         a = mfma16(ka[s], qo[s], a);   // S^T[key 4g+r][query l16]
@@ -167,30 +170,25 @@ __device__ __forceinline__ f4 nar_score(const float* Ks, const float (&qo)[DHP /
     return a;
 }
 
-__device__ __forceinline__ float max4(f4 a) { return fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])); }
-
-// One chunk of a query block's row: the blocks j0 + J < i (J < CH) in sc,
-// and the diagonal block (i) in sd when this chunk holds it.  Returns the
-// chunk's maximum for the lane's query (over the four lanes that share it).
-// Entries past the row are not written.
-template <int DHP, int CH>
-__device__ __forceinline__ float nar_chunk_scores(f4 (&sc)[CH], f4& sd, const float* Ks,
-                                                  const float (&qo)[DHP / 4], int i, int j0,
-                                                  int l16, int g)
+// max(a, b) of non-NaN values as one v_med3_f32 (the median of a, b and +inf).
+// fmaxf also quiets signalling NaNs: a v_max_f32 x, x per operand the compiler
+// cannot prove quiet, i.e. per MFMA result.
+__device__ __forceinline__ float fmax_nn(float a, float b)
 {
-    float cm = -INFINITY;
-#pragma unroll
-    for (int J = 0; J < CH; J++) {
-        if (j0 + J < i) {   // wave-uniform
-            sc[J] = nar_score<DHP, false>(Ks, qo, j0 + J, l16, g);
-            cm = fmaxf(cm, max4(sc[J]));
-        }
-    }
-    if (i < j0 + CH) {
-        sd = nar_score<DHP, true>(Ks, qo, i, l16, g);
-        cm = fmaxf(cm, max4(sd));
-    }
-    return xrow_max(cm);
+    // +inf from an opaque scalar move, so that the compiler keeps the median
+    // (with a constant +inf it folds it back into fmaxf)
+    float inf;
+    asm("s_mov_b32 %0, 0x7f800000" : "=s"(inf));
+    return __builtin_amdgcn_fmed3f(a, b, inf);
+}
+
+__device__ __forceinline__ float max4(f4 a) { return fmax_nn(fmax_nn(a[0], a[1]), fmax_nn(a[2], a[3])); }
+
+// Maximum over the four lanes l16 + 16g that share a query.
+__device__ __forceinline__ float nar_xrow_max(float v)
+{
+    v = fmax_nn(v, __shfl_xor(v, 16, 64));
+    return fmax_nn(v, __shfl_xor(v, 32, 64));
 }
 
 // 4x4x1 FP32 MFMA, 16 independent 4x4 blocks (2 passes, the 16x16x4 form's
@@ -218,7 +216,7 @@ __device__ __forceinline__ f4 xrow_sum4(f4 v)
 // ---------------------------------------------------------------------------
 // Waves per SIMD the forward is compiled for (16-column heads hold four O
 // accumulators a lane).
-constexpr int nar_fwd_waves(int dhp) { return dhp > 8 ? 4 : 5; }
+constexpr int nar_fwd_waves(int dhp) { return dhp > 8 ? 4 : 6; }
 
 template <int DHP, bool VEC, bool WRITE_O, bool ROPE>
 __global__ __launch_bounds__(NAR_THREADS) __attribute__((amdgpu_waves_per_eu(nar_fwd_waves(DHP))))
@@ -259,35 +257,33 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
     const int npair = (nb + 1) >> 1;
     const float* vrow = &Vt[(l16 & 3) * VLD + 4 * g];   // this lane's V^T operand row, group 0
-    for (int p = w; p < npair; p += 4) {
-#pragma unroll 1
-        for (int hf = 0; hf < 2; hf++) {
-            const int i = hf == 0 ? nb - 1 - p : p;
-            if (hf == 1 && i == nb - 1 - p)
-                break;   // the middle block of an odd count
+    auto qblock = [&](int i, float (&qo)[KW]) __attribute__((always_inline)) {
             const int qrow = 16 * i + l16;
             const bool qok = qrow < S;
-            float qo[KW];
-            ld_kw<KW, VEC>(qo, Q + base + (long)min(qrow, S - 1) * rs, qok, KW * g, Dh);
             if (ROPE)
                 rope_kw<KW>(qo, qrow, KW * g, rw);
 #pragma unroll
             for (int s = 0; s < KW; s++)
                 qo[s] *= qscale;
-            // chunks of NAR_CH key blocks: scores, the chunk's maximum, then
-            // the probabilities and O += P V (oacc[c]: O[query l16][4c + m]
-            // over keys 4g .. 4g+3 of each block); the sums are rescaled when a
-            // later chunk raises the maximum
+            // Online softmax with a lazy reference m (log2 units, the same in
+            // the four lanes of a query): block 0's exact maximum first (key 0
+            // is visible to every query, so it is finite), then every score
+            // accumulator starts at -m, so scores come out relative to m; m
+            // moves only when a score of the wave passes it by more than
+            // kNarHead, so the probabilities stay below 2^kNarHead and most
+            // blocks need no subtraction, no cross-lane maximum and no
+            // rescale.  O accumulates as oacc[c]: O[query l16][4c + m] over
+            // keys 4g .. 4g+3 of each block.
             f4 oacc[KW];
 #pragma unroll
             for (int c = 0; c < KW; c++)
                 oacc[c] = f4zero();
-            float m = -INFINITY, lsum = 0.0f;
+            float lsum = 0.0f;
             auto pv = [&](const f4& sv, int j) __attribute__((always_inline)) {
                 f4 pr;
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    pr[r] = fast_exp2(sv[r] - m);
+                    pr[r] = fast_exp2(sv[r]);
                 lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
                 if (WRITE_O) {
 #pragma unroll
@@ -300,24 +296,54 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
                     }
                 }
             };
-            for (int j0 = 0; j0 <= i; j0 += NAR_CH) {
-                f4 sc[NAR_CH], sd;
-                const float mn =
-                    fmaxf(m, nar_chunk_scores<DHP, NAR_CH>(sc, sd, Ks, qo, i, j0, l16, g));
-                if (j0 > 0) {
-                    const float f = fast_exp2(m - mn);
+            f4 s0 = i == 0 ? nar_score<DHP, true>(Ks, qo, 0, l16, g, f4zero())
+                           : nar_score<DHP, false>(Ks, qo, 0, l16, g, f4zero());
+            float m = nar_xrow_max(max4(s0));
+            s0 -= m;
+            f4 nm = f4zero() - m;
+            pv(s0, 0);
+            // raise m by d >= 0 (per query) when a relative score of the wave
+            // passes kNarHead; the scores in hand move with it
+            auto raise = [&](float bm, f4* sv, int n) __attribute__((always_inline)) {
+                if (__builtin_amdgcn_ballot_w64(bm > kNarHead) != 0) {   // wave-uniform
+                    const float d = fmax_nn(nar_xrow_max(bm), 0.0f);
+                    const float f = fast_exp2(-d);
 #pragma unroll
                     for (int c = 0; c < KW; c++)
                         oacc[c] *= f;
                     lsum *= f;
+                    m += d;
+                    nm = f4zero() - m;
+                    for (int J = 0; J < n; J++)
+                        sv[J] -= d;
                 }
-                m = mn;
+            };
+            // whole chunks of NAR_CH blocks below the diagonal (straight-line:
+            // every score first, one reference check), then single blocks,
+            // then the diagonal block with the causal mask
+            int j = 1;
+            for (; j + NAR_CH <= i; j += NAR_CH) {
+                f4 sc[NAR_CH];
+                float cm = -INFINITY;
+#pragma unroll
+                for (int J = 0; J < NAR_CH; J++) {
+                    sc[J] = nar_score<DHP, false>(Ks, qo, j + J, l16, g, nm);
+                    cm = fmax_nn(cm, max4(sc[J]));
+                }
+                raise(cm, sc, NAR_CH);
 #pragma unroll
                 for (int J = 0; J < NAR_CH; J++)
-                    if (j0 + J < i)
-                        pv(sc[J], j0 + J);
-                if (i < j0 + NAR_CH)
-                    pv(sd, i);
+                    pv(sc[J], j + J);
+            }
+            for (; j < i; j++) {
+                f4 sv = nar_score<DHP, false>(Ks, qo, j, l16, g, nm);
+                raise(max4(sv), &sv, 1);
+                pv(sv, j);
+            }
+            if (i > 0) {
+                f4 sv = nar_score<DHP, true>(Ks, qo, i, l16, g, nm);
+                raise(max4(sv), &sv, 1);
+                pv(sv, i);
             }
             const float l = xrow_sum(lsum);
             if (WRITE_O) {
@@ -331,7 +357,7 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
                         o = t;
                 }
                 if (qok && g < KW) {
-                    o *= 1.0f / l;
+                    o *= __builtin_amdgcn_rcpf(l);   // hardware reciprocal, within 1 ulp
                     float* orow = O + base + (long)qrow * rs;
                     if (VEC && 4 * g + 3 < Dh) {
                         *reinterpret_cast<f4*>(orow + 4 * g) = o;
@@ -345,6 +371,17 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
             }
             if (lse != nullptr && qok && g == 0)
                 lse[(long)bh * S + qrow] = (m + fast_log2(l)) * kLn2;
+    };
+    for (int p = w; p < npair; p += 4) {
+#pragma unroll 1
+        for (int hf = 0; hf < 2; hf++) {
+            const int i = hf == 0 ? nb - 1 - p : p;
+            if (hf == 1 && i == nb - 1 - p)
+                break;   // the middle block of an odd count
+            float qo[KW];
+            const int qrow = 16 * i + l16;
+            ld_kw<KW, VEC>(qo, Q + base + (long)min(qrow, S - 1) * rs, qrow < S, KW * g, Dh);
+            qblock(i, qo);
         }
     }
 }
@@ -385,8 +422,10 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
     float* Qt = nar_lds;                  // [DHP + 1][QLD]
     float* dOt = Qt + (DHP + 1) * QLD;    // [DHP + 1][QLD]
     float* Ks = dOt + (DHP + 1) * QLD;    // [SP][DHP]
-    float* L2 = Ks + SP * DHP;            // [SP] lse * log2(e); +inf past S
-    float* Dd = L2 + SP;              // [SP] Di
+    // negated, so that they start the S and dP accumulators: S - lse and
+    // dP - Di come out of the MFMAs
+    float* L2 = Ks + SP * DHP;            // [SP] -lse * log2(e); -inf past S
+    float* Dd = L2 + SP;              // [SP] -Di
     float* T = Dd + SP;               // [4][16][NAR_TLD] transpose tiles
     const int bh = nar_head((int)blockIdx.x, BH), b = bh / H, h = bh - b * H;
     const long rs = (long)H * Dh;
@@ -426,9 +465,9 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
                 di += (o4[0] * g4[0] + o4[1] * g4[1]) + (o4[2] * g4[2] + o4[3] * g4[3]);
             }
         }
-        Dd[row] = di;
+        Dd[row] = -di;
         if (!STATS)
-            L2[row] = row < S ? lse[(long)bh * S + row] * kLog2e : INFINITY;
+            L2[row] = row < S ? -lse[(long)bh * S + row] * kLog2e : -INFINITY;
     }
     __syncthreads();
 
@@ -448,28 +487,51 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
 #pragma unroll
                 for (int s = 0; s < KW; s++)
                     qo[s] = Qt[(KW * g + s) * QLD + 16 * i + l16];
-                float m = -INFINITY, lsum = 0.0f;
-                for (int j0 = 0; j0 <= i; j0 += NAR_CH_STATS) {
-                    f4 sc[NAR_CH_STATS], sd;
-                    const float mn = fmaxf(
-                        m, nar_chunk_scores<DHP, NAR_CH_STATS>(sc, sd, Ks, qo, i, j0, l16, g));
-                    lsum *= fast_exp2(m - mn);   // 0 * 0 on the first chunk
-                    m = mn;
-#pragma unroll
-                    for (int J = 0; J < NAR_CH_STATS; J++)
-                        if (j0 + J < i)
-#pragma unroll
-                            for (int r = 0; r < 4; r++)
-                                lsum += fast_exp2(sc[J][r] - m);
-                    if (i < j0 + NAR_CH_STATS)
+                // lazy reference, as in the forward
+                f4 s0 = i == 0 ? nar_score<DHP, true>(Ks, qo, 0, l16, g, f4zero())
+                               : nar_score<DHP, false>(Ks, qo, 0, l16, g, f4zero());
+                float m = nar_xrow_max(max4(s0));
+                s0 -= m;
+                f4 nm = f4zero() - m;
+                float lsum = (fast_exp2(s0[0]) + fast_exp2(s0[1])) +
+                             (fast_exp2(s0[2]) + fast_exp2(s0[3]));
+                auto take = [&](f4* sv, int n, float bm) __attribute__((always_inline)) {
+                    if (__builtin_amdgcn_ballot_w64(bm > kNarHead) != 0) {   // wave-uniform
+                        const float d = fmax_nn(nar_xrow_max(bm), 0.0f);
+                        lsum *= fast_exp2(-d);
+                        m += d;
+                        nm = f4zero() - m;
+                        for (int J = 0; J < n; J++)
+                            sv[J] -= d;
+                    }
+                    for (int J = 0; J < n; J++)
 #pragma unroll
                         for (int r = 0; r < 4; r++)
-                            lsum += fast_exp2(sd[r] - m);
+                            lsum += fast_exp2(sv[J][r]);
+                };
+                int j = 1;
+                for (; j + NAR_CH_STATS <= i; j += NAR_CH_STATS) {
+                    f4 sc[NAR_CH_STATS];
+                    float cm = -INFINITY;
+#pragma unroll
+                    for (int J = 0; J < NAR_CH_STATS; J++) {
+                        sc[J] = nar_score<DHP, false>(Ks, qo, j + J, l16, g, nm);
+                        cm = fmax_nn(cm, max4(sc[J]));
+                    }
+                    take(sc, NAR_CH_STATS, cm);
+                }
+                for (; j < i; j++) {
+                    f4 sv = nar_score<DHP, false>(Ks, qo, j, l16, g, nm);
+                    take(&sv, 1, max4(sv));
+                }
+                if (i > 0) {
+                    f4 sv = nar_score<DHP, true>(Ks, qo, i, l16, g, nm);
+                    take(&sv, 1, max4(sv));
                 }
                 const float l = xrow_sum(lsum);
                 const int qrow = 16 * i + l16;
                 if (g == 0)
-                    L2[qrow] = qrow < S ? m + fast_log2(l) : INFINITY;
+                    L2[qrow] = qrow < S ? -(m + fast_log2(l)) : -INFINITY;
             }
         }
         __syncthreads();
@@ -508,22 +570,22 @@ __attribute__((amdgpu_waves_per_eu(nar_bwd_waves(DHP, NBM)))) void mha_nar_bwd_k
                     qa[s] = Qt[(KW * g + s) * QLD + 16 * I + l16];
                     da[s] = dOt[(KW * g + s) * QLD + 16 * I + l16];
                 }
-                f4 sc = f4zero(), dp = f4zero();
+                // S[query 4g+r][key l16] - lse and dP[query 4g+r][key l16] - Di
+                f4 sc = *reinterpret_cast<const f4*>(&L2[16 * I + 4 * g]);
+                f4 dp = *reinterpret_cast<const f4*>(&Dd[16 * I + 4 * g]);
 #pragma unroll
                 for (int s = 0; s < KW; s++) {
-                    sc = mfma16(qa[s], kb[s], sc);   // S[query 4g+r][key l16]
-                    dp = mfma16(da[s], vb[s], dp);   // dP[query 4g+r][key l16]
+                    sc = mfma16(qa[s], kb[s], sc);
+                    dp = mfma16(da[s], vb[s], dp);
                 }
-                const f4 l2 = *reinterpret_cast<const f4*>(&L2[16 * I + 4 * g]);
-                const f4 di = *reinterpret_cast<const f4*>(&Dd[16 * I + 4 * g]);
                 f4 pr, ds;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    float pv = fast_exp2(sc[r] - l2[r]);
+                    float pv = fast_exp2(sc[r]);
                     if (I == j)
                         pv = (l16 <= 4 * g + r) ? pv : 0.0f;
                     pr[r] = pv;
-                    ds[r] = pv * (dp[r] - di[r]);
+                    ds[r] = pv * dp[r];
                 }
                 // dV[key][d] += sum_q P[q][key] dO[q][d], dK likewise with dS and
                 // Q: the B operands dO[16I + 4g + r][d = l16] (zero row past DHP)
