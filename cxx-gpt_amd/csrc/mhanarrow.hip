@@ -14,14 +14,15 @@
 //             16-row query blocks of pairs (nb-1-p, p), p = w, w+4, ... (each
 //             pair costs nb+1 key blocks), with S^T = K Q^T on MFMA (a lane
 //             holds one query, so a row's statistics need one cross-row max)
-//             and O += P V.  A row's scores are held in registers for 4 key
-//             blocks at a time: the maximum of each chunk is known before its
-//             probabilities are formed, and the sums are rescaled once per
-//             chunk.
+//             and O += P V.  The softmax reference is lazy: key block 0's
+//             exact maximum first, then the score accumulators start at -m
+//             (scores relative to m), and m moves only when a score passes it
+//             by 2^8 (a wave-uniform check per chunk of 4 key blocks).
 //   backward: Q (pre-scaled), dO (both transposed) and K of the head live in
 //             LDS; every row's Di = dO.O is formed at the start, and for the
 //             reference's signature (no lse) the statistics are recomputed by
-//             the same waves first.  Wave w then takes key blocks of pairs
+//             the same waves first.  -lse and -Di start the S and dP
+//             accumulators.  Wave w then takes key blocks of pairs
 //             (p, nb-1-p): S and dP in the key-column layout (a lane holds one
 //             key, four queries), dV += P^T dO and dK += dS^T Q in registers,
 //             dS transposed through a per-wave LDS tile for dQ^T = K^T dS^T,
