@@ -944,9 +944,10 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 t.q.template store<QS>(st, tid);
             t.d.template store<QS>(st + BM * QS, tid);
             if (tid < BM) {
-                st[2 * BM * QS + BM * TS + tid] = t.lse * kLog2e;
+                // negated: they start the S and dP accumulators
+                st[2 * BM * QS + BM * TS + tid] = -t.lse * kLog2e;
                 if constexpr (!IPREP)
-                    st[2 * BM * QS + BM * TS + BM + tid] = t.di * scale;   // scaled as dP is
+                    st[2 * BM * QS + BM * TS + BM + tid] = -t.di * scale;   // scaled as dP is
             }
             if constexpr (IPREP) {
                 // Di of rows tid/16 + 32i: a row's 16 units are the 16 lanes of a
@@ -961,7 +962,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     di += lane_xor16<4>(di);
                     di += lane_xor16<8>(di);
                     if ((tid & 15) == 0)
-                        st[2 * BM * QS + BM * TS + BM + (tid >> 4) + 32 * i] = di * scale;
+                        st[2 * BM * QS + BM * TS + BM + (tid >> 4) + 32 * i] = -di * scale;
                 }
             }
         };
@@ -988,10 +989,16 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             f4 P[NQW], dS[NQW];
 #pragma unroll
             for (int q1 = 0; q1 < NQW; q1 += QI) {
+                // S (K pre-scaled to log2 units) starts at -lse and dP at -Di,
+                // so the probabilities are exp2 of the accumulators and dS the
+                // product of two of them
                 f4 sa[QI], da[QI];
 #pragma unroll
-                for (int j = 0; j < QI; j++)
-                    sa[j] = da[j] = f4zero();
+                for (int j = 0; j < QI; j++) {
+                    const int qt = qs * NQW + q1 + j;
+                    sa[j] = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
+                    da[j] = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
+                }
 #pragma unroll
                 for (int dt = 0; dt < NDT; dt++) {
 #pragma unroll
@@ -1013,15 +1020,13 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                     const int qq = q1 + j, qt = qs * NQW + qq;
                     if (qq < F)
                         continue;
-                    const f4 l4 = *reinterpret_cast<const f4*>(&lse_s[16 * qt + 4 * g]);
-                    const f4 d4 = *reinterpret_cast<const f4*>(&di_s[16 * qt + 4 * g]);
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int q = q0 + 16 * qt + 4 * g + r;
                         const bool ok = (!diag || mykey <= q) && q < S;
-                        const float p = ok ? fast_exp2(sa[j][r] * c2 - l4[r]) : 0.0f;
+                        const float p = ok ? fast_exp2(sa[j][r]) : 0.0f;
                         P[qq][r] = p;
-                        dS[qq][r] = p * (da[j][r] - d4[r]);
+                        dS[qq][r] = p * da[j][r];
                         dSs[(16 * qt + 4 * g + r) * TS + kg * 16 + l16] = dS[qq][r];
                     }
                 }
@@ -1176,7 +1181,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             vreg[dt] = (BUF ? vreg[dt] : mask4(vreg[dt], 16 * dt + 4 * g, Dh, kok)) * scale;
         }
         // K^T tile for the dQ product, written from the K operand registers by
-        // the waves of query split 0 (their key blocks kg cover the tile).
+        // the waves of query split 0 (their key blocks kg cover the tile);
+        // then the K operand of S takes the softmax scale in log2 units.
         if (qs == 0) {
 #pragma unroll
             for (int dt = 0; dt < NDT; dt++)
@@ -1184,6 +1190,9 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
                 for (int r4 = 0; r4 < 4; r4++)
                     Kt[(16 * dt + 4 * g + r4) * TS + kg * 16 + l16] = kreg[dt][r4];
         }
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++)
+            kreg[dt] *= c2;
         if constexpr (SM::DB) {
             // Four-deep pipeline: two register stages loaded three query tiles
             // ahead of use, two LDS stages.  Tile qb is in stage qb&1 when
