@@ -37,6 +37,8 @@
 //   R-layout:  v[ct][r] = M[t0 + l16][16ct + 4g + r]   (row per lane)
 //   C-layout:  v[ct][r] = M[t0 + 4g + r][16ct + l16]   (column per lane)
 #include "common.hpp"
+
+#include <type_traits>
 #include "launch.hpp"
 #include "linattn.hpp"
 #include "linattn_dev.hpp"
@@ -126,7 +128,9 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     fetch(xa, ya, wa, min(tbeg, tlcl));
     fetch(xb, yb, wb, min(tbeg + 16, tlcl));
     float* stg = lds + half * 2 * AGG_STAGE;
-    auto chunk = [&](f4 (&ax)[2], f4 (&ay)[2], float& aw, int c) __attribute__((always_inline)) {
+    // WHOLE: the chunk is known to be whole (every chunk but the half's last),
+    // so its row masks are left out
+    auto chunk = [&](auto WHOLE, f4 (&ax)[2], f4 (&ay)[2], float& aw, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = stg + (c & 1) * AGG_STAGE;
         float* bX = st;
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
         float* bw = st + 2 * CHUNK;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const bool ok = t0 + crow + 4 * i < tend;
+            const bool ok = decltype(WHOLE)::value || t0 + crow + 4 * i < tend;
             if constexpr (PHI == PHI_HEXP) {
                 // the row's 64 columns lie in this lane's 16-lane group
                 const f4 hx = hexp_row4(ax[i], lane);
@@ -189,12 +193,14 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
         }
     };
     int c = 0;
-    for (; c + 1 < nh; c += 2) {
-        chunk(xa, ya, wa, c);
-        chunk(xb, yb, wb, c + 1);
+    for (; c + 2 < nh; c += 2) {
+        chunk(std::true_type{}, xa, ya, wa, c);
+        chunk(std::true_type{}, xb, yb, wb, c + 1);
     }
     if (c < nh)
-        chunk(xa, ya, wa, c);
+        chunk(std::false_type{}, xa, ya, wa, c);
+    if (c + 1 < nh)
+        chunk(std::false_type{}, xb, yb, wb, c + 1);
 
     // Sum the halves: the second publishes its state slice (and z partials)
     // through LDS, the first adds and writes the record.
@@ -366,13 +372,15 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     };
     fetch(qa, ka, va, tbeg);
     fetch(qb, kb, vb, min(tbeg + 16, tlc));
-    auto chunk = [&](f4 (&aq)[2], f4 (&ak)[2], f4 (&av)[2], int c) __attribute__((always_inline)) {
+    // WHOLE (a std::bool_constant): the chunk is known to be whole, so its
+    // row masks are left out (only a sequence's last chunk can be partial)
+    auto chunk = [&](auto WHOLE, f4 (&aq)[2], f4 (&ak)[2], f4 (&av)[2], int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * FWD_STAGE;
         float* bQ = st;
         float* bK = st + CHUNK;
         float* bV = st + 2 * CHUNK;
-        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        const bool full = decltype(WHOLE)::value || t0 + 16 <= tend, rok = t0 + l16 < tend;
         // context: the state before chunk 2^k of the sequence is anchor k (a
         // wave-uniform branch taken log2(S / 16) times per sequence)
         const int cabs = tbeg / 16 + c;
@@ -542,12 +550,14 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         }
     };
     int c = 0;
-    for (; c + 1 < nch; c += 2) {
-        chunk(qa, ka, va, c);
-        chunk(qb, kb, vb, c + 1);
+    for (; c + 2 < nch; c += 2) {
+        chunk(std::true_type{}, qa, ka, va, c);
+        chunk(std::true_type{}, qb, kb, vb, c + 1);
     }
     if (c < nch)
-        chunk(qa, ka, va, c);
+        chunk(std::false_type{}, qa, ka, va, c);
+    if (c + 1 < nch)
+        chunk(std::false_type{}, qb, kb, vb, c + 1);
 
     if (Sfin != nullptr && seg == nseg - 1) {
         // final state of the sequence: [d][e] (linear_cuda) or [e][d] (two_stage)
@@ -675,7 +685,9 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         ndd = dden[rb + t0 + ro];
     };
     fetch(tbeg);
-    for (int c = 0; c < nch; c++) {
+    // WHOLE: the chunk is known to be whole (every chunk but a sequence's
+    // last), so its row masks are left out
+    auto body = [&](auto WHOLE, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * DQ_STAGE;
         float* bK = st;
@@ -693,7 +705,7 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
         }
         const float dd = ndd;
         fetch(min(t0 + 16, tlc));
-        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        const bool full = decltype(WHOLE)::value || t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 2>(ak, full, rok, D, g, 2 * h);
         finRp<PHI, false, FW, 2>(av, full, rok, E, g, 2 * h);
         finRp<PHI, false, FW, 2>(an, full, rok, E, g, 2 * h);
@@ -767,7 +779,11 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
             for (int j = 0; j < 2; j++)
                 stR<VEC, FW>(qrow, 16 * (2 * h + j) + 4 * g, D, dq[j]);
         }
-    }
+    };
+    for (int c = 0; c + 1 < nch; c++)
+        body(std::true_type{}, c);
+    if (nch > 0)
+        body(std::false_type{}, nch - 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -839,7 +855,9 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
     };
     const int nchunk = (tend - tbeg + 15) / 16;
     fetch(tbeg + 16 * (nchunk - 1));
-    for (int c = nchunk - 1; c >= 0; c--) {
+    // WHOLE: the chunk is known to be whole (every chunk but a sequence's
+    // last, which this walk takes first), so its row masks are left out
+    auto body = [&](auto WHOLE, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * DKDV_STAGE;
         float* bQ = st;
@@ -850,7 +868,7 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
         f4 aq[1] = {nq[0]}, ak[1] = {nk[0]}, av[1] = {nv[0]}, an[1] = {nn[0]};
         const float dd = ndd;
         fetch(max(t0 - 16, tbeg));
-        const bool full = t0 + 16 <= tend, rok = t0 + l16 < tend;
+        const bool full = decltype(WHOLE)::value || t0 + 16 <= tend, rok = t0 + l16 < tend;
         finRp<PHI, true, FW, 1>(aq, full, rok, D, g, w);
         finRp<PHI, true, FW, 1>(ak, full, rok, D, g, w);
         finRp<PHI, false, FW, 1>(av, full, rok, E, g, w);
@@ -996,7 +1014,11 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
                     stR<VEC, FW>(krow, 16 * (2 * hh + j) + 4 * g, D, dk[j]);
             }
         }
-    }
+    };
+    if (nchunk > 0)
+        body(std::false_type{}, nchunk - 1);
+    for (int c = nchunk - 2; c >= 0; c--)
+        body(std::true_type{}, c);
 }
 
 // ---------------------------------------------------------------------------

@@ -44,6 +44,7 @@
 #include "linattn_dev.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace cxg {
 
@@ -135,13 +136,15 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
     Set sa, sb;
     fetch(sa, tbeg);
     fetch(sb, min(tbeg + 16, tlc));
-    auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
+    // WHOLE: the chunk is known to be whole (every chunk but the segment's
+    // last), so its row masks are left out
+    auto chunk = [&](auto WHOLE, Set& s, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * BAGG_STAGE;
         float* bX = st;
         float* bY = st + CHUNK;
         float* bw = st + 2 * CHUNK;
-        const bool ok = t0 + lrow < tend;
+        const bool ok = decltype(WHOLE)::value || t0 + lrow < tend;
         f4 x, y;
         float wv;
         const f4 px = phi_row<PHI>(rot_row<PHI>(s.a, t0 + lrow, lcol, rope_w), lane);
@@ -206,12 +209,14 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
             zrun = mfma16(xw[r], wt[r], zrun);
     };
     int c = 0;
-    for (; c + 1 < nch; c += 2) {
-        chunk(sa, c);
-        chunk(sb, c + 1);
+    for (; c + 2 < nch; c += 2) {
+        chunk(std::true_type{}, sa, c);
+        chunk(std::true_type{}, sb, c + 1);
     }
     if (c < nch)
-        chunk(sa, c);
+        chunk(std::false_type{}, sa, c);
+    if (c + 1 < nch)
+        chunk(std::false_type{}, sb, c + 1);
 
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
@@ -444,7 +449,9 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         buffer_store_f4(buf_rsrc(dQ + rb * 64), off, tq);
         buffer_store_f4(buf_rsrc(dK + rb * 64), off, tk);
     };
-    auto chunk = [&](Set& s, int c) __attribute__((always_inline)) {
+    // WHOLE: the chunk is known to be whole (every chunk but the segment's
+    // last, which this walk takes first), so its row masks are left out
+    auto chunk = [&](auto WHOLE, Set& s, int c) __attribute__((always_inline)) {
         const int t0 = tbeg + 16 * c;
         float* st = lds + (c & 1) * BWD_STAGE;
         float* bQ = st;
@@ -458,14 +465,14 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             // division costs ten VALU instructions, which on gfx950 add to the
             // chunk's MFMA time).  Rows past the end exist only in a
             // sequence's last, partial chunk (a wave-uniform branch).
-            const bool ok = t0 + lrow < tend;
+            const bool ok = decltype(WHOLE)::value || t0 + lrow < tend;
             const float inv = ok ? __builtin_amdgcn_rcpf(s.dn) : 0.0f;
             const float dot = row16_sum(s.d[0] * s.o[0] + s.d[1] * s.o[1] + s.d[2] * s.o[2] +
                                         s.d[3] * s.o[3]);
             f4 q = phi_row<PHI>(rot_row<PHI>(s.q, t0 + lrow, lcol, rope_w), lane);
             f4 k = phi_row<PHI>(rot_row<PHI>(s.k, t0 + lrow, lcol, rope_w), lane);
             f4 v = s.v;
-            if (t0 + 16 > tend) {
+            if (!decltype(WHOLE)::value && t0 + 16 > tend) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     q[i] = ok ? q[i] : 0.0f;
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
             M2[r] = sr >= l16 ? X[r] + ddS[r] : 0.0f;
             G[r] = sr <= l16 ? Xt[r] + ddT : 0.0f;
         }
-        const bool okt = t0 + l16 < tend;
+        const bool okt = decltype(WHOLE)::value || t0 + l16 < tend;
         const unsigned soff = (unsigned)(l16 * 64 + 16 * w + 4 * g);   // FW store offsets
 
         // dV^T[e][t] = sum_d S*[d][e] phi(K_t)[d] + sum_{s>=t} dnum_s[e] M1[s][t]
@@ -680,13 +687,14 @@ __global__ __launch_bounds__(BWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         }
         __builtin_amdgcn_s_setprio(0);
     };
-    int c = nch - 1;
+    chunk(std::false_type{}, sa, nch - 1);   // the segment's last chunk
+    int c = nch - 2;
     for (; c >= 1; c -= 2) {
-        chunk(sa, c);
-        chunk(sb, c - 1);
+        chunk(std::true_type{}, sb, c);
+        chunk(std::true_type{}, sa, c - 1);
     }
     if (c == 0)
-        chunk(sa, 0);
+        chunk(std::true_type{}, sb, 0);
     if constexpr (PHI == PHI_HEXP) {
         __syncthreads();
         flush();
