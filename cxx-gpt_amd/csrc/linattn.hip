@@ -116,12 +116,22 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     // 8h + 4i + l/16 (i = 0, 1), columns 4(l%16) .. +3, so each instruction
     // reads four whole rows.
     const int crow = 8 * h + (lane >> 4), ccol = 4 * (lane & 15);
+    // D = E = 64: whole rows through descriptors over the sequence (32-bit
+    // offsets instead of 64-bit address arithmetic)
+    const __amdgpu_buffer_rsrc_t rXs = buf_rsrc(FW ? X + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rYs = buf_rsrc(FW ? Y + rb * 64 : nullptr);
     auto fetch = [&](f4 (&fx)[2], f4 (&fy)[2], float& fw, int t0) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const long r = rb + min(t0 + crow + 4 * i, tlast);
-            fx[i] = load4c<VEC>(X + r * D, ccol, D);
-            fy[i] = load4c<VEC>(Y + r * E, ccol, E);
+            const int t = min(t0 + crow + 4 * i, tlast);
+            if constexpr (FW) {
+                fx[i] = buffer_load_f4(rXs, (unsigned)(t * 64 + ccol) * 4u);
+                fy[i] = buffer_load_f4(rYs, (unsigned)(t * 64 + ccol) * 4u);
+            } else {
+                const long r = rb + t;
+                fx[i] = load4c<VEC>(X + r * D, ccol, D);
+                fy[i] = load4c<VEC>(Y + r * E, ccol, E);
+            }
         }
         fw = buffer_load_f32(rw, (unsigned)min(t0 + l16, tlast) * 4u);
     };
@@ -352,8 +362,12 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const int nch = (tend - tbeg + 15) / 16;
     const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
     f4 qa[2], ka[2], va[2], qb[2], kb[2], vb[2];
+    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW ? Q + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
     auto fetch = [&](f4 (&fq)[2], f4 (&fk)[2], f4 (&fv)[2], int t0) {
         const int ro = min(l16, tlast - t0);
+        const unsigned fvo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u;   // FW: row ro, tile 2h
         if constexpr (PHI == PHI_HEXP) {
             // Hadamard+Exp transforms whole rows (D = 64): wave h takes chunk
             // rows 8h + 4i + g, columns 4 l16 .. +3, so that a row's 64 columns
@@ -364,11 +378,25 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                 fq[i] = *reinterpret_cast<const f4*>(Q + r * 64 + 4 * l16);
                 fk[i] = *reinterpret_cast<const f4*>(K + r * 64 + 4 * l16);
             }
+        } else if constexpr (FW) {
+            // whole 64-column rows through descriptors over the sequence: a
+            // per-lane row and column offset, the chunk's first row scalar
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                fq[i] = buffer_load_f4s(rQs, fvo + 64u * i, (unsigned)t0 * 256u);
+                fk[i] = buffer_load_f4s(rKs, fvo + 64u * i, (unsigned)t0 * 256u);
+            }
         } else {
             ldRp<VEC, 2>(fq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
             ldRp<VEC, 2>(fk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
         }
-        ldRp<VEC, 2>(fv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
+        if constexpr (FW) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                fv[i] = buffer_load_f4s(rVs, fvo + 64u * i, (unsigned)t0 * 256u);
+        } else {
+            ldRp<VEC, 2>(fv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
+        }
     };
     fetch(qa, ka, va, tbeg);
     fetch(qb, kb, vb, min(tbeg + 16, tlc));
@@ -674,14 +702,34 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
     f4 nk[2], nv[2], nn[2], nz[2], nq[2];
     float ndd = 0.0f;
+    // D = E = 64: whole rows through descriptors over the sequence, the
+    // chunk's first row a scalar offset
+    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rNs = buf_rsrc(FW ? dnum + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rZs = buf_rsrc(FW ? zcache + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW && HAS_Q ? Q + rb * 64 : nullptr);
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
-        ldRp<VEC, 2>(nv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
-        ldRp<VEC, 2>(nn, dnum + (rb + t0) * E, E, ro, E, g, 2 * h);
-        ldRp<VEC, 2>(nz, zcache + (rb + t0) * D, D, ro, D, g, 2 * h);
-        if (HAS_Q)
-            ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+        if constexpr (FW) {
+            const unsigned vo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u, so = (unsigned)t0 * 256u;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                nk[i] = buffer_load_f4s(rKs, vo + 64u * i, so);
+                nv[i] = buffer_load_f4s(rVs, vo + 64u * i, so);
+                nn[i] = buffer_load_f4s(rNs, vo + 64u * i, so);
+                nz[i] = buffer_load_f4s(rZs, vo + 64u * i, so);
+                if (HAS_Q)
+                    nq[i] = buffer_load_f4s(rQs, vo + 64u * i, so);
+            }
+        } else {
+            ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
+            ldRp<VEC, 2>(nv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
+            ldRp<VEC, 2>(nn, dnum + (rb + t0) * E, E, ro, E, g, 2 * h);
+            ldRp<VEC, 2>(nz, zcache + (rb + t0) * D, D, ro, D, g, 2 * h);
+            if (HAS_Q)
+                ldRp<VEC, 2>(nq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
+        }
         ndd = dden[rb + t0 + ro];
     };
     fetch(tbeg);
@@ -845,12 +893,26 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
     // stay exact.
     f4 nq[1], nk[1], nv[1], nn[1];
     float ndd = 0.0f;
+    // D = E = 64: whole rows through descriptors over the sequence, the
+    // chunk's first row a scalar offset
+    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW ? Q + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rNs = buf_rsrc(FW ? dnum + rb * 64 : nullptr);
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
-        ldRp<VEC, 1>(nq, Q + (rb + t0) * D, D, ro, D, g, w);
-        ldRp<VEC, 1>(nk, K + (rb + t0) * D, D, ro, D, g, w);
-        ldRp<VEC, 1>(nv, V + (rb + t0) * E, E, ro, E, g, w);
-        ldRp<VEC, 1>(nn, dnum + (rb + t0) * E, E, ro, E, g, w);
+        if constexpr (FW) {
+            const unsigned vo = (unsigned)(ro * 64 + 16 * w + 4 * g) * 4u, so = (unsigned)t0 * 256u;
+            nq[0] = buffer_load_f4s(rQs, vo, so);
+            nk[0] = buffer_load_f4s(rKs, vo, so);
+            nv[0] = buffer_load_f4s(rVs, vo, so);
+            nn[0] = buffer_load_f4s(rNs, vo, so);
+        } else {
+            ldRp<VEC, 1>(nq, Q + (rb + t0) * D, D, ro, D, g, w);
+            ldRp<VEC, 1>(nk, K + (rb + t0) * D, D, ro, D, g, w);
+            ldRp<VEC, 1>(nv, V + (rb + t0) * E, E, ro, E, g, w);
+            ldRp<VEC, 1>(nn, dnum + (rb + t0) * E, E, ro, E, g, w);
+        }
         ndd = dden[rb + t0 + ro];
     };
     const int nchunk = (tend - tbeg + 15) / 16;

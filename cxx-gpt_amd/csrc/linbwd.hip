@@ -121,9 +121,23 @@ __device__ __attribute__((always_inline)) inline void bagg_body(
         f4 a, b, c;
         float dn;
     };
+    // D = E = 64: whole rows through descriptors over the sequence (32-bit
+    // offsets instead of 64-bit address arithmetic)
+    const __amdgpu_buffer_rsrc_t rAs = buf_rsrc(FW ? (SUF ? Q : K) + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rBs = buf_rsrc(FW ? (SUF ? O : V) + rb * 64 : nullptr);
+    const __amdgpu_buffer_rsrc_t rCs = buf_rsrc(FW && SUF ? dO + rb * 64 : nullptr);
     auto fetch = [&](Set& s, int t0) {
-        const long r = rb + min(t0 + lrow, tlast);
-        if constexpr (!SUF) {
+        const int t = min(t0 + lrow, tlast);
+        const long r = rb + t;
+        if constexpr (FW) {
+            const unsigned off = (unsigned)(t * 64 + lcol) * 4u;
+            s.a = buffer_load_f4(rAs, off);
+            s.b = buffer_load_f4(rBs, off);
+            if constexpr (SUF) {
+                s.c = buffer_load_f4(rCs, off);
+                s.dn = den[r];
+            }
+        } else if constexpr (!SUF) {
             s.a = ld_row4<VEC, FW>(K, r, D, lcol, D);
             s.b = ld_row4<VEC, FW>(V, r, E, lcol, E);
         } else {
