@@ -203,13 +203,40 @@ __device__ __forceinline__ f4 mfma4(float a, float b, f4 c)
     return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
 }
 
-// Sum over the four lanes l16 + 16g of each element.
-__device__ __forceinline__ f4 xrow_sum4(f4 v)
+// Column group g of the sum over the four lanes l16 + 16g of a[0 .. KW-1]
+// (valid in lanes g < KW): lanes g and g^1 keep the groups whose bit 0 is
+// g & 1 and add the partner's copies, then lanes g and g^2 those whose bit 1
+// is g >> 1 (KW = 4; with KW = 2 the second step only adds).
+template <int KW>
+__device__ __forceinline__ f4 nar_colsum(const f4 (&a)[KW], int g)
 {
+    const bool b0 = (g & 1) != 0;
+    if constexpr (KW == 2) {
+        f4 keep = b0 ? a[1] : a[0];
+        const f4 send = b0 ? a[0] : a[1];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
-        v[r] = xrow_sum(v[r]);
-    return v;
+        for (int r = 0; r < 4; r++)
+            keep[r] += __shfl_xor(send[r], 16, 64);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            keep[r] += __shfl_xor(keep[r], 32, 64);
+        return keep;
+    } else {
+        f4 k0 = b0 ? a[1] : a[0], k1 = b0 ? a[3] : a[2];
+        const f4 s0 = b0 ? a[0] : a[1], s1 = b0 ? a[2] : a[3];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            k0[r] += __shfl_xor(s0[r], 16, 64);
+            k1[r] += __shfl_xor(s1[r], 16, 64);
+        }
+        const bool b1 = (g & 2) != 0;
+        f4 keep = b1 ? k1 : k0;
+        const f4 send = b1 ? k0 : k1;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            keep[r] += __shfl_xor(send[r], 32, 64);
+        return keep;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -348,15 +375,10 @@ void mha_nar_fwd_kernel(const float* __restrict__ Q, const float* __restrict__ K
             }
             const float l = xrow_sum(lsum);
             if (WRITE_O) {
-                // every key's share: sum over g; lane (l16, g < KW) stores
-                // columns 4g .. 4g+3
-                f4 o = f4zero();
-#pragma unroll
-                for (int c = 0; c < KW; c++) {
-                    const f4 t = xrow_sum4(oacc[c]);
-                    if (g == c)
-                        o = t;
-                }
+                // every key's share: sum over g, as a reduce-scatter (lanes
+                // g and g^1 trade half their column groups, then g and g^2),
+                // so that lane (l16, g < KW) ends with column group g
+                f4 o = nar_colsum<KW>(oacc, g);
                 if (qok && g < KW) {
                     o *= __builtin_amdgcn_rcpf(l);   // hardware reciprocal, within 1 ulp
                     float* orow = O + base + (long)qrow * rs;
