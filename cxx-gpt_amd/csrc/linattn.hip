@@ -76,7 +76,10 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     rope_tab_lds<PHI, 32>(rope_w, rope);
     if constexpr (phi_rope(PHI))
         __syncthreads();
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    // wave-uniform (scalar) wave index: the row ranges and descriptor bases
+    // below derive from it
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = wv & 1, half = wv >> 1;
     const int l16 = lane & 15, g = lane >> 4;
     const int wid = blockIdx.x;
@@ -116,19 +119,20 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
     // 8h + 4i + l/16 (i = 0, 1), columns 4(l%16) .. +3, so each instruction
     // reads four whole rows.
     const int crow = 8 * h + (lane >> 4), ccol = 4 * (lane & 15);
-    // D = E = 64: whole rows through descriptors over the sequence (32-bit
-    // offsets instead of 64-bit address arithmetic)
-    const __amdgpu_buffer_rsrc_t rXs = buf_rsrc(FW ? X + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rYs = buf_rsrc(FW ? Y + rb * 64 : nullptr);
+    // D = E = 64: whole rows through descriptors based at the chunk's first
+    // row (scalar), with small 32-bit lane offsets instead of 64-bit address
+    // arithmetic per load
     auto fetch = [&](f4 (&fx)[2], f4 (&fy)[2], float& fw, int t0) {
+        const __amdgpu_buffer_rsrc_t rXc = buf_rsrc(FW ? X + (rb + t0) * 64 : nullptr);
+        const __amdgpu_buffer_rsrc_t rYc = buf_rsrc(FW ? Y + (rb + t0) * 64 : nullptr);
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int t = min(t0 + crow + 4 * i, tlast);
             if constexpr (FW) {
-                fx[i] = buffer_load_f4(rXs, (unsigned)(t * 64 + ccol) * 4u);
-                fy[i] = buffer_load_f4(rYs, (unsigned)(t * 64 + ccol) * 4u);
+                const unsigned o = (unsigned)(min(crow + 4 * i, tlast - t0) * 64 + ccol) * 4u;
+                fx[i] = buffer_load_f4(rXc, o);
+                fy[i] = buffer_load_f4(rYc, o);
             } else {
-                const long r = rb + t;
+                const long r = rb + min(t0 + crow + 4 * i, tlast);
                 fx[i] = load4c<VEC>(X + r * D, ccol, D);
                 fy[i] = load4c<VEC>(Y + r * E, ccol, E);
             }
@@ -362,12 +366,14 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
     const int nch = (tend - tbeg + 15) / 16;
     const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
     f4 qa[2], ka[2], va[2], qb[2], kb[2], vb[2];
-    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW ? Q + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
     auto fetch = [&](f4 (&fq)[2], f4 (&fk)[2], f4 (&fv)[2], int t0) {
         const int ro = min(l16, tlast - t0);
-        const unsigned fvo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u;   // FW: row ro, tile 2h
+        // FW: descriptors based at the chunk's first row (scalar), lane
+        // offsets of row ro, tile 2h
+        const unsigned fvo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u;
+        const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW ? Q + (rb + t0) * 64 : nullptr);
+        const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + (rb + t0) * 64 : nullptr);
+        const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + (rb + t0) * 64 : nullptr);
         if constexpr (PHI == PHI_HEXP) {
             // Hadamard+Exp transforms whole rows (D = 64): wave h takes chunk
             // rows 8h + 4i + g, columns 4 l16 .. +3, so that a row's 64 columns
@@ -379,12 +385,10 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
                 fk[i] = *reinterpret_cast<const f4*>(K + r * 64 + 4 * l16);
             }
         } else if constexpr (FW) {
-            // whole 64-column rows through descriptors over the sequence: a
-            // per-lane row and column offset, the chunk's first row scalar
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                fq[i] = buffer_load_f4s(rQs, fvo + 64u * i, (unsigned)t0 * 256u);
-                fk[i] = buffer_load_f4s(rKs, fvo + 64u * i, (unsigned)t0 * 256u);
+                fq[i] = buffer_load_f4(rQs, fvo + 64u * i);
+                fk[i] = buffer_load_f4(rKs, fvo + 64u * i);
             }
         } else {
             ldRp<VEC, 2>(fq, Q + (rb + t0) * D, D, ro, D, g, 2 * h);
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(FWD_THREADS) __attribute__((amdgpu_waves_per_eu(2))
         if constexpr (FW) {
 #pragma unroll
             for (int i = 0; i < 2; i++)
-                fv[i] = buffer_load_f4s(rVs, fvo + 64u * i, (unsigned)t0 * 256u);
+                fv[i] = buffer_load_f4(rVs, fvo + 64u * i);
         } else {
             ldRp<VEC, 2>(fv, V + (rb + t0) * E, E, ro, E, g, 2 * h);
         }
@@ -702,25 +706,24 @@ __global__ __launch_bounds__(DQ_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
     const int tlc = tbeg + 16 * (nch - 1);   // first row of the last chunk
     f4 nk[2], nv[2], nn[2], nz[2], nq[2];
     float ndd = 0.0f;
-    // D = E = 64: whole rows through descriptors over the sequence, the
-    // chunk's first row a scalar offset
-    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rNs = buf_rsrc(FW ? dnum + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rZs = buf_rsrc(FW ? zcache + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW && HAS_Q ? Q + rb * 64 : nullptr);
+    // D = E = 64: whole rows through descriptors based at the chunk's first
+    // row (scalar), with small 32-bit lane offsets
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
         if constexpr (FW) {
-            const unsigned vo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u, so = (unsigned)t0 * 256u;
+            const long cb = (rb + t0) * 64;
+            const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(K + cb), rVs = buf_rsrc(V + cb),
+                                         rNs = buf_rsrc(dnum + cb), rZs = buf_rsrc(zcache + cb),
+                                         rQs = buf_rsrc(HAS_Q ? Q + cb : nullptr);
+            const unsigned vo = (unsigned)(ro * 64 + 32 * h + 4 * g) * 4u;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
-                nk[i] = buffer_load_f4s(rKs, vo + 64u * i, so);
-                nv[i] = buffer_load_f4s(rVs, vo + 64u * i, so);
-                nn[i] = buffer_load_f4s(rNs, vo + 64u * i, so);
-                nz[i] = buffer_load_f4s(rZs, vo + 64u * i, so);
+                nk[i] = buffer_load_f4(rKs, vo + 64u * i);
+                nv[i] = buffer_load_f4(rVs, vo + 64u * i);
+                nn[i] = buffer_load_f4(rNs, vo + 64u * i);
+                nz[i] = buffer_load_f4(rZs, vo + 64u * i);
                 if (HAS_Q)
-                    nq[i] = buffer_load_f4s(rQs, vo + 64u * i, so);
+                    nq[i] = buffer_load_f4(rQs, vo + 64u * i);
             }
         } else {
             ldRp<VEC, 2>(nk, K + (rb + t0) * D, D, ro, D, g, 2 * h);
@@ -893,20 +896,17 @@ __global__ __launch_bounds__(DKDV_THREADS) __attribute__((amdgpu_waves_per_eu(2)
     // stay exact.
     f4 nq[1], nk[1], nv[1], nn[1];
     float ndd = 0.0f;
-    // D = E = 64: whole rows through descriptors over the sequence, the
-    // chunk's first row a scalar offset
-    const __amdgpu_buffer_rsrc_t rQs = buf_rsrc(FW ? Q + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rKs = buf_rsrc(FW ? K + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rVs = buf_rsrc(FW ? V + rb * 64 : nullptr);
-    const __amdgpu_buffer_rsrc_t rNs = buf_rsrc(FW ? dnum + rb * 64 : nullptr);
+    // D = E = 64: whole rows through descriptors based at the chunk's first
+    // row (scalar), with small 32-bit lane offsets
     auto fetch = [&](int t0) {
         const int ro = min(l16, tlast - t0);
         if constexpr (FW) {
-            const unsigned vo = (unsigned)(ro * 64 + 16 * w + 4 * g) * 4u, so = (unsigned)t0 * 256u;
-            nq[0] = buffer_load_f4s(rQs, vo, so);
-            nk[0] = buffer_load_f4s(rKs, vo, so);
-            nv[0] = buffer_load_f4s(rVs, vo, so);
-            nn[0] = buffer_load_f4s(rNs, vo, so);
+            const long cb = (rb + t0) * 64;
+            const unsigned vo = (unsigned)(ro * 64 + 16 * w + 4 * g) * 4u;
+            nq[0] = buffer_load_f4(buf_rsrc(Q + cb), vo);
+            nk[0] = buffer_load_f4(buf_rsrc(K + cb), vo);
+            nv[0] = buffer_load_f4(buf_rsrc(V + cb), vo);
+            nn[0] = buffer_load_f4(buf_rsrc(dnum + cb), vo);
         } else {
             ldRp<VEC, 1>(nq, Q + (rb + t0) * D, D, ro, D, g, w);
             ldRp<VEC, 1>(nk, K + (rb + t0) * D, D, ro, D, g, w);

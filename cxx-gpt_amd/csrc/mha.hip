@@ -684,7 +684,10 @@ struct BwdSmem {
 // its dQ jobs and dK/dV reduction.
 //
 // The softmax scale is folded into V (so dP and dS come out scaled) and Di
-// once per job, which removes a multiply per dQ atomic and per dK element.
+// once per job, which removes a multiply per dQ atomic and per dK element;
+// scale * log2(e) is folded into the K operand of S, and the S and dP
+// accumulators start at -lse * log2(e) and -Di, so that P = exp2(S) and
+// dS = P * dP need no further arithmetic.
 // BUF (whole-width heads, double-buffered path): Q/dO/K/V rows through buffer
 // descriptors over the head's rows 0..S-1 with scalar row offsets, and dQ
 // atomics through one whose range drops rows past S, so neither loads nor
@@ -744,7 +747,8 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
     };
 
     // A query tile in registers on its way to LDS: Q and dO rows, and the
-    // tile's lse and Di entries (lse is scaled by log2 e on its way to LDS).
+    // tile's lse and Di entries (negated on their way to LDS, lse in log2
+    // units, Di scaled).
     struct QTile {
         TileRegs<DHP, BM, NT, VEC> q, d;
         TileRegs<DHP, BM, NT, VEC> o;   // in-kernel pre-pass: O rows, for the tile's Di

@@ -252,3 +252,69 @@ def test_hexp_vector_and_scalar_paths(dev, N, D, E):
     assert_close(out[0][0], orc.phi_hexp_forward(x, D, E), f"phi_hexp N{N}D{D}E{E}")
     assert np.all(out[0][0][:, (E // 64) * 64:] == 0.0)
     assert_close(out[0][1], orc.phi_hexp_backward(g, x, D, E), f"phi_hexp_bwd N{N}D{D}E{E}")
+
+
+def test_long_sequence_row_offsets(dev):
+    """One sequence of 2^23 + 40 rows, past where 32-bit byte offsets from the
+    sequence's first 256-byte row would wrap: the chunked kernels address
+    each chunk from its own first row.  With every Q row equal and every K
+    row equal, c = phi(q).phi(k) factors out of every sum, which gives closed
+    forms (float64, on the device) for the whole chain:
+      O_t = c cumV_t / (c (t+1) + 1e-8), den_t = c (t+1), z_t = (t+1) phi(k),
+      dQ_t = phi(k) (cumV_t . dnum_t + (t+1) dden_t) phi'(q),
+      dK_s = phi(q) (A_s . V_s + B_s) phi'(k), dV_s = c A_s,
+    with cumV the prefix sums of V and A, B the suffix sums of the step-1
+    outputs dnum, dden (the GPU's own, as the chain passes them on)."""
+    import torch
+    import cxxgpt_attn as cx
+    S, D, E = (1 << 23) + 40, 64, 64
+    gen = torch.Generator().manual_seed(23)
+    q = (0.5 * torch.randn(D, generator=gen)).to(dev)
+    k = (0.5 * torch.randn(D, generator=gen)).to(dev)
+    Q, K = q.expand(S, D).contiguous(), k.expand(S, D).contiguous()
+    t = torch.arange(S, device=dev, dtype=torch.float32)[:, None]
+    col = torch.arange(E, device=dev, dtype=torch.float32)[None, :]
+    V = 1.0 + 0.5 * torch.sin(t * 1e-3 + col)
+    dO = torch.cos(t * 7e-4 + 0.3 * col)
+    del t, col
+    O, den, zc = _nan(dev, S, E), _nan(dev, S), _nan(dev, S, D)
+    Sb, zb = _nan(dev, E, D), _nan(dev, 1, D)
+    cx.kattn_fwd(Q, K, V, O, den, zc, Sb, zb, 1, S, D, E)
+    dnum, dden = _nan(dev, S, E), _nan(dev, S)
+    cx.kattn_bwd_step1(O, dO, den, dnum, dden, S, E)
+    dQ, dK, dV = _nan(dev, S, D), _nan(dev, S, D), _nan(dev, S, E)
+    cx.kattn_bwd_dQ(K, V, dnum, dden, zc, Q, dQ, Sb, 1, S, D, E)
+    cx.kattn_bwd_dKdV(Q, K, V, dnum, dden, dK, dV, 1, S, D, E)
+    torch.cuda.synchronize()
+
+    def phi(x):
+        return torch.where(x > 0, x + 1.0, torch.exp(x))
+
+    def dphi(x):
+        return torch.where(x > 0, torch.ones_like(x), torch.exp(x))
+
+    def check(got, ref, name):
+        assert torch.isfinite(got).all(), f"{name}: non-finite values"
+        err = (got.double() - ref).abs()
+        excess = err - (1e-5 + 1e-4 * ref.abs())
+        worst = int(torch.argmax(excess.reshape(-1)))
+        assert float(excess.reshape(-1)[worst]) <= 0.0, (
+            f"{name}: {int((excess > 0).sum())} elements out of tolerance; worst flat index "
+            f"{worst}: got {float(got.reshape(-1)[worst])!r} ref {float(ref.reshape(-1)[worst])!r}")
+
+    pq, pk = phi(q.double()), phi(k.double())
+    c = float((pq * pk).sum())
+    n = torch.arange(1, S + 1, device=dev, dtype=torch.float64)[:, None]
+    cum = torch.cumsum(V.double(), 0)
+    check(O, cum * c / (c * n + 1e-8), "O")
+    check(den, c * n[:, 0], "den")
+    check(zc, n * pk[None, :], "z_cache")
+    dn, dd = dnum.double(), dden.double()[:, None]
+    check(dQ, ((cum * dn).sum(1, keepdim=True) + n * dd) * pk[None, :] * dphi(q.double())[None, :],
+          "dQ")
+    del cum
+    A = torch.flip(torch.cumsum(torch.flip(dn, [0]), 0), [0])
+    Bs = torch.flip(torch.cumsum(torch.flip(dd, [0]), 0), [0])
+    check(dV, c * A, "dV")
+    check(dK, ((A * V.double()).sum(1, keepdim=True) + Bs) * pq[None, :] * dphi(k.double())[None, :],
+          "dK")
