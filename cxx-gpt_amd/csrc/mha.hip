@@ -34,6 +34,8 @@
 // is a multiple of 8 all tiles of a head share an XCD (and its L2), since
 // workgroups are dealt to the 8 XCDs round-robin.
 #include "common.hpp"
+
+#include <type_traits>
 #include "launch.hpp"
 
 #include <math.h>
@@ -976,8 +978,11 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
         // first F of the wave's NQW query blocks lie wholly before its key
         // block (all masked: P = dS = 0) and are skipped; the dQ product never
         // reads their dS.
-        auto key_side_f = [&](float* st, int q0, auto first) __attribute__((always_inline)) {
+        // INTERIOR: the tile lies wholly below the causal boundary with every
+        // query row before S, so no score needs a mask.
+        auto key_side_f = [&](float* st, int q0, auto first, auto interior) __attribute__((always_inline)) {
             constexpr int F = decltype(first)::value;
+            constexpr bool INTERIOR = decltype(interior)::value;
             // Raised issue priority for this MFMA-dense section: the other
             // wave of the SIMD fills its stalls instead of interleaving.
             __builtin_amdgcn_s_setprio(1);
@@ -1027,7 +1032,7 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         const int q = q0 + 16 * qt + 4 * g + r;
-                        const bool ok = (!diag || mykey <= q) && q < S;
+                        const bool ok = INTERIOR || ((!diag || mykey <= q) && q < S);
                         const float p = ok ? fast_exp2(sa[j][r]) : 0.0f;
                         P[qq][r] = p;
                         dS[qq][r] = p * da[j][r];
@@ -1060,10 +1065,16 @@ __global__ __launch_bounds__(256 * NSPLIT) void mha_bwd_kernel(
             for (int qq = 0; qq < NQW; qq++)
                 if (q0 + 16 * (qs * NQW + qq) + 15 < k0 + 16 * kg)
                     f = qq + 1;
-            if (!SKIP || f == 0)
-                key_side_f(st, q0, ic<0>{});
+            // (only where a third copy of this section fits the registers:
+            // the whole-width buffer path without the in-kernel pre-pass or
+            // RoPE, at most 64 columns; elsewhere it spills)
+            constexpr bool kInterior = BUF && !IPREP && !ROPE && DHP <= 64;
+            if (kInterior && q0 >= k0 + MHA_BN && q0 + BM <= S)   // wave-uniform
+                key_side_f(st, q0, ic<0>{}, std::true_type{});
+            else if (!SKIP || f == 0)
+                key_side_f(st, q0, ic<0>{}, std::false_type{});
             else if (f == 1)
-                key_side_f(st, q0, ic<1>{});
+                key_side_f(st, q0, ic<1>{}, std::false_type{});
         };
         // dQ tiles (qt, dt) of the query block, dealt round-robin to the waves:
         // dS (LDS) x K (LDS, transposed), added into dQ with float atomics.  A
