@@ -206,15 +206,20 @@ __global__ __launch_bounds__(AGG_THREADS) __attribute__((amdgpu_waves_per_eu(3))
                     zp[dt] += wc[r] * xC[dt][r];   // rows past the half hold xC = 0
         }
     };
+    // Chunks whole in both halves: the second holds nh or nh - 1 chunks, its
+    // last one possibly partial (the sequence's end); the remaining steps keep
+    // the row masks.
+    const int nwhole = (send - min(sbeg + 16 * nh, send)) / 16;
     int c = 0;
-    for (; c + 2 < nh; c += 2) {
+    for (; c + 2 <= nwhole; c += 2) {
         chunk(std::true_type{}, xa, ya, wa, c);
         chunk(std::true_type{}, xb, yb, wb, c + 1);
     }
-    if (c < nh)
+    for (; c < nh; c += 2) {
         chunk(std::false_type{}, xa, ya, wa, c);
-    if (c + 1 < nh)
-        chunk(std::false_type{}, xb, yb, wb, c + 1);
+        if (c + 1 < nh)
+            chunk(std::false_type{}, xb, yb, wb, c + 1);
+    }
 
     // Sum the halves: the second publishes its state slice (and z partials)
     // through LDS, the first adds and writes the record.

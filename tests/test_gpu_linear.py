@@ -93,10 +93,15 @@ def test_config3_elu(dev, S):
 @pytest.mark.parametrize("B,S,D,E", [
     (1, 1, 64, 64), (3, 15, 64, 64), (2, 17, 32, 48), (2, 100, 64, 64), (1, 1000, 64, 64),
     (5, 333, 16, 8), (2, 40, 64, 1), (300, 16, 64, 64), (1, 50, 128, 64), (2, 20, 64, 96),
+    (24, 2040, 64, 64), (7, 3001, 64, 64), (96, 632, 64, 64),
 ])
 def test_ragged_shapes(dev, B, S, D, E):
     """Partial chunks, single and multi-segment plans, narrow D/E (the chunked scan) and
-    widths in (64, 512] (the quadratic form); widths above 512 are in test_gpu_lingeneric."""
+    widths in (64, 512] (the quadratic form); widths above 512 are in test_gpu_lingeneric.
+    The last three: multi-chunk segments whose sequence ends in a partial chunk.  At
+    B96 S632 (8 segments of 5 chunks on 256 compute units) the last segment holds 4.5
+    chunks, so the second half of its segment sum ends in a partial chunk that must keep
+    its row masks (its record feeds every earlier segment's dK/dV)."""
     Q, K, V, dO = normal_inputs((B * S, D), (B * S, E), 13 * S + D + E)
     check_kattn(dev, Q, K, V, dO, B, S, D, E, literal=(S <= 40), tag=f"B{B}S{S}D{D}E{E}")
 
