@@ -1477,8 +1477,14 @@ LinPlan lin_plan(int Bq, int S, int D, int E, int pass)
         // resident workgroups (rounding up past it leaves a round that runs
         // almost empty; two rounds cost more in agg/scan and segment start-up
         // than they gain), shorter ones about three segment workgroups per
-        // compute unit; at least two chunks per segment.
-        const int target = nchunk > 64 ? lin_slots(pass) : 3 * lin_cus();
+        // compute unit (the fused backward of sequences of at most 16 chunks
+        // one and a half: at B' = 96, S = 256 four segments of four chunks
+        // took 55.9 us a step against 57.8 with eight of two, 57.3 with two
+        // of eight; at S = 1024 eight segments stay best); at least two
+        // chunks per segment.
+        const int target = nchunk > 64                                 ? lin_slots(pass)
+                           : (pass == LIN_PASS_BWD && nchunk <= 16) ? 3 * lin_cus() / 2
+                                                                      : 3 * lin_cus();
         int want = target / Bq;
         if (want > nchunk / 2)
             want = nchunk / 2;
