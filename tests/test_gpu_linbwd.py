@@ -199,13 +199,14 @@ def test_linear_cuda_elu(dev, B, S, E):
     fused_lcu(dev, Qp, Kp, V, dO, B, S, D, E, tag=f"lcu fused ctx E{E}", use_ctx=True)
 
 
-@pytest.mark.parametrize("B,S,E", [(96, 256, 64), (2, 64, 64), (3, 77, 48), (2, 500, 20),
-                                   (1, 3000, 64), (2, 30, 100)])
+@pytest.mark.parametrize("B,S,E", [(96, 256, 64), (96, 250, 64), (2, 64, 64), (3, 77, 48),
+                                   (2, 500, 20), (1, 3000, 64), (2, 30, 100)])
 @pytest.mark.parametrize("use_ctx", [False, True])
 def test_linear_gpt_fused(dev, B, S, E, use_ctx):
     """cxg_lin_elu_fwd / _bwd against LinearGPT's own chain (linear_gpt.hpp:100-172):
     phi_elu_forward x2 -> causal_linear_attention_fwd; step1 -> dQ -> dKdV ->
-    phi_elu_backward x2, with D = next_pow2(E) zero-padded feature columns."""
+    phi_elu_backward x2, with D = next_pow2(E) zero-padded feature columns.  B96 S250:
+    four backward segments of four chunks a sequence, the last ending in a partial chunk."""
     import torch
     import cxxgpt_attn as cx
     D = 1 << (E - 1).bit_length()
